@@ -1,0 +1,274 @@
+/*
+ * it_kv.h -- C ABI of the MI355X (gfx950) KV-cache hot path.
+ *
+ * This is the drop-in boundary for InferTrain's KV-cache path.  Every entry
+ * point is `extern "C"`, takes plain pointers, sizes and a HIP stream passed
+ * as `void*`, and returns a status code that mirrors the reference's OpError
+ * (src/types.rs:227-231).  No call aborts: conditions the reference asserts
+ * on (src/backend/arm/flash_attn.rs:16-19, quant.rs:150) return
+ * IT_INVALID_INPUT, and it_last_error() holds a thread-local message.
+ *
+ * Memory: every tensor argument of a device entry point (it_kv_*, it_paged_*,
+ * it_flash_attention) is DEVICE memory owned by the caller; work is enqueued
+ * on `stream` and returns without synchronising.  Host-side objects
+ * (it_block_pool, it_kv_manager) take host memory.  Device-side checks that
+ * cannot be made before launch (a slot or block id out of range in a device
+ * array) never fault: the access is skipped or clamped, and the condition is
+ * latched in the cache and reported by it_kv_cache_check().
+ *
+ * dtype codes are the ggml QuantType ids of src/types.rs:106-144.
+ */
+#ifndef IT_KV_H
+#define IT_KV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes: OpError (src/types.rs:227-231) ----------------------- */
+#define IT_OK 0
+#define IT_NOT_IMPLEMENTED 1 /* OpError::NotImplemented */
+#define IT_INVALID_INPUT 2   /* OpError::InvalidInput  */
+#define IT_DEVICE_ERROR 3    /* OpError::DeviceError   */
+
+/* ---- dtype codes: QuantType (src/types.rs:106-144) ---------------------- */
+#define IT_F32 0
+#define IT_F16 1
+#define IT_Q8_0 8
+#define IT_BF16 30
+
+#define IT_BLOCK_SIZE 16        /* src/memory/paged.rs:9, default page size */
+#define IT_QK8_0 32             /* src/types.rs:11 */
+#define IT_BLOCK_Q8_0_BYTES 34  /* sizeof(BlockQ8_0), src/types.rs:34-41,250 */
+
+/* ---- operator ids for it_supports (Backend::supports_op/_quant,
+ *      src/backend.rs:184-186) ------------------------------------------- */
+#define IT_OP_KV_APPEND 1
+#define IT_OP_KV_GATHER 2
+#define IT_OP_KV_EVICT 3
+#define IT_OP_PAGED_DECODE 4
+#define IT_OP_PAGED_PREFILL 5
+#define IT_OP_FLASH_ATTENTION 6 /* CoreOperator::FlashAttention, src/types.rs:202-208 */
+#define IT_OP_KV_COPY_BLOCKS 7
+
+/* Thread-local message for the last non-OK status on this thread. */
+const char* it_last_error(void);
+int32_t it_abi_version(void);
+/* 1 if (op, dtype) is implemented, else 0.  dtype is the cache dtype. */
+int32_t it_supports(int32_t op, int32_t dtype);
+
+/* ======================================================================== */
+/* Host: block allocator.  Replaces memory::paged::BlockPool                */
+/* (src/memory/paged.rs:21-58).                                              */
+/* ======================================================================== */
+typedef struct it_block_pool it_block_pool;
+
+/* BlockPool::new (paged.rs:28-34): free list 0..capacity, refcounts 0. */
+int32_t it_block_pool_new(int64_t capacity, int32_t quant_type, it_block_pool** out);
+/* As new, but the free list is `order` (a permutation of 0..capacity-1),
+ * bottom to top, so the first allocate returns order[capacity-1]. */
+int32_t it_block_pool_new_ordered(const int64_t* order, int64_t capacity, int32_t quant_type,
+                                  it_block_pool** out);
+void it_block_pool_destroy(it_block_pool* pool);
+/* BlockPool::allocate (paged.rs:36-42): LIFO pop, refcount 1; -1 = None. */
+int64_t it_block_pool_allocate(it_block_pool* pool);
+/* BlockPool::share (paged.rs:44-46). */
+int32_t it_block_pool_share(it_block_pool* pool, int64_t id);
+/* BlockPool::free (paged.rs:48-53); a free at refcount 0 (a u32 underflow
+ * in the reference) is IT_INVALID_INPUT. */
+int32_t it_block_pool_free(it_block_pool* pool, int64_t id);
+/* BlockPool::quant_type (paged.rs:55-57). */
+int32_t it_block_pool_quant_type(const it_block_pool* pool);
+int64_t it_block_pool_num_free(const it_block_pool* pool);
+int64_t it_block_pool_capacity(const it_block_pool* pool);
+/* Refcount of `id`, -1 if out of range. */
+int64_t it_block_pool_ref_count(const it_block_pool* pool, int64_t id);
+
+/* ======================================================================== */
+/* Host: slot mapping, block tables and sliding-window eviction.  The        */
+/* reference batcher (src/batcher/continuous.rs:28-74) only admits requests; */
+/* this is the per-step state it lacks.                                      */
+/*   slot(pos) = table[pos / block_size] * block_size + pos % block_size     */
+/*   a block is allocated from the pool when pos % block_size == 0           */
+/*   window W > 0: before the token at position p, every held block whose    */
+/*   last position is < p - W + 1 is released with BlockPool::free, oldest   */
+/*   first; sequences are processed in the order the caller lists them.      */
+/* Block tables are indexed by absolute logical block (pos / block_size).    */
+/* ======================================================================== */
+typedef struct it_kv_manager it_kv_manager;
+
+/* The manager borrows `pool`; the pool must outlive it. window 0 = none. */
+int32_t it_kv_manager_new(it_block_pool* pool, int32_t block_size, int32_t max_seqs,
+                          int32_t max_blocks_per_seq, int32_t window, it_kv_manager** out);
+void it_kv_manager_destroy(it_kv_manager* mgr);
+/* Make sequence `seq` hold `blocks` (already allocated from the pool) as
+ * logical blocks first_block.., with the next token at position `pos`. */
+int32_t it_kv_manager_seed_seq(it_kv_manager* mgr, int32_t seq, int64_t pos, int64_t first_block,
+                               const int32_t* blocks, int32_t n_blocks);
+/* Append n_tokens[i] tokens to seqs[i], in list order.  Writes
+ * sum(n_tokens) slots into slots_out and the freed block ids, in free
+ * order, into evicted_out (capacity evicted_cap).  On error the manager
+ * state is unspecified. */
+int32_t it_kv_manager_append(it_kv_manager* mgr, const int32_t* seqs, const int32_t* n_tokens,
+                             int32_t n, int64_t* slots_out, int32_t* evicted_out,
+                             int32_t evicted_cap, int32_t* n_evicted);
+/* Release every block of `seq` (BlockPool::free, lowest logical block
+ * first) and reset it to position 0; the freed ids go to evicted_out. */
+int32_t it_kv_manager_release_seq(it_kv_manager* mgr, int32_t seq, int32_t* evicted_out,
+                                  int32_t evicted_cap, int32_t* n_evicted);
+/* Prefix sharing: dst takes src's blocks and position; each block gets
+ * BlockPool::share (paged.rs:44-46).  dst must be empty.  The first append
+ * to a shared partial block copies it (copy-on-write): the manager
+ * allocates a fresh block and reports the (src, dst) pair in cow_out. */
+int32_t it_kv_manager_fork(it_kv_manager* mgr, int32_t src_seq, int32_t dst_seq);
+int32_t it_kv_manager_append_cow(it_kv_manager* mgr, const int32_t* seqs, const int32_t* n_tokens,
+                                 int32_t n, int64_t* slots_out, int32_t* evicted_out,
+                                 int32_t evicted_cap, int32_t* n_evicted, int32_t* cow_src,
+                                 int32_t* cow_dst, int32_t cow_cap, int32_t* n_cow);
+/* Export tables [max_seqs][max_blocks] (-1 = not held), ctx_lens[max_seqs]
+ * (= next position) and start_pos[max_seqs] (window start, else 0).  Any
+ * output pointer may be NULL. */
+int32_t it_kv_manager_tables(const it_kv_manager* mgr, int32_t* tables, int32_t max_blocks,
+                             int32_t* ctx_lens, int32_t* start_pos);
+
+/* ======================================================================== */
+/* Device: the paged cache.  Replaces ForwardExecutor's contiguous           */
+/* kv_cache_k/kv_cache_v (src/inference/forward.rs:16-19, 31-37).            */
+/* Layout per pool (one for K, one for V), HBM:                              */
+/*   [num_blocks][n_kv_heads] pages; a page holds block_size token rows.     */
+/*   F32/F16/BF16 page: [block_size][head_dim] elements.                     */
+/*   Q8_0 page: int8 qs[block_size][head_dim], then fp16 d[block_size]       */
+/*   [head_dim/32] (structure of arrays of BlockQ8_0, src/types.rs:34-41).   */
+/* ======================================================================== */
+typedef struct it_kv_cache it_kv_cache;
+
+typedef struct {
+  void* k_pool;        /* device */
+  void* v_pool;        /* device */
+  int64_t num_blocks;
+  int64_t page_bytes;  /* bytes of one (block, head) page */
+  int32_t block_size;  /* power of two */
+  int32_t n_kv_heads;
+  int32_t head_dim;
+  int32_t dtype;
+  int32_t device;
+  int32_t owns_memory;
+} it_kv_cache_desc;
+
+int64_t it_kv_page_bytes(int32_t block_size, int32_t head_dim, int32_t dtype);
+/* Allocates both pools on `device` (hipMalloc) and zero-fills them. */
+int32_t it_kv_cache_new(int32_t device, int64_t num_blocks, int32_t block_size,
+                        int32_t n_kv_heads, int32_t head_dim, int32_t dtype, it_kv_cache** out);
+/* Wraps caller-owned pools (num_blocks * n_kv_heads * page_bytes each,
+ * 16-byte aligned).  The cache never frees them. */
+int32_t it_kv_cache_wrap(int32_t device, void* k_pool, void* v_pool, int64_t num_blocks,
+                         int32_t block_size, int32_t n_kv_heads, int32_t head_dim, int32_t dtype,
+                         it_kv_cache** out);
+int32_t it_kv_cache_destroy(it_kv_cache* cache);
+int32_t it_kv_cache_describe(const it_kv_cache* cache, it_kv_cache_desc* out);
+/* Synchronises `stream`, then reports (and clears) a latched device-side
+ * error: a slot, block id or block-table entry out of range seen by an
+ * earlier kernel on this cache.  IT_OK if none. */
+int32_t it_kv_cache_check(it_kv_cache* cache, void* stream);
+
+/* KV append: k_cache[slot/bs][h][slot%bs][:] = k[t][h][:], likewise v
+ * (forward.rs:219-229 with seq_pos generalised to a slot mapping).
+ *   k, v: [n_tokens][n_kv_heads][head_dim] of src_dtype, device.
+ *   slot_mapping: int64[n_tokens], device; slot < 0 = padding, skipped.
+ * F32/F16/BF16 caches take src_dtype == cache dtype (bit copy).  A Q8_0
+ * cache takes F32 and quantises each 32-group exactly as
+ * quantize_row_q8_0 (src/backend/arm/quant.rs:149-183). */
+int32_t it_kv_append(it_kv_cache* cache, const void* k, const void* v, int32_t src_dtype,
+                     const int64_t* slot_mapping, int32_t n_tokens, void* stream);
+
+/* Block-table gather: materialise the contiguous slices that
+ * forward.rs:233-243 reads, through a block table.
+ *   block_tables: int32[n_seqs][max_blocks] (absolute logical block index)
+ *   ctx_lens: int32[n_seqs]; start_pos: int32[n_seqs] or NULL (all 0)
+ *   cu_out: int64[n_seqs] output token offset of each sequence
+ *   max_tokens: upper bound of ctx_lens[b] - start_pos[b] (sizes the grid)
+ * Output for sequence b: [n_kv_heads][ctx_b - start_b][head_dim] at token
+ * offset cu_out[b] (element offset cu_out[b]*n_kv_heads*head_dim).  A Q8_0
+ * cache writes packed 34-byte BlockQ8_0 records, head_dim/32 per row. */
+int32_t it_kv_gather(const it_kv_cache* cache, const int32_t* block_tables, int32_t max_blocks,
+                     const int32_t* ctx_lens, const int32_t* start_pos, const int64_t* cu_out,
+                     int32_t n_seqs, int32_t max_tokens, void* k_out, void* v_out, void* stream);
+
+/* Evict: zero every page (all heads, K and V) of the given blocks, so a
+ * recycled block starts clean.  blocks: int32[n], device. */
+int32_t it_kv_evict(it_kv_cache* cache, const int32_t* blocks, int32_t n, void* stream);
+
+/* Copy-on-write page copy: block dst[i] := block src[i] (all heads, K, V). */
+int32_t it_kv_copy_blocks(it_kv_cache* cache, const int32_t* src, const int32_t* dst, int32_t n,
+                          void* stream);
+
+/* ======================================================================== */
+/* Device: attention over the cache.                                         */
+/* ======================================================================== */
+/* Workspace bytes it_paged_decode needs (fp32 partial (m, l, O) for every
+ * (sequence, head, partition)). */
+size_t it_paged_decode_workspace(int32_t n_seqs, int32_t n_heads, int32_t head_dim,
+                                 int32_t max_tokens, int32_t partition);
+
+/* Paged split-K flash-decode, one query per sequence.  For each sequence b
+ * and query head h the result equals flash_attn_f32 (flash_attn.rs:6-72)
+ * over keys start_b..ctx_b-1 of KV head h*Hkv/Hq (forward.rs:231-254),
+ * within fp32 tolerance.
+ *   q: [n_seqs][n_heads][head_dim]; q_dtype F32 (F32 and Q8_0 caches),
+ *      BF16 (BF16 cache) or F16 (F16 cache)
+ *   block_tables/ctx_lens/start_pos: as it_kv_gather
+ *   max_tokens: upper bound of ctx_b - start_b
+ *   partition: tokens per split (256, 512 or 1024)
+ *   ws: it_paged_decode_workspace(...) bytes, device
+ *   out: [n_seqs][n_heads][head_dim] of out_dtype (F32 or q_dtype)
+ * Two kernels: the split pass writes (m, l, O) per partition, the combine
+ * pass merges them.  n_heads must be a multiple of n_kv_heads. */
+int32_t it_paged_decode(const it_kv_cache* cache, const void* q, int32_t q_dtype, int32_t n_heads,
+                        const int32_t* block_tables, int32_t max_blocks, const int32_t* ctx_lens,
+                        const int32_t* start_pos, int32_t n_seqs, int32_t max_tokens, float scale,
+                        int32_t partition, void* ws, size_t ws_bytes, void* out,
+                        int32_t out_dtype, void* stream);
+
+/* The two passes of it_paged_decode as separate launches, same arguments:
+ * it_paged_decode_split then it_paged_decode_combine on one stream equals
+ * it_paged_decode (lets a caller time or schedule the passes apart). */
+int32_t it_paged_decode_split(const it_kv_cache* cache, const void* q, int32_t q_dtype, int32_t n_heads,
+                              const int32_t* block_tables, int32_t max_blocks, const int32_t* ctx_lens,
+                              const int32_t* start_pos, int32_t n_seqs, int32_t max_tokens, float scale,
+                              int32_t partition, void* ws, size_t ws_bytes, void* out, int32_t out_dtype,
+                              void* stream);
+int32_t it_paged_decode_combine(const it_kv_cache* cache, const void* q, int32_t q_dtype, int32_t n_heads,
+                                const int32_t* block_tables, int32_t max_blocks, const int32_t* ctx_lens,
+                                const int32_t* start_pos, int32_t n_seqs, int32_t max_tokens, float scale,
+                                int32_t partition, void* ws, size_t ws_bytes, void* out, int32_t out_dtype,
+                                void* stream);
+
+/* Chunked prefill attention over the cache (the chunk's K/V already
+ * appended).  Sequence b has q_len_b = cu_q[b+1]-cu_q[b] query rows at
+ * positions ctx_b - q_len_b + i; with causal != 0 row i attends keys
+ * 0..ctx_b - q_len_b + i, else all ctx_b keys.
+ *   q/out: [cu_q[n_seqs]][n_heads][head_dim], BF16 q; out F32 or BF16
+ *   cu_q: int32[n_seqs+1], device; max_q_len bounds q_len_b. */
+int32_t it_paged_prefill(const it_kv_cache* cache, const void* q, int32_t q_dtype, int32_t n_heads,
+                         const int32_t* cu_q, int32_t max_q_len, const int32_t* block_tables,
+                         int32_t max_blocks, const int32_t* ctx_lens, int32_t n_seqs, float scale,
+                         int32_t causal, void* out, int32_t out_dtype, void* stream);
+
+/* CoreOperator::FlashAttention as ArmCpuBackend executes it
+ * (src/backend/arm.rs:304-370): every one of n_heads query heads attends
+ * the same K/V [n_kv][head_dim] with scale 1/sqrtf(head_dim) and an
+ * optional additive mask [n_kv] (NULL = none; -inf skips the key).
+ *   q/out: [n_heads][head_dim] F32; k, v: [n_kv][head_dim] F32; device.
+ *   ws: it_flash_attention_workspace(...) bytes, device. */
+size_t it_flash_attention_workspace(int32_t n_heads, int32_t head_dim, int32_t n_kv);
+int32_t it_flash_attention(const float* q, const float* k, const float* v, const float* mask,
+                           float* out, int32_t n_heads, int32_t head_dim, int32_t n_kv, void* ws,
+                           size_t ws_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* IT_KV_H */

@@ -1,0 +1,221 @@
+// it_attn.hip -- C ABI of the attention entry points: paged split-K decode
+// (+ combine) and the Backend FlashAttention operator over contiguous K/V.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+
+#include "it_decode.hpp"
+#include "it_decode_launch.hpp"
+#include "it_internal.hpp"
+
+using namespace itkv;
+
+namespace {
+constexpr int kMaxParts = 4096;
+constexpr size_t kMaxDynLds = 64 * 1024;
+
+size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+struct WsLayout {
+  size_t o_bytes, ml_bytes, total;
+};
+WsLayout ws_layout(int64_t n_seqs, int64_t n_heads, int64_t head_dim, int64_t max_parts) {
+  WsLayout w;
+  w.o_bytes = align_up(size_t(n_seqs * n_heads * max_parts * head_dim) * 4, 256);
+  w.ml_bytes = align_up(size_t(n_seqs * n_heads * max_parts) * 8, 256);
+  w.total = w.o_bytes + w.ml_bytes;
+  return w;
+}
+
+int pick_chunk(int group) {
+  for (int g = 8; g >= 1; --g)
+    if (group % g == 0) return g;
+  return 1;
+}
+
+hipError_t launch_split(int32_t dt, int d, int gc, const DecodeArgs& a, dim3 grid, size_t smem, hipStream_t s) {
+  switch (dt) {
+    case IT_BF16: return launch_decode_bf16(d, gc, a, grid, smem, s);
+    case IT_F16: return launch_decode_f16(d, gc, a, grid, smem, s);
+    case IT_F32: return launch_decode_f32(d, gc, a, grid, smem, s);
+    case IT_Q8_0: return launch_decode_q8_0(d, gc, a, grid, smem, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_combine(int d, const DecodeArgs& a, int n_seqs, void* out, int32_t out_dtype, hipStream_t s) {
+  dim3 grid(unsigned(a.n_heads), unsigned(n_seqs));
+  if (d == 128)
+    hipLaunchKernelGGL(paged_decode_combine<128>, grid, dim3(64), 0, s, a.ws_o, a.ws_ml, a.ctx_lens,
+                       a.start_pos, a.ctx_const, a.n_heads, a.partition, a.max_parts, out, out_dtype);
+  else if (d == 256)
+    hipLaunchKernelGGL(paged_decode_combine<256>, grid, dim3(64), 0, s, a.ws_o, a.ws_ml, a.ctx_lens,
+                       a.start_pos, a.ctx_const, a.n_heads, a.partition, a.max_parts, out, out_dtype);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+// Shared driver of it_paged_decode and it_flash_attention.
+// phases: 1 = split pass, 2 = combine pass, 3 = both.
+int32_t run_decode(const char* who, int32_t cache_dt, int32_t q_dtype, int32_t out_dtype, int d,
+                   int n_seqs, int max_tokens, DecodeArgs a, void* ws, size_t ws_bytes, void* out,
+                   hipStream_t s, int phases = 3) {
+  const int32_t want_q = (cache_dt == IT_BF16 || cache_dt == IT_F16) ? cache_dt : IT_F32;
+  if (q_dtype != want_q)
+    return fail(IT_NOT_IMPLEMENTED, "%s: cache dtype %d takes q dtype %d, got %d", who, cache_dt, want_q, q_dtype);
+  if (out_dtype != IT_F32 && out_dtype != q_dtype)
+    return fail(IT_NOT_IMPLEMENTED, "%s: out dtype must be F32 or the q dtype", who);
+  if (d != 128 && d != 256) return fail(IT_NOT_IMPLEMENTED, "%s: head_dim %d (128 or 256 supported)", who, d);
+  if (a.log2_bs < 3) return fail(IT_NOT_IMPLEMENTED, "%s: block_size must be >= 8", who);
+  if (a.partition < 64 || a.partition > 2048 || a.partition % 64)
+    return fail(IT_INVALID_INPUT, "%s: partition %d must be a multiple of 64 in [64, 2048]", who, a.partition);
+  if (n_seqs <= 0 || n_seqs > 65535) return fail(IT_INVALID_INPUT, "%s: n_seqs %d outside [1, 65535]", who, n_seqs);
+  if (max_tokens < 0) return fail(IT_INVALID_INPUT, "%s: max_tokens %d < 0", who, max_tokens);
+  if (a.n_heads <= 0 || a.n_heads % a.n_kv_heads)
+    return fail(IT_INVALID_INPUT, "%s: n_heads %d must be a positive multiple of n_kv_heads %d", who, a.n_heads,
+                a.n_kv_heads);
+  if (!a.q || !out || !ws) return fail(IT_INVALID_INPUT, "%s: NULL tensor", who);
+  if ((reinterpret_cast<uintptr_t>(a.q) & 15u) || (reinterpret_cast<uintptr_t>(ws) & 255u))
+    return fail(IT_INVALID_INPUT, "%s: q must be 16-byte and ws 256-byte aligned", who);
+  a.max_parts = max_tokens > 0 ? (max_tokens + a.partition - 1) / a.partition : 1;
+  if (a.max_parts > kMaxParts) return fail(IT_INVALID_INPUT, "%s: %d partitions > %d", who, a.max_parts, kMaxParts);
+  const WsLayout w = ws_layout(n_seqs, a.n_heads, d, a.max_parts);
+  if (ws_bytes < w.total) return fail(IT_INVALID_INPUT, "%s: workspace %zu < %zu bytes", who, ws_bytes, w.total);
+  a.ws_o = static_cast<float*>(ws);
+  a.ws_ml = reinterpret_cast<float*>(static_cast<char*>(ws) + w.o_bytes);
+  a.group = a.n_heads / a.n_kv_heads;
+  const int gc = pick_chunk(a.group);
+  a.chunks = a.group / gc;
+  if (int64_t(a.n_kv_heads) * a.chunks > 65535) return fail(IT_NOT_IMPLEMENTED, "%s: too many head chunks", who);
+  const size_t smem = size_t(std::max(gc * a.partition, kDecodeWaves * gc * d)) * sizeof(float);
+  if (smem > kMaxDynLds) return fail(IT_INVALID_INPUT, "%s: partition %d needs %zu bytes of LDS", who, a.partition, smem);
+  if (max_tokens > 0 && (phases & 1)) {
+    dim3 grid(unsigned(a.max_parts), unsigned(a.n_kv_heads * a.chunks), unsigned(n_seqs));
+    hipError_t e = launch_split(cache_dt, d, gc, a, grid, smem, s);
+    if (e != hipSuccess) return fail(IT_DEVICE_ERROR, "%s: split launch: %s", who, hipGetErrorString(e));
+  }
+  if (phases & 2) {
+    hipError_t e = launch_combine(d, a, n_seqs, out, out_dtype, s);
+    if (e != hipSuccess) return fail(IT_DEVICE_ERROR, "%s: combine launch: %s", who, hipGetErrorString(e));
+  }
+  return IT_OK;
+}
+}  // namespace
+
+extern "C" size_t it_paged_decode_workspace(int32_t n_seqs, int32_t n_heads, int32_t head_dim,
+                                            int32_t max_tokens, int32_t partition) {
+  if (n_seqs <= 0 || n_heads <= 0 || head_dim <= 0 || partition <= 0 || max_tokens < 0) return 0;
+  const int64_t parts = max_tokens > 0 ? (int64_t(max_tokens) + partition - 1) / partition : 1;
+  return ws_layout(n_seqs, n_heads, head_dim, parts).total;
+}
+
+namespace {
+int32_t paged_decode_phases(const char* who, const it_kv_cache* c, const void* q, int32_t q_dtype,
+                            int32_t n_heads, const int32_t* block_tables, int32_t max_blocks,
+                            const int32_t* ctx_lens, const int32_t* start_pos, int32_t n_seqs,
+                            int32_t max_tokens, float scale, int32_t partition, void* ws, size_t ws_bytes,
+                            void* out, int32_t out_dtype, void* stream, int phases) {
+  if (!c) return fail(IT_INVALID_INPUT, "%s: cache is NULL", who);
+  if (!block_tables || !ctx_lens) return fail(IT_INVALID_INPUT, "%s: NULL block_tables/ctx_lens", who);
+  if (max_blocks <= 0) return fail(IT_INVALID_INPUT, "%s: max_blocks %d", who, max_blocks);
+  if (!(scale == scale)) return fail(IT_INVALID_INPUT, "%s: scale is NaN", who);
+  DecodeArgs a{};
+  a.q = q;
+  a.k_pool = static_cast<const char*>(c->k_pool);
+  a.v_pool = static_cast<const char*>(c->v_pool);
+  a.bt = block_tables;
+  a.ctx_lens = ctx_lens;
+  a.start_pos = start_pos;
+  a.mask = nullptr;
+  a.err = c->err_flag;
+  a.page_bytes = c->page_bytes;
+  a.num_blocks = c->num_blocks;
+  a.scale = scale;
+  a.scale_log2 = scale * kLog2e;
+  a.ctx_const = 0;
+  a.max_blocks = max_blocks;
+  a.n_heads = n_heads;
+  a.n_kv_heads = c->n_kv_heads;
+  a.log2_bs = c->log2_bs;
+  a.partition = partition;
+  int dev = -1;
+  (void)hipGetDevice(&dev);
+  if (dev != c->device) (void)hipSetDevice(c->device);
+  int32_t rc = run_decode(who, c->dtype, q_dtype, out_dtype, c->head_dim, n_seqs, max_tokens, a, ws, ws_bytes, out,
+                          (hipStream_t)stream, phases);
+  if (dev >= 0 && dev != c->device) (void)hipSetDevice(dev);
+  return rc;
+}
+}  // namespace
+
+#define IT_DECODE_ARGS                                                                                          \
+  const it_kv_cache *c, const void *q, int32_t q_dtype, int32_t n_heads, const int32_t *block_tables,          \
+      int32_t max_blocks, const int32_t *ctx_lens, const int32_t *start_pos, int32_t n_seqs, int32_t max_tokens, \
+      float scale, int32_t partition, void *ws, size_t ws_bytes, void *out, int32_t out_dtype, void *stream
+#define IT_DECODE_PASS \
+  c, q, q_dtype, n_heads, block_tables, max_blocks, ctx_lens, start_pos, n_seqs, max_tokens, scale, partition, ws, \
+      ws_bytes, out, out_dtype, stream
+
+extern "C" int32_t it_paged_decode(IT_DECODE_ARGS) {
+  return paged_decode_phases("it_paged_decode", IT_DECODE_PASS, 3);
+}
+extern "C" int32_t it_paged_decode_split(IT_DECODE_ARGS) {
+  return paged_decode_phases("it_paged_decode_split", IT_DECODE_PASS, 1);
+}
+extern "C" int32_t it_paged_decode_combine(IT_DECODE_ARGS) {
+  return paged_decode_phases("it_paged_decode_combine", IT_DECODE_PASS, 2);
+}
+
+// The Backend FlashAttention operator (src/backend/arm.rs:304-370) runs the
+// same kernels: contiguous K/V [n_kv][D] are pages of 16 rows under the
+// identity block table, one KV head shared by all n_heads query heads.
+namespace {
+constexpr int kFaPartition = 512;
+constexpr int kFaBlock = 16;
+}  // namespace
+
+extern "C" size_t it_flash_attention_workspace(int32_t n_heads, int32_t head_dim, int32_t n_kv) {
+  // Plus 256 bytes for the device error word.
+  return it_paged_decode_workspace(1, n_heads, head_dim, n_kv, kFaPartition) + 256;
+}
+
+extern "C" int32_t it_flash_attention(const float* q, const float* k, const float* v, const float* mask,
+                                      float* out, int32_t n_heads, int32_t head_dim, int32_t n_kv, void* ws,
+                                      size_t ws_bytes, void* stream) {
+  if (!q || !k || !v || !out || !ws) return fail(IT_INVALID_INPUT, "it_flash_attention: NULL tensor");
+  if (n_heads <= 0 || head_dim <= 0 || n_kv < 0)
+    return fail(IT_INVALID_INPUT, "it_flash_attention: n_heads=%d head_dim=%d n_kv=%d", n_heads, head_dim, n_kv);
+  if ((reinterpret_cast<uintptr_t>(k) & 15u) || (reinterpret_cast<uintptr_t>(v) & 15u))
+    return fail(IT_INVALID_INPUT, "it_flash_attention: k/v must be 16-byte aligned");
+  const size_t need = it_flash_attention_workspace(n_heads, head_dim, n_kv);
+  if (ws_bytes < need) return fail(IT_INVALID_INPUT, "it_flash_attention: workspace %zu < %zu bytes", ws_bytes, need);
+  DecodeArgs a{};
+  a.q = q;
+  a.k_pool = reinterpret_cast<const char*>(k);
+  a.v_pool = reinterpret_cast<const char*>(v);
+  a.bt = nullptr;
+  a.ctx_lens = nullptr;
+  a.start_pos = nullptr;
+  a.mask = mask;
+  a.err = reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + need - 256);
+  a.page_bytes = int64_t(kFaBlock) * head_dim * 4;
+  a.num_blocks = (int64_t(n_kv) + kFaBlock - 1) / kFaBlock;
+  if (a.num_blocks == 0) a.num_blocks = 1;
+  const float scale = 1.0f / sqrtf(float(head_dim));  // arm.rs:367
+  a.scale = scale;
+  a.scale_log2 = scale * kLog2e;
+  a.ctx_const = n_kv;
+  a.max_blocks = int32_t(a.num_blocks);
+  a.n_heads = n_heads;
+  a.n_kv_heads = 1;
+  a.log2_bs = 4;
+  a.partition = kFaPartition;
+  return run_decode("it_flash_attention", IT_F32, IT_F32, IT_F32, head_dim, 1, n_kv, a, ws, need - 256, out,
+                    (hipStream_t)stream);
+}
+
+extern "C" int32_t it_paged_prefill(const it_kv_cache* c, const void* q, int32_t q_dtype, int32_t n_heads,
+                                    const int32_t* cu_q, int32_t max_q_len, const int32_t* block_tables,
+                                    int32_t max_blocks, const int32_t* ctx_lens, int32_t n_seqs, float scale,
+                                    int32_t causal, void* out, int32_t out_dtype, void* stream);

@@ -1,0 +1,483 @@
+// it_cache.hip -- the paged KV cache on gfx950: pool allocation, slot-mapped
+// append (bit copy or Q8_0 quantise), block-table gather, evict (page clear)
+// and copy-on-write page copy.
+//
+// All of these are HBM-bound data movement.  Each lane moves one 16-byte
+// vector (global_load_dwordx4 / global_store_dwordx4) and consecutive lanes
+// cover consecutive bytes of a token row, so a wavefront touches whole
+// 128-byte lines of both source and destination.
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+
+#include "it_device.hpp"
+#include "it_internal.hpp"
+
+using namespace itkv;
+
+#define IT_HIP(call, what)                                                          \
+  do {                                                                              \
+    hipError_t e_ = (call);                                                         \
+    if (e_ != hipSuccess) return fail(IT_DEVICE_ERROR, "%s: %s", what, hipGetErrorString(e_)); \
+  } while (0)
+
+namespace {
+constexpr int kThreads = 256;
+
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// ---------------------------------------------------------------------------
+// Append, bit copy (F32 / F16 / BF16).  One lane = one 16-byte vector of one
+// (token, head) row, for K and for V.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void kv_append_copy(
+    const uint4* __restrict__ k, const uint4* __restrict__ v, char* __restrict__ kpool,
+    char* __restrict__ vpool, const int64_t* __restrict__ slots, int64_t total, int hkv,
+    int row_vecs, int log2_bs, int64_t page_bytes, int64_t n_slots, uint32_t* err) {
+  const int64_t gid = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  if (gid >= total) return;
+  const int c = int(gid % row_vecs);
+  const int64_t th = gid / row_vecs;
+  const int h = int(th % hkv);
+  const int64_t t = th / hkv;
+  const int64_t slot = slots[t];
+  if (slot < 0) return;  // padding token
+  if (slot >= n_slots) {
+    if (c == 0 && h == 0) atomicOr(err, kErrSlot);
+    return;
+  }
+  const int64_t blk = slot >> log2_bs;
+  const int64_t off = slot & ((int64_t(1) << log2_bs) - 1);
+  const int64_t dst = (blk * hkv + h) * page_bytes + (off * row_vecs + c) * 16;
+  st16(kpool + dst, k[gid]);
+  st16(vpool + dst, v[gid]);
+}
+
+// ---------------------------------------------------------------------------
+// Append with Q8_0 quantisation (quantize_row_q8_0, quant.rs:149-183).
+// Eight lanes own one 32-element group, four floats each (one 16-byte load).
+// blockIdx.y selects K (0) or V (1).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int32_t q8_round(float x, float scale) {
+  // quant.rs:176-178: (x / scale).round() as i32, then clamp to [-128, 127].
+  // IEEE division (v_div_scale/fmas/fixup), round half away from zero; NaN
+  // -> 0 as Rust's saturating `as` does.
+  float r = roundf(x / scale);
+  if (r != r) return 0;
+  r = fminf(fmaxf(r, -128.0f), 127.0f);
+  return int32_t(r);
+}
+
+__global__ __launch_bounds__(kThreads) void kv_append_q8_0(
+    const float4* __restrict__ k, const float4* __restrict__ v, char* __restrict__ kpool,
+    char* __restrict__ vpool, const int64_t* __restrict__ slots, int64_t total, int hkv, int d,
+    int log2_bs, int64_t page_bytes, int64_t n_slots, uint32_t* err) {
+  const int64_t gid = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  const bool is_v = blockIdx.y != 0;
+  const bool live = gid < total;
+  const float4 x = live ? (is_v ? v[gid] : k[gid]) : make_float4(0.f, 0.f, 0.f, 0.f);
+  // amax with NaN ignored (quant.rs:157-163 compares with `>`).
+  auto absn = [](float f) { return f == f ? fabsf(f) : 0.0f; };
+  float amax = fmaxf(fmaxf(absn(x.x), absn(x.y)), fmaxf(absn(x.z), absn(x.w)));
+  amax = group_max<8>(amax);  // the 8 lanes of the group are lane-aligned
+  if (!live) return;
+  const int vecs_per_row = d >> 2;
+  const int cv = int(gid % vecs_per_row);   // vector index in the row
+  const int64_t th = gid / vecs_per_row;
+  const int h = int(th % hkv);
+  const int64_t t = th / hkv;
+  const int64_t slot = slots[t];
+  if (slot < 0) return;
+  if (slot >= n_slots) {
+    if (cv == 0 && h == 0) atomicOr(err, kErrSlot);
+    return;
+  }
+  uint32_t packed = 0;
+  uint32_t dbits = 0;
+  if (amax != 0.0f) {  // quant.rs:166-170: an all-zero group stores d=0, qs=0
+    const float scale = amax / 127.0f;  // quant.rs:173
+    packed = (uint32_t(q8_round(x.x, scale)) & 0xFFu) | ((uint32_t(q8_round(x.y, scale)) & 0xFFu) << 8) |
+             ((uint32_t(q8_round(x.z, scale)) & 0xFFu) << 16) | ((uint32_t(q8_round(x.w, scale)) & 0xFFu) << 24);
+    dbits = f32_to_f16_bits(scale);  // quant.rs:181 (fp16 of the unrounded scale)
+  }
+  const int64_t blk = slot >> log2_bs;
+  const int64_t off = slot & ((int64_t(1) << log2_bs) - 1);
+  const int64_t bs = int64_t(1) << log2_bs;
+  char* page = (is_v ? vpool : kpool) + (blk * hkv + h) * page_bytes;
+  *reinterpret_cast<uint32_t*>(page + off * d + cv * 4) = packed;
+  if ((cv & 7) == 0) {
+    const int g = cv >> 3;
+    *reinterpret_cast<uint16_t*>(page + bs * d + (off * (d >> 5) + g) * 2) = uint16_t(dbits);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Gather.  grid.y = sequence; lane = one 16-byte vector of one output row.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void kv_gather_vec(
+    const char* __restrict__ kpool, const char* __restrict__ vpool, const int32_t* __restrict__ bt,
+    int max_blocks, const int32_t* __restrict__ ctx_lens, const int32_t* __restrict__ start_pos,
+    const int64_t* __restrict__ cu_out, int hkv, int row_vecs, int log2_bs, int64_t page_bytes,
+    int64_t num_blocks, uint4* __restrict__ kout, uint4* __restrict__ vout, uint32_t* err) {
+  const int b = blockIdx.y;
+  const int st = start_pos ? start_pos[b] : 0;
+  const int n = ctx_lens[b] - st;
+  if (n <= 0 || st < 0) return;
+  const int64_t gid = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  if (gid >= int64_t(hkv) * n * row_vecs) return;
+  const int c = int(gid % row_vecs);
+  const int64_t r = gid / row_vecs;
+  const int i = int(r % n);
+  const int h = int(r / n);
+  const int pos = st + i;
+  const int lb = pos >> log2_bs;
+  if (lb >= max_blocks) {
+    atomicOr(err, kErrTable);
+    return;
+  }
+  const int blk = bt[int64_t(b) * max_blocks + lb];
+  if (blk < 0 || blk >= num_blocks) {
+    atomicOr(err, kErrBlock);
+    return;
+  }
+  const int64_t src = (int64_t(blk) * hkv + h) * page_bytes +
+                      (int64_t(pos & ((1 << log2_bs) - 1)) * row_vecs + c) * 16;
+  const int64_t dst = (cu_out[b] * hkv + int64_t(h) * n + i) * row_vecs + c;
+  kout[dst] = ld16(kpool + src);
+  vout[dst] = ld16(vpool + src);
+}
+
+// Q8_0 gather: lane = one 32-element group, written as a packed 34-byte
+// BlockQ8_0 record {u16 d; i8 qs[32]} (types.rs:34-41).
+__global__ __launch_bounds__(kThreads) void kv_gather_q8_0(
+    const char* __restrict__ kpool, const char* __restrict__ vpool, const int32_t* __restrict__ bt,
+    int max_blocks, const int32_t* __restrict__ ctx_lens, const int32_t* __restrict__ start_pos,
+    const int64_t* __restrict__ cu_out, int hkv, int d, int log2_bs, int64_t page_bytes,
+    int64_t num_blocks, char* __restrict__ kout, char* __restrict__ vout, uint32_t* err) {
+  const int b = blockIdx.y;
+  const int st = start_pos ? start_pos[b] : 0;
+  const int n = ctx_lens[b] - st;
+  if (n <= 0 || st < 0) return;
+  const int ng = d >> 5;
+  const int64_t gid = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  if (gid >= int64_t(hkv) * n * ng) return;
+  const int g = int(gid % ng);
+  const int64_t r = gid / ng;
+  const int i = int(r % n);
+  const int h = int(r / n);
+  const int pos = st + i;
+  const int lb = pos >> log2_bs;
+  if (lb >= max_blocks) {
+    atomicOr(err, kErrTable);
+    return;
+  }
+  const int blk = bt[int64_t(b) * max_blocks + lb];
+  if (blk < 0 || blk >= num_blocks) {
+    atomicOr(err, kErrBlock);
+    return;
+  }
+  const int64_t bs = int64_t(1) << log2_bs;
+  const int64_t off = pos & (bs - 1);
+  const int64_t rec = ((cu_out[b] * hkv + int64_t(h) * n + i) * ng + g) * 34;
+  for (int which = 0; which < 2; ++which) {
+    const char* page = (which ? vpool : kpool) + (int64_t(blk) * hkv + h) * page_bytes;
+    const uint4 q0 = ld16(page + off * d + g * 32);
+    const uint4 q1 = ld16(page + off * d + g * 32 + 16);
+    const uint16_t dd = *reinterpret_cast<const uint16_t*>(page + bs * d + (off * ng + g) * 2);
+    uint16_t* o = reinterpret_cast<uint16_t*>((which ? vout : kout) + rec);  // 2-byte aligned
+    o[0] = dd;
+    const uint32_t w[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      o[1 + 2 * j] = uint16_t(w[j] & 0xFFFFu);
+      o[2 + 2 * j] = uint16_t(w[j] >> 16);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Evict (zero pages) and copy-on-write page copy.  grid.y = list entry.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void kv_clear_blocks(char* __restrict__ kpool,
+                                                            char* __restrict__ vpool,
+                                                            const int32_t* __restrict__ blocks,
+                                                            int64_t block_vecs, int64_t num_blocks,
+                                                            uint32_t* err) {
+  const int blk = blocks[blockIdx.y];
+  if (blk < 0 || blk >= num_blocks) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) atomicOr(err, kErrBlock);
+    return;
+  }
+  const uint4 z = make_uint4(0u, 0u, 0u, 0u);
+  for (int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x; i < block_vecs; i += int64_t(gridDim.x) * kThreads) {
+    st16(kpool + (blk * block_vecs + i) * 16, z);
+    st16(vpool + (blk * block_vecs + i) * 16, z);
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void kv_copy_blocks(char* __restrict__ kpool,
+                                                           char* __restrict__ vpool,
+                                                           const int32_t* __restrict__ src,
+                                                           const int32_t* __restrict__ dst,
+                                                           int64_t block_vecs, int64_t num_blocks,
+                                                           uint32_t* err) {
+  const int s = src[blockIdx.y], d = dst[blockIdx.y];
+  if (s < 0 || s >= num_blocks || d < 0 || d >= num_blocks) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) atomicOr(err, kErrBlock);
+    return;
+  }
+  for (int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x; i < block_vecs; i += int64_t(gridDim.x) * kThreads) {
+    st16(kpool + (d * block_vecs + i) * 16, ld16(kpool + (s * block_vecs + i) * 16));
+    st16(vpool + (d * block_vecs + i) * 16, ld16(vpool + (s * block_vecs + i) * 16));
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Cache set-up.
+// ---------------------------------------------------------------------------
+int32_t check_shape(int64_t num_blocks, int32_t block_size, int32_t n_kv_heads, int32_t head_dim,
+                    int32_t dtype) {
+  if (num_blocks <= 0 || n_kv_heads <= 0 || head_dim <= 0)
+    return fail(IT_INVALID_INPUT, "kv cache: num_blocks=%lld n_kv_heads=%d head_dim=%d must be > 0",
+                (long long)num_blocks, n_kv_heads, head_dim);
+  if (!is_pow2(block_size) || block_size > 1024)
+    return fail(IT_NOT_IMPLEMENTED, "kv cache: block_size %d must be a power of two <= 1024", block_size);
+  if (dtype == IT_Q8_0) {
+    if (head_dim % IT_QK8_0) return fail(IT_INVALID_INPUT, "kv cache: Q8_0 needs head_dim %% 32 == 0");
+    if (block_size < 8) return fail(IT_NOT_IMPLEMENTED, "kv cache: Q8_0 needs block_size >= 8");
+  } else if (dtype_bytes(dtype) == 0) {
+    return fail(IT_NOT_IMPLEMENTED, "kv cache: dtype %d not supported (F32=0, F16=1, Q8_0=8, BF16=30)", dtype);
+  } else if ((head_dim * dtype_bytes(dtype)) % 16) {
+    return fail(IT_NOT_IMPLEMENTED, "kv cache: head_dim*elem_bytes must be a multiple of 16");
+  }
+  return IT_OK;
+}
+
+int32_t make_cache(int32_t device, void* k, void* v, int64_t num_blocks, int32_t block_size,
+                   int32_t n_kv_heads, int32_t head_dim, int32_t dtype, int32_t owns, it_kv_cache** out) {
+  auto* c = new (std::nothrow) it_kv_cache;
+  if (!c) return fail(IT_DEVICE_ERROR, "kv cache: out of host memory");
+  c->k_pool = k;
+  c->v_pool = v;
+  c->num_blocks = num_blocks;
+  c->page_bytes = it_kv_page_bytes(block_size, head_dim, dtype);
+  c->block_size = block_size;
+  c->log2_bs = ilog2(block_size);
+  c->n_kv_heads = n_kv_heads;
+  c->head_dim = head_dim;
+  c->dtype = dtype;
+  c->device = device;
+  c->owns_memory = owns;
+  c->err_flag = nullptr;
+  hipError_t e = hipMalloc(&c->err_flag, 256);
+  if (e == hipSuccess) e = hipMemset(c->err_flag, 0, 256);
+  if (e != hipSuccess) {
+    delete c;
+    return fail(IT_DEVICE_ERROR, "kv cache: error word allocation: %s", hipGetErrorString(e));
+  }
+  *out = c;
+  return IT_OK;
+}
+
+struct DeviceGuard {
+  int prev = -1;
+  explicit DeviceGuard(int dev) {
+    if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+    if (prev != dev) (void)hipSetDevice(dev);
+  }
+  ~DeviceGuard() {
+    int cur = -1;
+    if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+  }
+};
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+}  // namespace
+
+extern "C" int64_t it_kv_page_bytes(int32_t block_size, int32_t head_dim, int32_t dtype) {
+  if (block_size <= 0 || head_dim <= 0) return -1;
+  if (dtype == IT_Q8_0) return int64_t(block_size) * head_dim + int64_t(block_size) * (head_dim / IT_QK8_0) * 2;
+  int64_t e = dtype_bytes(dtype);
+  return e ? int64_t(block_size) * head_dim * e : -1;
+}
+
+extern "C" int32_t it_kv_cache_new(int32_t device, int64_t num_blocks, int32_t block_size,
+                                   int32_t n_kv_heads, int32_t head_dim, int32_t dtype,
+                                   it_kv_cache** out) {
+  if (!out) return fail(IT_INVALID_INPUT, "it_kv_cache_new: out is NULL");
+  *out = nullptr;
+  if (int32_t rc = check_shape(num_blocks, block_size, n_kv_heads, head_dim, dtype)) return rc;
+  DeviceGuard g(device);
+  const size_t bytes = size_t(num_blocks) * size_t(n_kv_heads) * size_t(it_kv_page_bytes(block_size, head_dim, dtype));
+  void *k = nullptr, *v = nullptr;
+  hipError_t e = hipMalloc(&k, bytes);
+  if (e == hipSuccess) e = hipMalloc(&v, bytes);
+  if (e == hipSuccess) e = hipMemset(k, 0, bytes);
+  if (e == hipSuccess) e = hipMemset(v, 0, bytes);
+  if (e != hipSuccess) {
+    if (k) (void)hipFree(k);
+    if (v) (void)hipFree(v);
+    return fail(IT_DEVICE_ERROR, "it_kv_cache_new: %zu bytes per pool: %s", bytes, hipGetErrorString(e));
+  }
+  int32_t rc = make_cache(device, k, v, num_blocks, block_size, n_kv_heads, head_dim, dtype, 1, out);
+  if (rc) {
+    (void)hipFree(k);
+    (void)hipFree(v);
+  }
+  return rc;
+}
+
+extern "C" int32_t it_kv_cache_wrap(int32_t device, void* k_pool, void* v_pool, int64_t num_blocks,
+                                    int32_t block_size, int32_t n_kv_heads, int32_t head_dim,
+                                    int32_t dtype, it_kv_cache** out) {
+  if (!out) return fail(IT_INVALID_INPUT, "it_kv_cache_wrap: out is NULL");
+  *out = nullptr;
+  if (!k_pool || !v_pool) return fail(IT_INVALID_INPUT, "it_kv_cache_wrap: NULL pool");
+  if (!aligned16(k_pool) || !aligned16(v_pool)) return fail(IT_INVALID_INPUT, "it_kv_cache_wrap: pools must be 16-byte aligned");
+  if (int32_t rc = check_shape(num_blocks, block_size, n_kv_heads, head_dim, dtype)) return rc;
+  DeviceGuard g(device);
+  return make_cache(device, k_pool, v_pool, num_blocks, block_size, n_kv_heads, head_dim, dtype, 0, out);
+}
+
+extern "C" int32_t it_kv_cache_destroy(it_kv_cache* c) {
+  if (!c) return IT_OK;
+  DeviceGuard g(c->device);
+  if (c->owns_memory) {
+    (void)hipFree(c->k_pool);
+    (void)hipFree(c->v_pool);
+  }
+  (void)hipFree(c->err_flag);
+  delete c;
+  return IT_OK;
+}
+
+extern "C" int32_t it_kv_cache_describe(const it_kv_cache* c, it_kv_cache_desc* d) {
+  if (!c || !d) return fail(IT_INVALID_INPUT, "it_kv_cache_describe: NULL argument");
+  d->k_pool = c->k_pool;
+  d->v_pool = c->v_pool;
+  d->num_blocks = c->num_blocks;
+  d->page_bytes = c->page_bytes;
+  d->block_size = c->block_size;
+  d->n_kv_heads = c->n_kv_heads;
+  d->head_dim = c->head_dim;
+  d->dtype = c->dtype;
+  d->device = c->device;
+  d->owns_memory = c->owns_memory;
+  return IT_OK;
+}
+
+extern "C" int32_t it_kv_cache_check(it_kv_cache* c, void* stream) {
+  if (!c) return fail(IT_INVALID_INPUT, "it_kv_cache_check: cache is NULL");
+  DeviceGuard g(c->device);
+  uint32_t flag = 0;
+  IT_HIP(hipStreamSynchronize((hipStream_t)stream), "it_kv_cache_check: sync");
+  IT_HIP(hipMemcpy(&flag, c->err_flag, 4, hipMemcpyDeviceToHost), "it_kv_cache_check: read flag");
+  if (!flag) return IT_OK;
+  IT_HIP(hipMemset(c->err_flag, 0, 4), "it_kv_cache_check: clear flag");
+  return fail(IT_INVALID_INPUT, "kv cache: device-side range error (%s%s%s%s)", (flag & kErrSlot) ? "slot " : "",
+              (flag & kErrBlock) ? "block-id " : "", (flag & kErrTable) ? "table-index " : "", (flag & kErrCtx) ? "ctx>max_tokens" : "");
+}
+
+extern "C" int32_t it_kv_append(it_kv_cache* c, const void* k, const void* v, int32_t src_dtype,
+                                const int64_t* slots, int32_t n_tokens, void* stream) {
+  if (!c) return fail(IT_INVALID_INPUT, "it_kv_append: cache is NULL");
+  if (n_tokens < 0) return fail(IT_INVALID_INPUT, "it_kv_append: n_tokens %d < 0", n_tokens);
+  if (n_tokens == 0) return IT_OK;
+  if (!k || !v || !slots) return fail(IT_INVALID_INPUT, "it_kv_append: NULL tensor");
+  const int32_t want = c->dtype == IT_Q8_0 ? IT_F32 : c->dtype;
+  if (src_dtype != want)
+    return fail(IT_NOT_IMPLEMENTED, "it_kv_append: cache dtype %d takes source dtype %d, got %d", c->dtype, want, src_dtype);
+  if (!aligned16(k) || !aligned16(v)) return fail(IT_INVALID_INPUT, "it_kv_append: k/v must be 16-byte aligned");
+  DeviceGuard g(c->device);
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t n_slots = c->num_blocks << c->log2_bs;
+  if (c->dtype == IT_Q8_0) {
+    const int64_t total = int64_t(n_tokens) * c->n_kv_heads * (c->head_dim / 4);
+    dim3 grid(unsigned(cdiv(total, kThreads)), 2);
+    hipLaunchKernelGGL(kv_append_q8_0, grid, dim3(kThreads), 0, s, (const float4*)k, (const float4*)v,
+                       (char*)c->k_pool, (char*)c->v_pool, slots, total, c->n_kv_heads, c->head_dim,
+                       c->log2_bs, c->page_bytes, n_slots, c->err_flag);
+  } else {
+    const int row_vecs = int(c->head_dim * dtype_bytes(c->dtype) / 16);
+    const int64_t total = int64_t(n_tokens) * c->n_kv_heads * row_vecs;
+    hipLaunchKernelGGL(kv_append_copy, dim3(unsigned(cdiv(total, kThreads))), dim3(kThreads), 0, s,
+                       (const uint4*)k, (const uint4*)v, (char*)c->k_pool, (char*)c->v_pool, slots, total,
+                       c->n_kv_heads, row_vecs, c->log2_bs, c->page_bytes, n_slots, c->err_flag);
+  }
+  IT_HIP(hipGetLastError(), "it_kv_append: launch");
+  return IT_OK;
+}
+
+extern "C" int32_t it_kv_gather(const it_kv_cache* c, const int32_t* bt, int32_t max_blocks,
+                                const int32_t* ctx_lens, const int32_t* start_pos, const int64_t* cu_out,
+                                int32_t n_seqs, int32_t max_tokens, void* k_out, void* v_out,
+                                void* stream) {
+  if (!c) return fail(IT_INVALID_INPUT, "it_kv_gather: cache is NULL");
+  if (n_seqs < 0 || max_tokens < 0 || max_blocks <= 0)
+    return fail(IT_INVALID_INPUT, "it_kv_gather: n_seqs=%d max_tokens=%d max_blocks=%d", n_seqs, max_tokens, max_blocks);
+  if (n_seqs == 0 || max_tokens == 0) return IT_OK;
+  if (!bt || !ctx_lens || !cu_out || !k_out || !v_out) return fail(IT_INVALID_INPUT, "it_kv_gather: NULL tensor");
+  if (n_seqs > 65535) return fail(IT_NOT_IMPLEMENTED, "it_kv_gather: n_seqs %d > 65535", n_seqs);
+  DeviceGuard g(c->device);
+  hipStream_t s = (hipStream_t)stream;
+  if (c->dtype == IT_Q8_0) {
+    const int64_t per_seq = int64_t(c->n_kv_heads) * max_tokens * (c->head_dim / 32);
+    dim3 grid(unsigned(cdiv(per_seq, kThreads)), unsigned(n_seqs));
+    hipLaunchKernelGGL(kv_gather_q8_0, grid, dim3(kThreads), 0, s, (const char*)c->k_pool, (const char*)c->v_pool,
+                       bt, max_blocks, ctx_lens, start_pos, cu_out, c->n_kv_heads, c->head_dim, c->log2_bs,
+                       c->page_bytes, c->num_blocks, (char*)k_out, (char*)v_out, c->err_flag);
+  } else {
+    if (!aligned16(k_out) || !aligned16(v_out)) return fail(IT_INVALID_INPUT, "it_kv_gather: outputs must be 16-byte aligned");
+    const int row_vecs = int(c->head_dim * dtype_bytes(c->dtype) / 16);
+    const int64_t per_seq = int64_t(c->n_kv_heads) * max_tokens * row_vecs;
+    dim3 grid(unsigned(cdiv(per_seq, kThreads)), unsigned(n_seqs));
+    hipLaunchKernelGGL(kv_gather_vec, grid, dim3(kThreads), 0, s, (const char*)c->k_pool, (const char*)c->v_pool,
+                       bt, max_blocks, ctx_lens, start_pos, cu_out, c->n_kv_heads, row_vecs, c->log2_bs,
+                       c->page_bytes, c->num_blocks, (uint4*)k_out, (uint4*)v_out, c->err_flag);
+  }
+  IT_HIP(hipGetLastError(), "it_kv_gather: launch");
+  return IT_OK;
+}
+
+extern "C" int32_t it_kv_evict(it_kv_cache* c, const int32_t* blocks, int32_t n, void* stream) {
+  if (!c) return fail(IT_INVALID_INPUT, "it_kv_evict: cache is NULL");
+  if (n < 0 || n > 65535) return fail(IT_INVALID_INPUT, "it_kv_evict: n=%d outside [0, 65535]", n);
+  if (n == 0) return IT_OK;
+  if (!blocks) return fail(IT_INVALID_INPUT, "it_kv_evict: blocks is NULL");
+  DeviceGuard g(c->device);
+  const int64_t block_vecs = c->page_bytes * c->n_kv_heads / 16;
+  dim3 grid(unsigned(cdiv(block_vecs, kThreads) > 64 ? 64 : cdiv(block_vecs, kThreads)), unsigned(n));
+  hipLaunchKernelGGL(kv_clear_blocks, grid, dim3(kThreads), 0, (hipStream_t)stream, (char*)c->k_pool,
+                     (char*)c->v_pool, blocks, block_vecs, c->num_blocks, c->err_flag);
+  IT_HIP(hipGetLastError(), "it_kv_evict: launch");
+  return IT_OK;
+}
+
+extern "C" int32_t it_kv_copy_blocks(it_kv_cache* c, const int32_t* src, const int32_t* dst, int32_t n,
+                                     void* stream) {
+  if (!c) return fail(IT_INVALID_INPUT, "it_kv_copy_blocks: cache is NULL");
+  if (n < 0 || n > 65535) return fail(IT_INVALID_INPUT, "it_kv_copy_blocks: n=%d outside [0, 65535]", n);
+  if (n == 0) return IT_OK;
+  if (!src || !dst) return fail(IT_INVALID_INPUT, "it_kv_copy_blocks: NULL list");
+  DeviceGuard g(c->device);
+  const int64_t block_vecs = c->page_bytes * c->n_kv_heads / 16;
+  dim3 grid(unsigned(cdiv(block_vecs, kThreads) > 64 ? 64 : cdiv(block_vecs, kThreads)), unsigned(n));
+  hipLaunchKernelGGL(kv_copy_blocks, grid, dim3(kThreads), 0, (hipStream_t)stream, (char*)c->k_pool,
+                     (char*)c->v_pool, src, dst, block_vecs, c->num_blocks, c->err_flag);
+  IT_HIP(hipGetLastError(), "it_kv_copy_blocks: launch");
+  return IT_OK;
+}
+
+extern "C" int32_t it_supports(int32_t op, int32_t dtype) {
+  const bool kv = dtype == IT_F32 || dtype == IT_F16 || dtype == IT_BF16 || dtype == IT_Q8_0;
+  switch (op) {
+    case IT_OP_KV_APPEND:
+    case IT_OP_KV_GATHER:
+    case IT_OP_KV_EVICT:
+    case IT_OP_KV_COPY_BLOCKS:
+    case IT_OP_PAGED_DECODE: return kv ? 1 : 0;
+    case IT_OP_PAGED_PREFILL: return dtype == IT_BF16 ? 1 : 0;
+    case IT_OP_FLASH_ATTENTION: return dtype == IT_F32 ? 1 : 0;
+    default: return 0;
+  }
+}

@@ -1,0 +1,10 @@
+// it_decode_f32.hip -- instantiates the split-K decode kernels for F32 caches
+// (kept in its own translation unit so the instantiations build in parallel).
+#include "it_decode.hpp"
+#include "it_decode_launch.hpp"
+
+namespace itkv {
+hipError_t launch_decode_f32(int d, int gc, const DecodeArgs& a, dim3 grid, size_t smem, hipStream_t s) {
+  return launch_decode_typed<IT_F32>(d, gc, a, grid, smem, s);
+}
+}  // namespace itkv

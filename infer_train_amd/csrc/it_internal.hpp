@@ -1,0 +1,49 @@
+// it_internal.hpp -- shared declarations of the libit_kv implementation.
+#pragma once
+#include <cstdint>
+
+#include "it_kv.h"
+
+namespace itkv {
+// Sets the thread-local message and returns `code`.
+int32_t fail(int32_t code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+
+// Bits latched in it_kv_cache::err_flag by kernels (reported by
+// it_kv_cache_check).
+enum : uint32_t {
+  kErrSlot = 1u,        // slot_mapping entry >= num_blocks * block_size
+  kErrBlock = 2u,       // block id (table, evict or copy list) out of range
+  kErrTable = 4u,       // logical block beyond max_blocks
+  kErrCtx = 8u,         // context longer than the max_tokens bound
+};
+
+inline bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
+inline int ilog2(int64_t x) {
+  int r = 0;
+  while ((int64_t(1) << r) < x) ++r;
+  return r;
+}
+inline int64_t dtype_bytes(int32_t dt) {
+  switch (dt) {
+    case IT_F32: return 4;
+    case IT_F16: return 2;
+    case IT_BF16: return 2;
+    default: return 0;
+  }
+}
+}  // namespace itkv
+
+struct it_kv_cache {
+  void* k_pool;
+  void* v_pool;
+  uint32_t* err_flag;  // device word
+  int64_t num_blocks;
+  int64_t page_bytes;
+  int32_t block_size;
+  int32_t log2_bs;
+  int32_t n_kv_heads;
+  int32_t head_dim;
+  int32_t dtype;
+  int32_t device;
+  int32_t owns_memory;
+};

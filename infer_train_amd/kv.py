@@ -1,0 +1,174 @@
+"""Device-side KV cache and attention entry points.
+
+Thin wrappers that pass torch tensors' device pointers and the current HIP
+stream to libit_kv.so.  torch only provides device memory and streams; all
+work runs in the library's gfx950 kernels.  Shapes follow include/it_kv.h.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+from typing import Optional, Tuple
+
+import torch
+
+from ._lib import BF16, CacheDesc, F16, F32, Q8_0, check, lib
+
+__all__ = ["PagedKvCache", "flash_attention", "torch_dtype_id", "stream_handle"]
+
+_TORCH_IDS = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
+_ID_TORCH = {F32: torch.float32, F16: torch.float16, BF16: torch.bfloat16}
+
+
+def torch_dtype_id(t: torch.dtype) -> int:
+    try:
+        return _TORCH_IDS[t]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {t}") from None
+
+
+def stream_handle(device: Optional[torch.device] = None) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise ValueError("device tensor expected")
+    if not t.is_contiguous():
+        raise ValueError("contiguous tensor expected")
+    return t.data_ptr()
+
+
+class PagedKvCache:
+    """Paged K/V pools in HBM, [num_blocks][n_kv_heads] pages of block_size
+    token rows (Q8_0 pages: int8 rows then fp16 group scales)."""
+
+    def __init__(self, num_blocks: int, block_size: int, n_kv_heads: int, head_dim: int, dtype: int = BF16,
+                 device: int = 0):
+        page = lib.it_kv_page_bytes(block_size, head_dim, dtype)
+        if page <= 0:
+            raise ValueError("unsupported cache shape")
+        nbytes = num_blocks * n_kv_heads * page
+        dev = torch.device("cuda", device)
+        self.k_pool = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+        self.v_pool = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+        h = C.c_void_p()
+        check(lib.it_kv_cache_wrap(device, self.k_pool.data_ptr(), self.v_pool.data_ptr(), num_blocks, block_size,
+                                   n_kv_heads, head_dim, dtype, C.byref(h)))
+        self._h = h
+        self.num_blocks, self.block_size, self.n_kv_heads, self.head_dim = num_blocks, block_size, n_kv_heads, head_dim
+        self.dtype = dtype
+        self.page_bytes = page
+        self.device = dev
+
+    @property
+    def handle(self) -> C.c_void_p:
+        return self._h
+
+    def describe(self) -> CacheDesc:
+        d = CacheDesc()
+        check(lib.it_kv_cache_describe(self._h, C.byref(d)))
+        return d
+
+    def view(self, which: str = "k") -> torch.Tensor:
+        """Typed view [num_blocks, n_kv_heads, block_size, head_dim] (F32/F16/BF16)."""
+        pool = self.k_pool if which == "k" else self.v_pool
+        if self.dtype == Q8_0:
+            raise TypeError("use q8_planes() for a Q8_0 cache")
+        return pool.view(_ID_TORCH[self.dtype]).view(self.num_blocks, self.n_kv_heads, self.block_size, self.head_dim)
+
+    def q8_planes(self, which: str = "k") -> Tuple[torch.Tensor, torch.Tensor]:
+        """(qs int8 [nb, H, bs, D], d fp16 bits int16 [nb, H, bs, D/32]) of a Q8_0 cache."""
+        pool = (self.k_pool if which == "k" else self.v_pool).view(self.num_blocks, self.n_kv_heads, self.page_bytes)
+        bs, D = self.block_size, self.head_dim
+        qs = pool[:, :, : bs * D].view(torch.int8).reshape(self.num_blocks, self.n_kv_heads, bs, D)
+        d = pool[:, :, bs * D:].contiguous().view(torch.int16).reshape(self.num_blocks, self.n_kv_heads, bs, D // 32)
+        return qs, d
+
+    def check(self) -> None:
+        """Raise if a kernel latched a device-side range error (syncs the stream)."""
+        check(lib.it_kv_cache_check(self._h, stream_handle(self.device)))
+
+    # ---- data movement ----------------------------------------------------
+    def append(self, k: torch.Tensor, v: torch.Tensor, slot_mapping: torch.Tensor) -> None:
+        """k, v: [n_tokens, n_kv_heads, head_dim]; slot_mapping int64 [n_tokens]."""
+        if slot_mapping.dtype != torch.int64:
+            raise TypeError("slot_mapping must be int64")
+        n = slot_mapping.numel()
+        check(lib.it_kv_append(self._h, _ptr(k), _ptr(v), torch_dtype_id(k.dtype), _ptr(slot_mapping), n,
+                               stream_handle(self.device)))
+
+    def gather(self, block_tables: torch.Tensor, ctx_lens: torch.Tensor, start_pos: Optional[torch.Tensor],
+               cu_out: torch.Tensor, max_tokens: int, k_out: torch.Tensor, v_out: torch.Tensor) -> None:
+        check(lib.it_kv_gather(self._h, _ptr(block_tables), block_tables.shape[1], _ptr(ctx_lens), _ptr(start_pos),
+                               _ptr(cu_out), ctx_lens.numel(), max_tokens, _ptr(k_out), _ptr(v_out),
+                               stream_handle(self.device)))
+
+    def evict(self, blocks: torch.Tensor) -> None:
+        check(lib.it_kv_evict(self._h, _ptr(blocks), blocks.numel(), stream_handle(self.device)))
+
+    def copy_blocks(self, src: torch.Tensor, dst: torch.Tensor) -> None:
+        check(lib.it_kv_copy_blocks(self._h, _ptr(src), _ptr(dst), src.numel(), stream_handle(self.device)))
+
+    # ---- attention --------------------------------------------------------
+    def decode_workspace(self, n_seqs: int, n_heads: int, max_tokens: int, partition: int = 512) -> torch.Tensor:
+        nbytes = lib.it_paged_decode_workspace(n_seqs, n_heads, self.head_dim, max_tokens, partition)
+        return torch.empty(nbytes, dtype=torch.uint8, device=self.device)
+
+    def decode(self, q: torch.Tensor, block_tables: torch.Tensor, ctx_lens: torch.Tensor,
+               start_pos: Optional[torch.Tensor], max_tokens: int, scale: Optional[float] = None,
+               partition: int = 512, out: Optional[torch.Tensor] = None, ws: Optional[torch.Tensor] = None,
+               out_dtype: Optional[torch.dtype] = None, phase: str = "both") -> torch.Tensor:
+        """q: [n_seqs, n_heads, head_dim] -> out [n_seqs, n_heads, head_dim].
+        phase "split" / "combine" launches one pass (same arguments)."""
+        n_seqs, n_heads, D = q.shape
+        if scale is None:
+            scale = 1.0 / math.sqrt(D)
+        if out is None:
+            out = torch.empty(q.shape, dtype=out_dtype or q.dtype, device=q.device)
+        if ws is None:
+            ws = self.decode_workspace(n_seqs, n_heads, max_tokens, partition)
+        fn = {"both": lib.it_paged_decode, "split": lib.it_paged_decode_split,
+              "combine": lib.it_paged_decode_combine}[phase]
+        check(fn(self._h, _ptr(q), torch_dtype_id(q.dtype), n_heads, _ptr(block_tables),
+                                  block_tables.shape[1], _ptr(ctx_lens), _ptr(start_pos), n_seqs, max_tokens,
+                                  C.c_float(scale), partition, _ptr(ws), ws.numel(), _ptr(out),
+                                  torch_dtype_id(out.dtype), stream_handle(self.device)))
+        return out
+
+    def prefill(self, q: torch.Tensor, cu_q: torch.Tensor, max_q_len: int, block_tables: torch.Tensor,
+                ctx_lens: torch.Tensor, scale: Optional[float] = None, causal: bool = True,
+                out: Optional[torch.Tensor] = None, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+        """q: [total_q, n_heads, head_dim] bf16 -> out [total_q, n_heads, head_dim]."""
+        total, n_heads, D = q.shape
+        if scale is None:
+            scale = 1.0 / math.sqrt(D)
+        if out is None:
+            out = torch.empty(q.shape, dtype=out_dtype or q.dtype, device=q.device)
+        check(lib.it_paged_prefill(self._h, _ptr(q), torch_dtype_id(q.dtype), n_heads, _ptr(cu_q), max_q_len,
+                                   _ptr(block_tables), block_tables.shape[1], _ptr(ctx_lens), ctx_lens.numel(),
+                                   C.c_float(scale), int(bool(causal)), _ptr(out), torch_dtype_id(out.dtype),
+                                   stream_handle(self.device)))
+        return out
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h is not None and h.value:
+            lib.it_kv_cache_destroy(h)
+            self._h = C.c_void_p()
+
+
+def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask: Optional[torch.Tensor] = None,
+                    out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """CoreOperator::FlashAttention as ArmCpuBackend runs it (arm.rs:304-370):
+    q [n_heads, D] f32, k/v [n_kv, D] f32 shared by all heads, mask [n_kv]."""
+    n_heads, D = q.shape
+    n_kv = k.shape[0]
+    if out is None:
+        out = torch.empty_like(q)
+    ws = torch.empty(lib.it_flash_attention_workspace(n_heads, D, n_kv), dtype=torch.uint8, device=q.device)
+    check(lib.it_flash_attention(_ptr(q), _ptr(k), _ptr(v), _ptr(mask), _ptr(out), n_heads, D, n_kv, _ptr(ws),
+                                 ws.numel(), stream_handle(q.device)))
+    return out

@@ -1,0 +1,634 @@
+/*
+ * it_oracle.c -- CPU oracle for the KV-cache hot path (TEST INFRASTRUCTURE).
+ *
+ * A plain-C restatement of the reference crate's CPU arithmetic, used only
+ * as the checker for the HIP library (tests/, smoke()) and as bench.py's CPU
+ * baseline.  Never linked into the product library.  Built with
+ * -O2 -ffp-contract=off and no fast-math so that every a*b+c rounds twice, as
+ * the Rust reference does.  Reference paths are relative to the reference
+ * crate root.
+ */
+#include "it_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------------ */
+/* Seeded synthetic inputs (test plumbing, no reference counterpart).        */
+/* ------------------------------------------------------------------------ */
+uint64_t orc_splitmix64(uint64_t* state) {
+  uint64_t z = (*state += 0x9E3779B97F4A7C15ull);
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+static double u01_open(uint64_t* st) {
+  /* (0, 1]: never 0 so log() is finite. */
+  return ((double)(orc_splitmix64(st) >> 11) + 1.0) * (1.0 / 9007199254740992.0);
+}
+
+void orc_fill_normal_f32(uint64_t seed, float* out, size_t n) {
+  uint64_t st = seed;
+  const double two_pi = 6.283185307179586476925286766559;
+  size_t i = 0;
+  while (i < n) {
+    double u1 = u01_open(&st), u2 = u01_open(&st);
+    double r = sqrt(-2.0 * log(u1));
+    out[i++] = (float)(r * cos(two_pi * u2));
+    if (i < n) out[i++] = (float)(r * sin(two_pi * u2));
+  }
+}
+
+void orc_fill_uniform_i32(uint64_t seed, int32_t lo, int32_t hi, int32_t* out, size_t n) {
+  uint64_t st = seed;
+  uint64_t span = (uint64_t)((int64_t)hi - (int64_t)lo + 1);
+  for (size_t i = 0; i < n; ++i) out[i] = (int32_t)((int64_t)lo + (int64_t)(orc_splitmix64(&st) % span));
+}
+
+void orc_permutation_i64(uint64_t seed, int64_t* out, size_t n) {
+  uint64_t st = seed;
+  for (size_t i = 0; i < n; ++i) out[i] = (int64_t)i;
+  for (size_t i = n; i > 1; --i) {
+    size_t j = (size_t)(orc_splitmix64(&st) % i);
+    int64_t t = out[i - 1];
+    out[i - 1] = out[j];
+    out[j] = t;
+  }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Scalar conversions.                                                       */
+/* ------------------------------------------------------------------------ */
+static uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+/* IEEE binary32 -> binary16, round to nearest even, with subnormals, as the
+ * `half` crate's f16::from_f32 (types.rs:237-240 -> half 2.7.1). */
+uint16_t orc_f32_to_f16(float f) {
+  uint32_t x = f2u(f);
+  uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+  uint32_t exp = (x >> 23) & 0xFFu;
+  uint32_t man = x & 0x7FFFFFu;
+  if (exp == 0xFFu) {
+    if (man == 0) return sign | 0x7C00u;                       /* inf */
+    return sign | 0x7E00u | (uint16_t)(man >> 13);             /* quiet NaN */
+  }
+  int32_t e = (int32_t)exp - 127 + 15;                           /* rebias */
+  if (e >= 0x1F) return sign | 0x7C00u;                          /* overflow */
+  if (e <= 0) {                                                  /* subnormal/zero */
+    if (e < -10) return sign;                                    /* < half of min subnormal */
+    uint32_t m = man | 0x800000u;                                /* implicit bit */
+    uint32_t shift = (uint32_t)(14 - e);                         /* 14..24 */
+    uint32_t half_bit = 1u << (shift - 1);
+    uint32_t rem = m & ((1u << shift) - 1u);
+    uint32_t q = m >> shift;
+    if (rem > half_bit || (rem == half_bit && (q & 1u))) q += 1;
+    return sign | (uint16_t)q;                                   /* may carry into exp 1 */
+  }
+  uint32_t q = ((uint32_t)e << 10) | (man >> 13);
+  uint32_t rem = man & 0x1FFFu;
+  if (rem > 0x1000u || (rem == 0x1000u && (q & 1u))) q += 1;     /* carry may reach inf */
+  return sign | (uint16_t)q;
+}
+
+float orc_f16_to_f32(uint16_t h) {
+  uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+  uint32_t exp = (h >> 10) & 0x1Fu;
+  uint32_t man = h & 0x3FFu;
+  if (exp == 0) {
+    if (man == 0) return u2f(sign);
+    /* subnormal: value = man * 2^-24, exact in f32 */
+    float v = (float)man * (1.0f / 16777216.0f);
+    return (sign ? -v : v);
+  }
+  if (exp == 0x1F) return u2f(sign | 0x7F800000u | (man << 13));
+  return u2f(sign | ((exp - 15 + 127) << 23) | (man << 13));
+}
+
+uint16_t orc_f32_to_bf16(float f) {
+  uint32_t u = f2u(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u); /* quiet NaN */
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+float orc_bf16_to_f32(uint16_t h) { return u2f((uint32_t)h << 16); }
+
+void orc_f32_to_bf16_array(const float* in, uint16_t* out, size_t n) {
+  for (size_t i = 0; i < n; ++i) out[i] = orc_f32_to_bf16(in[i]);
+}
+void orc_bf16_to_f32_array(const uint16_t* in, float* out, size_t n) {
+  for (size_t i = 0; i < n; ++i) out[i] = orc_bf16_to_f32(in[i]);
+}
+void orc_f32_to_f16_array(const float* in, uint16_t* out, size_t n) {
+  for (size_t i = 0; i < n; ++i) out[i] = orc_f32_to_f16(in[i]);
+}
+void orc_f16_to_f32_array(const uint16_t* in, float* out, size_t n) {
+  for (size_t i = 0; i < n; ++i) out[i] = orc_f16_to_f32(in[i]);
+}
+
+/* ------------------------------------------------------------------------ */
+/* BlockPool -- src/memory/paged.rs:21-58                                     */
+/* ------------------------------------------------------------------------ */
+struct orc_block_pool {
+  int64_t* free_list; /* Vec<usize>; top of stack = free_list[n_free-1] */
+  int64_t n_free;
+  uint32_t* ref_counts; /* Vec<u32> */
+  int64_t capacity;
+  int32_t quant_type;
+};
+
+orc_block_pool* orc_pool_new(int64_t capacity, int32_t quant_type) {
+  /* paged.rs:28-34 */
+  if (capacity < 0) return NULL;
+  orc_block_pool* p = (orc_block_pool*)calloc(1, sizeof(*p));
+  p->free_list = (int64_t*)malloc(sizeof(int64_t) * (size_t)(capacity ? capacity : 1));
+  p->ref_counts = (uint32_t*)calloc((size_t)(capacity ? capacity : 1), sizeof(uint32_t));
+  for (int64_t i = 0; i < capacity; ++i) p->free_list[i] = i;
+  p->n_free = capacity;
+  p->capacity = capacity;
+  p->quant_type = quant_type;
+  return p;
+}
+
+orc_block_pool* orc_pool_new_ordered(const int64_t* order, int64_t capacity, int32_t quant_type) {
+  orc_block_pool* p = orc_pool_new(capacity, quant_type);
+  if (!p) return NULL;
+  for (int64_t i = 0; i < capacity; ++i) p->free_list[i] = order[i];
+  return p;
+}
+
+void orc_pool_destroy(orc_block_pool* p) {
+  if (!p) return;
+  free(p->free_list);
+  free(p->ref_counts);
+  free(p);
+}
+
+int64_t orc_pool_allocate(orc_block_pool* p) {
+  /* paged.rs:36-42: Vec::pop() takes the LAST element. */
+  if (p->n_free == 0) return -1;
+  int64_t id = p->free_list[--p->n_free];
+  p->ref_counts[id] = 1;
+  return id;
+}
+
+int orc_pool_share(orc_block_pool* p, int64_t id) {
+  /* paged.rs:44-46 */
+  if (id < 0 || id >= p->capacity || p->ref_counts[id] == 0) return ORC_INVALID_INPUT;
+  p->ref_counts[id] += 1;
+  return ORC_OK;
+}
+
+int orc_pool_free(orc_block_pool* p, int64_t id) {
+  /* paged.rs:48-53; ref 0 would underflow the reference's u32. */
+  if (id < 0 || id >= p->capacity || p->ref_counts[id] == 0) return ORC_INVALID_INPUT;
+  p->ref_counts[id] -= 1;
+  if (p->ref_counts[id] == 0) p->free_list[p->n_free++] = id;
+  return ORC_OK;
+}
+
+int32_t orc_pool_quant_type(const orc_block_pool* p) { return p->quant_type; }
+int64_t orc_pool_num_free(const orc_block_pool* p) { return p->n_free; }
+int64_t orc_pool_ref_count(const orc_block_pool* p, int64_t id) {
+  if (id < 0 || id >= p->capacity) return -1;
+  return (int64_t)p->ref_counts[id];
+}
+void orc_pool_free_list(const orc_block_pool* p, int64_t* out) {
+  memcpy(out, p->free_list, sizeof(int64_t) * (size_t)p->n_free);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Q8_0 -- src/backend/arm/quant.rs:149-183 (x86 scalar path, :265-268)     */
+/* ------------------------------------------------------------------------ */
+/* Rust `f as i32` saturates and maps NaN to 0. */
+static int32_t rust_f32_as_i32(float f) {
+  if (f != f) return 0;
+  if (f >= 2147483648.0f) return INT32_MAX;
+  if (f <= -2147483648.0f) return INT32_MIN;
+  return (int32_t)f;
+}
+
+int orc_quantize_row_q8_0(const float* x, size_t n, uint8_t* y) {
+  if (n % ORC_QK8_0) return ORC_INVALID_INPUT; /* quant.rs:150 assert */
+  size_t nb = n / ORC_QK8_0;
+  for (size_t i = 0; i < nb; ++i) {
+    const float* xb = x + i * ORC_QK8_0;
+    uint8_t* rec = y + i * ORC_BLOCK_Q8_0_BYTES;
+    float amax = 0.0f; /* quant.rs:157-163: `>` ignores NaN */
+    for (int j = 0; j < ORC_QK8_0; ++j) {
+      float a = fabsf(xb[j]);
+      if (a > amax) amax = a;
+    }
+    if (amax == 0.0f) { /* quant.rs:166-170 */
+      memset(rec, 0, ORC_BLOCK_Q8_0_BYTES);
+      continue;
+    }
+    float scale = amax / 127.0f; /* quant.rs:173, f32 divide */
+    for (int j = 0; j < ORC_QK8_0; ++j) {
+      int32_t v = rust_f32_as_i32(roundf(xb[j] / scale)); /* quant.rs:176-177 */
+      if (v > 127) v = 127;
+      if (v < -128) v = -128; /* quant.rs:178 */
+      rec[2 + j] = (uint8_t)(int8_t)v;
+    }
+    uint16_t d = orc_f32_to_f16(scale); /* quant.rs:181, unrounded scale above */
+    rec[0] = (uint8_t)(d & 0xFF);       /* little-endian u16, repr(C) */
+    rec[1] = (uint8_t)(d >> 8);
+  }
+  return ORC_OK;
+}
+
+void orc_dequantize_row_q8_0(const uint8_t* y, size_t n, float* x) {
+  size_t nb = n / ORC_QK8_0;
+  for (size_t i = 0; i < nb; ++i) {
+    const uint8_t* rec = y + i * ORC_BLOCK_Q8_0_BYTES;
+    float d = orc_f16_to_f32((uint16_t)(rec[0] | (rec[1] << 8)));
+    for (int j = 0; j < ORC_QK8_0; ++j) x[i * ORC_QK8_0 + j] = d * (float)(int8_t)rec[2 + j];
+  }
+}
+
+/* ------------------------------------------------------------------------ */
+/* flash_attn_f32 -- src/backend/arm/flash_attn.rs:6-72                       */
+/* ------------------------------------------------------------------------ */
+void orc_flash_attn_f32(const float* q, const float* k, const float* v, const float* mask,
+                        float* out, int32_t head_dim, int32_t n_kv, float scale) {
+  for (int32_t i = 0; i < head_dim; ++i) out[i] = 0.0f; /* :21-23 */
+  float m = -INFINITY, s = 0.0f;                         /* :25-26 */
+  for (int32_t i_kv = 0; i_kv < n_kv; ++i_kv) {          /* :28 */
+    float kq = 0.0f;
+    const float* kr = k + (size_t)i_kv * head_dim;
+    for (int32_t d = 0; d < head_dim; ++d) kq += q[d] * kr[d]; /* :29-32 sequential */
+    kq *= scale;                                               /* :33 */
+    if (mask) {                                                /* :35-40 */
+      kq += mask[i_kv];
+      if (mask[i_kv] == -INFINITY) continue;
+    }
+    float m_old = m, k_vs, m_scale;
+    if (kq > m) { /* :46-53 */
+      m = kq;
+      m_scale = expf(m_old - m);
+      k_vs = 1.0f;
+    } else {
+      m_scale = 1.0f;
+      k_vs = expf(kq - m);
+    }
+    const float* vr = v + (size_t)i_kv * head_dim;
+    for (int32_t d = 0; d < head_dim; ++d) out[d] *= m_scale;     /* :55-57 */
+    for (int32_t d = 0; d < head_dim; ++d) out[d] += vr[d] * k_vs; /* :59-61 */
+    s = s * m_scale + k_vs;                                         /* :63 */
+  }
+  if (s > 0.0f) { /* :66-71 */
+    float inv_s = 1.0f / s;
+    for (int32_t d = 0; d < head_dim; ++d) out[d] *= inv_s;
+  }
+}
+
+int orc_backend_flash_attention(const float* q, const float* k, const float* v,
+                                const float* mask, float* out, int32_t n_heads,
+                                int32_t head_dim, int32_t n_kv) {
+  /* src/backend/arm.rs:304-370: every head reads the same K/V and mask. */
+  if (n_heads <= 0 || head_dim <= 0 || n_kv < 0) return ORC_INVALID_INPUT;
+  float scale = 1.0f / sqrtf((float)head_dim);
+  for (int32_t h = 0; h < n_heads; ++h)
+    orc_flash_attn_f32(q + (size_t)h * head_dim, k, v, mask, out + (size_t)h * head_dim,
+                       head_dim, n_kv, scale);
+  return ORC_OK;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Paged cache restatement.                                                  */
+/* ------------------------------------------------------------------------ */
+static size_t elem_bytes(int32_t dtype) {
+  switch (dtype) {
+    case ORC_F32: return 4;
+    case ORC_F16: return 2;
+    case ORC_BF16: return 2;
+    default: return 0;
+  }
+}
+
+static int desc_ok(const orc_cache_desc* c) {
+  if (c->num_blocks <= 0 || c->block_size <= 0 || c->n_kv_heads <= 0 || c->head_dim <= 0) return 0;
+  if (c->dtype == ORC_Q8_0) return c->head_dim % ORC_QK8_0 == 0;
+  return elem_bytes(c->dtype) != 0;
+}
+
+size_t orc_page_bytes(const orc_cache_desc* c) {
+  size_t bs = (size_t)c->block_size, d = (size_t)c->head_dim;
+  if (c->dtype == ORC_Q8_0) return bs * d + bs * (d / ORC_QK8_0) * 2;
+  return bs * d * elem_bytes(c->dtype);
+}
+
+static uint8_t* page_ptr(const orc_cache_desc* c, const uint8_t* pool, int64_t block, int32_t h) {
+  return (uint8_t*)pool + ((size_t)block * (size_t)c->n_kv_heads + (size_t)h) * orc_page_bytes(c);
+}
+
+/* Write one token row (head_dim values) of one head into its page slot. */
+static void put_row(const orc_cache_desc* c, uint8_t* page, int32_t slot, const void* src_row) {
+  size_t d = (size_t)c->head_dim;
+  if (c->dtype == ORC_Q8_0) {
+    size_t ng = d / ORC_QK8_0;
+    uint8_t rec[ORC_BLOCK_Q8_0_BYTES];
+    uint8_t* qs = page + (size_t)slot * d;
+    uint8_t* sc = page + (size_t)c->block_size * d + (size_t)slot * ng * 2;
+    for (size_t g = 0; g < ng; ++g) {
+      orc_quantize_row_q8_0((const float*)src_row + g * ORC_QK8_0, ORC_QK8_0, rec);
+      memcpy(qs + g * ORC_QK8_0, rec + 2, ORC_QK8_0);
+      sc[g * 2] = rec[0];
+      sc[g * 2 + 1] = rec[1];
+    }
+  } else {
+    size_t rb = d * elem_bytes(c->dtype);
+    memcpy(page + (size_t)slot * rb, src_row, rb);
+  }
+}
+
+int orc_kv_append(const orc_cache_desc* c, uint8_t* k_pool, uint8_t* v_pool,
+                  const void* k, const void* v, const int64_t* slots, int32_t n_tokens) {
+  if (!desc_ok(c) || n_tokens < 0) return ORC_INVALID_INPUT;
+  size_t src_eb = c->dtype == ORC_Q8_0 ? 4 : elem_bytes(c->dtype);
+  size_t row = (size_t)c->head_dim * src_eb;
+  int64_t n_slots = c->num_blocks * c->block_size;
+  for (int32_t t = 0; t < n_tokens; ++t) {
+    int64_t slot = slots[t];
+    if (slot < 0) continue; /* padding token */
+    if (slot >= n_slots) return ORC_INVALID_INPUT;
+    int64_t blk = slot / c->block_size;
+    int32_t off = (int32_t)(slot % c->block_size);
+    for (int32_t h = 0; h < c->n_kv_heads; ++h) {
+      size_t src_off = ((size_t)t * c->n_kv_heads + h) * row;
+      put_row(c, page_ptr(c, k_pool, blk, h), off, (const uint8_t*)k + src_off);
+      put_row(c, page_ptr(c, v_pool, blk, h), off, (const uint8_t*)v + src_off);
+    }
+  }
+  return ORC_OK;
+}
+
+/* Copy the stored row of `slot` in a page: native bytes, or a BlockQ8_0 AoS
+ * record sequence for Q8_0. */
+static void get_row_raw(const orc_cache_desc* c, const uint8_t* page, int32_t slot, uint8_t* dst) {
+  size_t d = (size_t)c->head_dim;
+  if (c->dtype == ORC_Q8_0) {
+    size_t ng = d / ORC_QK8_0;
+    const uint8_t* qs = page + (size_t)slot * d;
+    const uint8_t* sc = page + (size_t)c->block_size * d + (size_t)slot * ng * 2;
+    for (size_t g = 0; g < ng; ++g) {
+      uint8_t* rec = dst + g * ORC_BLOCK_Q8_0_BYTES;
+      rec[0] = sc[g * 2];
+      rec[1] = sc[g * 2 + 1];
+      memcpy(rec + 2, qs + g * ORC_QK8_0, ORC_QK8_0);
+    }
+  } else {
+    size_t rb = d * elem_bytes(c->dtype);
+    memcpy(dst, page + (size_t)slot * rb, rb);
+  }
+}
+
+static size_t row_out_bytes(const orc_cache_desc* c) {
+  if (c->dtype == ORC_Q8_0) return (size_t)(c->head_dim / ORC_QK8_0) * ORC_BLOCK_Q8_0_BYTES;
+  return (size_t)c->head_dim * elem_bytes(c->dtype);
+}
+
+/* Widen one stored row to f32 (bf16/f16 exact, Q8_0 = f32(d)*q). */
+static void get_row_f32(const orc_cache_desc* c, const uint8_t* page, int32_t slot, float* dst) {
+  size_t d = (size_t)c->head_dim;
+  switch (c->dtype) {
+    case ORC_F32: memcpy(dst, page + (size_t)slot * d * 4, d * 4); break;
+    case ORC_BF16: orc_bf16_to_f32_array((const uint16_t*)(page + (size_t)slot * d * 2), dst, d); break;
+    case ORC_F16: orc_f16_to_f32_array((const uint16_t*)(page + (size_t)slot * d * 2), dst, d); break;
+    case ORC_Q8_0: {
+      uint8_t rec[8 * ORC_BLOCK_Q8_0_BYTES * 4];
+      size_t ng = d / ORC_QK8_0;
+      uint8_t* buf = ng * ORC_BLOCK_Q8_0_BYTES <= sizeof(rec) ? rec : (uint8_t*)malloc(ng * ORC_BLOCK_Q8_0_BYTES);
+      get_row_raw(c, page, slot, buf);
+      orc_dequantize_row_q8_0(buf, d, dst);
+      if (buf != rec) free(buf);
+      break;
+    }
+  }
+}
+
+int orc_kv_gather(const orc_cache_desc* c, const uint8_t* k_pool, const uint8_t* v_pool,
+                  const int32_t* block_tables, int32_t max_blocks, const int32_t* ctx_lens,
+                  const int32_t* start_pos, const int64_t* cu_out, int32_t n_seqs,
+                  void* k_out, void* v_out) {
+  if (!desc_ok(c) || n_seqs < 0) return ORC_INVALID_INPUT;
+  size_t rb = row_out_bytes(c);
+  for (int32_t b = 0; b < n_seqs; ++b) {
+    int32_t st = start_pos ? start_pos[b] : 0;
+    int32_t n = ctx_lens[b] - st;
+    if (st < 0 || n < 0) return ORC_INVALID_INPUT;
+    for (int32_t h = 0; h < c->n_kv_heads; ++h)
+      for (int32_t i = 0; i < n; ++i) {
+        int32_t pos = st + i;
+        int32_t lb = pos / c->block_size;
+        if (lb >= max_blocks) return ORC_INVALID_INPUT;
+        int32_t blk = block_tables[(size_t)b * max_blocks + lb];
+        if (blk < 0 || blk >= c->num_blocks) return ORC_INVALID_INPUT;
+        size_t o = (((size_t)cu_out[b] * c->n_kv_heads) + (size_t)h * n + i) * rb;
+        get_row_raw(c, page_ptr(c, k_pool, blk, h), pos % c->block_size, (uint8_t*)k_out + o);
+        get_row_raw(c, page_ptr(c, v_pool, blk, h), pos % c->block_size, (uint8_t*)v_out + o);
+      }
+  }
+  return ORC_OK;
+}
+
+int orc_kv_evict(const orc_cache_desc* c, uint8_t* k_pool, uint8_t* v_pool,
+                 const int32_t* blocks, int32_t n) {
+  if (!desc_ok(c) || n < 0) return ORC_INVALID_INPUT;
+  size_t pb = orc_page_bytes(c) * (size_t)c->n_kv_heads;
+  for (int32_t i = 0; i < n; ++i) {
+    if (blocks[i] < 0 || blocks[i] >= c->num_blocks) return ORC_INVALID_INPUT;
+    memset(k_pool + (size_t)blocks[i] * pb, 0, pb);
+    memset(v_pool + (size_t)blocks[i] * pb, 0, pb);
+  }
+  return ORC_OK;
+}
+
+/* Widen keys/values [st, st+n) of kv head h of sequence b to f32 rows. */
+static int widen_seq(const orc_cache_desc* c, const uint8_t* k_pool, const uint8_t* v_pool,
+                     const int32_t* table, int32_t max_blocks, int32_t h, int32_t st, int32_t n,
+                     float* kf, float* vf) {
+  for (int32_t i = 0; i < n; ++i) {
+    int32_t pos = st + i, lb = pos / c->block_size;
+    if (lb >= max_blocks) return ORC_INVALID_INPUT;
+    int32_t blk = table[lb];
+    if (blk < 0 || blk >= c->num_blocks) return ORC_INVALID_INPUT;
+    get_row_f32(c, page_ptr(c, k_pool, blk, h), pos % c->block_size, kf + (size_t)i * c->head_dim);
+    get_row_f32(c, page_ptr(c, v_pool, blk, h), pos % c->block_size, vf + (size_t)i * c->head_dim);
+  }
+  return ORC_OK;
+}
+
+int orc_paged_decode(const orc_cache_desc* c, const uint8_t* k_pool, const uint8_t* v_pool,
+                     const float* q, int32_t n_heads, const int32_t* block_tables,
+                     int32_t max_blocks, const int32_t* ctx_lens, const int32_t* start_pos,
+                     int32_t n_seqs, float scale, float* out) {
+  if (!desc_ok(c) || n_heads <= 0 || n_heads % c->n_kv_heads) return ORC_INVALID_INPUT;
+  const int32_t D = c->head_dim, Hkv = c->n_kv_heads;
+  for (int32_t b = 0; b < n_seqs; ++b) {
+    int32_t st = start_pos ? start_pos[b] : 0;
+    int32_t n = ctx_lens[b] - st;
+    if (st < 0 || n < 0) return ORC_INVALID_INPUT;
+    float* kf = (float*)malloc(sizeof(float) * (size_t)(n ? n : 1) * D);
+    float* vf = (float*)malloc(sizeof(float) * (size_t)(n ? n : 1) * D);
+    for (int32_t kvh = 0; kvh < Hkv; ++kvh) {
+      int rc = widen_seq(c, k_pool, v_pool, block_tables + (size_t)b * max_blocks, max_blocks,
+                         kvh, st, n, kf, vf);
+      if (rc) { free(kf); free(vf); return rc; }
+      for (int32_t h = 0; h < n_heads; ++h) {
+        if (h * Hkv / n_heads != kvh) continue; /* forward.rs:234 GQA map */
+        size_t qo = ((size_t)b * n_heads + h) * D;
+        orc_flash_attn_f32(q + qo, kf, vf, NULL, out + qo, D, n, scale);
+      }
+    }
+    free(kf);
+    free(vf);
+  }
+  return ORC_OK;
+}
+
+int orc_paged_prefill_rows(const orc_cache_desc* c, const uint8_t* k_pool, const uint8_t* v_pool,
+                           const float* q, int32_t n_heads, const int32_t* cu_q,
+                           const int32_t* block_tables, int32_t max_blocks,
+                           const int32_t* ctx_lens, int32_t b, int32_t row_begin,
+                           int32_t row_end, float scale, int32_t causal, float* out) {
+  if (!desc_ok(c) || n_heads <= 0 || n_heads % c->n_kv_heads) return ORC_INVALID_INPUT;
+  const int32_t D = c->head_dim, Hkv = c->n_kv_heads;
+  int32_t ql = cu_q[b + 1] - cu_q[b];
+  int32_t ctx = ctx_lens[b];
+  if (ql < 0 || ql > ctx) return ORC_INVALID_INPUT;
+  float* kf = (float*)malloc(sizeof(float) * (size_t)(ctx ? ctx : 1) * D);
+  float* vf = (float*)malloc(sizeof(float) * (size_t)(ctx ? ctx : 1) * D);
+  for (int32_t kvh = 0; kvh < Hkv; ++kvh) {
+    int rc = widen_seq(c, k_pool, v_pool, block_tables + (size_t)b * max_blocks, max_blocks, kvh,
+                       0, ctx, kf, vf);
+    if (rc) { free(kf); free(vf); return rc; }
+    for (int32_t i = row_begin; i < row_end; ++i) {
+      int32_t n_kv = causal ? (ctx - ql + i + 1) : ctx; /* causal prefix of the chunk row */
+      for (int32_t h = 0; h < n_heads; ++h) {
+        if (h * Hkv / n_heads != kvh) continue;
+        size_t qo = ((size_t)(cu_q[b] + i) * n_heads + h) * D;
+        orc_flash_attn_f32(q + qo, kf, vf, NULL, out + qo, D, n_kv, scale);
+      }
+    }
+  }
+  free(kf);
+  free(vf);
+  return ORC_OK;
+}
+
+int orc_paged_prefill(const orc_cache_desc* c, const uint8_t* k_pool, const uint8_t* v_pool,
+                      const float* q, int32_t n_heads, const int32_t* cu_q,
+                      const int32_t* block_tables, int32_t max_blocks, const int32_t* ctx_lens,
+                      int32_t n_seqs, float scale, int32_t causal, float* out) {
+  for (int32_t b = 0; b < n_seqs; ++b) {
+    int rc = orc_paged_prefill_rows(c, k_pool, v_pool, q, n_heads, cu_q, block_tables, max_blocks,
+                                    ctx_lens, b, 0, cu_q[b + 1] - cu_q[b], scale, causal, out);
+    if (rc) return rc;
+  }
+  return ORC_OK;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Sequence / window manager over BlockPool.                                 */
+/* ------------------------------------------------------------------------ */
+struct orc_kv_manager {
+  orc_block_pool* pool;
+  int32_t bs, max_seqs, max_blocks, window;
+  int32_t* table;     /* [max_seqs][max_blocks], -1 = not held */
+  int64_t* pos;       /* next position (= ctx len) */
+  int64_t* first;     /* lowest logical block still held */
+};
+
+orc_kv_manager* orc_mgr_new(orc_block_pool* pool, int32_t block_size, int32_t max_seqs,
+                            int32_t max_blocks_per_seq, int32_t window) {
+  if (!pool || block_size <= 0 || max_seqs <= 0 || max_blocks_per_seq <= 0 || window < 0) return NULL;
+  orc_kv_manager* m = (orc_kv_manager*)calloc(1, sizeof(*m));
+  m->pool = pool;
+  m->bs = block_size;
+  m->max_seqs = max_seqs;
+  m->max_blocks = max_blocks_per_seq;
+  m->window = window;
+  m->table = (int32_t*)malloc(sizeof(int32_t) * (size_t)max_seqs * max_blocks_per_seq);
+  for (size_t i = 0; i < (size_t)max_seqs * max_blocks_per_seq; ++i) m->table[i] = -1;
+  m->pos = (int64_t*)calloc((size_t)max_seqs, sizeof(int64_t));
+  m->first = (int64_t*)calloc((size_t)max_seqs, sizeof(int64_t));
+  return m;
+}
+
+void orc_mgr_destroy(orc_kv_manager* m) {
+  if (!m) return;
+  free(m->table);
+  free(m->pos);
+  free(m->first);
+  free(m);
+}
+
+int orc_mgr_seed_seq(orc_kv_manager* m, int32_t s, int64_t pos, int64_t first_block,
+                     const int32_t* blocks, int32_t n) {
+  if (s < 0 || s >= m->max_seqs || first_block < 0 || first_block + n > m->max_blocks) return ORC_INVALID_INPUT;
+  int32_t* row = m->table + (size_t)s * m->max_blocks;
+  for (int32_t j = 0; j < m->max_blocks; ++j) row[j] = -1;
+  for (int32_t j = 0; j < n; ++j) row[first_block + j] = blocks[j];
+  m->pos[s] = pos;
+  m->first[s] = first_block;
+  return ORC_OK;
+}
+
+int orc_mgr_append(orc_kv_manager* m, const int32_t* seqs, const int32_t* n_tokens, int32_t n,
+                   int64_t* slots_out, int32_t* evicted_out, int32_t evicted_cap,
+                   int32_t* n_evicted) {
+  int32_t ne = 0;
+  size_t t = 0;
+  for (int32_t i = 0; i < n; ++i) {
+    int32_t s = seqs[i];
+    if (s < 0 || s >= m->max_seqs || n_tokens[i] < 0) return ORC_INVALID_INPUT;
+    int32_t* row = m->table + (size_t)s * m->max_blocks;
+    for (int32_t k = 0; k < n_tokens[i]; ++k) {
+      int64_t p = m->pos[s];
+      if (m->window > 0) { /* free blocks that fall out of [p-W+1, p] */
+        while (m->first[s] * m->bs + m->bs - 1 < p - m->window + 1) {
+          int64_t j = m->first[s];
+          if (j >= m->max_blocks) return ORC_INVALID_INPUT;
+          if (row[j] >= 0) {
+            if (orc_pool_free(m->pool, row[j])) return ORC_INVALID_INPUT;
+            if (ne >= evicted_cap) return ORC_INVALID_INPUT;
+            evicted_out[ne++] = row[j];
+            row[j] = -1;
+          }
+          m->first[s] = j + 1;
+        }
+      }
+      int64_t lb = p / m->bs;
+      if (lb >= m->max_blocks) return ORC_INVALID_INPUT;
+      if (p % m->bs == 0) {
+        int64_t id = orc_pool_allocate(m->pool);
+        if (id < 0) return ORC_INVALID_INPUT; /* pool exhausted */
+        row[lb] = (int32_t)id;
+      }
+      if (row[lb] < 0) return ORC_INVALID_INPUT;
+      slots_out[t++] = (int64_t)row[lb] * m->bs + p % m->bs;
+      m->pos[s] = p + 1;
+    }
+  }
+  *n_evicted = ne;
+  return ORC_OK;
+}
+
+int orc_mgr_tables(const orc_kv_manager* m, int32_t* tables, int32_t max_blocks,
+                   int32_t* ctx_lens, int32_t* start_pos) {
+  if (max_blocks < m->max_blocks) return ORC_INVALID_INPUT;
+  for (int32_t s = 0; s < m->max_seqs; ++s) {
+    for (int32_t j = 0; j < max_blocks; ++j)
+      tables[(size_t)s * max_blocks + j] = j < m->max_blocks ? m->table[(size_t)s * m->max_blocks + j] : -1;
+    if (ctx_lens) ctx_lens[s] = (int32_t)m->pos[s];
+    if (start_pos) {
+      int64_t st = m->window > 0 ? m->pos[s] - m->window : 0;
+      start_pos[s] = (int32_t)(st > 0 ? st : 0);
+    }
+  }
+  return ORC_OK;
+}

@@ -1,0 +1,191 @@
+/*
+ * it_oracle.h -- CPU oracle for the KV-cache hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This is a plain-C restatement of the reference
+ * crate's CPU arithmetic (OpenMachineware/infer_train, Rust).  It is the
+ * checker that the HIP library is compared against and the CPU baseline that
+ * bench.py times.  Only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load it; the product library (libit_kv.so) never
+ * links, loads or calls it.
+ *
+ * Every function names the reference file:line it follows.  Functions that
+ * restate behaviour the reference does not have (slot mapping, paged reads,
+ * window eviction, chunked prefill) are defined here as compositions of the
+ * reference functions and say so.
+ *
+ * Build: oracle/Makefile (gcc -O2 -ffp-contract=off, no fast-math), because
+ * Rust never contracts a*b+c into an FMA.
+ */
+#ifndef IT_ORACLE_H
+#define IT_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes, same values as the product ABI (OpError, types.rs:227-231). */
+#define ORC_OK 0
+#define ORC_NOT_IMPLEMENTED 1
+#define ORC_INVALID_INPUT 2
+
+/* dtype codes = ggml QuantType ids (types.rs:106-144). */
+#define ORC_F32 0
+#define ORC_F16 1
+#define ORC_Q8_0 8
+#define ORC_BF16 30
+
+#define ORC_QK8_0 32          /* types.rs:11 */
+#define ORC_BLOCK_Q8_0_BYTES 34 /* types.rs:34-41: repr(C) {u16 d; i8 qs[32]} */
+
+/* ---- seeded synthetic inputs (not a reference function: test plumbing) -- */
+uint64_t orc_splitmix64(uint64_t* state);
+/* N(0,1) via Box-Muller in double, rounded to f32. */
+void orc_fill_normal_f32(uint64_t seed, float* out, size_t n);
+/* Uniform integers in [lo, hi] (inclusive). */
+void orc_fill_uniform_i32(uint64_t seed, int32_t lo, int32_t hi, int32_t* out, size_t n);
+/* Fisher-Yates permutation of 0..n-1. */
+void orc_permutation_i64(uint64_t seed, int64_t* out, size_t n);
+
+/* ---- scalar conversions ------------------------------------------------- */
+/* fp32 -> fp16 round-to-nearest-even (half 2.7.1 f16::from_f32, called by
+ * fp32_to_fp16, types.rs:237-240). */
+uint16_t orc_f32_to_f16(float f);
+/* fp16 -> fp32, exact (types.rs:233-235). */
+float orc_f16_to_f32(uint16_t h);
+/* fp32 -> bf16 round-to-nearest-even (NaN kept quiet). */
+uint16_t orc_f32_to_bf16(float f);
+float orc_bf16_to_f32(uint16_t h);
+void orc_f32_to_bf16_array(const float* in, uint16_t* out, size_t n);
+void orc_bf16_to_f32_array(const uint16_t* in, float* out, size_t n);
+void orc_f32_to_f16_array(const float* in, uint16_t* out, size_t n);
+void orc_f16_to_f32_array(const uint16_t* in, float* out, size_t n);
+
+/* ---- BlockPool (src/memory/paged.rs:21-58) ------------------------------ */
+typedef struct orc_block_pool orc_block_pool;
+/* paged.rs:28-34: free_list = 0..capacity, all refcounts 0. */
+orc_block_pool* orc_pool_new(int64_t capacity, int32_t quant_type);
+/* Same pool, but the free list holds `order` (a permutation of 0..cap-1), so
+ * allocate() pops order[cap-1] first.  Used for the configs' "seeded random
+ * permutation of the pool". */
+orc_block_pool* orc_pool_new_ordered(const int64_t* order, int64_t capacity, int32_t quant_type);
+void orc_pool_destroy(orc_block_pool* p);
+/* paged.rs:36-42: LIFO pop, refcount := 1.  Returns -1 for None. */
+int64_t orc_pool_allocate(orc_block_pool* p);
+/* paged.rs:44-46: refcount += 1.  ORC_INVALID_INPUT on a bad id or ref 0. */
+int orc_pool_share(orc_block_pool* p, int64_t id);
+/* paged.rs:48-53: refcount -= 1, push on 0.  The reference underflows a u32
+ * on ref 0; here that is ORC_INVALID_INPUT. */
+int orc_pool_free(orc_block_pool* p, int64_t id);
+int32_t orc_pool_quant_type(const orc_block_pool* p); /* paged.rs:55-57 */
+int64_t orc_pool_num_free(const orc_block_pool* p);
+int64_t orc_pool_ref_count(const orc_block_pool* p, int64_t id);
+/* Copies the free list bottom..top into out (n = num_free). */
+void orc_pool_free_list(const orc_block_pool* p, int64_t* out);
+
+/* ---- Q8_0 (src/backend/arm/quant.rs:149-183, x86 scalar path) ----------- */
+/* x: n floats (n % 32 == 0); y: n/32 packed 34-byte BlockQ8_0 records. */
+int orc_quantize_row_q8_0(const float* x, size_t n, uint8_t* y);
+/* Dequant semantics fp16_to_fp32(d) * q (gemv.rs:48-59, 151-160). */
+void orc_dequantize_row_q8_0(const uint8_t* y, size_t n, float* x);
+
+/* ---- attention ---------------------------------------------------------- */
+/* src/backend/arm/flash_attn.rs:6-72, same operation order. mask may be NULL. */
+void orc_flash_attn_f32(const float* q, const float* k, const float* v, const float* mask,
+                        float* out, int32_t head_dim, int32_t n_kv, float scale);
+
+/* ArmCpuBackend FlashAttention arm (src/backend/arm.rs:304-370): all n_heads
+ * share one K/V [n_kv][head_dim]; optional mask [n_kv]; scale 1/sqrtf(D). */
+int orc_backend_flash_attention(const float* q, const float* k, const float* v,
+                                const float* mask, float* out, int32_t n_heads,
+                                int32_t head_dim, int32_t n_kv);
+
+/* ---- paged cache restatement ------------------------------------------- */
+/* Pool layout: [num_blocks][n_kv_heads][block_size][head_dim] elements of
+ * elem_bytes each, one pool for K and one for V.  For Q8_0 each
+ * (block, head) page holds block_size*head_dim int8 values followed by
+ * block_size*head_dim/32 fp16 scales (slot-major). */
+typedef struct {
+  int64_t num_blocks;
+  int32_t block_size;
+  int32_t n_kv_heads;
+  int32_t head_dim;
+  int32_t dtype;
+} orc_cache_desc;
+
+size_t orc_page_bytes(const orc_cache_desc* c);
+
+/* KV append (forward.rs:219-229 generalised from `seq_pos` to a slot):
+ * k_cache[slot/bs][h][slot%bs][:] = k[t][h][:].  Negative slots are skipped.
+ * F32/F16/BF16: bit copy (src dtype == cache dtype).  Q8_0: src is f32 and
+ * each 32-group is quantised with orc_quantize_row_q8_0. */
+int orc_kv_append(const orc_cache_desc* c, uint8_t* k_pool, uint8_t* v_pool,
+                  const void* k, const void* v, const int64_t* slots, int32_t n_tokens);
+
+/* Block-table gather: the contiguous slice k_cache[kv][start..ctx] of
+ * forward.rs:233-243 read through a block table.  Output per sequence b is
+ * [n_kv_heads][ctx_b - start_b][head_dim] at token offset cu_out[b].  Q8_0
+ * outputs packed 34-byte BlockQ8_0 records. */
+int orc_kv_gather(const orc_cache_desc* c, const uint8_t* k_pool, const uint8_t* v_pool,
+                  const int32_t* block_tables, int32_t max_blocks, const int32_t* ctx_lens,
+                  const int32_t* start_pos, const int64_t* cu_out, int32_t n_seqs,
+                  void* k_out, void* v_out);
+
+/* Evict: zero the pages of the given blocks (all heads, K and V). */
+int orc_kv_evict(const orc_cache_desc* c, uint8_t* k_pool, uint8_t* v_pool,
+                 const int32_t* blocks, int32_t n);
+
+/* Paged decode: for each seq b and q-head h, flash_attn_f32 over the
+ * widened (bf16/f16 -> f32, Q8_0 -> f32(d)*q) keys start_b..ctx_b-1 of KV
+ * head h*Hkv/Hq (forward.rs:231-254).  q: [n_seqs][n_heads][D] f32,
+ * out: [n_seqs][n_heads][D] f32.  start_pos may be NULL (all zero). */
+int orc_paged_decode(const orc_cache_desc* c, const uint8_t* k_pool, const uint8_t* v_pool,
+                     const float* q, int32_t n_heads, const int32_t* block_tables,
+                     int32_t max_blocks, const int32_t* ctx_lens, const int32_t* start_pos,
+                     int32_t n_seqs, float scale, float* out);
+
+/* Chunked prefill, causal: query row i of sequence b sits at position
+ * ctx_b - q_len_b + i and runs flash_attn_f32 over keys 0..that position
+ * (n_kv = cached + i + 1).  q/out: [total_q][n_heads][D] f32, rows of seq b
+ * at cu_q[b]..cu_q[b+1]. causal=0 attends all ctx_b keys. */
+int orc_paged_prefill(const orc_cache_desc* c, const uint8_t* k_pool, const uint8_t* v_pool,
+                      const float* q, int32_t n_heads, const int32_t* cu_q,
+                      const int32_t* block_tables, int32_t max_blocks, const int32_t* ctx_lens,
+                      int32_t n_seqs, float scale, int32_t causal, float* out);
+/* Same, only rows [row_begin,row_end) of sequence `seq` (CPU baseline sample). */
+int orc_paged_prefill_rows(const orc_cache_desc* c, const uint8_t* k_pool, const uint8_t* v_pool,
+                           const float* q, int32_t n_heads, const int32_t* cu_q,
+                           const int32_t* block_tables, int32_t max_blocks,
+                           const int32_t* ctx_lens, int32_t seq, int32_t row_begin,
+                           int32_t row_end, float scale, int32_t causal, float* out);
+
+/* ---- sequence / window manager (restated on BlockPool) ----------------- */
+/* Slot rule: slot = table[pos / bs] * bs + pos % bs; a new block is taken
+ * from the pool (paged.rs:36-42) when pos % bs == 0.  With window W > 0,
+ * before each token at position p every block whose last position is
+ * < p - W + 1 is released with BlockPool::free (paged.rs:48-53), oldest
+ * first.  Sequences of one step are processed in the order given. */
+typedef struct orc_kv_manager orc_kv_manager;
+orc_kv_manager* orc_mgr_new(orc_block_pool* pool, int32_t block_size, int32_t max_seqs,
+                            int32_t max_blocks_per_seq, int32_t window);
+void orc_mgr_destroy(orc_kv_manager* m);
+/* Start sequence s at position `pos` holding the blocks `blocks` for logical
+ * blocks first_block..first_block+n-1 (already allocated by the caller). */
+int orc_mgr_seed_seq(orc_kv_manager* m, int32_t s, int64_t pos, int64_t first_block,
+                     const int32_t* blocks, int32_t n);
+/* Append n_tokens[i] tokens to sequence seqs[i], i = 0..n-1 in order.
+ * Writes sum(n_tokens) slots and the freed block ids (in free order). */
+int orc_mgr_append(orc_kv_manager* m, const int32_t* seqs, const int32_t* n_tokens, int32_t n,
+                   int64_t* slots_out, int32_t* evicted_out, int32_t evicted_cap,
+                   int32_t* n_evicted);
+/* Export block tables (absolute logical index, -1 = not held), positions
+ * (ctx lens) and window starts. */
+int orc_mgr_tables(const orc_kv_manager* m, int32_t* tables, int32_t max_blocks,
+                   int32_t* ctx_lens, int32_t* start_pos);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,185 @@
+"""GPU parity of the data-movement kernels: slot-mapped append (bit copy and
+Q8_0 quantise), block-table gather, evict and copy-on-write page copy.  Every
+result is compared byte for byte with the oracle on the same seeded inputs;
+pools start filled with a sentinel so stray writes show up."""
+import numpy as np
+import pytest
+
+import oracle as orc
+from kvutil import from_dev, kv_values, random_tables, slots_for, to_dev
+
+pytestmark = pytest.mark.gpu
+
+SENTINEL = 0xA5
+
+
+def _pair(num_blocks, bs, hkv, D, dt):
+    import torch
+    from infer_train_amd.kv import PagedKvCache
+
+    dev = PagedKvCache(num_blocks, bs, hkv, D, dt)
+    dev.k_pool.fill_(SENTINEL)
+    dev.v_pool.fill_(SENTINEL)
+    ref = orc.Cache(num_blocks, bs, hkv, D, dt)
+    ref.k[:] = SENTINEL
+    ref.v[:] = SENTINEL
+    torch.cuda.synchronize()
+    return dev, ref
+
+
+def _src(seed, n_tokens, hkv, D, dt):
+    if dt == orc.Q8_0:
+        k = kv_values(seed, n_tokens * hkv * D, orc.F32, outliers=True)
+        v = kv_values(seed + 1, n_tokens * hkv * D, orc.F32, outliers=True)
+    else:
+        k = kv_values(seed, n_tokens * hkv * D, dt)
+        v = kv_values(seed + 1, n_tokens * hkv * D, dt)
+    return k.reshape(n_tokens, hkv, D), v.reshape(n_tokens, hkv, D)
+
+
+def _dev_src(a, dt):
+    import torch
+
+    if dt in (orc.F32, orc.Q8_0):
+        return to_dev(a)
+    return to_dev(a.view(np.int16), torch.bfloat16 if dt == orc.BF16 else torch.float16)
+
+
+def _assert_pools(dev, ref, what):
+    dev.check()
+    for name, d, r in (("K", dev.k_pool, ref.k), ("V", dev.v_pool, ref.v)):
+        got = from_dev(d)
+        if not np.array_equal(got, r):
+            i = np.flatnonzero(got != r)
+            raise AssertionError(f"{what}: {name} pool differs at {i.size} bytes, first {i[0]} "
+                                 f"(page {i[0] // dev.page_bytes}) got {got[i[0]]} want {r[i[0]]}")
+
+
+@pytest.mark.parametrize("dt,D,bs", [(orc.BF16, 128, 16), (orc.F32, 128, 16), (orc.F16, 128, 16),
+                                     (orc.BF16, 256, 32), (orc.Q8_0, 256, 32), (orc.Q8_0, 128, 16)])
+def test_append_bit_exact(dt, D, bs):
+    hkv, nb, n = 4, 64, 300
+    dev, ref = _pair(nb, bs, hkv, D, dt)
+    perm = orc.permutation(7, nb * bs)
+    slots = perm[:n].copy()
+    slots[::37] = -1  # padding tokens are skipped
+    k, v = _src(11, n, hkv, D, dt)
+    ref.append(k, v, slots)
+    dev.append(_dev_src(k, dt), _dev_src(v, dt), to_dev(slots))
+    _assert_pools(dev, ref, f"append dt={dt}")
+
+
+def test_append_q8_special_groups():
+    """Ties, all-zero, constant, subnormal-scale, NaN and inf groups."""
+    hkv, D, bs, nb = 1, 256, 32, 4
+    dev, ref = _pair(nb, bs, hkv, D, orc.Q8_0)
+    rows = []
+    g = np.zeros((8, 32), np.float32)
+    g[0, 0] = 127.0
+    g[0, 1:7] = [2.5, -2.5, 0.5, -0.5, 3.5, -126.5]  # exact .5 ties, scale exactly 1
+    g[1] = 0.0
+    g[2] = 0.75
+    g[3] = orc.normal(3, 32) * np.float32(1e-30)  # fp16-subnormal scale
+    g[4] = orc.normal(4, 32) * np.float32(1e-40)  # fp32-subnormal inputs
+    g[5] = orc.normal(5, 32)
+    g[5, 9] = np.nan
+    g[6] = orc.normal(6, 32)
+    g[6, 2] = np.inf
+    g[7] = orc.normal(7, 32) * np.float32(6e4)  # scale near the fp16 max
+    rows.append(g.reshape(-1))
+    for s in range(1, 8):
+        rows.append(np.roll(g.reshape(-1), 32 * s))
+    k = np.stack(rows).reshape(8, hkv, D)
+    v = -k
+    slots = np.array([0, 5, 31, 32, 63, 64, 100, 127], np.int64)
+    ref.append(k, v, slots)
+    dev.append(to_dev(k), to_dev(v), to_dev(slots))
+    _assert_pools(dev, ref, "append q8 special")
+
+
+def test_append_config1_full_step():
+    # Config 1: fp32, Hkv 2, D 128, bs 16, 64 blocks, identity table; 1023
+    # cached tokens then the token at position 1023.
+    hkv, D, bs, nb = 2, 128, 16, 64
+    dev, ref = _pair(nb, bs, hkv, D, orc.F32)
+    k, v = _src(1, 1024, hkv, D, orc.F32)
+    slots = np.arange(1024, dtype=np.int64)  # identity block table
+    ref.append(k[:1023], v[:1023], slots[:1023])
+    dev.append(to_dev(k[:1023]), to_dev(v[:1023]), to_dev(slots[:1023]))
+    ref.append(k[1023:], v[1023:], slots[1023:])
+    dev.append(to_dev(k[1023:]), to_dev(v[1023:]), to_dev(slots[1023:]))
+    _assert_pools(dev, ref, "config1 append")
+
+
+def test_append_bad_slot_is_latched_not_written():
+    from infer_train_amd import InvalidInput
+
+    hkv, D, bs, nb = 2, 128, 16, 8
+    dev, ref = _pair(nb, bs, hkv, D, orc.BF16)
+    k, v = _src(2, 3, hkv, D, orc.BF16)
+    slots = np.array([3, nb * bs + 5, 9], np.int64)  # middle slot is out of range
+    dev.append(_dev_src(k, orc.BF16), _dev_src(v, orc.BF16), to_dev(slots))
+    with pytest.raises(InvalidInput):
+        dev.check()
+    ref.append(k[[0, 2]], v[[0, 2]], slots[[0, 2]])
+    _assert_pools(dev, ref, "bad slot")  # nothing else written; flag cleared
+
+
+@pytest.mark.parametrize("dt,D,bs", [(orc.BF16, 128, 16), (orc.F32, 128, 16), (orc.Q8_0, 256, 32)])
+def test_gather_bit_exact(dt, D, bs):
+    import torch
+
+    hkv, nb = 2, 128
+    ctx = np.array([0, 1, 17, 300, 511], np.int32)
+    start = np.array([0, 0, 5, 33, 100], np.int32)  # windowed starts, not block aligned
+    mb = 40
+    tables = random_tables(5, ctx, bs, nb, mb)
+    dev, ref = _pair(nb, bs, hkv, D, dt)
+    seqs, pos = [], []
+    for b, c in enumerate(ctx):
+        seqs += [b] * int(c)
+        pos += list(range(int(c)))
+    slots = slots_for(tables, seqs, pos, bs)
+    k, v = _src(3, len(slots), hkv, D, dt)
+    ref.append(k, v, slots)
+    dev.append(_dev_src(k, dt), _dev_src(v, dt), to_dev(slots))
+    n = ctx - start
+    cu = np.concatenate([[0], np.cumsum(n)[:-1]]).astype(np.int64)
+    total = int(n.sum())
+    rk, rv = ref.gather(tables, ctx, start, cu, total)
+    ko = torch.zeros(rk.size, dtype=torch.uint8, device="cuda:0")
+    vo = torch.zeros(rv.size, dtype=torch.uint8, device="cuda:0")
+    dev.gather(to_dev(tables), to_dev(ctx), to_dev(start), to_dev(cu), int(n.max()), ko, vo)
+    dev.check()
+    np.testing.assert_array_equal(from_dev(ko), rk)
+    np.testing.assert_array_equal(from_dev(vo), rv)
+    if dt == orc.Q8_0:  # AoS records equal quantize_row_q8_0 of the source rows
+        b = 3
+        rows = []
+        for h in range(hkv):
+            for i in range(n[b]):
+                t = int(sum(ctx[:b])) + int(start[b]) + i
+                rows.append(orc.quantize_row_q8_0(k[t, h]))
+        want = np.concatenate(rows).ravel()
+        off = int(cu[b]) * hkv * (D // 32) * 34
+        np.testing.assert_array_equal(from_dev(ko)[off:off + want.size], want)
+
+
+def test_evict_and_copy_blocks():
+    hkv, D, bs, nb = 2, 128, 16, 32
+    dev, ref = _pair(nb, bs, hkv, D, orc.BF16)
+    slots = np.arange(nb * bs, dtype=np.int64)
+    k, v = _src(9, nb * bs, hkv, D, orc.BF16)
+    ref.append(k, v, slots)
+    dev.append(_dev_src(k, orc.BF16), _dev_src(v, orc.BF16), to_dev(slots))
+    ev = np.array([3, 17, 31, 0], np.int32)
+    ref.evict(ev)
+    dev.evict(to_dev(ev))
+    _assert_pools(dev, ref, "evict")
+    src, dst = np.array([5, 6], np.int32), np.array([3, 0], np.int32)
+    dev.copy_blocks(to_dev(src), to_dev(dst))
+    pb = dev.page_bytes * hkv
+    for s, d in zip(src, dst):
+        ref.k[d * pb:(d + 1) * pb] = ref.k[s * pb:(s + 1) * pb]
+        ref.v[d * pb:(d + 1) * pb] = ref.v[s * pb:(s + 1) * pb]
+    _assert_pools(dev, ref, "copy_blocks")

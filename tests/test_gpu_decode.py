@@ -1,0 +1,185 @@
+"""GPU parity of paged split-K flash-decode (+ combine) and of the Backend
+FlashAttention operator against the oracle's flash_attn_f32 restatement.
+Tolerances (|got - ref| <= atol + rtol |ref|): fp32 rtol 1e-5 / atol 1e-6;
+bf16 rtol 2e-3 / atol 1e-2; softmax accumulates in fp32 throughout."""
+import math
+import os
+
+import numpy as np
+import pytest
+
+import oracle as orc
+from kvutil import assert_close, from_dev, kv_values, random_tables, slots_for, to_dev, widen
+
+pytestmark = pytest.mark.gpu
+
+TOL = {orc.F32: (1e-5, 1e-6), orc.Q8_0: (1e-5, 1e-6), orc.BF16: (2e-3, 1e-2), orc.F16: (2e-3, 1e-2)}
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def _build(dt, hq, hkv, D, bs, ctx, start=None, nb=None, seed=1, mb=None):
+    """Fill oracle + device caches with every position of every sequence."""
+    import torch
+    from infer_train_amd.kv import PagedKvCache
+
+    ctx = np.asarray(ctx, np.int32)
+    mb = mb or int(max(1, (ctx.max() + bs - 1) // bs))
+    need = int(sum((int(c) + bs - 1) // bs for c in ctx))
+    nb = nb or max(need, 1)
+    tables = random_tables(seed, ctx, bs, nb, mb)
+    seqs, pos = [], []
+    for b, c in enumerate(ctx):
+        seqs += [b] * int(c)
+        pos += list(range(int(c)))
+    slots = slots_for(tables, seqs, pos, bs)
+    n = len(slots)
+    src_dt = orc.F32 if dt == orc.Q8_0 else dt
+    k = kv_values(seed + 10, n * hkv * D, src_dt, outliers=dt == orc.Q8_0).reshape(n, hkv, D)
+    v = kv_values(seed + 11, n * hkv * D, src_dt, outliers=dt == orc.Q8_0).reshape(n, hkv, D)
+    ref = orc.Cache(nb, bs, hkv, D, dt)
+    ref.append(k, v, slots)
+    dev = PagedKvCache(nb, bs, hkv, D, dt)
+    if n:
+        if src_dt == orc.F32:
+            dk, dv = to_dev(k), to_dev(v)
+        else:
+            td = torch.bfloat16 if dt == orc.BF16 else torch.float16
+            dk, dv = to_dev(k.view(np.int16), td), to_dev(v.view(np.int16), td)
+        dev.append(dk, dv, to_dev(slots))
+    qdt = orc.F32 if dt in (orc.F32, orc.Q8_0) else dt
+    q = kv_values(seed + 12, len(ctx) * hq * D, qdt).reshape(len(ctx), hq, D)
+    return dev, ref, tables, ctx, q, qdt
+
+
+def _run(dev, ref, tables, ctx, q, qdt, hq, start=None, partition=512, out_f32=True):
+    import torch
+
+    D = q.shape[2]
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))  # forward.rs:252
+    n = ctx - (start if start is not None else 0)
+    want = ref.decode(widen(q, qdt), hq, tables, ctx, start, scale)
+    if qdt == orc.F32:
+        dq = to_dev(q)
+    else:
+        dq = to_dev(q.view(np.int16), torch.bfloat16 if qdt == orc.BF16 else torch.float16)
+    out = dev.decode(dq, to_dev(tables), to_dev(ctx), None if start is None else to_dev(start),
+                     max(int(n.max()), 0), scale=scale, partition=partition,
+                     out_dtype=torch.float32 if out_f32 else dq.dtype)
+    dev.check()
+    got = from_dev(out)
+    if not out_f32 and qdt != orc.F32:
+        got = widen(got, qdt)
+    return got.reshape(want.shape), want
+
+
+def test_config1_fp32_decode():
+    """Config 1: Hq 12, Hkv 2, D 128, bs 16, one sequence of 1024 tokens over
+    a 64-block pool with the identity table."""
+    import torch
+    from infer_train_amd.kv import PagedKvCache
+
+    hq, hkv, D, bs = 12, 2, 128, 16
+    k = kv_values(101, 1024 * hkv * D, orc.F32).reshape(1024, hkv, D)
+    v = kv_values(102, 1024 * hkv * D, orc.F32).reshape(1024, hkv, D)
+    q = kv_values(103, hq * D, orc.F32).reshape(1, hq, D)
+    tables = np.arange(64, dtype=np.int32)[None, :]
+    slots = np.arange(1024, dtype=np.int64)
+    ref = orc.Cache(64, bs, hkv, D, orc.F32)
+    ref.append(k, v, slots)
+    dev = PagedKvCache(64, bs, hkv, D, orc.F32)
+    dev.append(to_dev(k[:1023]), to_dev(v[:1023]), to_dev(slots[:1023]))
+    dev.append(to_dev(k[1023:]), to_dev(v[1023:]), to_dev(slots[1023:]))
+    ctx = np.array([1024], np.int32)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(128)))
+    want = ref.decode(q, hq, tables, ctx, None, scale)
+    out = dev.decode(to_dev(q), to_dev(tables), to_dev(ctx), None, 1024, scale=scale)
+    dev.check()
+    got = from_dev(out)
+    assert_close(got, want, *TOL[orc.F32], what="config1")
+    golden = np.load(os.path.join(GOLDEN, "config1_decode_out.npy"))
+    assert_close(got.reshape(golden.shape), golden, *TOL[orc.F32], what="config1 golden")
+
+
+@pytest.mark.parametrize("partition", [512, 256, 1024])
+def test_config2_shape_bf16_ragged(partition):
+    """Config-2 heads (Hq 28, Hkv 4, D 128, bs 16) with ragged contexts that
+    exercise partial pages and partitions."""
+    hq, hkv, D, bs = 28, 4, 128, 16
+    ctx = [1, 15, 16, 17, 511, 512, 513, 1500, 2049, 0]
+    dev, ref, tables, ctx, q, qdt = _build(orc.BF16, hq, hkv, D, bs, ctx, seed=3, nb=400)
+    for out_f32 in (True, False):
+        got, want = _run(dev, ref, tables, ctx, q, qdt, hq, partition=partition, out_f32=out_f32)
+        assert_close(got, want, *TOL[orc.BF16], what=f"config2 ragged P={partition} f32out={out_f32}")
+    assert np.all(got[-1] == 0)  # empty sequence -> zeros (flash_attn.rs:66-71)
+
+
+def test_config2_full_size_bf16():
+    """Config 2 at full size: B 32, ctx U[256, 4096] (+1 appended), pool of
+    16384 blocks in seeded random order."""
+    hq, hkv, D, bs = 28, 4, 128, 16
+    ctx = orc.uniform_i32(2, 256, 4096, 32) + 1
+    dev, ref, tables, ctx, q, qdt = _build(orc.BF16, hq, hkv, D, bs, ctx, seed=2, nb=16384, mb=257)
+    got, want = _run(dev, ref, tables, ctx, q, qdt, hq, partition=512, out_f32=False)
+    assert_close(got, want, *TOL[orc.BF16], what="config2 full")
+
+
+@pytest.mark.parametrize("dt", [orc.F16, orc.F32])
+def test_other_dtypes(dt):
+    hq, hkv, D, bs = 8, 2, 128, 16
+    dev, ref, tables, ctx, q, qdt = _build(dt, hq, hkv, D, bs, [700, 64, 1], seed=5)
+    got, want = _run(dev, ref, tables, ctx, q, qdt, hq)
+    assert_close(got, want, *TOL[dt], what=f"dtype {dt}")
+
+
+def test_window_start_positions_bf16():
+    """Config-4 heads (Hq 16, Hkv 2, G 8) reading only [start, ctx)."""
+    hq, hkv, D, bs = 16, 2, 128, 16
+    ctx = np.array([900, 1200, 300, 4097], np.int32)
+    start = np.array([0, 1200 - 777, 299, 4097 - 4096], np.int32)
+    dev, ref, tables, ctx, q, qdt = _build(orc.BF16, hq, hkv, D, bs, ctx, seed=6)
+    got, want = _run(dev, ref, tables, ctx, q, qdt, hq, start=start)
+    assert_close(got, want, *TOL[orc.BF16], what="window")
+
+
+def test_q8_0_decode_d256():
+    """Config-5 heads (Hq 24, Hkv 4, D 256, bs 32) on a Q8_0 cache; fp32 q and
+    fp32 tolerance against the oracle on the same quantised cache."""
+    hq, hkv, D, bs = 24, 4, 256, 32
+    dev, ref, tables, ctx, q, qdt = _build(orc.Q8_0, hq, hkv, D, bs, [3000, 1025, 33], seed=7)
+    for partition in (512, 1024, 2048):
+        got, want = _run(dev, ref, tables, ctx, q, qdt, hq, partition=partition)
+        assert_close(got, want, *TOL[orc.Q8_0], what=f"q8_0 P={partition}")
+
+
+def test_bf16_d256_and_group_sizes():
+    for hq, hkv in ((3, 1), (10, 2), (12, 12)):
+        dev, ref, tables, ctx, q, qdt = _build(orc.BF16, hq, hkv, 256, 16, [333, 1029], seed=8)
+        got, want = _run(dev, ref, tables, ctx, q, qdt, hq)
+        assert_close(got, want, *TOL[orc.BF16], what=f"bf16 d256 hq={hq} hkv={hkv}")
+
+
+def test_backend_flash_attention_op():
+    """CoreOperator::FlashAttention contract (arm.rs:304-370): K/V shared by
+    all heads, optional additive mask with -inf keys skipped."""
+    import torch
+    from infer_train_amd.kv import flash_attention
+
+    for n_heads, D, n_kv in ((12, 128, 1024), (7, 256, 77), (4, 128, 1)):
+        q = kv_values(30, n_heads * D, orc.F32).reshape(n_heads, D)
+        k = kv_values(31, n_kv * D, orc.F32).reshape(n_kv, D)
+        v = kv_values(32, n_kv * D, orc.F32).reshape(n_kv, D)
+        mask = (orc.normal(33, n_kv) * np.float32(2)).astype(np.float32)
+        mask[::5] = -np.inf
+        if n_kv == 1:
+            mask[:] = 0
+        for m in (None, mask):
+            want = orc.backend_flash_attention(q, k, v, m)
+            got = flash_attention(to_dev(q), to_dev(k), to_dev(v), None if m is None else to_dev(m))
+            torch.cuda.synchronize()
+            assert_close(from_dev(got), want, *TOL[orc.F32], what=f"backend op H={n_heads} D={D} n={n_kv}")
+    # all keys masked -> zeros, as flash_attn_f32 leaves them
+    q = kv_values(34, 4 * 128, orc.F32).reshape(4, 128)
+    k = kv_values(35, 10 * 128, orc.F32).reshape(10, 128)
+    got = flash_attention(to_dev(q), to_dev(k), to_dev(k), to_dev(np.full(10, -np.inf, np.float32)))
+    torch.cuda.synchronize()
+    assert np.all(from_dev(got) == 0)

@@ -1,0 +1,157 @@
+"""The product's host-side allocator and slot manager (native, in
+libit_kv.so) against the oracle's restatement: bit-exact block ids, slots,
+eviction order and tables."""
+import hashlib
+import json
+import os
+
+import numpy as np
+import pytest
+
+import oracle as orc
+from infer_train_amd import BlockPool, ContinuousBatcher, InvalidInput, KvManager
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def test_block_pool_mirrors_reference():
+    p = BlockPool(5)
+    assert [p.allocate() for _ in range(5)] == [4, 3, 2, 1, 0]  # paged.rs:36-42
+    assert p.allocate() is None
+    p.free(3)
+    p.share(1)
+    p.free(1)
+    assert p.ref_count(1) == 1 and p.num_free() == 1
+    assert p.allocate() == 3
+    with pytest.raises(InvalidInput):
+        p.free(3) or p.free(3)
+    assert BlockPool(3, quant_type=8).quant_type() == 8
+
+
+def test_block_pool_random_ops_equal_oracle():
+    rng = np.random.default_rng(5)
+    cap = 64
+    order = orc.permutation(9, cap)
+    a, b = BlockPool(cap, order=order), orc.Pool(cap, order=order)
+    for _ in range(20000):
+        op, i = int(rng.integers(3)), int(rng.integers(cap))
+        if op == 0:
+            assert a.allocate() == b.allocate()
+        elif op == 1:
+            rb = b.share(i)
+            if rb:
+                with pytest.raises(InvalidInput):
+                    a.share(i)
+            else:
+                a.share(i)
+        else:
+            rb = b.free(i)
+            if rb:
+                with pytest.raises(InvalidInput):
+                    a.free(i)
+            else:
+                a.free(i)
+        assert a.num_free() == b.num_free()
+
+
+def _sha(x):
+    return hashlib.sha256(np.ascontiguousarray(x).tobytes()).hexdigest()
+
+
+def test_window_manager_config4_equals_oracle_and_golden():
+    cap, bs, W, start = 16512, 16, 4096, 30000
+    order = orc.permutation(4, cap)
+    pa, pb = BlockPool(cap, order=order), orc.Pool(cap, order=order)
+    mb = 32768 // bs + 1
+    ma, mo = KvManager(pa, bs, 64, mb, W), orc.Manager(pb, bs, 64, mb, W)
+    first, last = (start - W) // bs, (start - 1) // bs
+    for s in range(64):
+        blocks = [pa.allocate() for _ in range(last - first + 1)]
+        assert blocks == [pb.allocate() for _ in range(last - first + 1)]
+        ma.seed_seq(s, start, first, blocks)
+        mo.seed_seq(s, start, first, blocks)
+    slots, evs = [], []
+    for _ in range(2768):
+        plan = ma.append(list(range(64)))
+        so, eo = mo.append(list(range(64)))
+        np.testing.assert_array_equal(plan.slots, so)
+        np.testing.assert_array_equal(plan.evicted, eo)
+        slots.append(plan.slots)
+        evs.append(plan.evicted)
+    ta, ca, sa = ma.tables()
+    to, co, so_ = mo.tables()
+    np.testing.assert_array_equal(ta, to)
+    np.testing.assert_array_equal(ca, co)
+    np.testing.assert_array_equal(sa, so_)
+    man = json.load(open(os.path.join(GOLDEN, "manifest.json")))["config4_schedule"]
+    assert _sha(np.concatenate(slots)) == man["slots_sha256"]
+    assert _sha(np.concatenate(evs)) == man["evicted_sha256"]
+    assert _sha(ta) == man["tables_sha256"]
+
+
+def test_manager_random_ragged_equals_oracle():
+    rng = np.random.default_rng(7)
+    cap, bs = 4096, 16
+    order = orc.permutation(12, cap)
+    pa, pb = BlockPool(cap, order=order), orc.Pool(cap, order=order)
+    for W in (0, 100, 257):
+        ma, mo = KvManager(pa, bs, 8, 400, W), orc.Manager(pb, bs, 8, 400, W)
+        for _ in range(40):
+            seqs = rng.permutation(8)[: int(rng.integers(1, 8))]
+            nt = rng.integers(0, 40, seqs.size)
+            plan = ma.append(seqs, nt)
+            so, eo = mo.append(seqs, nt)
+            np.testing.assert_array_equal(plan.slots, so)
+            np.testing.assert_array_equal(plan.evicted, eo)
+        for x, y in zip(ma.tables(), mo.tables()):
+            np.testing.assert_array_equal(x, y)
+        for s in range(8):
+            ma.release(s)
+            t, _, _ = mo.tables()
+            for blk in t[s][t[s] >= 0]:
+                assert pb.free(int(blk)) == 0
+        assert pa.num_free() == pb.num_free() == cap
+
+
+def test_slots_unique_and_exhaustion():
+    pool = BlockPool(4)
+    m = KvManager(pool, 16, 2, 8)
+    with pytest.raises(InvalidInput, match="exhausted"):
+        m.append([0, 1], [40, 20])  # 3 + 2 blocks > 4
+    m2 = KvManager(BlockPool(64), 16, 2, 8)
+    plan = m2.append([0, 1, 0], [33, 7, 2])
+    assert len(set(plan.slots.tolist())) == 42
+
+
+def test_fork_copy_on_write():
+    pool = BlockPool(16)
+    m = KvManager(pool, 16, 3, 8)
+    a = m.append([0], [20])  # blocks 15 (full) and 14 (partial)
+    m.fork(0, 1)
+    assert pool.ref_count(15) == 2 and pool.ref_count(14) == 2
+    plan = m.append([1], [1], cow=True)  # writing into shared partial block 14
+    assert list(plan.cow_src) == [14] and pool.ref_count(14) == 1
+    new = int(plan.cow_dst[0])
+    assert plan.slots[0] == new * 16 + 4
+    t, cl, _ = m.tables()
+    assert t[1, 0] == 15 and t[1, 1] == new and t[0, 1] == 14 and cl[1] == 21
+    plan0 = m.append([0], [1], cow=True)  # seq 0 now owns 14 alone: no copy
+    assert plan0.cow_src.size == 0 and plan0.slots[0] == 14 * 16 + 4
+
+
+def test_batcher_fifo_admission_and_plans():
+    pool = BlockPool(64)
+    m = KvManager(pool, 16, 4, 16)
+    b = ContinuousBatcher(2, m)
+    for rid, n in ((10, 5), (11, 17), (12, 3)):
+        b.add_request(rid, list(range(n)), 4)
+    assert b.schedule() == [10, 11]  # continuous.rs:62-73, FIFO up to max_batch_size
+    assert b.requests[12].state.value == "Waiting"
+    plan = b.plan_prefill([10, 11])
+    assert plan.slots.size == 22
+    assert plan.slots[0] == 63 * 16 and plan.slots[5] == 62 * 16  # LIFO blocks: 63 for seq 0, 62 for seq 1
+    d = b.plan_decode()
+    assert d.slots.size == 2
+    freed = b.finish(10)
+    assert list(freed) == [63]
+    assert b.schedule() == [11, 12]

@@ -1,0 +1,266 @@
+"""Pins the CPU oracle (oracle/it_oracle.c) before it is trusted as the
+checker: the reference's own known-answer test, closed forms, special cases,
+float64 brute force, and an exhaustive conversion check."""
+import math
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+# ---------------- flash_attn_f32 (src/backend/arm/flash_attn.rs:6-72) ------
+def test_flash_attn_reference_kat(orc):
+    # flash_attn.rs:78-97: q=e0, keys e0,e1,e2, V = 1..12, scale 1.
+    q = np.array([1, 0, 0, 0], np.float32)
+    k = np.array([1, 0, 0, 0, 0, 1, 0, 0, 0, 0, 1, 0], np.float32)
+    v = np.arange(1, 13, dtype=np.float32)
+    out = orc.flash_attn_f32(q, k, v, 1.0)
+    assert np.all(out > 0) and abs(out[0] - 3.54) < 0.1  # the reference's own assertion
+    e = math.e
+    # Closed form: softmax weights (e, 1, 1)/(e+2) over rows (1..4, 5..8, 9..12).
+    want = [(e * (1 + d) + (5 + d) + (9 + d)) / (e + 2) for d in range(4)]
+    np.testing.assert_allclose(out, want, rtol=2e-7)
+    assert abs(out[0] - (e + 14) / (e + 2)) < 1e-6
+
+
+def test_flash_attn_single_key_is_value(orc):
+    q, k, v = orc.normal(1, 64), orc.normal(2, 64), orc.normal(3, 64)
+    np.testing.assert_array_equal(orc.flash_attn_f32(q, k, v, 0.125), v)
+
+
+def test_flash_attn_equal_scores_is_mean(orc):
+    D, n = 32, 50
+    q = orc.normal(4, D)
+    k = np.tile(orc.normal(5, D), n)
+    v = orc.normal(6, n * D).reshape(n, D)
+    np.testing.assert_allclose(orc.flash_attn_f32(q, k, v, 0.3), v.astype(np.float64).mean(0), rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("n,D,scale", [(1, 8, 1.0), (7, 16, 0.25), (300, 128, 1 / math.sqrt(128)), (1000, 64, 0.9)])
+def test_flash_attn_matches_float64_softmax(orc, n, D, scale):
+    q, k, v = orc.normal(7, D), orc.normal(8, n * D).reshape(n, D), orc.normal(9, n * D).reshape(n, D)
+    s = (k.astype(np.float64) @ q.astype(np.float64)) * scale
+    p = np.exp(s - s.max())
+    want = (p @ v.astype(np.float64)) / p.sum()
+    np.testing.assert_allclose(orc.flash_attn_f32(q, k, v, scale), want, rtol=1e-5, atol=1e-6)
+
+
+def test_flash_attn_mask_skips_and_shifts(orc):
+    D, n = 16, 9
+    q, k, v = orc.normal(10, D), orc.normal(11, n * D).reshape(n, D), orc.normal(12, n * D).reshape(n, D)
+    mask = np.zeros(n, np.float32)
+    mask[[1, 4, 8]] = -np.inf
+    keep = mask == 0
+    a = orc.flash_attn_f32(q, k, v, 0.5, mask)
+    b = orc.flash_attn_f32(q, k[keep], v[keep], 0.5)
+    np.testing.assert_array_equal(a, b)  # -inf keys are skipped (flash_attn.rs:35-40)
+    shift = np.linspace(-1, 1, n).astype(np.float32)
+    s = (k.astype(np.float64) @ q) * 0.5 + shift
+    p = np.exp(s - s.max())
+    np.testing.assert_allclose(orc.flash_attn_f32(q, k, v, 0.5, shift), p @ v / p.sum(), rtol=1e-5, atol=1e-6)
+    assert np.all(orc.flash_attn_f32(q, k, v, 0.5, np.full(n, -np.inf, np.float32)) == 0)  # s == 0 -> zeros
+
+
+def test_backend_op_gqa_shares_kv(orc):
+    # arm.rs:304-370: every head reads the same K/V; scale 1/sqrtf(D).
+    H, D, n = 5, 32, 40
+    q = orc.normal(13, H * D).reshape(H, D)
+    k, v = orc.normal(14, n * D).reshape(n, D), orc.normal(15, n * D).reshape(n, D)
+    out = orc.backend_flash_attention(q, k, v)
+    scale = np.float32(1.0) / np.sqrt(np.float32(D))
+    for h in range(H):
+        np.testing.assert_array_equal(out[h], orc.flash_attn_f32(q[h], k, v, float(scale)))
+
+
+# ---------------- Q8_0 (src/backend/arm/quant.rs:149-183) ------------------
+def _q8_numpy(x):
+    """Independent numpy formulation of the x86 scalar Q8_0 semantics."""
+    x = x.astype(np.float32).reshape(-1, 32)
+    ax = np.where(np.isnan(x), np.float32(0), np.abs(x))
+    amax = ax.max(1)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        scale = (amax / np.float32(127)).astype(np.float32)
+        y = (x / scale[:, None]).astype(np.float32).astype(np.float64)
+    r = np.sign(y) * np.floor(np.abs(y) + 0.5)  # half away from zero, exact in f64
+    r = np.where(np.isnan(r), 0, np.clip(r, -128, 127)).astype(np.int8)
+    r[amax == 0] = 0
+    d = scale.astype(np.float16).view(np.uint16)
+    d = np.where(amax == 0, 0, d).astype(np.uint16)
+    rec = np.zeros((x.shape[0], 34), np.uint8)
+    rec[:, 0] = d & 0xFF
+    rec[:, 1] = d >> 8
+    rec[:, 2:] = r.view(np.uint8)
+    return rec
+
+
+def test_q8_zero_group(orc):
+    assert np.all(orc.quantize_row_q8_0(np.zeros(32, np.float32)) == 0)
+    assert np.all(orc.quantize_row_q8_0(-np.zeros(32, np.float32)) == 0)
+
+
+def test_q8_constant_and_spike(orc):
+    rec = orc.quantize_row_q8_0(np.full(32, 0.75, np.float32))
+    assert np.all(rec[0, 2:].view(np.int8) == 127)
+    assert int(rec[0, 0]) | (int(rec[0, 1]) << 8) == np.float16(np.float32(0.75) / np.float32(127)).view(np.uint16)
+    x = np.zeros(32, np.float32)
+    x[5] = -8.0
+    q = orc.quantize_row_q8_0(x)[0, 2:].view(np.int8)
+    assert q[5] == -127 and np.count_nonzero(q) == 1
+
+
+def test_q8_ties_round_half_away_from_zero(orc):
+    # amax = 127 makes scale exactly 1, so x/scale = x: 2.5 -> 3 (RNE would
+    # give 2), -2.5 -> -3, 0.5 -> 1, -0.5 -> -1, 3.5 -> 4.
+    x = np.zeros(32, np.float32)
+    x[0] = 127.0
+    x[1:6] = [2.5, -2.5, 0.5, -0.5, 3.5]
+    q = orc.quantize_row_q8_0(x)[0, 2:].view(np.int8)
+    assert list(q[:6]) == [127, 3, -3, 1, -1, 4]
+
+
+def test_q8_nan_inf(orc):
+    x = np.linspace(-1, 1, 32).astype(np.float32)
+    x[3] = np.nan
+    rec = orc.quantize_row_q8_0(x)
+    q = rec[0, 2:].view(np.int8)
+    assert q[3] == 0 and q[0] == -127 and q[31] == 127  # NaN ignored by the `>` amax
+    x[7] = np.inf
+    rec = orc.quantize_row_q8_0(x)
+    assert int(rec[0, 0]) | (int(rec[0, 1]) << 8) == 0x7C00
+    assert np.all(rec[0, 2:] == 0)  # finite/inf = 0, inf/inf = NaN -> 0 (Rust `as`)
+
+
+def test_q8_matches_numpy_formulation(orc):
+    x = orc.normal(20, 32 * 4096)
+    rng = np.random.default_rng(0)
+    x[rng.random(x.size) < 0.01] *= 8  # the C5 outlier model
+    x[:32] *= 1e-30  # fp16-subnormal and fp32-subnormal scales
+    x[32:64] *= 1e-40
+    x[64:96] *= 3e4
+    np.testing.assert_array_equal(orc.quantize_row_q8_0(x), _q8_numpy(x))
+
+
+def test_q8_dequant_is_d_times_q(orc):
+    x = orc.normal(21, 32 * 64)
+    rec = orc.quantize_row_q8_0(x)
+    deq = orc.dequantize_row_q8_0(rec).reshape(-1, 32)
+    d = (rec[:, 0].astype(np.uint16) | (rec[:, 1].astype(np.uint16) << 8)).view(np.float16).astype(np.float32)
+    np.testing.assert_array_equal(deq, d[:, None] * rec[:, 2:].view(np.int8).astype(np.float32))
+    assert np.max(np.abs(deq - x.reshape(-1, 32))) <= np.max(d) * 0.5 * (1 + 1e-3) + 1e-7
+
+
+# ---------------- conversions --------------------------------------------
+def test_f16_bf16_converters_exhaustive():
+    exe = os.path.join(ROOT, "oracle", "check_f16")
+    if not os.path.exists(exe):
+        subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "oracle")], check=True)
+    r = subprocess.run([exe, "1"], capture_output=True, text=True, timeout=600)
+    assert r.returncode == 0, r.stdout + r.stderr
+
+
+def test_converters_match_numpy(orc):
+    x = orc.normal(22, 100000) * np.float32(300)
+    np.testing.assert_array_equal(orc.f32_to_f16(x), x.astype(np.float16).view(np.uint16))
+    np.testing.assert_array_equal(orc.f16_to_f32(orc.f32_to_f16(x)), x.astype(np.float16).astype(np.float32))
+
+
+# ---------------- BlockPool (src/memory/paged.rs:21-58) ------------------
+def test_pool_lifo_closed_form(orc):
+    p = orc.Pool(6)
+    assert [p.allocate() for _ in range(6)] == [5, 4, 3, 2, 1, 0]
+    assert p.allocate() is None
+    assert p.free(2) == 0 and p.free(4) == 0
+    assert p.allocate() == 4 and p.allocate() == 2  # most recently freed first
+
+
+def test_pool_refcounts(orc):
+    p = orc.Pool(3)
+    b = p.allocate()
+    assert p.share(b) == 0 and p.ref_count(b) == 2
+    assert p.free(b) == 0 and p.num_free() == 2  # still referenced
+    assert p.free(b) == 0 and p.num_free() == 3
+    assert p.free(b) != 0  # would underflow the reference's u32
+    assert p.share(0) != 0 and p.free(99) != 0
+
+
+def test_pool_ordered(orc):
+    order = orc.permutation(3, 10)
+    p = orc.Pool(10, order=order)
+    assert [p.allocate() for _ in range(10)] == list(order[::-1])
+
+
+def test_pool_random_ops_against_list_model(orc):
+    rng = np.random.default_rng(1)
+    cap = 32
+    p = orc.Pool(cap)
+    free_list, refs = list(range(cap)), [0] * cap
+    for _ in range(5000):
+        op = rng.integers(3)
+        if op == 0:
+            got = p.allocate()
+            want = free_list.pop() if free_list else None
+            if want is not None:
+                refs[want] = 1
+            assert got == want
+        else:
+            i = int(rng.integers(cap))
+            rc = p.share(i) if op == 1 else p.free(i)
+            if refs[i] == 0:
+                assert rc != 0
+                continue
+            assert rc == 0
+            if op == 1:
+                refs[i] += 1
+            else:
+                refs[i] -= 1
+                if refs[i] == 0:
+                    free_list.append(i)
+        assert p.num_free() == len(free_list)
+    assert list(p.free_list()) == free_list
+
+
+# ---------------- window manager: config-4 closed forms --------------------
+def _c4_manager(orc, n_seqs=64, start=30000, W=4096, bs=16, cap=16512, seed=4):
+    pool = orc.Pool(cap, order=orc.permutation(seed, cap))
+    first = (start - W) // bs
+    last = (start - 1) // bs
+    max_blocks = 32768 // bs + 1
+    m = orc.Manager(pool, bs, n_seqs, max_blocks, W)
+    for s in range(n_seqs):
+        blocks = [pool.allocate() for _ in range(last - first + 1)]
+        m.seed_seq(s, start, first, blocks)
+    return pool, m, first, last
+
+
+def test_window_c4_schedule(orc):
+    pool, m, first, last = _c4_manager(orc)
+    assert (first, last, last - first + 1) == (1619, 1874, 256)
+    seqs = list(range(64))
+    frees = allocs = 0
+    prev_free_top = None
+    for p in range(30000, 32768):
+        n_free_before = pool.num_free()
+        slots, ev = m.append(seqs)
+        if p % 16 == 15:
+            assert len(ev) == 64
+            prev_free_top = ev[-1]  # seq 63 frees last
+        else:
+            assert len(ev) == 0
+        if p % 16 == 0:
+            allocs += 1
+            if prev_free_top is not None and p == 30016:
+                # LIFO: seq 0 is handed the block seq 63 freed at p = 30015.
+                assert slots[0] // 16 == prev_free_top
+        frees += len(ev) // 64
+        assert pool.num_free() == n_free_before + len(ev) - (64 if p % 16 == 0 else 0)
+        assert np.all(slots % 16 == p % 16)
+    assert frees == 173 and allocs == 173
+    t, cl, sp = m.tables()
+    assert np.all(cl == 32768) and np.all(sp == 32768 - 4096)
+    held = (t >= 0).sum(1)
+    assert np.all(held == 256)
+    live = t[t >= 0]
+    assert len(np.unique(live)) == live.size  # no block owned twice
