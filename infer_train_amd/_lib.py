@@ -114,6 +114,16 @@ def _load() -> C.CDLL:
         raise ImportError(
             f"{LIB_PATH} is missing: build it with `python -c 'import __graft_entry__ as g; g.build()'` "
             "(there is no CPU fallback for the KV-cache kernels)")
+    # One HIP runtime per process.  torch ships its own libamdhip64 and asks
+    # for it as "libamdhip64.so"; this library asks for "libamdhip64.so.7".
+    # If this library loaded first, torch would map a second runtime next to
+    # /opt/rocm's, and whichever came second sees no device.  Loading torch
+    # first makes the dynamic loader satisfy "libamdhip64.so.7" with torch's
+    # copy (same SONAME), so device pointers and streams are shared.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     lib = C.CDLL(LIB_PATH)
     for name, (res, args) in SIGNATURES.items():
         fn = getattr(lib, name)
