@@ -175,6 +175,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--all", action="store_true", help="also measure configs 1, 3, 4 and 5")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="first run 4 device copies of 256 MiB (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus > 1 is not supported (each GPU would own "
@@ -185,6 +187,16 @@ def main():
     import infer_train_amd as it
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.copy_probe:
+        # A plain copy of known size: 256 MiB read + 256 MiB written per
+        # dispatch.  Its counter readings give the KiB-per-byte factor used to
+        # turn the decode kernel's FETCH_SIZE/WRITE_SIZE into HBM bytes.
+        src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda:0").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(4):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     # Headline: config 2 at the 4k target.
     w = DecodeWorkload(it.BF16, 28, 4, 128, 16, np.full(32, 4096), 16384, 512, seed=2)
     cold = w.time(args.steps, args.warmup, rotate=True)

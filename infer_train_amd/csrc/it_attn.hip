@@ -12,7 +12,6 @@ using namespace itkv;
 
 namespace {
 constexpr int kMaxParts = 4096;
-constexpr size_t kMaxDynLds = 64 * 1024;
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
@@ -33,12 +32,12 @@ int pick_chunk(int group) {
   return 1;
 }
 
-hipError_t launch_split(int32_t dt, int d, int gc, const DecodeArgs& a, dim3 grid, size_t smem, hipStream_t s) {
+hipError_t launch_split(int32_t dt, int d, int gc, const DecodeArgs& a, dim3 grid, hipStream_t s) {
   switch (dt) {
-    case IT_BF16: return launch_decode_bf16(d, gc, a, grid, smem, s);
-    case IT_F16: return launch_decode_f16(d, gc, a, grid, smem, s);
-    case IT_F32: return launch_decode_f32(d, gc, a, grid, smem, s);
-    case IT_Q8_0: return launch_decode_q8_0(d, gc, a, grid, smem, s);
+    case IT_BF16: return launch_decode_bf16(d, gc, a, grid, s);
+    case IT_F16: return launch_decode_f16(d, gc, a, grid, s);
+    case IT_F32: return launch_decode_f32(d, gc, a, grid, s);
+    case IT_Q8_0: return launch_decode_q8_0(d, gc, a, grid, s);
     default: return hipErrorInvalidValue;
   }
 }
@@ -88,11 +87,12 @@ int32_t run_decode(const char* who, int32_t cache_dt, int32_t q_dtype, int32_t o
   const int gc = pick_chunk(a.group);
   a.chunks = a.group / gc;
   if (int64_t(a.n_kv_heads) * a.chunks > 65535) return fail(IT_NOT_IMPLEMENTED, "%s: too many head chunks", who);
-  const size_t smem = size_t(std::max(gc * a.partition, kDecodeWaves * gc * d)) * sizeof(float);
-  if (smem > kMaxDynLds) return fail(IT_INVALID_INPUT, "%s: partition %d needs %zu bytes of LDS", who, a.partition, smem);
+  a.max_pages = (a.partition >> a.log2_bs) + 2;
+  const size_t smem = decode_lds_bytes(cache_dt, gc, d, a.partition, a.max_pages);
+  if (smem > kMaxDecodeLds) return fail(IT_INVALID_INPUT, "%s: partition %d needs %zu bytes of LDS", who, a.partition, smem);
   if (max_tokens > 0 && (phases & 1)) {
     dim3 grid(unsigned(a.max_parts), unsigned(a.n_kv_heads * a.chunks), unsigned(n_seqs));
-    hipError_t e = launch_split(cache_dt, d, gc, a, grid, smem, s);
+    hipError_t e = launch_split(cache_dt, d, gc, a, grid, s);
     if (e != hipSuccess) return fail(IT_DEVICE_ERROR, "%s: split launch: %s", who, hipGetErrorString(e));
   }
   if (phases & 2) {

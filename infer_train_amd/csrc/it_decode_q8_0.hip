@@ -4,7 +4,7 @@
 #include "it_decode_launch.hpp"
 
 namespace itkv {
-hipError_t launch_decode_q8_0(int d, int gc, const DecodeArgs& a, dim3 grid, size_t smem, hipStream_t s) {
-  return launch_decode_typed<IT_Q8_0>(d, gc, a, grid, smem, s);
+hipError_t launch_decode_q8_0(int d, int gc, const DecodeArgs& a, dim3 grid, hipStream_t s) {
+  return launch_decode_typed<IT_Q8_0>(d, gc, a, grid, s);
 }
 }  // namespace itkv

@@ -33,11 +33,14 @@ __device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
 constexpr int kDppQuadXor1 = 0xB1;   // quad_perm [1,0,3,2]
 constexpr int kDppQuadXor2 = 0x4E;   // quad_perm [2,3,0,1]
 constexpr int kDppHalfMirror = 0x141; // lane i -> 7-i within 8
-constexpr int kDppRowMirror = 0x140;  // lane i -> 15-i within 16
+constexpr int kDppRowRor8 = 0x128;    // lane i -> (i+8) mod 16 within 16
 
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float x) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+  // Every control used here reads a lane of the same row, so bound_ctrl is
+  // moot; setting it lets the compiler fold the move into the consuming
+  // v_add/v_max (one DPP-modified VALU op per reduction step).
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
 }
 // xor-16 within each 32-lane half: ds_swizzle bit mode (and 0x1F, xor 0x10).
 __device__ __forceinline__ float swz_xor16(float x) {
@@ -56,7 +59,7 @@ __device__ __forceinline__ float group_sum(float x) {
   if constexpr (N >= 2) x += dpp_f<kDppQuadXor1>(x);
   if constexpr (N >= 4) x += dpp_f<kDppQuadXor2>(x);
   if constexpr (N >= 8) x += dpp_f<kDppHalfMirror>(x);
-  if constexpr (N >= 16) x += dpp_f<kDppRowMirror>(x);
+  if constexpr (N >= 16) x += dpp_f<kDppRowRor8>(x);
   if constexpr (N >= 32) x += swz_xor16(x);
   if constexpr (N >= 64) x += swap_halves(x);
   return x;
@@ -66,7 +69,7 @@ __device__ __forceinline__ float group_max(float x) {
   if constexpr (N >= 2) x = fmaxf(x, dpp_f<kDppQuadXor1>(x));
   if constexpr (N >= 4) x = fmaxf(x, dpp_f<kDppQuadXor2>(x));
   if constexpr (N >= 8) x = fmaxf(x, dpp_f<kDppHalfMirror>(x));
-  if constexpr (N >= 16) x = fmaxf(x, dpp_f<kDppRowMirror>(x));
+  if constexpr (N >= 16) x = fmaxf(x, dpp_f<kDppRowRor8>(x));
   if constexpr (N >= 32) x = fmaxf(x, swz_xor16(x));
   if constexpr (N >= 64) x = fmaxf(x, swap_halves(x));
   return x;
