@@ -201,6 +201,16 @@ int32_t it_kv_gather(const it_kv_cache* cache, const int32_t* block_tables, int3
  * recycled block starts clean.  blocks: int32[n], device. */
 int32_t it_kv_evict(it_kv_cache* cache, const int32_t* blocks, int32_t n, void* stream);
 
+/* Keep a device block table in step with the slot mapping: for each token
+ * i with slots[i] >= 0, tables[seq[i]][pos[i] / block_size] :=
+ * slots[i] / block_size (every token of a block writes the same id).
+ * tables: int32[n_seqs][max_blocks]; seq, pos: int32[n]; slots:
+ * int64[n]; all device.  Out-of-range entries are skipped and latched
+ * (it_kv_cache_check). */
+int32_t it_kv_sync_tables(it_kv_cache* cache, int32_t* tables, int32_t max_blocks, int32_t n_seqs,
+                          const int32_t* seq, const int32_t* pos, const int64_t* slots, int32_t n,
+                          void* stream);
+
 /* Copy-on-write page copy: block dst[i] := block src[i] (all heads, K, V). */
 int32_t it_kv_copy_blocks(it_kv_cache* cache, const int32_t* src, const int32_t* dst, int32_t n,
                           void* stream);

@@ -27,6 +27,9 @@ class StepPlan:
     evicted: np.ndarray
     cow_src: np.ndarray = field(default_factory=lambda: np.zeros(0, np.int32))
     cow_dst: np.ndarray = field(default_factory=lambda: np.zeros(0, np.int32))
+    # Sequence and position of every new token (for it_kv_sync_tables).
+    token_seq: np.ndarray = field(default_factory=lambda: np.zeros(0, np.int32))
+    token_pos: np.ndarray = field(default_factory=lambda: np.zeros(0, np.int32))
 
 
 class KvManager:
@@ -59,6 +62,9 @@ class KvManager:
         else:
             nt = np.ascontiguousarray(np.asarray(n_tokens, dtype=np.int32))
         total = int(nt.sum())
+        before = self.positions()
+        token_seq = np.repeat(seqs_a, nt).astype(np.int32)
+        token_pos = (before[token_seq] + (np.arange(total) - np.repeat(np.cumsum(nt) - nt, nt))).astype(np.int32)
         slots = np.empty(max(total, 1), dtype=np.int64)
         # Upper bound of frees: every block of every listed sequence.
         cap = int(seqs_a.size * self.max_blocks + 1)
@@ -71,10 +77,17 @@ class KvManager:
             check(lib.it_kv_manager_append_cow(self._h, seqs_a.ctypes.data, nt.ctypes.data, seqs_a.size,
                                                slots.ctypes.data, ev.ctypes.data, cap, C.byref(nev),
                                                cs.ctypes.data, cd.ctypes.data, cap, C.byref(nc)))
-            return StepPlan(slots[:total], ev[:nev.value].copy(), cs[:nc.value].copy(), cd[:nc.value].copy())
+            return StepPlan(slots[:total], ev[:nev.value].copy(), cs[:nc.value].copy(), cd[:nc.value].copy(),
+                            token_seq, token_pos)
         check(lib.it_kv_manager_append(self._h, seqs_a.ctypes.data, nt.ctypes.data, seqs_a.size,
                                        slots.ctypes.data, ev.ctypes.data, cap, C.byref(nev)))
-        return StepPlan(slots[:total], ev[:nev.value].copy())
+        return StepPlan(slots[:total], ev[:nev.value].copy(), token_seq=token_seq, token_pos=token_pos)
+
+    def positions(self) -> np.ndarray:
+        """Next position (= context length) of every sequence slot."""
+        cl = np.empty(self.max_seqs, dtype=np.int32)
+        check(lib.it_kv_manager_tables(self._h, None, 0, cl.ctypes.data, None))
+        return cl
 
     def release(self, seq: int) -> np.ndarray:
         cap = self.max_blocks

@@ -233,6 +233,27 @@ __global__ __launch_bounds__(kThreads) void kv_copy_blocks(char* __restrict__ kp
 }
 
 // ---------------------------------------------------------------------------
+// Block-table sync: tables[seq][pos >> log2_bs] = slot >> log2_bs.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void kv_sync_tables(int32_t* __restrict__ tables, int max_blocks, int n_seqs,
+                                                           const int32_t* __restrict__ seq,
+                                                           const int32_t* __restrict__ pos,
+                                                           const int64_t* __restrict__ slots, int n, int log2_bs,
+                                                           int64_t num_blocks, uint32_t* err) {
+  const int i = blockIdx.x * kThreads + threadIdx.x;
+  if (i >= n) return;
+  const int64_t slot = slots[i];
+  if (slot < 0) return;  // padding token
+  const int s = seq[i], p = pos[i];
+  const int64_t blk = slot >> log2_bs;
+  if (s < 0 || s >= n_seqs || p < 0 || (p >> log2_bs) >= max_blocks || blk >= num_blocks) {
+    atomicOr(err, kErrTable);
+    return;
+  }
+  tables[int64_t(s) * max_blocks + (p >> log2_bs)] = int32_t(blk);
+}
+
+// ---------------------------------------------------------------------------
 // Cache set-up.
 // ---------------------------------------------------------------------------
 int32_t check_shape(int64_t num_blocks, int32_t block_size, int32_t n_kv_heads, int32_t head_dim,
@@ -450,6 +471,21 @@ extern "C" int32_t it_kv_evict(it_kv_cache* c, const int32_t* blocks, int32_t n,
   hipLaunchKernelGGL(kv_clear_blocks, grid, dim3(kThreads), 0, (hipStream_t)stream, (char*)c->k_pool,
                      (char*)c->v_pool, blocks, block_vecs, c->num_blocks, c->err_flag);
   IT_HIP(hipGetLastError(), "it_kv_evict: launch");
+  return IT_OK;
+}
+
+extern "C" int32_t it_kv_sync_tables(it_kv_cache* c, int32_t* tables, int32_t max_blocks, int32_t n_seqs,
+                                     const int32_t* seq, const int32_t* pos, const int64_t* slots, int32_t n,
+                                     void* stream) {
+  if (!c) return fail(IT_INVALID_INPUT, "it_kv_sync_tables: cache is NULL");
+  if (n < 0 || max_blocks <= 0 || n_seqs <= 0)
+    return fail(IT_INVALID_INPUT, "it_kv_sync_tables: n=%d max_blocks=%d n_seqs=%d", n, max_blocks, n_seqs);
+  if (n == 0) return IT_OK;
+  if (!tables || !seq || !pos || !slots) return fail(IT_INVALID_INPUT, "it_kv_sync_tables: NULL tensor");
+  DeviceGuard g(c->device);
+  hipLaunchKernelGGL(kv_sync_tables, dim3(unsigned(cdiv(n, kThreads))), dim3(kThreads), 0, (hipStream_t)stream,
+                     tables, max_blocks, n_seqs, seq, pos, slots, n, c->log2_bs, c->num_blocks, c->err_flag);
+  IT_HIP(hipGetLastError(), "it_kv_sync_tables: launch");
   return IT_OK;
 }
 

@@ -109,6 +109,11 @@ class PagedKvCache:
     def evict(self, blocks: torch.Tensor) -> None:
         check(lib.it_kv_evict(self._h, _ptr(blocks), blocks.numel(), stream_handle(self.device)))
 
+    def sync_tables(self, tables: torch.Tensor, seq: torch.Tensor, pos: torch.Tensor, slots: torch.Tensor) -> None:
+        """tables[seq[i], pos[i] // bs] = slots[i] // bs (device int32 table [n_seqs, max_blocks])."""
+        check(lib.it_kv_sync_tables(self._h, _ptr(tables), tables.shape[1], tables.shape[0], _ptr(seq), _ptr(pos),
+                                    _ptr(slots), slots.numel(), stream_handle(self.device)))
+
     def copy_blocks(self, src: torch.Tensor, dst: torch.Tensor) -> None:
         check(lib.it_kv_copy_blocks(self._h, _ptr(src), _ptr(dst), src.numel(), stream_handle(self.device)))
 
