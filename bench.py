@@ -1,18 +1,25 @@
-"""Benchmark of the MI355X KV-cache hot path.
+"""Benchmark of the MI355X KV-cache hot path (BASELINE.json's five configs).
 
-Headline workload (BASELINE.json metric, config 2 at its 4k target): batched
-paged decode, bf16, Hq 28 / Hkv 4 / D 128, block size 16, batch 32 with every
-sequence at 4096 tokens after the step's append, pages scattered by a seeded
-permutation of a 16384-block pool, split-K over 512-token partitions.  One
-step = slot-mapped append of 1 token per sequence + split-K decode + combine.
+Headline (`value`): config 2 at its 4k target -- batched paged decode,
+bf16, Hq 28 / Hkv 4 / D 128, block size 16, batch 32 with every sequence at
+4096 tokens after the step's append, pages a seeded permutation of a
+16384-block pool, split-K over 512-token partitions.  One step = slot-mapped
+append of 1 token per sequence + split-K decode + combine; value = KV bytes
+read per step / mean(split + combine time), the algorithmic bytes
+sum_b ctx_b * Hkv * 2 * D * 2.  Three pool replicas are rotated so the 256 MB
+last-level cache does not hold the previous step's pages (cold); warm numbers
+(one replica) are reported beside it.  Kernel times are HIP events recorded
+on the stream the kernels run on (torch's current stream).
 
-value = KV bytes read per step / median(split + combine time), the
-algorithmic bytes sum_b ctx_b * Hkv * 2 * D * 2.  Three pool replicas are
-rotated so the 256 MB last-level cache does not hold the previous step's
-pages (cold); warm numbers (one replica) are reported beside it.  Timing uses
-HIP events on the stream the kernels run on.
+The other configs run at their full shapes and are reported under
+"configs": config 1 (fp32 single-sequence step), config 2 as specified
+(ragged contexts), config 3 (chunk append + MFMA causal prefill), config 4
+(sliding-window steps with eviction and block reuse) and config 5 (Q8_0
+quantise-append + long-context decode).  Each carries a bounded CPU sample
+of the oracle (the C restatement of the reference's arithmetic, 1 thread).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--all]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 1,2,3,4,5]
+                    [--no-cpu] [--copy-probe]
 """
 from __future__ import annotations
 
@@ -28,8 +35,9 @@ import numpy as np
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-HBM_PEAK_GBS = 8000.0      # MI355X HBM3E, AMD-published
-MFMA_BF16_PEAK_TFS = 2500.0  # dense bf16
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, AMD-published
+MFMA_BF16_PEAK_TFS = 2500.0  # MI355X dense bf16 MFMA, AMD-published
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_split_config2_4k_traffic.json")
 
 
 def _events(n):
@@ -38,10 +46,23 @@ def _events(n):
     return [torch.cuda.Event(enable_timing=True) for _ in range(n)]
 
 
+def _dev():
+    import torch
+
+    return torch.device("cuda", 0)
+
+
+def _cpu_threads():
+    return 1  # the oracle is scalar C, run on one host thread
+
+
+# ---------------------------------------------------------------------------
+# Decode (configs 1, 2, 5)
+# ---------------------------------------------------------------------------
 class DecodeWorkload:
     """A paged decode batch with `replicas` copies of the pools."""
 
-    def __init__(self, dtype, hq, hkv, D, bs, ctx, pool_blocks, partition, seed, replicas=3, q_dtype=None):
+    def __init__(self, dtype, hq, hkv, D, bs, ctx, pool_blocks, partition, seed, replicas=3, identity=False):
         import torch
 
         import infer_train_amd as it
@@ -54,7 +75,7 @@ class DecodeWorkload:
         B = self.ctx.size
         self.B = B
         rng = np.random.default_rng(seed)
-        perm = rng.permutation(pool_blocks).astype(np.int32)
+        perm = np.arange(pool_blocks, dtype=np.int32) if identity else rng.permutation(pool_blocks).astype(np.int32)
         self.max_blocks = int((self.ctx.max() + bs - 1) // bs)
         t = np.full((B, self.max_blocks), -1, np.int32)
         k = 0
@@ -63,7 +84,7 @@ class DecodeWorkload:
             t[b, :nb] = perm[k:k + nb]
             k += nb
         assert k <= pool_blocks, "pool too small"
-        dev = torch.device("cuda", 0)
+        dev = _dev()
         self.tables = torch.from_numpy(t).to(dev)
         self.ctx_d = torch.from_numpy(self.ctx).to(dev)
         # The step appends the token at position ctx-1 of each sequence.
@@ -75,22 +96,25 @@ class DecodeWorkload:
         for _ in range(replicas):
             c = PagedKvCache(pool_blocks, bs, hkv, D, dtype)
             if dtype == it.Q8_0:
-                # Fill through the quantising append so pages hold valid Q8_0.
-                n_rows = pool_blocks * bs
+                # Only the pages the tables name are filled, through the
+                # quantising append (N(0,1) with 1% of elements x8).
+                used = np.concatenate([t[b, : (int(cc) + bs - 1) // bs] for b, cc in enumerate(self.ctx)])
+                rows = (used.astype(np.int64)[:, None] * bs + np.arange(bs)[None, :]).reshape(-1)
+                rows_d = torch.from_numpy(rows).to(dev)
                 step = 1 << 16
-                for s0 in range(0, n_rows, step):
-                    n = min(step, n_rows - s0)
+                for s0 in range(0, rows.size, step):
+                    n = min(step, rows.size - s0)
                     kk = torch.randn((n, hkv, D), generator=g, device=dev)
                     kk[torch.rand((n, hkv, D), generator=g, device=dev) < 0.01] *= 8
                     vv = torch.randn((n, hkv, D), generator=g, device=dev)
-                    c.append(kk, vv, torch.arange(s0, s0 + n, device=dev, dtype=torch.int64))
+                    vv[torch.rand((n, hkv, D), generator=g, device=dev) < 0.01] *= 8
+                    c.append(kk, vv, rows_d[s0:s0 + n])
             else:
                 td = {it.BF16: torch.bfloat16, it.F16: torch.float16, it.F32: torch.float32}[dtype]
                 c.view("k").copy_(torch.randn(c.view("k").shape, generator=g, device=dev).to(td))
                 c.view("v").copy_(torch.randn(c.view("v").shape, generator=g, device=dev).to(td))
             self.caches.append(c)
-        qd = q_dtype if q_dtype is not None else ({it.Q8_0: torch.float32, it.F32: torch.float32,
-                                                   it.BF16: torch.bfloat16, it.F16: torch.float16}[dtype])
+        qd = {it.Q8_0: torch.float32, it.F32: torch.float32, it.BF16: torch.bfloat16, it.F16: torch.float16}[dtype]
         self.q = torch.randn((B, hq, D), generator=g, device=dev).to(qd)
         src_t = torch.float32 if dtype in (it.Q8_0, it.F32) else qd
         self.k_new = torch.randn((B, hkv, D), generator=g, device=dev).to(src_t)
@@ -119,8 +143,8 @@ class DecodeWorkload:
                 ev[2 + j].record()
 
     def time(self, steps, warmup, rotate=True):
-        """Per-kernel times (ms) over `steps` event-bracketed steps: medians of
-        append and split+combine, mean of split alone, and wall ms per step."""
+        """Per-kernel times (ms) over `steps` event-bracketed steps: mean and
+        median of append and split+combine, mean of split alone, wall per step."""
         torch = self.torch
         n_rep = len(self.caches) if rotate else 1
         for i in range(warmup):
@@ -137,35 +161,390 @@ class DecodeWorkload:
         dec = np.array([e[1].elapsed_time(e[3]) for e in evs])
         for c in self.caches:
             c.check()
-        return {"append": float(np.median(app)), "decode": float(np.median(dec)), "split_mean": float(split.mean()),
-                "split_median": float(np.median(split)), "step_wall": wall * 1e3 / steps}
+        return {"append": float(app.mean()), "decode": float(dec.mean()), "decode_median": float(np.median(dec)),
+                "split": float(split.mean()), "step_wall": wall * 1e3 / steps}
+
+    def release(self):
+        self.caches = []
+        self.torch.cuda.empty_cache()
 
 
-def cpu_baseline_c2(n_seqs_total, ctx, hq=28, hkv=4, D=128, bs=16, budget_s=10.0):
-    """The oracle (scalar C restatement of flash_attn_f32 + the GQA driver) on
-    a bounded sample of the headline workload, on this host, 1 thread."""
+def cpu_decode_sample(dtype, hq, hkv, D, bs, ctx, budget_s=8.0, seqs_per_call=2):
+    """The oracle's paged decode (flash_attn_f32 per head) on `seqs_per_call`
+    sequences of context `ctx`, repeated for about budget_s; KV GB/s."""
     import oracle as orc
 
-    B = 4
+    B = seqs_per_call
     nb = B * ((ctx + bs - 1) // bs)
-    c = orc.Cache(nb, bs, hkv, D, orc.BF16)
-    bits = orc.f32_to_bf16(orc.normal(1, c.k.size // 2))
-    c.k[:] = np.frombuffer(bits.tobytes(), np.uint8)
-    c.v[:] = np.frombuffer(orc.f32_to_bf16(orc.normal(2, c.v.size // 2)).tobytes(), np.uint8)
+    c = orc.Cache(nb, bs, hkv, D, dtype)
+    if dtype == orc.Q8_0:
+        n = nb * bs
+        x = orc.normal(1, n * hkv * D).reshape(n, hkv, D)
+        c.append(x, orc.normal(2, n * hkv * D).reshape(n, hkv, D), np.arange(n, dtype=np.int64))
+        elem = 34.0 / 32.0
+    else:
+        n_el = c.k.size // (4 if dtype == orc.F32 else 2)  # elements per pool
+        if dtype == orc.F32:
+            c.k[:] = np.frombuffer(orc.normal(1, n_el).tobytes(), np.uint8)
+            c.v[:] = np.frombuffer(orc.normal(2, n_el).tobytes(), np.uint8)
+            elem = 4.0
+        else:
+            c.k[:] = np.frombuffer(orc.f32_to_bf16(orc.normal(1, n_el)).tobytes(), np.uint8)
+            c.v[:] = np.frombuffer(orc.f32_to_bf16(orc.normal(2, n_el)).tobytes(), np.uint8)
+            elem = 2.0
     t = np.arange(nb, dtype=np.int32).reshape(B, -1)
     cl = np.full(B, ctx, np.int32)
-    q = orc.bf16_to_f32(orc.f32_to_bf16(orc.normal(3, B * hq * D)))
+    q = orc.normal(3, B * hq * D)
     done, t0 = 0, time.perf_counter()
     while True:
         c.decode(q, hq, t, cl, None, 1.0 / math.sqrt(D))
         done += B
         el = time.perf_counter() - t0
-        if el >= budget_s or done >= 8 * n_seqs_total:
+        if el >= budget_s:
             break
-    gbs = done * ctx * hkv * 2 * D * 2 / el / 1e9
-    return {"value": round(gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"oracle decode of {done} sequences x ctx {ctx} (Hq {hq}/Hkv {hkv}/D {D} bf16 widened to f32) "
-                      f"in {el:.1f} s; full step = {n_seqs_total} sequences"}
+    return done, el, done * ctx * hkv * 2 * D * elem / el / 1e9
+
+
+# ---------------------------------------------------------------------------
+# Config 1
+# ---------------------------------------------------------------------------
+def bench_config1(steps, warmup, cpu):
+    import infer_train_amd as it
+
+    w = DecodeWorkload(it.F32, 12, 2, 128, 16, [1024], 64, 512, seed=1, replicas=1, identity=True)
+    r = w.time(steps, warmup, rotate=False)
+    out = {"workload": "config 1: fp32 GQA decode step, Hq 12 / Hkv 2 / D 128, block 16, 1023 cached + 1 "
+                       "appended, identity table over 64 blocks",
+           "step_us": round((r["append"] + r["decode"]) * 1e3, 2), "append_us": round(r["append"] * 1e3, 2),
+           "decode_us": round(r["decode"] * 1e3, 2), "split_us": round(r["split"] * 1e3, 2),
+           "kv_bytes": int(w.kv_bytes), "kv_gbs": round(w.kv_bytes / (r["decode"] * 1e-3) / 1e9, 1),
+           "note": "launch-bound: 2 MB of KV"}
+    w.release()
+    if cpu:
+        import oracle as orc
+
+        done, el, gbs = cpu_decode_sample(orc.F32, 12, 2, 128, 16, 1024, budget_s=3.0, seqs_per_call=1)
+        out["cpu"] = {"decode_us": round(el / done * 1e6, 1), "kv_gbs": round(gbs, 3), "cores": _cpu_threads(),
+                      "sample": f"{done} oracle decode steps of the config-1 shape in {el:.1f} s"}
+    return out
+
+
+# ---------------------------------------------------------------------------
+# Config 2
+# ---------------------------------------------------------------------------
+def bench_config2(steps, warmup, cpu):
+    import torch
+
+    import infer_train_amd as it
+
+    w = DecodeWorkload(it.BF16, 28, 4, 128, 16, np.full(32, 4096), 16384, 512, seed=2)
+    cold = w.time(steps, warmup, rotate=True)
+    warm = w.time(steps, warmup, rotate=False)
+    head = {"kv_bytes": int(w.kv_bytes), "append_bytes": int(w.append_bytes), "B": w.B, "cold": cold, "warm": warm}
+    w.release()
+    rng = np.random.default_rng(22)
+    ctx2 = rng.integers(256, 4097, 32) + 1
+    w2 = DecodeWorkload(it.BF16, 28, 4, 128, 16, ctx2, 16384, 512, seed=3)
+    r2 = w2.time(steps, warmup, rotate=True)
+    ragged = {"workload": "config 2 as specified: ctx U[256, 4096] + 1 appended, batch 32",
+              "kv_gbs": round(w2.kv_bytes / (r2["decode"] * 1e-3) / 1e9, 1), "decode_us": round(r2["decode"] * 1e3, 2),
+              "split_us": round(r2["split"] * 1e3, 2), "kv_bytes": int(w2.kv_bytes),
+              "append_us": round(r2["append"] * 1e3, 2),
+              "pct_hbm_peak": round(100 * w2.kv_bytes / (r2["decode"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 2)}
+    w2.release()
+    torch.cuda.empty_cache()
+    cpu_b = None
+    if cpu:
+        import oracle as orc
+
+        done, el, gbs = cpu_decode_sample(orc.BF16, 28, 4, 128, 16, 4096, budget_s=10.0, seqs_per_call=4)
+        cpu_b = {"value": round(gbs, 4), "unit": "GB/s", "cores": _cpu_threads(), "kind": "port",
+                 "sample": f"oracle paged decode (flash_attn_f32 per head, bf16 widened to f32) of {done} sequences "
+                           f"x 4096 tokens, Hq 28 / Hkv 4 / D 128, in {el:.1f} s on 1 host thread; the full step is "
+                           f"32 sequences"}
+    return head, ragged, cpu_b
+
+
+# ---------------------------------------------------------------------------
+# Config 3
+# ---------------------------------------------------------------------------
+def bench_config3(steps, warmup, cpu):
+    import torch
+
+    import infer_train_amd as it
+    from infer_train_amd.kv import PagedKvCache
+
+    hq, hkv, D, bs, B, cached, chunk, nb = 32, 8, 128, 16, 8, 2048, 512, 4096
+    dev = _dev()
+    rng = np.random.default_rng(3)
+    perm = rng.permutation(nb).astype(np.int32)
+    mb = (cached + chunk) // bs
+    t = perm[: B * mb].reshape(B, mb)
+    c = PagedKvCache(nb, bs, hkv, D, it.BF16)
+    g = torch.Generator(device=dev)
+    g.manual_seed(3)
+    c.view("k").copy_(torch.randn(c.view("k").shape, generator=g, device=dev).to(torch.bfloat16))
+    c.view("v").copy_(torch.randn(c.view("v").shape, generator=g, device=dev).to(torch.bfloat16))
+    pos = np.arange(cached, cached + chunk)
+    slots = np.concatenate([t[b, pos // bs].astype(np.int64) * bs + pos % bs for b in range(B)])
+    slots_d = torch.from_numpy(slots).to(dev)
+    kn = torch.randn((B * chunk, hkv, D), generator=g, device=dev).to(torch.bfloat16)
+    vn = torch.randn((B * chunk, hkv, D), generator=g, device=dev).to(torch.bfloat16)
+    q = torch.randn((B * chunk, hq, D), generator=g, device=dev).to(torch.bfloat16)
+    cu = torch.arange(0, (B + 1) * chunk, chunk, dtype=torch.int32, device=dev)
+    tables = torch.from_numpy(np.ascontiguousarray(t)).to(dev)
+    ctx = torch.full((B,), cached + chunk, dtype=torch.int32, device=dev)
+    out = torch.empty_like(q)
+    scale = 1.0 / math.sqrt(D)
+
+    def step(ev=None):
+        if ev is not None:
+            ev[0].record()
+        c.append(kn, vn, slots_d)
+        if ev is not None:
+            ev[1].record()
+        c.prefill(q, cu, chunk, tables, ctx, scale=scale, causal=True, out=out)
+        if ev is not None:
+            ev[2].record()
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    evs = [_events(3) for _ in range(steps)]
+    for i in range(steps):
+        step(evs[i])
+    torch.cuda.synchronize()
+    c.check()
+    app = float(np.mean([e[0].elapsed_time(e[1]) for e in evs]))
+    pre = float(np.mean([e[1].elapsed_time(e[2]) for e in evs]))
+    # Causal-exact flops: 4 D Hq sum over rows of the keys each row attends.
+    flops = 4.0 * D * hq * B * sum(cached + i + 1 for i in range(chunk))
+    n_tok = B * chunk
+    res = {"workload": "config 3: chunk append (8 x 512 tokens) + causal MFMA prefill, bf16, Hq 32 / Hkv 8 / D 128, "
+                       "block 16, 2048 cached, table a permutation of a 4096-block pool",
+           "prefill_us": round(pre * 1e3, 2), "flops": flops, "tflops": round(flops / (pre * 1e-3) / 1e12, 1),
+           "pct_mfma_peak": round(100 * flops / (pre * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFS, 2),
+           "append_us": round(app * 1e3, 2), "append_mtok_s": round(n_tok / (app * 1e-3) / 1e6, 1),
+           "append_gbs": round(n_tok * hkv * 2 * D * 2 * 2 / (app * 1e-3) / 1e9, 1)}
+    if cpu:
+        import oracle as orc
+
+        oc = orc.Cache(mb, bs, hkv, D, orc.BF16)
+        oc.k[:] = np.frombuffer(orc.f32_to_bf16(orc.normal(5, oc.k.size // 2)).tobytes(), np.uint8)
+        oc.v[:] = np.frombuffer(orc.f32_to_bf16(orc.normal(6, oc.v.size // 2)).tobytes(), np.uint8)
+        qq = orc.normal(7, chunk * hq * D).reshape(chunk, hq, D)
+        cuq = np.array([0, chunk], np.int32)
+        tt = np.arange(mb, dtype=np.int32)[None, :]
+        cl = np.array([cached + chunk], np.int32)
+        rows, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < 5.0 and rows < chunk:
+            oc.prefill(qq, hq, cuq, tt, cl, scale, causal=True, rows=(0, chunk - 1 - rows, chunk - rows))
+            rows += 1
+        el = time.perf_counter() - t0
+        row_flops = 4.0 * D * hq * sum(cached + chunk - r for r in range(rows))
+        res["cpu"] = {"gflops": round(row_flops / el / 1e9, 3), "cores": _cpu_threads(),
+                      "sample": f"oracle prefill of the last {rows} query rows (all 32 heads) of one sequence in "
+                                f"{el:.1f} s; the full step is 8 x 512 rows"}
+    del c
+    torch.cuda.empty_cache()
+    return res
+
+
+# ---------------------------------------------------------------------------
+# Config 4
+# ---------------------------------------------------------------------------
+def bench_config4(steps, warmup, cpu):
+    import torch
+
+    import infer_train_amd as it
+    from infer_train_amd import BlockPool, KvManager
+    from infer_train_amd.kv import PagedKvCache
+
+    n_seqs, hq, hkv, D, bs, W, start, cap = 64, 16, 2, 128, 16, 4096, 30000, 16512
+    dev = _dev()
+    rng = np.random.default_rng(4)
+    pool = BlockPool(cap, it.BF16, order=rng.permutation(cap))
+    mb = 32768 // bs + 1
+    mgr = KvManager(pool, bs, n_seqs, mb, W)
+    first, last = (start - W) // bs, (start - 1) // bs
+    c = PagedKvCache(cap, bs, hkv, D, it.BF16)
+    g = torch.Generator(device=dev)
+    g.manual_seed(4)
+    c.view("k").copy_(torch.randn(c.view("k").shape, generator=g, device=dev).to(torch.bfloat16))
+    c.view("v").copy_(torch.randn(c.view("v").shape, generator=g, device=dev).to(torch.bfloat16))
+    tables = torch.full((n_seqs, mb), -1, dtype=torch.int32, device=dev)
+    t_host = np.full((n_seqs, mb), -1, np.int32)
+    for s in range(n_seqs):
+        blocks = [pool.allocate() for _ in range(last - first + 1)]
+        mgr.seed_seq(s, start, first, blocks)
+        t_host[s, first:last + 1] = blocks
+    tables.copy_(torch.from_numpy(t_host))
+    q = torch.randn((n_seqs, hq, D), generator=g, device=dev).to(torch.bfloat16)
+    kn = torch.randn((n_seqs, hkv, D), generator=g, device=dev).to(torch.bfloat16)
+    vn = torch.randn((n_seqs, hkv, D), generator=g, device=dev).to(torch.bfloat16)
+    out = torch.empty_like(q)
+    ws = c.decode_workspace(n_seqs, hq, W, 512)
+    scale = 1.0 / math.sqrt(D)
+    seqs = list(range(n_seqs))
+
+    def step(ev=None):
+        t0 = time.perf_counter()
+        plan = mgr.append(seqs)
+        ctx = mgr.positions()  # context lengths after the append
+        st = np.maximum(ctx - W, 0).astype(np.int32)
+        host_s = time.perf_counter() - t0
+        ev_d = torch.from_numpy(plan.evicted).to(dev, non_blocking=False) if plan.evicted.size else None
+        slots = torch.from_numpy(plan.slots).to(dev)
+        tseq = torch.from_numpy(plan.token_seq).to(dev)
+        tpos = torch.from_numpy(plan.token_pos).to(dev)
+        ctx_d = torch.from_numpy(ctx).to(dev)
+        st_d = torch.from_numpy(st).to(dev)
+        if ev is not None:
+            ev[0].record()
+        if ev_d is not None:
+            c.evict(ev_d)
+        c.append(kn, vn, slots)
+        c.sync_tables(tables, tseq, tpos, slots)
+        if ev is not None:
+            ev[1].record()
+        c.decode(q, tables, ctx_d, st_d, W, scale=scale, partition=512, out=out, ws=ws)
+        if ev is not None:
+            ev[2].record()
+        return host_s, int(plan.evicted.size)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    evs = [_events(3) for _ in range(steps)]
+    hosts, n_ev = [], 0
+    t0 = time.perf_counter()
+    for i in range(steps):
+        h, ne = step(evs[i])
+        hosts.append(h)
+        n_ev += ne
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    c.check()
+    upd = float(np.mean([e[0].elapsed_time(e[1]) for e in evs]))
+    dec = float(np.mean([e[1].elapsed_time(e[2]) for e in evs]))
+    kv_bytes = n_seqs * W * hkv * 2 * D * 2
+    res = {"workload": f"config 4: {steps} sliding-window steps from position {start + warmup}, 64 sequences, "
+                       "Hq 16 / Hkv 2 / D 128, W 4096, block 16, 16512-block pool in seeded order; step = host "
+                       "window manager + evict + append + table sync + windowed split-K decode",
+           "decode_us": round(dec * 1e3, 2), "kv_gbs": round(kv_bytes / (dec * 1e-3) / 1e9, 1),
+           "pct_hbm_peak": round(100 * kv_bytes / (dec * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
+           "evict_append_sync_us": round(upd * 1e3, 2), "host_manager_us": round(1e6 * float(np.mean(hosts)), 1),
+           "step_wall_us": round(wall * 1e6 / steps, 1), "blocks_evicted": n_ev, "kv_bytes": kv_bytes}
+    if cpu:
+        import oracle as orc
+
+        done, el, gbs = cpu_decode_sample(orc.BF16, hq, hkv, D, bs, W, budget_s=4.0, seqs_per_call=2)
+        res["cpu"] = {"kv_gbs": round(gbs, 4), "cores": _cpu_threads(),
+                      "sample": f"oracle decode of {done} windows of 4096 tokens (Hq 16 / Hkv 2) in {el:.1f} s; "
+                                f"a step is 64 windows"}
+    del c
+    torch.cuda.empty_cache()
+    return res
+
+
+# ---------------------------------------------------------------------------
+# Config 5
+# ---------------------------------------------------------------------------
+def bench_config5(steps, warmup, cpu):
+    import torch
+
+    import infer_train_amd as it
+
+    rng = np.random.default_rng(5)
+    ctx = rng.integers(32768, 131073, 16).astype(np.int32)
+    pool_blocks = int(sum((int(c) + 31) // 32 for c in ctx)) + 16
+    w = DecodeWorkload(it.Q8_0, 24, 4, 256, 32, ctx, pool_blocks, 512, seed=5, replicas=1)
+    r = w.time(steps, warmup, rotate=False)
+    res = {"workload": "config 5: Q8_0 KV, Hq 24 / Hkv 4 / D 256, block 32, batch 16, ctx U[32768, 131072], "
+                       "quantise-append 1 token per sequence + split-K decode (512-token partitions) dequantising "
+                       "in registers",
+           "kv_bytes": int(w.kv_bytes), "decode_us": round(r["decode"] * 1e3, 2), "split_us": round(r["split"] * 1e3, 2),
+           "kv_gbs": round(w.kv_bytes / (r["decode"] * 1e-3) / 1e9, 1),
+           "pct_hbm_peak": round(100 * w.kv_bytes / (r["decode"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
+           "append_us": round(r["append"] * 1e3, 2), "append_mtok_s": round(w.B / (r["append"] * 1e-3) / 1e6, 3),
+           "note": "working set 2.8 GB, far beyond the 256 MB last-level cache: one replica"}
+    w.release()
+    if cpu:
+        import oracle as orc
+
+        done, el, gbs = cpu_decode_sample(orc.Q8_0, 24, 4, 256, 32, 32768, budget_s=5.0, seqs_per_call=1)
+        res["cpu"] = {"kv_gbs": round(gbs, 4), "cores": _cpu_threads(),
+                      "sample": f"oracle Q8_0 decode of {done} sequences x 32768 tokens in {el:.1f} s"}
+    return res
+
+
+def summarize_profile(d, args):
+    """Summarise rocprofv3 CSVs of `bench.py --only-headline --copy-probe`
+    runs: DIR/trace (--kernel-trace --stats), DIR/fetch (--pmc FETCH_SIZE),
+    DIR/write (--pmc WRITE_SIZE).  The 256 MiB copies (kernel
+    __amd_rocclr_copyBuffer, grid 131072) calibrate each counter: true bytes
+    per reported KiB.  Writes profiles/decode_split_config2_4k.md and the
+    traffic JSON bench.py reports as roofline.traffic."""
+    import csv
+
+    def rows(sub, name):
+        return list(csv.DictReader(open(os.path.join(d, sub, "run_" + name + ".csv"))))
+
+    kname = "paged_decode_split<30, 128, 7>"
+    stats = [r for r in rows("trace", "kernel_stats") if kname in r["Name"] or "combine" in r["Name"]
+             or "append" in r["Name"]]
+    trace = [r for r in rows("trace", "kernel_trace") if kname in r["Kernel_Name"]]
+    durs = np.array([(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in trace])
+
+    def counter(sub, cname):
+        rs = rows(sub, "counter_collection")
+        copy = [float(r["Counter_Value"]) for r in rs if "copyBuffer" in r["Kernel_Name"] and r["Grid_Size"] == "131072"]
+        dec = [float(r["Counter_Value"]) for r in rs if kname in r["Kernel_Name"]]
+        return float(np.mean(copy)), float(np.mean(dec)), len(dec)
+
+    f_copy, f_dec, nf = counter("fetch", "FETCH_SIZE")
+    w_copy, w_dec, nw = counter("write", "WRITE_SIZE")
+    copy_bytes = 256 << 20
+    f_scale = copy_bytes / (f_copy * 1024.0)  # true bytes per counted byte
+    w_scale = copy_bytes / (w_copy * 1024.0)
+    fetch_b = f_dec * 1024.0 * f_scale
+    write_b = w_dec * 1024.0 * w_scale
+    kv = 32 * 4096 * 4 * 2 * 128 * 2
+    traffic = {"kernel": "paged_decode_split<bf16,128,7>", "workload": "config 2 at 4k, cold",
+               "hbm_bytes_per_launch": int(round(fetch_b + write_b)), "fetch_bytes": int(round(fetch_b)),
+               "write_bytes": int(round(write_b)), "algorithmic_bytes": kv,
+               "fetch_counter_kib": round(f_dec, 1), "write_counter_kib": round(w_dec, 1),
+               "fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4),
+               "mean_duration_us": round(float(durs.mean()), 2), "dispatches": int(durs.size)}
+    os.makedirs(os.path.join(ROOT, "profiles"), exist_ok=True)
+    json.dump(traffic, open(TRAFFIC_FILE, "w"), indent=1)
+    cmd = ("python3 bench.py --only-headline --steps {s} --warmup {w} --no-cpu --copy-probe").format(
+        s=args.steps, w=args.warmup)
+    lines = ["# paged_decode_split<bf16,128,7> -- config 2 at 4k (cold)", "",
+             "Commands (from the repository root on the GPU box; `cd /tmp && export TMPDIR=/tmp` first):", "",
+             "```",
+             f"rocprofv3 --kernel-trace --stats --output-format csv -d OUT/trace -o run -- {cmd}",
+             f"rocprofv3 --pmc FETCH_SIZE --output-format csv -d OUT/fetch -o run -- {cmd}",
+             f"rocprofv3 --pmc WRITE_SIZE --output-format csv -d OUT/write -o run -- {cmd}",
+             f"python3 bench.py --summarize-profile OUT --steps {args.steps} --warmup {args.warmup}",
+             "```", "",
+             "## rocprofv3 --stats (kernel_stats.csv rows of the path's kernels)", "",
+             "| Name | Calls | AverageNs | MinNs | MaxNs |", "|---|---|---|---|---|"]
+    for r in stats:
+        lines.append(f"| `{r['Name'][:70]}` | {r['Calls']} | {float(r['AverageNs']):.0f} | {r['MinNs']} | {r['MaxNs']} |")
+    lines += ["", f"Split kernel, kernel trace: {durs.size} dispatches, mean {durs.mean():.2f} us, "
+                  f"median {np.median(durs):.2f} us -> {kv / (durs.mean() * 1e-6) / 1e9:.1f} GB/s of algorithmic "
+                  f"KV bytes ({kv} B per launch) = {100 * kv / (durs.mean() * 1e-6) / 1e9 / HBM_PEAK_GBS:.1f}% of "
+                  "8 TB/s.", "",
+              "## HBM traffic per launch (rocprofv3 --pmc, calibrated)", "",
+              f"Calibration: a 256 MiB device copy (`__amd_rocclr_copyBuffer`, grid 131072) reads {f_copy:.0f} KiB "
+              f"by FETCH_SIZE and writes {w_copy:.0f} KiB by WRITE_SIZE per dispatch, so one counted byte is "
+              f"{f_scale:.3f} B fetched and {w_scale:.3f} B written.", "",
+              f"Split kernel ({nf} / {nw} dispatches): FETCH_SIZE {f_dec:.0f} KiB -> {fetch_b / 1e6:.1f} MB, "
+              f"WRITE_SIZE {w_dec:.0f} KiB -> {write_b / 1e6:.2f} MB; total {(fetch_b + write_b) / 1e6:.1f} MB "
+              f"per launch against {kv / 1e6:.1f} MB algorithmic ({(fetch_b + write_b) / kv:.3f}x)."]
+    open(os.path.join(ROOT, "profiles", "decode_split_config2_4k.md"), "w").write("\n".join(lines) + "\n")
+    print(json.dumps(traffic, indent=1))
 
 
 def main():
@@ -173,52 +552,67 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--all", action="store_true", help="also measure configs 1, 3, 4 and 5")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--configs", default="1,2,3,4,5", help="configs to run; 2 (the headline) always runs")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--copy-probe", action="store_true",
                     help="first run 4 device copies of 256 MiB (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
+    ap.add_argument("--only-headline", action="store_true",
+                    help="run only the cold config-2 (4k) headline steps (for rocprofv3 runs)")
+    ap.add_argument("--summarize-profile", metavar="DIR",
+                    help="CPU only: summarise rocprofv3 output DIR/{trace,fetch,write} of an --only-headline "
+                         "--copy-probe run into profiles/")
     args = ap.parse_args()
+    if args.summarize_profile:
+        summarize_profile(args.summarize_profile, args)
+        return
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; --gpus > 1 is not supported (each GPU would own "
-                                   "its sequences' pages and run the same kernels with no exchange)"}))
+        print(json.dumps({"error": "this build runs on one GPU; --gpus > 1 is not supported. Decode would shard by "
+                                   "sequence (each GPU owns its sequences' pages and block pool, no exchange)"}))
         sys.exit(2)
     import torch
 
-    import infer_train_amd as it
-
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    want = {int(x) for x in args.configs.split(",") if x.strip()}
+    cpu = not args.no_cpu
     if args.copy_probe:
         # A plain copy of known size: 256 MiB read + 256 MiB written per
-        # dispatch.  Its counter readings give the KiB-per-byte factor used to
-        # turn the decode kernel's FETCH_SIZE/WRITE_SIZE into HBM bytes.
+        # dispatch, to calibrate the counters' KiB per byte.
         src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda:0").fill_(1)
         dst = torch.empty_like(src)
         for _ in range(4):
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    # Headline: config 2 at the 4k target.
-    w = DecodeWorkload(it.BF16, 28, 4, 128, 16, np.full(32, 4096), 16384, 512, seed=2)
-    cold = w.time(args.steps, args.warmup, rotate=True)
-    warm = w.time(args.steps, args.warmup, rotate=False)
-    app_ms, dec_ms, step_ms = cold["append"], cold["decode"], cold["step_wall"]
-    gbs = w.kv_bytes / (dec_ms * 1e-3) / 1e9
-    gbs_warm = w.kv_bytes / (warm["decode"] * 1e-3) / 1e9
-    split_gbs = w.kv_bytes / (cold["split_mean"] * 1e-3) / 1e9
-    append_mtok = w.B / (app_ms * 1e-3) / 1e6
-    kv_bytes = w.kv_bytes
-    del w
-    torch.cuda.empty_cache()
-    # Config 2 as specified: ragged contexts U[256, 4096] (+1 appended).
-    rng = np.random.default_rng(22)
-    ctx2 = rng.integers(256, 4097, 32) + 1
-    w2 = DecodeWorkload(it.BF16, 28, 4, 128, 16, ctx2, 16384, 512, seed=3)
-    r2 = w2.time(args.steps, args.warmup, rotate=True)
-    ragged = {"kv_gbs": round(w2.kv_bytes / (r2["decode"] * 1e-3) / 1e9, 1), "decode_us": round(r2["decode"] * 1e3, 2),
-              "kv_bytes": int(w2.kv_bytes), "append_us": round(r2["append"] * 1e3, 2),
-              "pct_hbm_peak": round(100 * w2.kv_bytes / (r2["decode"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 2)}
-    del w2
-    torch.cuda.empty_cache()
+
+    if args.only_headline:
+        import infer_train_amd as it
+
+        w = DecodeWorkload(it.BF16, 28, 4, 128, 16, np.full(32, 4096), 16384, 512, seed=2)
+        r = w.time(args.steps, args.warmup, rotate=True)
+        print(json.dumps({"only_headline": True, "split_us": round(r["split"] * 1e3, 2),
+                          "decode_us": round(r["decode"] * 1e3, 2),
+                          "split_gbs": round(w.kv_bytes / (r["split"] * 1e-3) / 1e9, 1)}), flush=True)
+        return
+
+    head, ragged, cpu_b = bench_config2(args.steps, args.warmup, cpu)
+    configs = {"2_ragged": ragged}
+    small = max(5, args.steps // 5)
+    if 1 in want:
+        configs["1"] = bench_config1(args.steps, args.warmup, cpu)
+    if 3 in want:
+        configs["3"] = bench_config3(small, 2, cpu)
+    if 4 in want:
+        configs["4"] = bench_config4(max(16, args.steps // 2), 4, cpu)
+    if 5 in want:
+        configs["5"] = bench_config5(small, 2, cpu)
+
+    cold, warm = head["cold"], head["warm"]
+    kv_bytes = head["kv_bytes"]
+    gbs = kv_bytes / (cold["decode"] * 1e-3) / 1e9
+    split_gbs = kv_bytes / (cold["split"] * 1e-3) / 1e9
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        traffic = json.load(open(TRAFFIC_FILE)).get("hbm_bytes_per_launch")
     line = {
         "metric": "paged flash-decode KV-read GB/s (% of HBM peak) + KV append Mtok/s",
         "value": round(gbs, 1),
@@ -226,31 +620,33 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(step_ms, 4),
+        "ms_per_step": round(cold["step_wall"], 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic N(0,1) bf16 K/V/Q, seeded; pages a seeded permutation of the pool",
+        "data": "synthetic N(0,1) K/V/Q of each config's shape, seeded; pages a seeded permutation of the pool",
         "config": {"workload": "config 2 at its 4k target: batched paged decode, Hq 28 / Hkv 4 / D 128, block 16, "
-                               "batch 32, ctx 4096 each (4095 cached + 1 appended), 16384-block pool, "
-                               "split-K 512-token partitions + combine",
+                               "batch 32, ctx 4096 each (4095 cached + 1 appended), 16384-block pool, split-K "
+                               "512-token partitions + combine; cold (3 pool replicas rotated)",
                    "global_batch": 32, "seq_len": 4096, "parallelism": "none (1 GPU)"},
         "pct_hbm_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2),
-        "decode_us": round(dec_ms * 1e3, 2),
-        "split_us_mean": round(cold["split_mean"] * 1e3, 2),
+        "decode_us": round(cold["decode"] * 1e3, 2),
+        "decode_us_median": round(cold["decode_median"] * 1e3, 2),
+        "split_us": round(cold["split"] * 1e3, 2),
         "kv_bytes_per_step": int(kv_bytes),
-        "warm_kv_gbs": round(gbs_warm, 1),
-        "append_mtok_s": round(append_mtok, 3),
-        "append_us": round(app_ms * 1e3, 2),
-        "config2_ragged": ragged,
+        "warm_kv_gbs": round(kv_bytes / (warm["decode"] * 1e-3) / 1e9, 1),
+        "append_mtok_s": round(head["B"] / (cold["append"] * 1e-3) / 1e6, 3),
+        "append_gbs": round(head["append_bytes"] / (cold["append"] * 1e-3) / 1e9, 2),
+        "append_us": round(cold["append"] * 1e3, 2),
         "roofline": {"bound": "hbm", "achieved": round(split_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(split_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "paged_decode_split<bf16,128,7> (mean of its HIP-event durations)",
+                     "frac": round(split_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": "paged_decode_split<bf16,128,7> (mean of its HIP-event durations, cold)",
                      "algorithmic_bytes_per_launch": int(kv_bytes)},
+        "configs": configs,
     }
-    if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline_c2(32, 4096)
+    if cpu_b is not None:
+        line["cpu_baseline"] = cpu_b
     print(json.dumps(line), flush=True)
 
 

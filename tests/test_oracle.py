@@ -264,3 +264,143 @@ def test_window_c4_schedule(orc):
     assert np.all(held == 256)
     live = t[t >= 0]
     assert len(np.unique(live)) == live.size  # no block owned twice
+
+
+# ---------------- paged cache restatement (append / gather / evict) --------
+def _page_row(pool, page_bytes, hkv, D, e, slot, h, bs):
+    """The documented pool layout: page (block, head) holds bs rows of D
+    elements; row slot % bs of page (slot // bs) * Hkv + h."""
+    off = ((slot // bs) * hkv + h) * page_bytes + (slot % bs) * D * e
+    return pool[off:off + D * e]
+
+
+@pytest.mark.parametrize("dt,e", [(0, 4), (30, 2), (1, 2)])
+def test_oracle_append_layout_and_gather_round_trip(orc, dt, e):
+    nb, bs, hkv, D = 12, 16, 3, 32
+    c = orc.Cache(nb, bs, hkv, D, dt)
+    c.k[:] = 0xA5
+    c.v[:] = 0xA5
+    slots = orc.permutation(5, nb * bs)[:40].copy()
+    slots[7] = -1  # padding token: skipped
+    n = slots.size
+    if dt == orc.F32:
+        k, v = orc.normal(6, n * hkv * D), orc.normal(7, n * hkv * D)
+    else:
+        conv = orc.f32_to_bf16 if dt == orc.BF16 else orc.f32_to_f16
+        k, v = conv(orc.normal(6, n * hkv * D)), conv(orc.normal(7, n * hkv * D))
+    k, v = k.reshape(n, hkv, D), v.reshape(n, hkv, D)
+    c.append(k, v, slots)
+    page_bytes = bs * D * e
+    touched = np.zeros(c.k.size, bool)
+    for t, s in enumerate(slots):
+        if s < 0:
+            continue
+        for h in range(hkv):
+            got = _page_row(c.k, page_bytes, hkv, D, e, int(s), h, bs)
+            assert bytes(got) == k[t, h].tobytes()
+            assert bytes(_page_row(c.v, page_bytes, hkv, D, e, int(s), h, bs)) == v[t, h].tobytes()
+            off = ((s // bs) * hkv + h) * page_bytes + (s % bs) * D * e
+            touched[off:off + D * e] = True
+    assert np.all(c.k[~touched] == 0xA5) and np.all(c.v[~touched] == 0xA5)  # no stray writes
+    # Gather through a block table reproduces the rows in logical order.
+    seq_slots = np.array([s for s in slots if s >= 0][:20], np.int64)
+    blocks = np.unique(seq_slots // bs)
+    # one sequence holding those blocks in this order, positions = rows of those pages
+    tables = blocks.astype(np.int32)[None, :]
+    ctx = np.array([blocks.size * bs], np.int32)
+    start = np.array([5], np.int32)
+    cu = np.array([0], np.int64)
+    gk, gv = c.gather(tables, ctx, start, cu, int(ctx[0] - start[0]))
+    gk = gk.view(k.dtype).reshape(hkv, -1, D)
+    for i in range(int(ctx[0] - start[0])):
+        p = int(start[0]) + i
+        s = int(blocks[p // bs]) * bs + p % bs
+        for h in range(hkv):
+            assert bytes(gk[h, i]) == bytes(_page_row(c.k, page_bytes, hkv, D, e, s, h, bs))
+
+
+def test_oracle_evict_zeroes_exactly_the_listed_blocks(orc):
+    nb, bs, hkv, D = 10, 16, 2, 32
+    c = orc.Cache(nb, bs, hkv, D, orc.BF16)
+    c.k[:] = 7
+    c.v[:] = 9
+    c.evict(np.array([2, 7], np.int32))
+    pb = bs * D * 2 * hkv
+    for b in range(nb):
+        want_k, want_v = (0, 0) if b in (2, 7) else (7, 9)
+        assert np.all(c.k[b * pb:(b + 1) * pb] == want_k) and np.all(c.v[b * pb:(b + 1) * pb] == want_v)
+
+
+def test_oracle_q8_gather_records_equal_quantize_row(orc):
+    nb, bs, hkv, D = 4, 32, 2, 64
+    c = orc.Cache(nb, bs, hkv, D, orc.Q8_0)
+    n = nb * bs
+    x = (orc.normal(13, n * hkv * D) * np.float32(3)).reshape(n, hkv, D)
+    c.append(x, -x, np.arange(n, dtype=np.int64))
+    tables = np.arange(nb, dtype=np.int32)[None, :]
+    gk, gv = c.gather(tables, np.array([n], np.int32), None, np.array([0], np.int64), n)
+    rec = gk.reshape(hkv, n, D // 32 * 34)
+    for h in range(hkv):
+        for t in (0, 1, 77, n - 1):
+            assert bytes(rec[h, t]) == bytes(orc.quantize_row_q8_0(x[t, h]))
+
+
+# ---------------- paged attention restatement vs float64 brute force --------
+def _softmax_av(q, K, V, scale):
+    s = (K.astype(np.float64) @ q.astype(np.float64)) * scale
+    p = np.exp(s - s.max())
+    return (p @ V.astype(np.float64)) / p.sum()
+
+
+def _fill(orc, nb, bs, hkv, D, seed):
+    c = orc.Cache(nb, bs, hkv, D, orc.F32)
+    c.k[:] = np.frombuffer(orc.normal(seed, c.k.size // 4).tobytes(), np.uint8)
+    c.v[:] = np.frombuffer(orc.normal(seed + 1, c.v.size // 4).tobytes(), np.uint8)
+    kf = c.k.view(np.float32).reshape(nb, hkv, bs, D)
+    vf = c.v.view(np.float32).reshape(nb, hkv, bs, D)
+    return c, kf, vf
+
+
+def test_oracle_paged_decode_gqa_window_vs_float64(orc):
+    """Paging (scrambled table), the GQA map h -> h * Hkv / Hq
+    (forward.rs:234) and window starts, against float64 softmax over rows
+    collected with numpy."""
+    nb, bs, hkv, hq, D = 24, 16, 2, 6, 32
+    c, kf, vf = _fill(orc, nb, bs, hkv, D, 21)
+    perm = orc.permutation(22, nb).astype(np.int32)
+    tables = np.stack([perm[:10], perm[10:20]])
+    ctx = np.array([150, 97], np.int32)
+    start = np.array([0, 40], np.int32)
+    q = orc.normal(23, 2 * hq * D).reshape(2, hq, D)
+    scale = 0.17
+    got = c.decode(q, hq, tables, ctx, start, scale)
+    for b in range(2):
+        for h in range(hq):
+            kvh = h * hkv // hq
+            rows = range(int(start[b]), int(ctx[b]))
+            K = np.stack([kf[tables[b, p // bs], kvh, p % bs] for p in rows])
+            V = np.stack([vf[tables[b, p // bs], kvh, p % bs] for p in rows])
+            np.testing.assert_allclose(got[b, h], _softmax_av(q[b, h], K, V, scale), rtol=2e-5, atol=2e-6)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_oracle_paged_prefill_vs_float64(orc, causal):
+    nb, bs, hkv, hq, D = 20, 16, 2, 4, 32
+    c, kf, vf = _fill(orc, nb, bs, hkv, D, 31)
+    perm = orc.permutation(32, nb).astype(np.int32)
+    tables = np.stack([perm[:10], perm[10:20]])
+    ctx = np.array([120, 41], np.int32)
+    ql = np.array([30, 41], np.int32)
+    cu = np.array([0, 30, 71], np.int32)
+    q = orc.normal(33, 71 * hq * D).reshape(71, hq, D)
+    scale = 0.2
+    got = c.prefill(q, hq, cu, tables, ctx, scale, causal=causal)
+    for b in range(2):
+        for i in range(int(ql[b])):
+            last = int(ctx[b] - ql[b] + i) if causal else int(ctx[b]) - 1  # row i sits at ctx - q_len + i
+            for h in range(hq):
+                kvh = h * hkv // hq
+                K = np.stack([kf[tables[b, p // bs], kvh, p % bs] for p in range(last + 1)])
+                V = np.stack([vf[tables[b, p // bs], kvh, p % bs] for p in range(last + 1)])
+                np.testing.assert_allclose(got[cu[b] + i, h], _softmax_av(q[cu[b] + i, h], K, V, scale),
+                                           rtol=2e-5, atol=2e-6)
