@@ -52,6 +52,11 @@ def _dev():
     return torch.device("cuda", 0)
 
 
+def _progress(msg):
+    """One line per finished phase on stderr, so a long run shows it is alive."""
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
 def _cpu_threads():
     return 1  # the oracle is scalar C, run on one host thread
 
@@ -595,16 +600,21 @@ def main():
         return
 
     head, ragged, cpu_b = bench_config2(args.steps, args.warmup, cpu)
+    _progress("config 2 done")
     configs = {"2_ragged": ragged}
     small = max(5, args.steps // 5)
     if 1 in want:
         configs["1"] = bench_config1(args.steps, args.warmup, cpu)
+        _progress("config 1 done")
     if 3 in want:
         configs["3"] = bench_config3(small, 2, cpu)
+        _progress("config 3 done")
     if 4 in want:
         configs["4"] = bench_config4(max(16, args.steps // 2), 4, cpu)
+        _progress("config 4 done")
     if 5 in want:
         configs["5"] = bench_config5(small, 2, cpu)
+        _progress("config 5 done")
 
     cold, warm = head["cold"], head["warm"]
     kv_bytes = head["kv_bytes"]
