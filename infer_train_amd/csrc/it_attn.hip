@@ -88,7 +88,8 @@ int32_t run_decode(const char* who, int32_t cache_dt, int32_t q_dtype, int32_t o
   a.chunks = a.group / gc;
   if (int64_t(a.n_kv_heads) * a.chunks > 65535) return fail(IT_NOT_IMPLEMENTED, "%s: too many head chunks", who);
   a.max_pages = (a.partition >> a.log2_bs) + 2;
-  const size_t smem = decode_lds_bytes(cache_dt, gc, d, a.partition, a.max_pages);
+  const size_t smem = decode_smem_bytes(cache_dt, gc, d, a.partition, a.max_pages,
+                                        int64_t(a.max_parts) * a.n_kv_heads * a.chunks * n_seqs);
   if (smem > kMaxDecodeLds) return fail(IT_INVALID_INPUT, "%s: partition %d needs %zu bytes of LDS", who, a.partition, smem);
   if (max_tokens > 0 && (phases & 1)) {
     dim3 grid(unsigned(a.max_parts), unsigned(a.n_kv_heads * a.chunks), unsigned(n_seqs));

@@ -2,28 +2,72 @@
 // head_dim (128, 256) and heads per workgroup (1..8).
 #pragma once
 #include "it_decode.hpp"
+#include "it_decode16.hpp"
 
 namespace itkv {
 // Largest dynamic LDS a decode workgroup may ask for (160 KiB per CU).
 constexpr size_t kMaxDecodeLds = 160 * 1024;
 
+// Dynamic LDS of the split kernel that serves (dtype, heads per workgroup,
+// head_dim, partition).
+inline size_t decode_smem_bytes(int32_t dt, int gc, int d, int partition, int max_pages, int64_t n_workgroups) {
+  if (dt == IT_BF16 || dt == IT_F16) {
+    const Decode16Shape sh = decode16_shape(d, gc, partition, max_pages, n_workgroups);
+    return decode16_lds_bytes(d, gc, partition, max_pages, sh.nw, sh.ring);
+  }
+  return decode_lds_bytes(dt, gc, d, partition, max_pages);
+}
+
+// Above 64 KiB of LDS a kernel must opt in.  Idempotent, so a race between
+// threads setting it is harmless.
+template <const void* (*Fn)()>
+hipError_t opt_in_lds() {
+  static bool opted = false;
+  if (!opted) {
+    hipError_t e = hipFuncSetAttribute(Fn(), hipFuncAttributeMaxDynamicSharedMemorySize, int(kMaxDecodeLds));
+    if (e != hipSuccess) return e;
+    opted = true;
+  }
+  return hipSuccess;
+}
+template <int DT, int D, int GC, int NW, int R>
+const void* split16_fn() { return reinterpret_cast<const void*>(&paged_decode_split16<DT, D, GC, NW, R>); }
+template <int DT, int D, int GC>
+const void* split_fn() { return reinterpret_cast<const void*>(&paged_decode_split<DT, D, GC>); }
+
+template <int DT, int D, int GC, int NW, int R>
+hipError_t launch_split16(const DecodeArgs& a, dim3 grid, size_t smem, hipStream_t s) {
+  if (smem > 64 * 1024) {
+    hipError_t e = opt_in_lds<&split16_fn<DT, D, GC, NW, R>>();
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL((paged_decode_split16<DT, D, GC, NW, R>), grid, dim3(64 * NW), smem, s, a);
+  return hipGetLastError();
+}
+
 template <int DT, int D, int GC>
 hipError_t launch_decode_gc(const DecodeArgs& a, dim3 grid, hipStream_t s) {
-  const size_t smem = decode_lds_bytes(DT, GC, D, a.partition, a.max_pages);
+  const int64_t n_wg = int64_t(grid.x) * grid.y * grid.z;
+  const size_t smem = decode_smem_bytes(DT, GC, D, a.partition, a.max_pages, n_wg);
   if (smem > kMaxDecodeLds) return hipErrorInvalidValue;
-  if (smem > 64 * 1024) {
-    // Above 64 KiB the kernel must opt in.  Idempotent, so a race between
-    // threads setting it is harmless.
-    static bool opted = false;
-    if (!opted) {
-      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&paged_decode_split<DT, D, GC>),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, int(kMaxDecodeLds));
-      if (e != hipSuccess) return e;
-      opted = true;
+  if constexpr (DT == IT_BF16 || DT == IT_F16) {
+    const Decode16Shape sh = decode16_shape(D, GC, a.partition, a.max_pages, n_wg);
+    if constexpr (D == 128) {
+      if (sh.nw == 2 && sh.ring == 3) return launch_split16<DT, D, GC, 2, 3>(a, grid, smem, s);
+      if (sh.nw == 2) return launch_split16<DT, D, GC, 2, 2>(a, grid, smem, s);
+      return launch_split16<DT, D, GC, 4, 4>(a, grid, smem, s);
+    } else {
+      if (sh.nw == 2) return launch_split16<DT, D, GC, 2, 2>(a, grid, smem, s);
+      return launch_split16<DT, D, GC, 4, 2>(a, grid, smem, s);
     }
+  } else {
+    if (smem > 64 * 1024) {
+      hipError_t e = opt_in_lds<&split_fn<DT, D, GC>>();
+      if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL((paged_decode_split<DT, D, GC>), grid, dim3(kDecodeThreads), smem, s, a);
+    return hipGetLastError();
   }
-  hipLaunchKernelGGL((paged_decode_split<DT, D, GC>), grid, dim3(kDecodeThreads), smem, s, a);
-  return hipGetLastError();
 }
 
 template <int DT, int D>
