@@ -133,37 +133,60 @@ class DecodeWorkload:
         src_elem = 4.0 if dtype in (it.Q8_0, it.F32) else 2.0
         self.append_bytes = B * hkv * 2 * D * (src_elem + elem)
 
+    def _split(self, c):
+        c.decode(self.q, self.tables, self.ctx_d, None, self.max_tokens, scale=self.scale,
+                 partition=self.partition, out=self.out, ws=self.ws, phase="split")
+
+    def _combine(self, c):
+        c.decode(self.q, self.tables, self.ctx_d, None, self.max_tokens, scale=self.scale,
+                 partition=self.partition, out=self.out, ws=self.ws, phase="combine")
+
     def step(self, i, ev=None):
-        """append -> split -> combine; events (if given) bracket each kernel."""
+        """append -> split -> combine.  Events (if given) bracket the append
+        and the decode (split + combine, nothing recorded between them)."""
         c = self.caches[i % len(self.caches)]
         if ev is not None:
             ev[0].record()
         c.append(self.k_new, self.v_new, self.slots)
         if ev is not None:
             ev[1].record()
-        for j, phase in enumerate(("split", "combine")):
-            c.decode(self.q, self.tables, self.ctx_d, None, self.max_tokens, scale=self.scale,
-                     partition=self.partition, out=self.out, ws=self.ws, phase=phase)
-            if ev is not None:
-                ev[2 + j].record()
+        self._split(c)
+        self._combine(c)
+        if ev is not None:
+            ev[2].record()
+
+    def step_split_timed(self, i, ev):
+        """The same step with events around the split kernel alone."""
+        c = self.caches[i % len(self.caches)]
+        c.append(self.k_new, self.v_new, self.slots)
+        ev[0].record()
+        self._split(c)
+        ev[1].record()
+        self._combine(c)
 
     def time(self, steps, warmup, rotate=True):
         """Per-kernel times (ms) over `steps` event-bracketed steps: mean and
-        median of append and split+combine, mean of split alone, wall per step."""
+        median of append and of decode (split + combine), wall per step; then
+        `steps` more steps with events around the split kernel alone (its mean
+        is the roofline's kernel duration)."""
         torch = self.torch
         n_rep = len(self.caches) if rotate else 1
         for i in range(warmup):
             self.step(i % n_rep)
         torch.cuda.synchronize()
-        evs = [_events(4) for _ in range(steps)]
+        evs = [_events(3) for _ in range(steps)]
         t0 = time.perf_counter()
         for i in range(steps):
             self.step(i % n_rep, evs[i])
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
         app = np.array([e[0].elapsed_time(e[1]) for e in evs])
-        split = np.array([e[1].elapsed_time(e[2]) for e in evs])
-        dec = np.array([e[1].elapsed_time(e[3]) for e in evs])
+        dec = np.array([e[1].elapsed_time(e[2]) for e in evs])
+        evs2 = [_events(2) for _ in range(steps)]
+        for i in range(steps):
+            self.step_split_timed(i % n_rep, evs2[i])
+        torch.cuda.synchronize()
+        split = np.array([e[0].elapsed_time(e[1]) for e in evs2])
         for c in self.caches:
             c.check()
         return {"append": float(app.mean()), "decode": float(dec.mean()), "decode_median": float(np.median(dec)),

@@ -561,7 +561,12 @@ void paged_decode_split(DecodeArgs a) {
 }
 
 // Merge the partitions of one (sequence, head).  64 lanes; lane owns D/64
-// output dims.
+// output dims.  M = max m_p, L = sum l_p 2^(m_p - M), O = sum O_p 2^(m_p - M)
+// / L (the split-K form of flash_attn_f32's rescaling, flash_attn.rs:42-71).
+// The partials are read in chunks of kChunk partitions whose loads are all in
+// flight together (every lane reads the chunk's (m, l) pairs itself, so no
+// cross-lane step sits between them and the O loads).  With more than one
+// chunk, M comes from a first pass over the (m, l) pairs.
 template <int D>
 __global__ __launch_bounds__(64) void paged_decode_combine(const float* __restrict__ ws_o,
                                                            const float* __restrict__ ws_ml,
@@ -572,33 +577,44 @@ __global__ __launch_bounds__(64) void paged_decode_combine(const float* __restri
   // Partitions beyond max_parts were never computed (the split pass latched
   // the error); only the computed ones are merged.
   constexpr int DL = D / 64;
-  __shared__ float s_w[4096];
+  constexpr int kChunk = 8;
   const int h = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
   const int ctx = ctx_lens ? ctx_lens[b] : ctx_const;
   const int st = start_pos ? start_pos[b] : 0;
   const int n = ctx - st;
   const int np = n > 0 ? min((n + partition - 1) / partition, max_parts) : 0;
   const int64_t row = int64_t(b) * n_heads + h;
-  const float* ml = ws_ml + row * max_parts * 2;
+  const float2* ml = reinterpret_cast<const float2*>(ws_ml) + row * max_parts;
+  const float* op = ws_o + row * max_parts * D + lane;
   float mx = -INFINITY;
-  for (int p = lane; p < np; p += 64) mx = fmaxf(mx, ml[2 * p]);
-  mx = group_max<64>(mx);
-  float l = 0.0f;
-  for (int p = lane; p < np; p += 64) {
-    const float w = (mx == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(ml[2 * p] - mx);
-    s_w[p] = w;
-    l += ml[2 * p + 1] * w;
+  if (np > kChunk) {
+    for (int p = lane; p < np; p += 64) mx = fmaxf(mx, ml[p].x);
+    mx = group_max<64>(mx);
   }
-  l = group_sum<64>(l);
-  __syncthreads();
-  float o[DL];
+  float l = 0.0f, o[DL];
 #pragma unroll
   for (int j = 0; j < DL; ++j) o[j] = 0.0f;
-  const float* op = ws_o + row * max_parts * D;
-  for (int p = 0; p < np; ++p) {
-    const float w = s_w[p];
+  for (int p0 = 0; p0 < np; p0 += kChunk) {
+    float2 mlc[kChunk];
+    float oc[kChunk][DL];
 #pragma unroll
-    for (int j = 0; j < DL; ++j) o[j] = fmaf(op[int64_t(p) * D + lane + 64 * j], w, o[j]);
+    for (int c = 0; c < kChunk; ++c) {
+      const bool in = p0 + c < np;
+      mlc[c] = in ? ml[p0 + c] : make_float2(-INFINITY, 0.0f);
+#pragma unroll
+      for (int j = 0; j < DL; ++j) oc[c][j] = in ? op[int64_t(p0 + c) * D + 64 * j] : 0.0f;
+    }
+    if (np <= kChunk) {
+#pragma unroll
+      for (int c = 0; c < kChunk; ++c) mx = fmaxf(mx, mlc[c].x);
+    }
+#pragma unroll
+    for (int c = 0; c < kChunk; ++c) {
+      const float w = (mlc[c].x == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mlc[c].x - mx);
+      l = fmaf(mlc[c].y, w, l);
+#pragma unroll
+      for (int j = 0; j < DL; ++j) o[j] = fmaf(oc[c][j], w, o[j]);
+    }
   }
   // flash_attn.rs:66-71: multiply by 1/s when s > 0, else zeros.
   const float inv = l > 0.0f ? 1.0f / l : 0.0f;

@@ -63,30 +63,29 @@ struct D16Geo {
 };
 
 // Dynamic LDS of a workgroup of NW waves: the rings (R slots per wave),
-// scores [GC][P] fp32 (then the probability pairs [GC][P/2] in place),
-// per-wave max and sum [NW][8] each, the page list.  The final cross-wave
-// buffer [NW][GC][D] fp32 reuses the rings.
+// scores [GC][P + 16] fp32, per-wave max and sum [NW][8] each, a 256-byte
+// probability scratch per wave, the page list.  The final cross-wave buffer
+// [NW][GC][D] fp32 reuses the rings.
 inline size_t decode16_lds_bytes(int d, int gc, int partition, int max_pages, int nw, int ring_slots) {
   const size_t ring = size_t(nw) * ring_slots * kD16Tok * 2 * d;
   const size_t red = size_t(nw) * 8 * d * 4;
-  return (ring > red ? ring : red) + size_t(gc) * partition * 4 + 2 * size_t(nw) * 8 * 4 + size_t(max_pages + 1) * 4;
+  return (ring > red ? ring : red) + size_t(gc) * (partition + 16) * 4 + 2 * size_t(nw) * 8 * 4 + size_t(nw) * 256 +
+         size_t(max_pages + 1) * 4;
 }
 
 // Launch shape (waves per workgroup, ring slots per wave).  A grid of many
-// workgroups wants four of them resident per CU (<= 40 KiB of LDS each), so
-// that one workgroup's start, softmax barrier and final reduction are covered
-// by the others' loads: 2 waves with the deepest ring that fits.  A small
-// grid is bound by each workgroup's own chain of dependent loads instead and
-// takes 4 waves with a deep ring.
+// workgroups wants four or more of them resident per CU (<= 40 KiB of LDS
+// each), so that one workgroup's start, barrier and final reduction are
+// covered by the others' loads: 2 waves with 2-slot rings (measured on
+// config 2: as fast as 3 slots at 4k, 5% faster with ragged contexts).  A
+// small grid is bound by each workgroup's own chain of dependent loads and
+// takes 4 waves with a 4-slot ring.
 struct Decode16Shape {
   int nw, ring;
 };
 inline Decode16Shape decode16_shape(int d, int gc, int partition, int max_pages, int64_t n_workgroups) {
   constexpr size_t kQuarterCu = 40 * 1024;
-  if (n_workgroups >= 512) {
-    for (int r = d == 128 ? 3 : 2; r >= 2; --r)
-      if (decode16_lds_bytes(d, gc, partition, max_pages, 2, r) <= kQuarterCu) return {2, r};
-  }
+  if (n_workgroups >= 512 && decode16_lds_bytes(d, gc, partition, max_pages, 2, 2) <= kQuarterCu) return {2, 2};
   return {4, d == 128 ? 4 : 2};
 }
 
@@ -227,6 +226,31 @@ __device__ __forceinline__ float fold16(float x, float y) {
   return __uint_as_float(s[0]) + __uint_as_float(s[1]);
 }
 
+// Reduce eight per-lane values over all 64 lanes without LDS: two permlane
+// folds, then a DPP sum (or max) within each 16-lane row.  Row r of the
+// first result holds value {0, 2, 1, 3}[r], of the second {4, 6, 5, 7}[r],
+// in every lane of the row.
+template <bool kMax>
+__device__ __forceinline__ void fold8(const float (&x)[8], float& ra, float& rb) {
+  auto f32 = [](float p, float q) {
+    const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(p), __float_as_uint(q), false, false);
+    return kMax ? fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1])) : __uint_as_float(s[0]) + __uint_as_float(s[1]);
+  };
+  auto f16 = [](float p, float q) {
+    const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(p), __float_as_uint(q), false, false);
+    return kMax ? fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1])) : __uint_as_float(s[0]) + __uint_as_float(s[1]);
+  };
+  ra = f16(f32(x[0], x[1]), f32(x[2], x[3]));
+  rb = f16(f32(x[4], x[5]), f32(x[6], x[7]));
+  if constexpr (kMax) {
+    ra = group_max<16>(ra);
+    rb = group_max<16>(rb);
+  } else {
+    ra = group_sum<16>(ra);
+    rb = group_sum<16>(rb);
+  }
+}
+
 template <int DT, int D, int GC, int NW, int R>
 __global__ __launch_bounds__(64 * NW) void paged_decode_split16(DecodeArgs a) {
   using G = D16Geo<D>;
@@ -243,11 +267,12 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split16(DecodeArgs a) {
   constexpr size_t kRed = size_t(NW) * 8 * D * 4;
   char* const ring = smem;
   float* const sc = reinterpret_cast<float*>(smem + (kRingAll > kRed ? kRingAll : kRed));
-  float* const s_mx = sc + GC * a.partition;  // [NW][8]
-  float* const s_l = s_mx + NW * 8;            // [NW][8]
-  int32_t* const s_pages = reinterpret_cast<int32_t*>(s_l + NW * 8);
-  // Score of head h, token i (partition-relative): sc[h * P + i]; after the
-  // softmax the packed probabilities of pair t sit at word h * P + t.
+  const int SP = a.partition + 16;              // plane stride (staggers heads over the banks)
+  float* const s_mx = sc + GC * SP;             // [NW][8] partition max per wave and head
+  float* const s_l = s_mx + NW * 8;             // [NW][8] probability sums
+  uint32_t* const s_pp = reinterpret_cast<uint32_t*>(s_l + NW * 8);  // [NW][8 heads][8 pairs]
+  int32_t* const s_pages = reinterpret_cast<int32_t*>(s_pp + NW * 64);
+  // Score of head h, token i (partition-relative): sc[h * SP + i].
 
   const int part = blockIdx.x;
   const int kvh = blockIdx.y / a.chunks;
@@ -417,8 +442,8 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split16(DecodeArgs a) {
     }
     const int i_tok = (s * NW + wave) * kD16Tok + qk_tok;
     if (i_tok < nt) {
-      if (h_a < GC) sc[h_a * P + i_tok] = s_a;
-      if (GC > 4 && 4 + h_a < GC) sc[(4 + h_a) * P + i_tok] = s_b;
+      if (h_a < GC) sc[h_a * SP + i_tok] = s_a;
+      if (GC > 4 && 4 + h_a < GC) sc[(4 + h_a) * SP + i_tok] = s_b;
       m_a = fmaxf(m_a, s_a);
       m_b = fmaxf(m_b, s_b);
     }
@@ -431,95 +456,47 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split16(DecodeArgs a) {
   }
   lds_barrier();
 
-  // ---------------- phase 2: softmax over the partition ---------------------
-  // Pairs [0, n16 * 8) cover every token a V group reads; tokens >= nt get 0.
-  const int np2 = n16 * (kD16Tok / 2);
-  float mx[GC];
+  // ---------------- the Backend op's additive mask ----------------------------
+  // (arm.rs:304-370) Scores become (x * scale + mask) * log2 e, -inf where the
+  // mask is -inf (flash_attn.rs:35-40), and the maxima are taken again.
   if (masked) {
-    // Scores become (x * scale + mask) * log2 e, -inf where the mask is -inf.
+    float mx[GC];
 #pragma unroll
     for (int g = 0; g < GC; ++g) mx[g] = -INFINITY;
-    for (int t = tid; t < np2; t += NT) {
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int i = 2 * t + u;
-        if (i >= nt) break;
-        const float mk = a.mask[tok0 + i];
-#pragma unroll
-        for (int g = 0; g < GC; ++g) {
-          float& x = sc[g * P + i];
-          const float y = (mk == -INFINITY) ? -INFINITY : (x * a.scale + mk) * kLog2e;
-          x = y;
-          mx[g] = fmaxf(mx[g], y);
-        }
-      }
-    }
-#pragma unroll
-    for (int g = 0; g < GC; ++g) mx[g] = group_max<64>(mx[g]);
-    if (lane == 0) {
-#pragma unroll
-      for (int g = 0; g < GC; ++g) s_mx[wave * 8 + g] = mx[g];
-    }
-    lds_barrier();
-  }
-#pragma unroll
-  for (int g = 0; g < GC; ++g) {
-    float m = s_mx[g];
-#pragma unroll
-    for (int w = 1; w < NW; ++w) m = fmaxf(m, s_mx[w * 8 + g]);
-    mx[g] = m;
-  }
-  // Chunks of NT pairs, in order: every thread reads its pair's scores, then
-  // (after a barrier) writes the packed probabilities of pair t over word t
-  // of each head's plane.  Those words hold scores of pairs < (c + 1) NT / 2,
-  // all read by then; the next chunk reads words >= 2 (c + 1) NT only.
-  float lsum[GC];
-#pragma unroll
-  for (int g = 0; g < GC; ++g) lsum[g] = 0.0f;
-  for (int c0 = 0; c0 < np2; c0 += NT) {
-    const int t = c0 + tid;
-    uint32_t ppr[GC];
-    if (t < np2) {
-      const bool v0 = 2 * t < nt, v1 = 2 * t + 1 < nt;
+    for (int i = tid; i < nt; i += NT) {
+      const float mk = a.mask[tok0 + i];
 #pragma unroll
       for (int g = 0; g < GC; ++g) {
-        const float2 sv = *reinterpret_cast<const float2*>(&sc[g * P + 2 * t]);
-        const bool none = mx[g] == -INFINITY;  // every key skipped: zeros (flash_attn.rs:66-71)
-        const float p0 = (v0 && !none) ? __builtin_amdgcn_exp2f(sv.x - mx[g]) : 0.0f;
-        const float p1 = (v1 && !none) ? __builtin_amdgcn_exp2f(sv.y - mx[g]) : 0.0f;
-        const uint32_t pp = pack16<DT>(p0, p1);
-        lsum[g] += lo16<DT>(pp) + hi16<DT>(pp);
-        ppr[g] = pp;
+        float& x = sc[g * SP + i];
+        const float y = (mk == -INFINITY) ? -INFINITY : (x * a.scale + mk) * kLog2e;
+        x = y;
+        mx[g] = fmaxf(mx[g], y);
       }
     }
+    float x8[8], ra, rb;
+#pragma unroll
+    for (int g = 0; g < 8; ++g) x8[g] = g < GC ? mx[g] : -INFINITY;
+    fold8<true>(x8, ra, rb);
+    if (qk_tok == 0) {
+      s_mx[wave * 8 + h_a] = ra;
+      s_mx[wave * 8 + 4 + h_a] = rb;
+    }
     lds_barrier();
-    if (t < np2) {
-#pragma unroll
-      for (int g = 0; g < GC; ++g) reinterpret_cast<uint32_t*>(sc)[g * P + t] = ppr[g];
-    }
   }
+
+  // Softmax is folded into the PV loop: lane L computes the probability pair
+  // (pair L % 8 of the group, head L / 8) from the partition max, rounds it to
+  // the cache's 16-bit type (the weight PV applies) and adds the rounded
+  // values to its running sum, so the output is an exact convex combination
+  // of V rows (flash_attn.rs:42-71 with the max taken first).
+  const int h_l = lane >> 3, k_l = lane & 7;
+  float m_l = s_mx[h_l];
 #pragma unroll
-  for (int g = 0; g < GC; ++g) {
-    lsum[g] = group_sum<64>(lsum[g]);
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  if (lane == 0) {
-#pragma unroll
-    for (int g = 0; g < GC; ++g) s_l[wave * 8 + g] = lsum[g];
-  }
-  lds_barrier();
-  const int64_t part_row = (int64_t(b) * a.n_heads + head0) * a.max_parts + part;
-  if (tid < GC) {
-    float* ml = a.ws_ml + (part_row + int64_t(tid) * a.max_parts) * 2;
-    float m = s_mx[tid], l = s_l[tid];
-#pragma unroll
-    for (int w = 1; w < NW; ++w) {
-      m = fmaxf(m, s_mx[w * 8 + tid]);
-      l += s_l[w * 8 + tid];
-    }
-    ml[0] = m;
-    ml[1] = l;
-  }
+  for (int w = 1; w < NW; ++w) m_l = fmaxf(m_l, s_mx[w * 8 + h_l]);
+  const bool none_l = m_l == -INFINITY;  // every key skipped: zeros (flash_attn.rs:66-71)
+  const float* const sc_l = sc + (h_l < GC ? h_l : 0) * SP;
+  uint32_t* const pp_w = s_pp + wave * 64;
+  float lsum = 0.0f;
 
   // ---------------- phase 3: P.V over the V groups ---------------------------
   float acc2[DPV][8];  // [dim of the lane][head]; heads >= GC stay 0
@@ -542,13 +519,21 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split16(DecodeArgs a) {
         if (tb + o / RB >= nt) *reinterpret_cast<uint4*>(grp + o) = make_uint4(0u, 0u, 0u, 0u);
       }
     }
-    // Probability pairs of the group, pair j in lane j of every row.
-    uint32_t ppv[8];
+    // Probability pairs of the group: computed one (pair, head) per lane,
+    // then read back with pair j in lane j of every row (same-wave LDS ops
+    // stay in order).
     {
-      const uint32_t* pr = reinterpret_cast<const uint32_t*>(sc) + (tb >> 1) + (qk_tok & 7);
-#pragma unroll
-      for (int g = 0; g < 8; ++g) ppv[g] = pr[(g < GC ? g : 0) * P];
+      const int i0 = tb + 2 * k_l;
+      const float2 sv = *reinterpret_cast<const float2*>(sc_l + i0);
+      const float p0 = (i0 < nt && !none_l) ? __builtin_amdgcn_exp2f(sv.x - m_l) : 0.0f;
+      const float p1 = (i0 + 1 < nt && !none_l) ? __builtin_amdgcn_exp2f(sv.y - m_l) : 0.0f;
+      const uint32_t pp = pack16<DT>(p0, p1);
+      lsum += lo16<DT>(pp) + hi16<DT>(pp);
+      pp_w[lane] = pp;
     }
+    uint32_t ppv[8];
+#pragma unroll
+    for (int g = 0; g < 8; ++g) ppv[g] = pp_w[(g < GC ? g : 0) * 8 + (qk_tok & 7)];
     Unroll<0, kD16Tok / 2>::run([&](auto jc) {
       constexpr int j = decltype(jc)::value;
       if constexpr (DPV == 2) {
@@ -567,7 +552,9 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split16(DecodeArgs a) {
     });
   }
 
-  // ---------------- across the 4 waves, in a fixed order ---------------------
+  // ---------------- across the waves, in a fixed order -----------------------
+  lsum = group_sum<8>(lsum);  // the 8 pairs of head h_l
+  if (k_l == 0) s_l[wave * 8 + h_l] = lsum;
   lds_barrier();  // every wave is done with its ring (its last wait was vmcnt(0))
   float* const red = reinterpret_cast<float*>(smem);  // [NW][GC][D]
 #pragma unroll
@@ -577,6 +564,18 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split16(DecodeArgs a) {
     else *reinterpret_cast<float4*>(dst) = make_float4(acc2[0][g], acc2[1][g], acc2[2][g], acc2[3][g]);
   }
   lds_barrier();
+  const int64_t part_row = (int64_t(b) * a.n_heads + head0) * a.max_parts + part;
+  if (tid < GC) {
+    float* ml = a.ws_ml + (part_row + int64_t(tid) * a.max_parts) * 2;
+    float m = s_mx[tid], l = s_l[tid];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) {
+      m = fmaxf(m, s_mx[w * 8 + tid]);
+      l += s_l[w * 8 + tid];
+    }
+    ml[0] = m;
+    ml[1] = l;
+  }
   for (int i = tid; i < GC * D; i += NT) {
     float o;
     if constexpr (NW == 2) o = red[i] + red[GC * D + i];

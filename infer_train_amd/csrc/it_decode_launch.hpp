@@ -53,7 +53,6 @@ hipError_t launch_decode_gc(const DecodeArgs& a, dim3 grid, hipStream_t s) {
   if constexpr (DT == IT_BF16 || DT == IT_F16) {
     const Decode16Shape sh = decode16_shape(D, GC, a.partition, a.max_pages, n_wg);
     if constexpr (D == 128) {
-      if (sh.nw == 2 && sh.ring == 3) return launch_split16<DT, D, GC, 2, 3>(a, grid, smem, s);
       if (sh.nw == 2) return launch_split16<DT, D, GC, 2, 2>(a, grid, smem, s);
       return launch_split16<DT, D, GC, 4, 4>(a, grid, smem, s);
     } else {
