@@ -43,7 +43,7 @@ hipError_t launch_split(int32_t dt, int d, int gc, const DecodeArgs& a, dim3 gri
 }
 
 hipError_t launch_combine(int d, const DecodeArgs& a, int n_seqs, void* out, int32_t out_dtype, hipStream_t s) {
-  dim3 grid(unsigned(a.n_heads), unsigned(n_seqs));
+  dim3 grid(unsigned(a.n_heads), unsigned(n_seqs), unsigned(d / 64));
   if (d == 128)
     hipLaunchKernelGGL(paged_decode_combine<128>, grid, dim3(64), 0, s, a.ws_o, a.ws_ml, a.ctx_lens,
                        a.start_pos, a.ctx_const, a.n_heads, a.partition, a.max_parts, out, out_dtype);
@@ -171,14 +171,21 @@ extern "C" int32_t it_paged_decode_combine(IT_DECODE_ARGS) {
 // The Backend FlashAttention operator (src/backend/arm.rs:304-370) runs the
 // same kernels: contiguous K/V [n_kv][D] are pages of 16 rows under the
 // identity block table, one KV head shared by all n_heads query heads.
+// The partition grows with the key count: one query's keys are spread over
+// up to 16 partitions (64..512 tokens each), so a short context still
+// streams through many workgroups instead of one long chain of loads.
 namespace {
-constexpr int kFaPartition = 512;
 constexpr int kFaBlock = 16;
+int fa_partition(int32_t n_kv) {
+  const int per = (n_kv + 15) / 16;
+  const int p = (per + 63) / 64 * 64;
+  return p < 64 ? 64 : (p > 512 ? 512 : p);
+}
 }  // namespace
 
 extern "C" size_t it_flash_attention_workspace(int32_t n_heads, int32_t head_dim, int32_t n_kv) {
   // Plus 256 bytes for the device error word.
-  return it_paged_decode_workspace(1, n_heads, head_dim, n_kv, kFaPartition) + 256;
+  return it_paged_decode_workspace(1, n_heads, head_dim, n_kv, fa_partition(n_kv)) + 256;
 }
 
 extern "C" int32_t it_flash_attention(const float* q, const float* k, const float* v, const float* mask,
@@ -211,7 +218,7 @@ extern "C" int32_t it_flash_attention(const float* q, const float* k, const floa
   a.n_heads = n_heads;
   a.n_kv_heads = 1;
   a.log2_bs = 4;
-  a.partition = kFaPartition;
+  a.partition = fa_partition(n_kv);
   return run_decode("it_flash_attention", IT_F32, IT_F32, IT_F32, head_dim, 1, n_kv, a, ws, need - 256, out,
                     (hipStream_t)stream);
 }

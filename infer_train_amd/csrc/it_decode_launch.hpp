@@ -1,72 +1,46 @@
 // it_decode_launch.hpp -- compile-time dispatch of paged_decode_split over
-// head_dim (128, 256) and heads per workgroup (1..8).
+// head_dim (128, 256), heads per workgroup (1..8) and launch shape.
 #pragma once
 #include "it_decode.hpp"
-#include "it_decode16.hpp"
+#include "it_decode_split.hpp"
 
 namespace itkv {
 // Largest dynamic LDS a decode workgroup may ask for (160 KiB per CU).
 constexpr size_t kMaxDecodeLds = 160 * 1024;
 
-// Dynamic LDS of the split kernel that serves (dtype, heads per workgroup,
-// head_dim, partition).
+// Dynamic LDS of the split launch that serves these arguments.
 inline size_t decode_smem_bytes(int32_t dt, int gc, int d, int partition, int max_pages, int64_t n_workgroups) {
-  if (dt == IT_BF16 || dt == IT_F16) {
-    const Decode16Shape sh = decode16_shape(d, gc, partition, max_pages, n_workgroups);
-    return decode16_lds_bytes(d, gc, partition, max_pages, sh.nw, sh.ring);
-  }
-  return decode_lds_bytes(dt, gc, d, partition, max_pages);
+  const SplitShape sh = split_shape(dt, d, gc, partition, max_pages, n_workgroups);
+  return split_lds_bytes(dt, d, gc, partition, max_pages, sh.nw, sh.ring);
 }
 
-// Above 64 KiB of LDS a kernel must opt in.  Idempotent, so a race between
-// threads setting it is harmless.
-template <const void* (*Fn)()>
-hipError_t opt_in_lds() {
-  static bool opted = false;
-  if (!opted) {
-    hipError_t e = hipFuncSetAttribute(Fn(), hipFuncAttributeMaxDynamicSharedMemorySize, int(kMaxDecodeLds));
-    if (e != hipSuccess) return e;
-    opted = true;
-  }
-  return hipSuccess;
-}
 template <int DT, int D, int GC, int NW, int R>
-const void* split16_fn() { return reinterpret_cast<const void*>(&paged_decode_split16<DT, D, GC, NW, R>); }
-template <int DT, int D, int GC>
-const void* split_fn() { return reinterpret_cast<const void*>(&paged_decode_split<DT, D, GC>); }
-
-template <int DT, int D, int GC, int NW, int R>
-hipError_t launch_split16(const DecodeArgs& a, dim3 grid, size_t smem, hipStream_t s) {
+hipError_t launch_split_shape(const DecodeArgs& a, dim3 grid, size_t smem, hipStream_t s) {
   if (smem > 64 * 1024) {
-    hipError_t e = opt_in_lds<&split16_fn<DT, D, GC, NW, R>>();
-    if (e != hipSuccess) return e;
+    // Above 64 KiB the kernel must opt in.  Idempotent, so a race between
+    // threads setting it is harmless.
+    static bool opted = false;
+    if (!opted) {
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&paged_decode_split<DT, D, GC, NW, R>),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, int(kMaxDecodeLds));
+      if (e != hipSuccess) return e;
+      opted = true;
+    }
   }
-  hipLaunchKernelGGL((paged_decode_split16<DT, D, GC, NW, R>), grid, dim3(64 * NW), smem, s, a);
+  hipLaunchKernelGGL((paged_decode_split<DT, D, GC, NW, R>), grid, dim3(64 * NW), smem, s, a);
   return hipGetLastError();
 }
 
 template <int DT, int D, int GC>
 hipError_t launch_decode_gc(const DecodeArgs& a, dim3 grid, hipStream_t s) {
   const int64_t n_wg = int64_t(grid.x) * grid.y * grid.z;
-  const size_t smem = decode_smem_bytes(DT, GC, D, a.partition, a.max_pages, n_wg);
+  const SplitShape sh = split_shape(DT, D, GC, a.partition, a.max_pages, n_wg);
+  const size_t smem = split_lds_bytes(DT, D, GC, a.partition, a.max_pages, sh.nw, sh.ring);
   if (smem > kMaxDecodeLds) return hipErrorInvalidValue;
-  if constexpr (DT == IT_BF16 || DT == IT_F16) {
-    const Decode16Shape sh = decode16_shape(D, GC, a.partition, a.max_pages, n_wg);
-    if constexpr (D == 128) {
-      if (sh.nw == 2) return launch_split16<DT, D, GC, 2, 2>(a, grid, smem, s);
-      return launch_split16<DT, D, GC, 4, 4>(a, grid, smem, s);
-    } else {
-      if (sh.nw == 2) return launch_split16<DT, D, GC, 2, 2>(a, grid, smem, s);
-      return launch_split16<DT, D, GC, 4, 2>(a, grid, smem, s);
-    }
-  } else {
-    if (smem > 64 * 1024) {
-      hipError_t e = opt_in_lds<&split_fn<DT, D, GC>>();
-      if (e != hipSuccess) return e;
-    }
-    hipLaunchKernelGGL((paged_decode_split<DT, D, GC>), grid, dim3(kDecodeThreads), smem, s, a);
-    return hipGetLastError();
-  }
+  if (sh.nw == 2) return launch_split_shape<DT, D, GC, 2, 2>(a, grid, smem, s);
+  if (sh.ring == 4) return launch_split_shape<DT, D, GC, 4, 4>(a, grid, smem, s);
+  if (sh.ring == 3) return launch_split_shape<DT, D, GC, 4, 3>(a, grid, smem, s);
+  return launch_split_shape<DT, D, GC, 4, 2>(a, grid, smem, s);
 }
 
 template <int DT, int D>

@@ -1,0 +1,722 @@
+// it_decode_split.hpp -- the split pass of paged split-K flash-decode on
+// gfx950, for BF16, F16, F32 and Q8_0 caches (device code).
+//
+// One workgroup (NW wave64s) owns one (sequence, KV head, head chunk,
+// partition of P tokens); the GC query heads of the chunk share every K/V
+// byte it reads.  The partition's tokens are cut into 16-token groups and
+// group i belongs to wave i % NW: each wave streams its own groups' K rows,
+// then their V rows, through a private ring of R LDS slots filled by direct
+// global->LDS loads (global_load_lds_dwordx4: 64 lanes x 16 B per
+// instruction, each lane naming its own source, so the block table is
+// applied per token; Q8_0 scales ride along in global_load_lds_dword).  A
+// wave only reads what it loaded itself, so the ring needs no workgroup
+// barrier; explicit vmcnt counts order it.
+//
+// Lane layouts, chosen so that no per-token cross-lane reduction is left:
+//  QK   lane (r, k) = (lane / 16, lane % 16) takes token k of the group and
+//       quarter r of the head dimension.  q of head g over quarter r sits in
+//       registers, lane k of each 16-lane row holding its k-th word, and every
+//       multiply-add reads its q word straight from lane k of its row through
+//       DPP row_newbcast:k (v_dot2c_f32_{bf16,f16} on packed 16-bit pairs,
+//       v_fmac_f32 for F32 and for Q8_0 after a sign-extending SDWA convert).
+//       The four quarter sums of every head are then folded with
+//       v_permlane32_swap / v_permlane16_swap (6 swaps, 6 adds for 8 heads).
+//       K rows sit in LDS with their 16-byte pieces XOR-swizzled by token,
+//       so a row of 16 lanes reads distinct bank groups.
+//  PV   lane l takes dims [D/64 l, D/64 (l+1)) of every token.  The
+//       probability of token t (16-bit caches: of token pair t) comes from
+//       lane t of the row through row_newbcast:t; 16-bit caches v_perm
+//       (v_t[d], v_t+1[d]) pairs for v_dot2c.
+//
+// The softmax follows flash_attn_f32 (src/backend/arm/flash_attn.rs:6-72)
+// with the partition max taken first: phase 1 writes the scores (log2
+// domain, x * scale * log2 e) to LDS and tracks the max; one barrier
+// publishes the per-wave maxima; the PV loop turns each group's scores into
+// probabilities (one (pair, head) per lane, 16-bit caches rounding them to
+// the cache type, the weights PV applies) and sums them, so a 16-bit result
+// is an exact convex combination of V rows.  The Backend op's additive mask
+// (arm.rs:304-370) rewrites the scores between the two, a -inf key being
+// skipped (flash_attn.rs:35-40).  The waves' partial outputs are summed in a
+// fixed order; (m, l, O) of the partition go to the workspace and
+// paged_decode_combine merges the partitions.
+//
+// Q8_0 (BlockQ8_0, src/types.rs:34-41): a page is int8 qs[bs][D] then fp16
+// d[bs][D/32]; a key dot product is sum over 32-groups of f32(d) * sum q *
+// qs, and a value element is f32(d) * qs, exact in fp32 (gemv.rs:151-160).
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <type_traits>
+
+#include "it_decode.hpp"
+
+namespace itkv {
+
+constexpr int kGroupTok = 16;  // tokens per group (one wave step)
+
+// Geometry of a cache dtype at head_dim D.
+template <int DT, int D>
+struct SplitFmt {
+  static constexpr bool k16 = DT == IT_BF16 || DT == IT_F16;
+  static constexpr bool kQ8 = DT == IT_Q8_0;
+  static constexpr int kElem = DT == IT_F32 ? 4 : (kQ8 ? 1 : 2);  // bytes per main-plane element
+  static constexpr int kRow = D * kElem;                          // main-plane bytes per token
+  static constexpr int kGroup = kGroupTok * kRow;                 // main-plane bytes per group
+  static constexpr int kDma = kGroup / 1024;                      // 16-byte-per-lane loads per group
+  static constexpr int kScaleRow = kQ8 ? D / 16 : 0;              // fp16 scales per token (bytes)
+  static constexpr int kScaleGroup = kGroupTok * kScaleRow;       // 128 or 256 B (one dword load)
+  static constexpr int kSlot = kGroup + kScaleGroup;
+  static constexpr int kLoads = kDma + (kQ8 ? 1 : 0);             // vmcnt units per group
+  static constexpr int kPieces = D / 4 * kElem / 16;              // 16-byte pieces per lane in QK
+  static constexpr int kRowPieces = kRow / 16;
+  static constexpr int kSwz = (kRowPieces < 16 ? kRowPieces : 16) - 1;  // piece swizzle mask
+  static constexpr int kQRegs = (k16 ? D / 8 : D / 4) / 16;       // q VGPRs per head (16 words each)
+  static constexpr int kDpv = D / 64;                             // PV dims per lane
+  static constexpr int kScratch = k16 ? 256 : 512;                // probability scratch per wave (B)
+  static_assert(D == 128 || D == 256, "head_dim 128 or 256");
+  static_assert(kGroup % 1024 == 0 && kScaleGroup <= 256, "group geometry");
+};
+
+template <int DT>
+inline int split_slot_bytes(int d) {
+  return d == 128 ? SplitFmt<DT, 128>::kSlot : SplitFmt<DT, 256>::kSlot;
+}
+inline int split_slot_bytes(int32_t dt, int d) {
+  switch (dt) {
+    case IT_BF16: return split_slot_bytes<IT_BF16>(d);
+    case IT_F16: return split_slot_bytes<IT_F16>(d);
+    case IT_F32: return split_slot_bytes<IT_F32>(d);
+    default: return split_slot_bytes<IT_Q8_0>(d);
+  }
+}
+
+// Dynamic LDS of a workgroup of NW waves: the rings (R slots per wave),
+// scores [GC][P + 16] fp32, per-wave max and sum [NW][8] each, a probability
+// scratch per wave, the page list.  The final cross-wave buffer [NW][GC][D]
+// fp32 reuses the rings.
+inline size_t split_lds_bytes(int32_t dt, int d, int gc, int partition, int max_pages, int nw, int ring) {
+  const size_t rings = size_t(nw) * ring * split_slot_bytes(dt, d);
+  const size_t red = size_t(nw) * 8 * d * 4;
+  const size_t scratch = (dt == IT_BF16 || dt == IT_F16) ? 256 : 512;
+  return (rings > red ? rings : red) + size_t(gc) * (partition + 16) * 4 + 2 * size_t(nw) * 8 * 4 + nw * scratch +
+         size_t(max_pages + 1) * 4;
+}
+
+// Launch shape (waves per workgroup, ring slots per wave).  A grid of many
+// workgroups wants four or more of them resident per CU (<= 40 KiB of LDS
+// each), so that one workgroup's start, barrier and final reduction are
+// covered by the others' loads: 2 waves with 2-slot rings (measured on
+// config 2: as fast as 3 slots at 4k, 5% faster with ragged contexts); when
+// that does not fit, 4 waves with 2-slot rings at two per CU.  A small grid
+// is bound by each workgroup's own chain of dependent loads and takes 4
+// waves with the deepest ring that fits.
+struct SplitShape {
+  int nw, ring;
+};
+inline SplitShape split_shape(int32_t dt, int d, int gc, int partition, int max_pages, int64_t n_workgroups) {
+  constexpr size_t kQuarterCu = 40 * 1024, kHalfCu = 80 * 1024, kCu = 160 * 1024;
+  if (n_workgroups >= 512) {
+    if (split_lds_bytes(dt, d, gc, partition, max_pages, 2, 2) <= kQuarterCu) return {2, 2};
+    if (split_lds_bytes(dt, d, gc, partition, max_pages, 4, 2) <= kHalfCu) return {4, 2};
+  }
+  for (int r = 4; r > 2; --r)
+    if (split_lds_bytes(dt, d, gc, partition, max_pages, 4, r) <= kCu) return {4, r};
+  return {4, 2};
+}
+
+// Compile-time loop: f(integral_constant<int, I>) for I in [B, E).
+template <int B, int E>
+struct Unroll {
+  template <class F>
+  __device__ __forceinline__ static void run(F&& f) {
+    if constexpr (B < E) {
+      f(std::integral_constant<int, B>{});
+      Unroll<B + 1, E>::run(f);
+    }
+  }
+};
+
+// ---- multiply-adds with DPP row_newbcast, in asm blocks --------------------
+// A DPP instruction must not read a VGPR (any of its sources, the
+// accumulator included) within 2 wait states of a VALU write to it, and the
+// compiler cannot see DPP inside inline asm.  So the DPP multiply-adds are
+// emitted in blocks that begin with s_nop 1 (covering every VALU write before
+// the block) and order their instructions so that an accumulator is read
+// again only >= 2 instructions after it was written (heads interleaved;
+// explicit nops when fewer than 3 heads).
+#define IT_DPP(OP, A, Q, K, L) OP " %[" A "], %[" Q "], %[" K "] row_newbcast:%[" L "] row_mask:0xf bank_mask:0xf\n\t"
+// QK: acc[g] += q[g] (lane l_j of the row) . k_j, j = 0..3.
+#define IT_QK1(OP, j) IT_DPP(OP, "a0", "q0", "k" #j, "l" #j)
+#define IT_QK2(OP, j) IT_QK1(OP, j) IT_DPP(OP, "a1", "q1", "k" #j, "l" #j)
+#define IT_QK3(OP, j) IT_QK2(OP, j) IT_DPP(OP, "a2", "q2", "k" #j, "l" #j)
+#define IT_QK4(OP, j) IT_QK3(OP, j) IT_DPP(OP, "a3", "q3", "k" #j, "l" #j)
+#define IT_QK5(OP, j) IT_QK4(OP, j) IT_DPP(OP, "a4", "q4", "k" #j, "l" #j)
+#define IT_QK6(OP, j) IT_QK5(OP, j) IT_DPP(OP, "a5", "q5", "k" #j, "l" #j)
+#define IT_QK7(OP, j) IT_QK6(OP, j) IT_DPP(OP, "a6", "q6", "k" #j, "l" #j)
+#define IT_QK8(OP, j) IT_QK7(OP, j) IT_DPP(OP, "a7", "q7", "k" #j, "l" #j)
+#define IT_QK_BLOCK(OP, G, NOP) "s_nop 1\n\t" G(OP, 0) NOP G(OP, 1) NOP G(OP, 2) NOP G(OP, 3)
+#define IT_QK_OPS                                                                                       \
+  : [a0] "+v"(acc[0]), [a1] "+v"(acc[1]), [a2] "+v"(acc[2]), [a3] "+v"(acc[3]), [a4] "+v"(acc[4]),       \
+    [a5] "+v"(acc[5]), [a6] "+v"(acc[6]), [a7] "+v"(acc[7])                                              \
+  : [q0] "v"(q[0]), [q1] "v"(q[1]), [q2] "v"(q[2]), [q3] "v"(q[3]), [q4] "v"(q[4]), [q5] "v"(q[5]),        \
+    [q6] "v"(q[6]), [q7] "v"(q[7]), [k0] "v"(k0), [k1] "v"(k1), [k2] "v"(k2), [k3] "v"(k3), [l0] "n"(L0),  \
+    [l1] "n"(L0 + 1), [l2] "n"(L0 + 2), [l3] "n"(L0 + 3)
+#define IT_QK_CASES(OP)                                                                  \
+  if constexpr (GC == 1) asm(IT_QK_BLOCK(OP, IT_QK1, "s_nop 1\n\t") IT_QK_OPS);         \
+  else if constexpr (GC == 2) asm(IT_QK_BLOCK(OP, IT_QK2, "s_nop 0\n\t") IT_QK_OPS);    \
+  else if constexpr (GC == 3) asm(IT_QK_BLOCK(OP, IT_QK3, "") IT_QK_OPS);               \
+  else if constexpr (GC == 4) asm(IT_QK_BLOCK(OP, IT_QK4, "") IT_QK_OPS);               \
+  else if constexpr (GC == 5) asm(IT_QK_BLOCK(OP, IT_QK5, "") IT_QK_OPS);               \
+  else if constexpr (GC == 6) asm(IT_QK_BLOCK(OP, IT_QK6, "") IT_QK_OPS);               \
+  else if constexpr (GC == 7) asm(IT_QK_BLOCK(OP, IT_QK7, "") IT_QK_OPS);               \
+  else asm(IT_QK_BLOCK(OP, IT_QK8, "") IT_QK_OPS);
+
+// acc[g] += sum_j q[g] (of lane L0 + j of the row) . k_j for g < GC; the
+// words are packed 16-bit pairs for BF16 / F16 (v_dot2c), fp32 otherwise.
+template <int DT, int GC, int L0>
+__device__ __forceinline__ void qk_words(float (&acc)[8], const uint32_t (&q)[8], uint32_t k0, uint32_t k1,
+                                         uint32_t k2, uint32_t k3) {
+  static_assert(L0 % 4 == 0 && L0 + 3 < 16, "word lanes");
+  if constexpr (DT == IT_BF16) {
+    IT_QK_CASES("v_dot2c_f32_bf16_dpp")
+  } else if constexpr (DT == IT_F16) {
+    IT_QK_CASES("v_dot2c_f32_f16_dpp")
+  } else {
+    IT_QK_CASES("v_fmac_f32_dpp")
+  }
+}
+
+// PV: a0[g] += p[g] (lane L of the row) . v0, a1[g] += p[g] . v1.  Each
+// accumulator is written once per block; the leading s_nop covers the
+// converted / permuted values the block reads.
+#define IT_PV1(OP) IT_DPP(OP, "a00", "p0", "v0", "l") IT_DPP(OP, "a01", "p0", "v1", "l")
+#define IT_PV2(OP) IT_PV1(OP) IT_DPP(OP, "a10", "p1", "v0", "l") IT_DPP(OP, "a11", "p1", "v1", "l")
+#define IT_PV3(OP) IT_PV2(OP) IT_DPP(OP, "a20", "p2", "v0", "l") IT_DPP(OP, "a21", "p2", "v1", "l")
+#define IT_PV4(OP) IT_PV3(OP) IT_DPP(OP, "a30", "p3", "v0", "l") IT_DPP(OP, "a31", "p3", "v1", "l")
+#define IT_PV5(OP) IT_PV4(OP) IT_DPP(OP, "a40", "p4", "v0", "l") IT_DPP(OP, "a41", "p4", "v1", "l")
+#define IT_PV6(OP) IT_PV5(OP) IT_DPP(OP, "a50", "p5", "v0", "l") IT_DPP(OP, "a51", "p5", "v1", "l")
+#define IT_PV7(OP) IT_PV6(OP) IT_DPP(OP, "a60", "p6", "v0", "l") IT_DPP(OP, "a61", "p6", "v1", "l")
+#define IT_PV8(OP) IT_PV7(OP) IT_DPP(OP, "a70", "p7", "v0", "l") IT_DPP(OP, "a71", "p7", "v1", "l")
+#define IT_PV_OPS                                                                                       \
+  : [a00] "+v"(a0[0]), [a01] "+v"(a1[0]), [a10] "+v"(a0[1]), [a11] "+v"(a1[1]), [a20] "+v"(a0[2]),      \
+    [a21] "+v"(a1[2]), [a30] "+v"(a0[3]), [a31] "+v"(a1[3]), [a40] "+v"(a0[4]), [a41] "+v"(a1[4]),       \
+    [a50] "+v"(a0[5]), [a51] "+v"(a1[5]), [a60] "+v"(a0[6]), [a61] "+v"(a1[6]), [a70] "+v"(a0[7]),       \
+    [a71] "+v"(a1[7])                                                                                   \
+  : [p0] "v"(p[0]), [p1] "v"(p[1]), [p2] "v"(p[2]), [p3] "v"(p[3]), [p4] "v"(p[4]), [p5] "v"(p[5]),        \
+    [p6] "v"(p[6]), [p7] "v"(p[7]), [v0] "v"(v0), [v1] "v"(v1), [l] "n"(L)
+#define IT_PV_CASES(OP)                                                                 \
+  if constexpr (GC == 1) asm("s_nop 1\n\t" IT_PV1(OP) IT_PV_OPS);                      \
+  else if constexpr (GC == 2) asm("s_nop 1\n\t" IT_PV2(OP) IT_PV_OPS);                 \
+  else if constexpr (GC == 3) asm("s_nop 1\n\t" IT_PV3(OP) IT_PV_OPS);                 \
+  else if constexpr (GC == 4) asm("s_nop 1\n\t" IT_PV4(OP) IT_PV_OPS);                 \
+  else if constexpr (GC == 5) asm("s_nop 1\n\t" IT_PV5(OP) IT_PV_OPS);                 \
+  else if constexpr (GC == 6) asm("s_nop 1\n\t" IT_PV6(OP) IT_PV_OPS);                 \
+  else if constexpr (GC == 7) asm("s_nop 1\n\t" IT_PV7(OP) IT_PV_OPS);                 \
+  else asm("s_nop 1\n\t" IT_PV8(OP) IT_PV_OPS);
+
+template <int DT, int GC, int L>
+__device__ __forceinline__ void pv_words(float (&a0)[8], float (&a1)[8], const uint32_t (&p)[8], uint32_t v0,
+                                         uint32_t v1) {
+  static_assert(L >= 0 && L < 16, "probability lane");
+  if constexpr (DT == IT_BF16) {
+    IT_PV_CASES("v_dot2c_f32_bf16_dpp")
+  } else if constexpr (DT == IT_F16) {
+    IT_PV_CASES("v_dot2c_f32_f16_dpp")
+  } else {
+    IT_PV_CASES("v_fmac_f32_dpp")
+  }
+}
+
+// Two fp32 -> packed 16-bit pair (lo = a), round to nearest even.
+template <int DT>
+__device__ __forceinline__ uint32_t pack16(float a, float b) {
+  if constexpr (DT == IT_BF16) {
+    typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+    bf2 p;
+    p[0] = (__bf16)a;  // v_cvt_pk_bf16_f32 (RNE)
+    p[1] = (__bf16)b;
+    return __builtin_bit_cast(uint32_t, p);
+  } else {
+    return f32_to_f16_bits(a) | (f32_to_f16_bits(b) << 16);
+  }
+}
+template <int DT>
+__device__ __forceinline__ float lo16(uint32_t w) {
+  if constexpr (DT == IT_BF16) return __uint_as_float(w << 16);
+  else return f16_bits_to_f32(w & 0xFFFFu);
+}
+template <int DT>
+__device__ __forceinline__ float hi16(uint32_t w) {
+  if constexpr (DT == IT_BF16) return __uint_as_float(w & 0xFFFF0000u);
+  else return f16_bits_to_f32(w >> 16);
+}
+// Signed byte J of w as fp32 (v_cvt_f32_i32 with an SDWA sign-extended byte).
+template <int J>
+__device__ __forceinline__ uint32_t i8_f32(uint32_t w) {
+  return __float_as_uint(float(int32_t(w << (24 - 8 * J)) >> 24));
+}
+
+// (x, y) -> (x_lo + x_hi, y_lo + y_hi) across the two 32-lane halves:
+// lanes 0-31 receive x's sum, lanes 32-63 y's.
+__device__ __forceinline__ float fold32(float x, float y) {
+  const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(y), false, false);
+  return __uint_as_float(s[0]) + __uint_as_float(s[1]);
+}
+// Rows (0,1) and (2,3) of x and y: row 0 <- x0 + x1, row 1 <- y0 + y1,
+// row 2 <- x2 + x3, row 3 <- y2 + y3.
+__device__ __forceinline__ float fold16(float x, float y) {
+  const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(y), false, false);
+  return __uint_as_float(s[0]) + __uint_as_float(s[1]);
+}
+// Reduce eight per-lane values over all 64 lanes without LDS: two permlane
+// folds, then a DPP sum (or max) within each 16-lane row.  Row r of the
+// first result holds value {0, 2, 1, 3}[r], of the second {4, 6, 5, 7}[r],
+// in every lane of the row.
+template <bool kMax>
+__device__ __forceinline__ void fold8(const float (&x)[8], float& ra, float& rb) {
+  auto f32 = [](float p, float q) {
+    const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(p), __float_as_uint(q), false, false);
+    return kMax ? fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1])) : __uint_as_float(s[0]) + __uint_as_float(s[1]);
+  };
+  auto f16 = [](float p, float q) {
+    const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(p), __float_as_uint(q), false, false);
+    return kMax ? fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1])) : __uint_as_float(s[0]) + __uint_as_float(s[1]);
+  };
+  ra = f16(f32(x[0], x[1]), f32(x[2], x[3]));
+  rb = f16(f32(x[4], x[5]), f32(x[6], x[7]));
+  if constexpr (kMax) {
+    ra = group_max<16>(ra);
+    rb = group_max<16>(rb);
+  } else {
+    ra = group_sum<16>(ra);
+    rb = group_sum<16>(rb);
+  }
+}
+
+template <int DT, int D, int GC, int NW, int R>
+__global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
+  using F = SplitFmt<DT, D>;
+  constexpr int RB = F::kRow, GB = F::kGroup, SLOT = F::kSlot, NI = F::kDma, NL = F::kLoads;
+  constexpr int PQ = F::kPieces, NQ = F::kQRegs, DPV = F::kDpv;
+  constexpr bool k16 = F::k16, kQ8 = F::kQ8;
+  constexpr int NT = 64 * NW;  // threads
+  static_assert(GC >= 1 && GC <= 8, "1..8 heads per workgroup");
+  static_assert(NW == 2 || NW == 4, "2 or 4 waves");
+  static_assert(R >= 2 && R <= 4, "ring wait covers R = 2..4");
+  static_assert((R - 2) * NL < 64, "vmcnt is 6 bits");
+
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  constexpr size_t kRingAll = size_t(NW) * R * SLOT;
+  constexpr size_t kRed = size_t(NW) * 8 * D * 4;
+  char* const ring = smem;
+  float* const sc = reinterpret_cast<float*>(smem + (kRingAll > kRed ? kRingAll : kRed));
+  const int SP = a.partition + 16;  // plane stride (staggers heads over the banks)
+  float* const s_mx = sc + GC * SP;  // [NW][8] partition max per wave and head
+  float* const s_l = s_mx + NW * 8;  // [NW][8] probability sums
+  uint32_t* const s_pp = reinterpret_cast<uint32_t*>(s_l + NW * 8);  // [NW][kScratch / 4]
+  int32_t* const s_pages = reinterpret_cast<int32_t*>(s_pp + NW * (F::kScratch / 4));
+  // Score of head h, token i (partition-relative): sc[h * SP + i].
+
+  const int part = blockIdx.x;
+  const int kvh = blockIdx.y / a.chunks;
+  const int chunk = blockIdx.y - kvh * a.chunks;
+  const int b = blockIdx.z;
+  const int head0 = kvh * a.group + chunk * GC;
+
+  const int ctx = a.ctx_lens ? a.ctx_lens[b] : a.ctx_const;
+  const int st = a.start_pos ? a.start_pos[b] : 0;
+  const int n = ctx - st;
+  const int P = a.partition;
+  if (n <= 0 || part * P >= n) return;  // uniform for the workgroup
+  if (part == a.max_parts - 1 && n > a.max_parts * P && threadIdx.x == 0)
+    atomicOr(a.err, 8u);  // context longer than the caller's max_tokens: tail ignored
+  const int tok0 = st + part * P;
+  const int nt = min(P, n - part * P);
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int bs_mask = (1 << a.log2_bs) - 1;
+  const int bs = bs_mask + 1;
+
+  // Page indices (block * n_kv_heads + kvh) of the partition, via LDS.
+  const int lb0 = tok0 >> a.log2_bs;
+  const int nlb = ((tok0 + nt - 1) >> a.log2_bs) - lb0 + 1;  // <= max_pages
+  for (int i = tid; i < nlb; i += NT) {
+    const int lb = lb0 + i;
+    int blk = lb;
+    if (a.bt) {
+      if (lb >= a.max_blocks) {
+        atomicOr(a.err, 4u);
+        blk = 0;
+      } else {
+        blk = a.bt[int64_t(b) * a.max_blocks + lb];
+      }
+    }
+    if (blk < 0 || blk >= a.num_blocks) {
+      atomicOr(a.err, 2u);
+      blk = 0;
+    }
+    s_pages[i] = blk * a.n_kv_heads + kvh;
+  }
+
+  // q in the QK layout: lane (r, k) holds, per head, words k, 16 + k, ... of
+  // quarter r of the head dimension (packed 16-bit pairs, or fp32).
+  const int qr_row = lane >> 4, qk_tok = lane & 15;
+  uint32_t qv[GC][NQ];
+  {
+    const uint32_t* qp = static_cast<const uint32_t*>(a.q) +
+                         (int64_t(b) * a.n_heads + head0) * (k16 ? D / 2 : D) + qr_row * (k16 ? D / 8 : D / 4) +
+                         qk_tok;
+#pragma unroll
+    for (int g = 0; g < GC; ++g)
+#pragma unroll
+      for (int j = 0; j < NQ; ++j) qv[g][j] = qp[g * (k16 ? D / 2 : D) + 16 * j];
+  }
+  // Consume q and the block-table loads before any DMA is issued (the
+  // compiler's wait for them would not know about the ring loads), and give
+  // the DPP readers of q their wait states.
+#pragma unroll
+  for (int g = 0; g < GC; ++g)
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) asm volatile("" : "+v"(qv[g][j]));
+  asm volatile("s_waitcnt vmcnt(0)\n\ts_nop 4" ::: "memory");
+  lds_barrier();
+
+  // This wave's groups: w, w + NW, ...; the stream is their K rows, then
+  // their V rows.
+  const int ng = (nt + kGroupTok - 1) / kGroupTok;
+  const int ns = ng > wave ? (ng - 1 - wave) / NW + 1 : 0;
+  const int S = 2 * ns;
+  char* const my_ring = ring + size_t(wave) * R * SLOT;
+  const uint32_t ring_m0 = lds_offset(my_ring);
+  const uint32_t page_bytes = uint32_t(a.page_bytes);
+
+  // Load stream item s (K or V group) into slot s % R: instruction j, lane i
+  // moves bytes [1024 j + 16 i, +16) of the group's main plane, i.e. piece
+  // slot ps of token row tt (K rows hold logical piece ps ^ (tt & kSwz)
+  // there); Q8_0 adds one dword load of the group's scale rows.  Rows past
+  // the partition load the group's first row as a stand-in.
+  int lane_row[NI], lane_off_k[NI], lane_off_v[NI];
+#pragma unroll
+  for (int j = 0; j < NI; ++j) {
+    const int o = 1024 * j + 16 * lane;
+    const int tt = o / RB, ps = (o % RB) / 16;
+    lane_row[j] = tt;
+    lane_off_k[j] = tt * RB + ((ps ^ (tt & F::kSwz)) << 4);
+    lane_off_v[j] = tt * RB + (ps << 4);
+  }
+  const int s_row = kQ8 ? (4 * lane) / (F::kScaleRow > 0 ? F::kScaleRow : 1) : 0;  // scale row of this lane
+  const bool s_lane = 4 * lane < F::kScaleGroup;
+  auto issue = [&](int s) {
+    const bool is_v = s >= ns;
+    const int gi = is_v ? s - ns : s;
+    const int tb = (gi * NW + wave) * kGroupTok;  // partition-relative first token
+    const int t0 = tok0 + tb;
+    const char* pool = is_v ? a.v_pool : a.k_pool;
+    const uint32_t m0 = ring_m0 + uint32_t(s % R) * SLOT;
+    const int in_page = t0 & bs_mask;
+    if (in_page + kGroupTok <= bs) {
+      // The whole group lies in one page: one uniform base, one add per load.
+      const uint32_t page = uint32_t(__builtin_amdgcn_readfirstlane(s_pages[(t0 >> a.log2_bs) - lb0]));
+      const char* pbase = pool + uint64_t(page) * page_bytes;
+      const char* base = pbase + uint32_t(in_page * RB);
+      const bool full = tb + kGroupTok <= nt;
+#pragma unroll
+      for (int j = 0; j < NI; ++j) {
+        int off = is_v ? lane_off_v[j] : lane_off_k[j];
+        if (!full && tb + lane_row[j] >= nt) off -= lane_row[j] * RB;
+        dma_b128(base + off, __builtin_amdgcn_readfirstlane(m0 + 1024u * j));
+      }
+      if constexpr (kQ8) {
+        int row = s_row;
+        if (!full && tb + row >= nt) row = 0;
+        const char* g = pbase + uint32_t(bs * D + (in_page + row) * F::kScaleRow + (4 * lane) % F::kScaleRow);
+        if (s_lane) dma_b32(g, __builtin_amdgcn_readfirstlane(m0 + uint32_t(GB)));
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < NI; ++j) {
+        const int tt = lane_row[j];
+        int tr = tb + tt;
+        const int off = (is_v ? lane_off_v[j] : lane_off_k[j]) - tt * RB;  // piece offset within the row
+        if (tr >= nt) tr = tb;
+        const int t = tok0 + tr;
+        const uint32_t page = uint32_t(s_pages[(t >> a.log2_bs) - lb0]);
+        const char* g = pool + (uint64_t(page) * page_bytes + uint32_t((t & bs_mask) * RB + off));
+        dma_b128(g, __builtin_amdgcn_readfirstlane(m0 + 1024u * j));
+      }
+      if constexpr (kQ8) {
+        int tr = tb + s_row;
+        if (tr >= nt) tr = tb;
+        const int t = tok0 + tr;
+        const uint32_t page = uint32_t(s_pages[(t >> a.log2_bs) - lb0]);
+        const char* g = pool + (uint64_t(page) * page_bytes +
+                                uint32_t(bs * D + (t & bs_mask) * F::kScaleRow + (4 * lane) % F::kScaleRow));
+        if (s_lane) dma_b32(g, __builtin_amdgcn_readfirstlane(m0 + uint32_t(GB)));
+      }
+    }
+  };
+  // Before consuming item s: its loads are done (at most the items issued
+  // after it are outstanding) and this wave's LDS reads are done, so the
+  // slot read at step s-1 may be refilled.
+  auto wait_item = [&](int s) {
+    const int later = min(R - 2, S - 1 - s);  // items issued after s
+    if (R >= 4 && later >= 2) asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)" ::"n"(2 * NL) : "memory");
+    else if (R >= 3 && later >= 1) asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)" ::"n"(NL) : "memory");
+    else asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)" ::: "memory");
+  };
+  for (int s = 0; s < R - 1 && s < S; ++s) issue(s);
+
+  // ---------------- phase 1: scores -----------------------------------------
+  const bool masked = a.mask != nullptr;
+  const float qk_mult = masked ? 1.0f : a.scale_log2;
+  // Head held by lane row r after the fold: {0, 2, 1, 3}[r] (+4 in s_b).
+  const int h_a = ((qr_row & 1) << 1) | (qr_row >> 1);
+  float m_a = -INFINITY, m_b = -INFINITY;
+  for (int s = 0; s < ns; ++s) {
+    wait_item(s);
+    if (s + R - 1 < S) issue(s + R - 1);
+    const char* slot = my_ring + (s % R) * SLOT;
+    const char* row = slot + qk_tok * RB;
+    float acc[8];
+#pragma unroll
+    for (int g = 0; g < 8; ++g) acc[g] = 0.0f;
+    uint4 kk[PQ];
+#pragma unroll
+    for (int i = 0; i < PQ; ++i) kk[i] = ld16(row + (((qr_row * PQ + i) ^ (qk_tok & F::kSwz)) << 4));
+    if constexpr (!kQ8) {
+      Unroll<0, PQ>::run([&](auto ic) {
+        constexpr int i = decltype(ic)::value;
+        constexpr int w0 = 4 * i;  // first q word of the piece (mod 16: lane; / 16: VGPR)
+        uint32_t qi[8];
+#pragma unroll
+        for (int g = 0; g < 8; ++g) qi[g] = qv[g < GC ? g : 0][w0 / 16];
+        qk_words<DT, GC, w0 % 16>(acc, qi, kk[i].x, kk[i].y, kk[i].z, kk[i].w);
+      });
+    } else {
+      // Each 32-group of the quarter (two pieces) has its own accumulators,
+      // scaled by the group's f32(d) once summed.
+      constexpr int NG8 = D / 128;  // 32-groups per quarter
+      float accg[NG8][8];
+#pragma unroll
+      for (int u = 0; u < NG8; ++u)
+#pragma unroll
+        for (int g = 0; g < 8; ++g) accg[u][g] = 0.0f;
+      Unroll<0, PQ>::run([&](auto ic) {
+        constexpr int i = decltype(ic)::value;  // piece: 16 int8 = q VGPR i, lanes 0..15
+        uint32_t qi[8];
+#pragma unroll
+        for (int g = 0; g < 8; ++g) qi[g] = qv[g < GC ? g : 0][i];
+        const uint32_t kw[4] = {kk[i].x, kk[i].y, kk[i].z, kk[i].w};
+        Unroll<0, 4>::run([&](auto jc) {
+          constexpr int j = decltype(jc)::value;
+          qk_words<DT, GC, 4 * j>(accg[i / 2], qi, i8_f32<0>(kw[j]), i8_f32<1>(kw[j]), i8_f32<2>(kw[j]),
+                                  i8_f32<3>(kw[j]));
+        });
+      });
+      asm volatile("s_nop 1" ::: "memory");
+      const char* srow = slot + GB + qk_tok * F::kScaleRow + qr_row * NG8 * 2;
+#pragma unroll
+      for (int u = 0; u < NG8; ++u) {
+        const float d = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(srow + 2 * u));
+#pragma unroll
+        for (int g = 0; g < 8; ++g) acc[g] = fmaf(d, accg[u][g], acc[g]);
+      }
+    }
+    // v_permlane*_swap must not read the accumulators within a few wait
+    // states of the asm that wrote them.
+    asm volatile("s_nop 4" : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]), "+v"(acc[4]), "+v"(acc[5]),
+                 "+v"(acc[6]), "+v"(acc[7]));
+    // Fold the four quarter sums: s_a rows hold heads {0,2,1,3}, s_b {4,6,5,7}.
+    const float a01 = fold32(acc[0], acc[1]);
+    const float a23 = GC > 2 ? fold32(acc[2], acc[3]) : 0.0f;
+    const float s_a = fold16(a01, a23) * qk_mult;
+    float s_b = 0.0f;
+    if constexpr (GC > 4) {
+      const float a45 = fold32(acc[4], acc[5]);
+      const float a67 = GC > 6 ? fold32(acc[6], acc[7]) : 0.0f;
+      s_b = fold16(a45, a67) * qk_mult;
+    }
+    const int i_tok = (s * NW + wave) * kGroupTok + qk_tok;
+    if (i_tok < nt) {
+      if (h_a < GC) sc[h_a * SP + i_tok] = s_a;
+      if (GC > 4 && 4 + h_a < GC) sc[(4 + h_a) * SP + i_tok] = s_b;
+      m_a = fmaxf(m_a, s_a);
+      m_b = fmaxf(m_b, s_b);
+    }
+  }
+  m_a = group_max<16>(m_a);
+  m_b = group_max<16>(m_b);
+  if (qk_tok == 0) {
+    s_mx[wave * 8 + h_a] = m_a;
+    s_mx[wave * 8 + 4 + h_a] = m_b;
+  }
+  lds_barrier();
+
+  // ---------------- the Backend op's additive mask ----------------------------
+  // (arm.rs:304-370) Scores become (x * scale + mask) * log2 e, -inf where the
+  // mask is -inf (flash_attn.rs:35-40), and the maxima are taken again.
+  if (masked) {
+    float mx[GC];
+#pragma unroll
+    for (int g = 0; g < GC; ++g) mx[g] = -INFINITY;
+    for (int i = tid; i < nt; i += NT) {
+      const float mk = a.mask[tok0 + i];
+#pragma unroll
+      for (int g = 0; g < GC; ++g) {
+        float& x = sc[g * SP + i];
+        const float y = (mk == -INFINITY) ? -INFINITY : (x * a.scale + mk) * kLog2e;
+        x = y;
+        mx[g] = fmaxf(mx[g], y);
+      }
+    }
+    float x8[8], ra, rb;
+#pragma unroll
+    for (int g = 0; g < 8; ++g) x8[g] = g < GC ? mx[g] : -INFINITY;
+    fold8<true>(x8, ra, rb);
+    if (qk_tok == 0) {
+      s_mx[wave * 8 + h_a] = ra;
+      s_mx[wave * 8 + 4 + h_a] = rb;
+    }
+    lds_barrier();
+  }
+
+  // The softmax is folded into the PV loop: lane L computes the probabilities
+  // of tokens 2 (L % 8) and 2 (L % 8) + 1 of the group for head L / 8 from the
+  // partition max (16-bit caches round them, as a pair, to the cache's type:
+  // the weights PV applies) and adds them to its running sum.
+  const int h_l = lane >> 3, k_l = lane & 7;
+  float m_l = s_mx[h_l];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) m_l = fmaxf(m_l, s_mx[w * 8 + h_l]);
+  const bool none_l = m_l == -INFINITY;  // every key skipped: zeros (flash_attn.rs:66-71)
+  const float* const sc_l = sc + (h_l < GC ? h_l : 0) * SP;
+  uint32_t* const pp_w = s_pp + wave * (F::kScratch / 4);
+  float lsum = 0.0f;
+
+  // ---------------- phase 3: P.V over the V groups ---------------------------
+  float acc2[DPV][8];  // [dim of the lane][head]; heads >= GC stay 0
+#pragma unroll
+  for (int x = 0; x < DPV; ++x)
+#pragma unroll
+    for (int g = 0; g < 8; ++g) acc2[x][g] = 0.0f;
+  for (int s = ns; s < S; ++s) {
+    wait_item(s);
+    if (s + R - 1 < S) issue(s + R - 1);
+    const int gi = s - ns;
+    const int tb = (gi * NW + wave) * kGroupTok;
+    char* const slot = my_ring + (s % R) * SLOT;
+    if (tb + kGroupTok > nt) {
+      // Rows past the partition hold a stand-in row: each lane zeroes the
+      // bytes its own loads brought (this wave's LDS ops stay in order).
+#pragma unroll
+      for (int j = 0; j < NI; ++j) {
+        const int o = 1024 * j + 16 * lane;
+        if (tb + o / RB >= nt) *reinterpret_cast<uint4*>(slot + o) = make_uint4(0u, 0u, 0u, 0u);
+      }
+      if constexpr (kQ8) {
+        if (s_lane && tb + s_row >= nt) *reinterpret_cast<uint32_t*>(slot + GB + 4 * lane) = 0u;
+      }
+    }
+    // Probabilities of the group: computed per lane, then read back with
+    // token (pair) t in lane t of every row (same-wave LDS ops stay in order).
+    uint32_t pv[8];
+    {
+      const int i0 = tb + 2 * k_l;
+      const float2 sv = *reinterpret_cast<const float2*>(sc_l + i0);
+      const float p0 = (i0 < nt && !none_l) ? __builtin_amdgcn_exp2f(sv.x - m_l) : 0.0f;
+      const float p1 = (i0 + 1 < nt && !none_l) ? __builtin_amdgcn_exp2f(sv.y - m_l) : 0.0f;
+      if constexpr (k16) {
+        const uint32_t pp = pack16<DT>(p0, p1);
+        lsum += lo16<DT>(pp) + hi16<DT>(pp);
+        pp_w[lane] = pp;
+      } else {
+        lsum += p0 + p1;
+        *reinterpret_cast<float2*>(pp_w + 2 * lane) = make_float2(p0, p1);
+      }
+#pragma unroll
+      for (int g = 0; g < 8; ++g)
+        pv[g] = k16 ? pp_w[(g < GC ? g : 0) * 8 + (qk_tok & 7)] : pp_w[(g < GC ? g : 0) * 16 + qk_tok];
+    }
+    if constexpr (k16) {
+      Unroll<0, kGroupTok / 2>::run([&](auto jc) {
+        constexpr int j = decltype(jc)::value;  // token pair
+        if constexpr (DPV == 2) {
+          const uint32_t w0 = *reinterpret_cast<const uint32_t*>(slot + (2 * j) * RB + 4 * lane);
+          const uint32_t w1 = *reinterpret_cast<const uint32_t*>(slot + (2 * j + 1) * RB + 4 * lane);
+          pv_words<DT, GC, j>(acc2[0], acc2[1], pv, __builtin_amdgcn_perm(w1, w0, 0x05040100u),
+                              __builtin_amdgcn_perm(w1, w0, 0x07060302u));
+        } else {
+          const uint2 w0 = *reinterpret_cast<const uint2*>(slot + (2 * j) * RB + 8 * lane);
+          const uint2 w1 = *reinterpret_cast<const uint2*>(slot + (2 * j + 1) * RB + 8 * lane);
+          pv_words<DT, GC, j>(acc2[0], acc2[1], pv, __builtin_amdgcn_perm(w1.x, w0.x, 0x05040100u),
+                              __builtin_amdgcn_perm(w1.x, w0.x, 0x07060302u));
+          pv_words<DT, GC, j>(acc2[2], acc2[3], pv, __builtin_amdgcn_perm(w1.y, w0.y, 0x05040100u),
+                              __builtin_amdgcn_perm(w1.y, w0.y, 0x07060302u));
+        }
+      });
+    } else if constexpr (DT == IT_F32) {
+      Unroll<0, kGroupTok>::run([&](auto tc) {
+        constexpr int t = decltype(tc)::value;  // token
+        if constexpr (DPV == 2) {
+          const uint2 w = *reinterpret_cast<const uint2*>(slot + t * RB + 8 * lane);
+          pv_words<DT, GC, t>(acc2[0], acc2[1], pv, w.x, w.y);
+        } else {
+          const uint4 w = *reinterpret_cast<const uint4*>(slot + t * RB + 16 * lane);
+          pv_words<DT, GC, t>(acc2[0], acc2[1], pv, w.x, w.y);
+          pv_words<DT, GC, t>(acc2[2], acc2[3], pv, w.z, w.w);
+        }
+      });
+    } else {
+      // Q8_0: v = f32(d) * qs, d of the lane's 32-group of token t.
+      const char* sbase = slot + GB + ((DPV * lane) / 32) * 2;
+      Unroll<0, kGroupTok>::run([&](auto tc) {
+        constexpr int t = decltype(tc)::value;
+        const float d = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(sbase + t * F::kScaleRow));
+        if constexpr (DPV == 2) {
+          const uint32_t w = *reinterpret_cast<const uint16_t*>(slot + t * RB + 2 * lane);
+          pv_words<DT, GC, t>(acc2[0], acc2[1], pv, __float_as_uint(d * __uint_as_float(i8_f32<0>(w))),
+                              __float_as_uint(d * __uint_as_float(i8_f32<1>(w))));
+        } else {
+          const uint32_t w = *reinterpret_cast<const uint32_t*>(slot + t * RB + 4 * lane);
+          pv_words<DT, GC, t>(acc2[0], acc2[1], pv, __float_as_uint(d * __uint_as_float(i8_f32<0>(w))),
+                              __float_as_uint(d * __uint_as_float(i8_f32<1>(w))));
+          pv_words<DT, GC, t>(acc2[2], acc2[3], pv, __float_as_uint(d * __uint_as_float(i8_f32<2>(w))),
+                              __float_as_uint(d * __uint_as_float(i8_f32<3>(w))));
+        }
+      });
+    }
+  }
+
+  // ---------------- across the waves, in a fixed order -----------------------
+  lsum = group_sum<8>(lsum);  // the 8 lanes of head h_l
+  if (k_l == 0) s_l[wave * 8 + h_l] = lsum;
+  lds_barrier();  // every wave is done with its ring (its last wait was vmcnt(0))
+  float* const red = reinterpret_cast<float*>(smem);  // [NW][GC][D]
+#pragma unroll
+  for (int g = 0; g < GC; ++g) {
+    float* dst = &red[(wave * GC + g) * D + DPV * lane];
+    if constexpr (DPV == 2) *reinterpret_cast<float2*>(dst) = make_float2(acc2[0][g], acc2[1][g]);
+    else *reinterpret_cast<float4*>(dst) = make_float4(acc2[0][g], acc2[1][g], acc2[2][g], acc2[3][g]);
+  }
+  lds_barrier();
+  const int64_t part_row = (int64_t(b) * a.n_heads + head0) * a.max_parts + part;
+  if (tid < GC) {
+    float* ml = a.ws_ml + (part_row + int64_t(tid) * a.max_parts) * 2;
+    float m = s_mx[tid], l = s_l[tid];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) {
+      m = fmaxf(m, s_mx[w * 8 + tid]);
+      l += s_l[w * 8 + tid];
+    }
+    ml[0] = m;
+    ml[1] = l;
+  }
+  for (int i = tid; i < GC * D; i += NT) {
+    float o;
+    if constexpr (NW == 2) o = red[i] + red[GC * D + i];
+    else o = (red[i] + red[GC * D + i]) + (red[2 * GC * D + i] + red[3 * GC * D + i]);
+    const int g = i / D, d = i - g * D;
+    a.ws_o[(part_row + int64_t(g) * a.max_parts) * D + d] = o;
+  }
+}
+
+}  // namespace itkv

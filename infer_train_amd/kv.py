@@ -58,6 +58,8 @@ class PagedKvCache:
         check(lib.it_kv_cache_wrap(device, self.k_pool.data_ptr(), self.v_pool.data_ptr(), num_blocks, block_size,
                                    n_kv_heads, head_dim, dtype, C.byref(h)))
         self._h = h
+        # Bound now: at interpreter exit the module global may already be gone.
+        self._destroy = lib.it_kv_cache_destroy
         self.num_blocks, self.block_size, self.n_kv_heads, self.head_dim = num_blocks, block_size, n_kv_heads, head_dim
         self.dtype = dtype
         self.page_bytes = page
@@ -160,8 +162,9 @@ class PagedKvCache:
 
     def __del__(self):
         h = getattr(self, "_h", None)
-        if h is not None and h.value:
-            lib.it_kv_cache_destroy(h)
+        destroy = getattr(self, "_destroy", None)
+        if h is not None and h.value and destroy is not None:
+            destroy(h)
             self._h = C.c_void_p()
 
 

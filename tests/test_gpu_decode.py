@@ -183,3 +183,42 @@ def test_backend_flash_attention_op():
     got = flash_attention(to_dev(q), to_dev(k), to_dev(k), to_dev(np.full(10, -np.inf, np.float32)))
     torch.cuda.synchronize()
     assert np.all(from_dev(got) == 0)
+
+
+def test_decode_graph_replay():
+    """append + split + combine captured in a HIP graph: every replay, with
+    eager decodes and synchronisations between replays, equals the eager
+    result bit for bit (the kernels sum in a fixed order)."""
+    import torch
+
+    hq, hkv, D, bs = 28, 4, 128, 16
+    dev, ref, tables, ctx, q, qdt = _build(orc.BF16, hq, hkv, D, bs, [300, 17, 1023, 512], seed=9)
+    dq = to_dev(q.view(np.int16), torch.bfloat16)
+    t_d, c_d = to_dev(tables), to_dev(ctx)
+    max_t = int(ctx.max())
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
+    ws = dev.decode_workspace(len(ctx), hq, max_t, 512)
+    out_g = torch.empty(dq.shape, dtype=torch.float32, device=dq.device)
+    out_e = torch.empty_like(out_g)
+    dev.decode(dq, t_d, c_d, None, max_t, scale=scale, out=out_e, ws=ws)
+    torch.cuda.synchronize()
+    eager = out_e.clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        dev.decode(dq, t_d, c_d, None, max_t, scale=scale, out=out_g, ws=ws)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        dev.decode(dq, t_d, c_d, None, max_t, scale=scale, out=out_g, ws=ws)
+    for _ in range(3):
+        out_g.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out_g, eager), "graph replay differs from the eager decode"
+        dev.decode(dq, t_d, c_d, None, max_t, scale=scale, out=out_e, ws=ws)
+        torch.cuda.synchronize()
+        assert torch.equal(out_e, eager)
+    dev.check()
+    want = ref.decode(widen(q, qdt), hq, tables, ctx, None, scale)
+    assert_close(from_dev(out_g).reshape(want.shape), want, *TOL[orc.BF16], what="graph replay vs oracle")
