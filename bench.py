@@ -38,6 +38,9 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, AMD-published
 MFMA_BF16_PEAK_TFS = 2500.0  # MI355X dense bf16 MFMA, AMD-published
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_split_config2_4k_traffic.json")
+# Instruction-mix counters of the profile's fourth pass (one pass: 8 SQ counters).
+SQ_COUNTERS = ["SQ_WAVES", "SQ_INSTS_VALU", "SQ_INSTS_SALU", "SQ_INSTS_VMEM_RD", "SQ_INSTS_LDS", "SQ_INSTS_MFMA",
+               "SQ_LDS_BANK_CONFLICT", "SQ_LDS_IDX_ACTIVE"]
 
 
 def _events(n):
@@ -554,7 +557,7 @@ def summarize_profile(d, args):
     def rows(sub, name):
         return list(csv.DictReader(open(os.path.join(d, sub, "run_" + name + ".csv"))))
 
-    kname = "paged_decode_split<30, 128, 7>"
+    kname = "paged_decode_split<30, 128, 7, 2, 2>"  # bf16, D 128, 7 heads, 2 waves, 2 ring slots
     stats = [r for r in rows("trace", "kernel_stats") if kname in r["Name"] or "combine" in r["Name"]
              or "append" in r["Name"]]
     trace = [r for r in rows("trace", "kernel_trace") if kname in r["Kernel_Name"]]
@@ -574,7 +577,7 @@ def summarize_profile(d, args):
     fetch_b = f_dec * 1024.0 * f_scale
     write_b = w_dec * 1024.0 * w_scale
     kv = 32 * 4096 * 4 * 2 * 128 * 2
-    traffic = {"kernel": "paged_decode_split<bf16,128,7>", "workload": "config 2 at 4k, cold",
+    traffic = {"kernel": "paged_decode_split<bf16,128,7,2,2>", "workload": "config 2 at 4k, cold",
                "hbm_bytes_per_launch": int(round(fetch_b + write_b)), "fetch_bytes": int(round(fetch_b)),
                "write_bytes": int(round(write_b)), "algorithmic_bytes": kv,
                "fetch_counter_kib": round(f_dec, 1), "write_counter_kib": round(w_dec, 1),
@@ -584,12 +587,13 @@ def summarize_profile(d, args):
     json.dump(traffic, open(TRAFFIC_FILE, "w"), indent=1)
     cmd = ("python3 bench.py --only-headline --steps {s} --warmup {w} --no-cpu --copy-probe").format(
         s=args.steps, w=args.warmup)
-    lines = ["# paged_decode_split<bf16,128,7> -- config 2 at 4k (cold)", "",
+    lines = ["# paged_decode_split<bf16,128,7,2,2> -- config 2 at 4k (cold)", "",
              "Commands (from the repository root on the GPU box; `cd /tmp && export TMPDIR=/tmp` first):", "",
              "```",
              f"rocprofv3 --kernel-trace --stats --output-format csv -d OUT/trace -o run -- {cmd}",
              f"rocprofv3 --pmc FETCH_SIZE --output-format csv -d OUT/fetch -o run -- {cmd}",
              f"rocprofv3 --pmc WRITE_SIZE --output-format csv -d OUT/write -o run -- {cmd}",
+             f"rocprofv3 --pmc {' '.join(SQ_COUNTERS)} --output-format csv -d OUT/sq -o run -- {cmd}",
              f"python3 bench.py --summarize-profile OUT --steps {args.steps} --warmup {args.warmup}",
              "```", "",
              "## rocprofv3 --stats (kernel_stats.csv rows of the path's kernels)", "",
@@ -607,6 +611,23 @@ def summarize_profile(d, args):
               f"Split kernel ({nf} / {nw} dispatches): FETCH_SIZE {f_dec:.0f} KiB -> {fetch_b / 1e6:.1f} MB, "
               f"WRITE_SIZE {w_dec:.0f} KiB -> {write_b / 1e6:.2f} MB; total {(fetch_b + write_b) / 1e6:.1f} MB "
               f"per launch against {kv / 1e6:.1f} MB algorithmic ({(fetch_b + write_b) / kv:.3f}x)."]
+    sq_dir = os.path.join(d, "sq")
+    if os.path.isdir(sq_dir):
+        rs = [r for r in rows("sq", "counter_collection") if kname in r["Kernel_Name"]]
+        per = {}
+        for r in rs:
+            per.setdefault(r["Counter_Name"], {}).setdefault(r["Dispatch_Id"], 0.0)
+            per[r["Counter_Name"]][r["Dispatch_Id"]] += float(r["Counter_Value"])
+        med = {k: float(np.median(list(v.values()))) for k, v in per.items()}
+        rows_kv = int(32 * 4096 * 4)  # (sequence, KV head, token) rows read per launch
+        lines += ["", "## Instruction mix per launch (rocprofv3 --pmc, split kernel, median over dispatches)", "",
+                  "| Counter | Value | Per KV token row |", "|---|---|---|"]
+        for k in SQ_COUNTERS:
+            if k in med:
+                lines.append(f"| {k} | {med[k]:.0f} | {med[k] / rows_kv:.2f} |")
+        lines += ["", "SQ_INSTS_MFMA is 0: the decode multiplies on VALU (v_dot2c_f32_bf16 with DPP row_newbcast); "
+                      "its K/V loads are global_load_lds_dwordx4 (SQ_INSTS_VMEM_RD: 16-byte lanes, 1 KiB per "
+                      "instruction)."]
     open(os.path.join(ROOT, "profiles", "decode_split_config2_4k.md"), "w").write("\n".join(lines) + "\n")
     print(json.dumps(traffic, indent=1))
 
