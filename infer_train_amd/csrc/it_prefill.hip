@@ -8,21 +8,30 @@
 // the chunked prefill itself has no counterpart in the reference, whose
 // generate loop feeds one token at a time (forward.rs:811).
 //
-// One workgroup = (sequence, KV head, block of 32 query positions); wave w
-// handles query head kvh * G + w for those 32 positions, so the G waves of a
-// group share every K/V byte the workgroup reads.  Per 64-key block:
+// One workgroup = (sequence, KV head, block of 32 QT query positions) with
+// W = G QT waves: wave w takes query head kvh G + w % G for the 32 positions
+// of tile w / G.  All W waves share every K/V byte the workgroup stages, so
+// a 64-key block is read from L2 once per 32 QT queries.  Per 64-key block:
 //   S^T = K Q^T   v_mfma_f32_32x32x16 (keys are MFMA rows, queries columns),
 //                 so each lane owns one query column: its row max and sum
-//                 are in-lane (plus one exchange with lane ^ 32);
+//                 are in-lane plus one v_permlane32_swap with lane ^ 32;
 //   O^T += V^T P^T the probabilities go back into MFMA operands straight
-//                 from the S^T registers (bf16/f16), and V^T comes from the
-//                 row-major V tile through ds_read_b64_tr_b16 transposing
-//                 loads; the contraction runs over keys in the order the S^T
-//                 registers hold them, and the V^T loads follow that order.
-// K and V blocks (16 KiB each) are staged in LDS by direct global->LDS loads,
-// 16-byte chunks XOR-swizzled by row so MFMA operand reads are conflict-free,
-// double-buffered: block j+1 loads while block j is computed.  Online
-// softmax in fp32 (exp2 domain), accumulators fp32.
+//                 from the S^T registers (bf16/f16 pairs, v_cvt_pk), and
+//                 V^T comes from the row-major V tile through
+//                 ds_read_b64_tr_b16 transposing loads, in the key order the
+//                 S^T registers hold.
+// Software pipelining: the loop body issues S^T of block kb + 1 and the
+// softmax and O update of block kb in one basic block, so the MFMA pipe
+// works on the next block's scores while the VALU turns this block's scores
+// into probabilities.  Fully visible blocks (every key precedes every query
+// of the workgroup and kend) run a loop without per-key masks; the blocks
+// the causal diagonal or kend cut run a masked copy of it.
+// K and V blocks (16 KiB each) are staged in LDS by direct global->LDS loads
+// into rings of 4 K and 3 V slots, issued two blocks ahead; 16-byte chunks
+// are XOR-swizzled by row so MFMA operand reads are conflict-free.  Page ids
+// come from the block table through scalar loads (they do not count against
+// the vector-memory counter that orders the rings).  Online softmax in fp32
+// (exp2 domain), accumulators fp32.
 #include <hip/hip_runtime.h>
 
 #include "it_device.hpp"
@@ -31,13 +40,15 @@
 using namespace itkv;
 
 namespace {
-constexpr int kD = 128;           // head_dim
-constexpr int kQB = 32;           // query positions per workgroup
-constexpr int kKB = 64;           // keys per block
-constexpr int kRowB = kD * 2;     // bytes per K/V row
+constexpr int kD = 128;               // head_dim
+constexpr int kQB = 32;               // query positions per wave tile
+constexpr int kKB = 64;               // keys per block
+constexpr int kRowB = kD * 2;         // bytes per K/V row
 constexpr int kPlaneB = kKB * kRowB;  // 16 KiB
-constexpr int kStageB = 2 * kPlaneB;  // K + V
-constexpr int kMaxGroup = 8;      // waves per workgroup (512 threads)
+constexpr int kRingK = 4;             // K slots
+constexpr int kRingV = 3;             // V slots
+constexpr int kLds = (kRingK + kRingV) * kPlaneB;  // 112 KiB
+constexpr int kMaxGroup = 8;          // query heads per KV head
 
 typedef short v4s __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
@@ -52,10 +63,13 @@ struct PrefillArgs {
   void* out;              // [total_q][n_heads][D]
   uint32_t* err;
   int64_t page_bytes;
-  int64_t num_blocks;
+  uint32_t num_blocks32;  // pool blocks (clamped to 2^31 - 1)
   float scale_log2;
-  int n_heads, n_kv_heads, group, max_blocks, log2_bs, causal, out_f32;
+  int n_heads, n_kv_heads, group, q_tiles, max_blocks, log2_bs, causal, out_f32;
 };
+
+// Query tiles per workgroup for a GQA group: up to 8 waves of work.
+inline int prefill_q_tiles(int group) { return group >= kMaxGroup ? 1 : kMaxGroup / group; }
 
 __device__ __forceinline__ uint32_t lds_off(const void* p) {
   return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)p));
@@ -63,8 +77,13 @@ __device__ __forceinline__ uint32_t lds_off(const void* p) {
 __device__ __forceinline__ void dma_b128(const void* g, uint32_t m0) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(m0), "v"(g) : "memory", "m0");
 }
+// The 16 chunks of row r are XOR-permuted by sw(r) = ((r & 3) << 2) | ((r >> 2) & 3),
+// a bijection of r mod 16: the A-operand reads (16 consecutive rows, one
+// chunk each) hit 16 distinct bank groups, and the transposing V reads (4
+// consecutive rows x 4 consecutive chunks per 32 lanes) hit 16 distinct ones.
+__device__ __forceinline__ int sw(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
 // Byte offset of 16-byte chunk c of row r in a swizzled tile.
-__device__ __forceinline__ int swz(int r, int c) { return r * kRowB + ((c ^ (r & 7)) << 4); }
+__device__ __forceinline__ int swz(int r, int c) { return r * kRowB + ((c ^ sw(r)) << 4); }
 
 template <bool kBf16>
 __device__ __forceinline__ v16f mfma(const uint4& a, const uint4& b, const v16f& c) {
@@ -76,34 +95,55 @@ __device__ __forceinline__ v16f mfma(const uint4& a, const uint4& b, const v16f&
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8, a), __builtin_bit_cast(v8, b), c, 0, 0, 0);
   }
 }
+// Two fp32 -> packed 16-bit pair (lo first), round to nearest even.
 template <bool kBf16>
 __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-  if constexpr (kBf16) return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
-  else return f32_to_f16_bits(lo) | (f32_to_f16_bits(hi) << 16);
+  if constexpr (kBf16) {
+    typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+    bf2 p;
+    p[0] = (__bf16)lo;  // v_cvt_pk_bf16_f32
+    p[1] = (__bf16)hi;
+    return __builtin_bit_cast(uint32_t, p);
+  } else {
+    return f32_to_f16_bits(lo) | (f32_to_f16_bits(hi) << 16);
+  }
+}
+// max / sum of x over this lane and lane ^ 32 (v_permlane32_swap, no LDS).
+__device__ __forceinline__ float max_halves(float x) {
+  const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
+}
+__device__ __forceinline__ float sum_halves(float x) {
+  const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(s[0]) + __uint_as_float(s[1]);
 }
 
-// MAXW: the largest group this instantiation serves (sets the register budget).
-template <bool kBf16, int MAXW>
-__global__ __launch_bounds__(64 * MAXW) __attribute__((amdgpu_waves_per_eu(2)))
-void paged_prefill_kernel(PrefillArgs a) {
-  extern __shared__ __attribute__((aligned(16))) char smem[];  // 2 stages x (K tile, V tile)
+// W: waves per workgroup (G query heads x QT query tiles).
+template <bool kBf16, int W>
+__global__ __launch_bounds__(64 * W) void paged_prefill_kernel(PrefillArgs a) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];  // K ring, then V ring
+  constexpr int kDmaPerWave = (16 + W - 1) / W;  // 1 KiB loads per wave per plane (16 per plane)
   const int qb = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
   const int q_begin = a.cu_q[b];
   const int q_len = a.cu_q[b + 1] - q_begin;
   const int ctx = a.ctx_lens[b];
-  if (qb * kQB >= q_len) return;  // uniform
+  const int wg_q = kQB * a.q_tiles;  // query positions per workgroup
+  if (qb * wg_q >= q_len) return;    // uniform
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int nw = a.group;
-  const int head = kvh * a.group + wave;
+  const int tile = wave / a.group;
+  const int head = kvh * a.group + (wave - tile * a.group);
   const int half = lane >> 5;  // 0 / 1
-  const int col = lane & 31;   // this lane's query within the block
-  const int qi = qb * kQB + col;
+  const int col = lane & 31;   // this lane's query within the tile
+  const int qi = qb * wg_q + tile * kQB + col;
   const bool q_ok = qi < q_len;
   const int q_pos = ctx - q_len + qi;  // absolute position of this lane's query
-  // Keys this workgroup needs: up to the last valid query's position.
-  const int last_q = min(q_len, (qb + 1) * kQB) - 1;
+  // Keys this workgroup needs: up to its last valid query's position.
+  const int last_q = min(q_len, (qb + 1) * wg_q) - 1;
   const int kend = a.causal ? min(ctx, ctx - q_len + last_q + 1) : ctx;
   const int nkb = (kend + kKB - 1) / kKB;
+  const int first_pos = ctx - q_len + qb * wg_q;  // position of the workgroup's first query
+  const int vis_end = a.causal ? min(kend, first_pos + 1) : kend;
+  const int n_vis = max(vis_end, 0) / kKB;  // blocks every query of the workgroup sees whole
 
   // q: B operand of S^T = K Q^T, k-step ks holds dims 16 ks + 8 half + [0, 8).
   uint4 qv[kD / 16];
@@ -112,51 +152,83 @@ void paged_prefill_kernel(PrefillArgs a) {
 #pragma unroll
     for (int ks = 0; ks < kD / 16; ++ks) {
       qv[ks] = q_ok ? ld16(qp + 16 * ks) : make_uint4(0u, 0u, 0u, 0u);
+      if (a.scale_log2 < 0.0f) {  // scale's sign into q (exact): the scaled max is the raw max
+        qv[ks].x ^= 0x80008000u;
+        qv[ks].y ^= 0x80008000u;
+        qv[ks].z ^= 0x80008000u;
+        qv[ks].w ^= 0x80008000u;
+      }
       asm volatile("" : "+v"(qv[ks].x), "+v"(qv[ks].y), "+v"(qv[ks].z), "+v"(qv[ks].w));
     }
   }
+  // q must be in registers before the first ring load: the compiler's wait
+  // for it would not count the ring loads issued after it.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   const int bs_mask = (1 << a.log2_bs) - 1;
-  const int32_t* bt = a.bt + int64_t(b) * a.max_blocks;
-  // Loads of key block kb into stage st: 32 1-KiB instructions (K then V),
-  // spread over the waves.  Lane l of instruction i covers tile row
-  // 4 (i % 16) + l / 16 and, swizzled, global chunk (l % 16) ^ (row & 7).
-  auto issue = [&](int kb, int st) {
-    for (int i = wave; i < 32; i += nw) {
-      const int plane = i >> 4;
-      const int row = 4 * (i & 15) + (lane >> 4);
-      const int chunk = (lane & 15) ^ (row & 7);
-      int key = kb * kKB + row;
-      if (key >= kend) key = kend - 1;  // rows past the keys: a valid row, masked out later
-      const int lb = key >> a.log2_bs;
-      int blk = lb < a.max_blocks ? bt[lb] : -1;
-      if (blk < 0 || blk >= a.num_blocks) {
-        atomicOr(a.err, 2u);
-        blk = 0;
-      }
-      const char* pool = plane ? a.v_pool : a.k_pool;
-      const char* g = pool + (int64_t(blk) * a.n_kv_heads + kvh) * a.page_bytes + int64_t(key & bs_mask) * kRowB + chunk * 16;
-      dma_b128(g, __builtin_amdgcn_readfirstlane(lds_off(smem) + uint32_t(st * kStageB + plane * kPlaneB + (i & 15) * 1024)));
+  // Block table row through scalar loads (constant address space).
+  const __attribute__((address_space(4))) int32_t* bt =
+      (const __attribute__((address_space(4))) int32_t*)(a.bt + int64_t(b) * a.max_blocks);
+  char* const k_ring = smem;
+  char* const v_ring = smem + kRingK * kPlaneB;
+  const uint32_t k_m0 = lds_off(k_ring), v_m0 = lds_off(v_ring);
+  const int64_t page_stride = int64_t(a.n_kv_heads) * a.page_bytes;  // bytes per pool block
+  const char* const k_head = a.k_pool + int64_t(kvh) * a.page_bytes;
+  const char* const v_head = a.v_pool + int64_t(kvh) * a.page_bytes;
+  // Loads of plane (K or V) of key block kb into LDS at m0: 16 1-KiB
+  // instructions spread over the waves (instruction i covers tile rows
+  // 4 i .. 4 i + 3; lane l row 4 i + l / 16 and, swizzled, global chunk
+  // (l % 16) ^ sw(row)).  Waves past the 16th instruction repeat one (the
+  // same bytes to the same place), so every wave issues kDmaPerWave.
+  // Blocks past the last are replaced by the last: harmless refills of
+  // slots no iteration reads again.  A page id outside the pool (or a
+  // block past the table) is replaced by page 0 and reported once, after
+  // the loop; no branch in the issue path.
+  bool bad_page = false;
+  // Pool block of each of this wave's instructions for key block kb.
+  auto page_ids = [&](int kb, int (&blk)[kDmaPerWave]) __attribute__((always_inline)) {
+    kb = min(kb, nkb - 1);
+#pragma unroll
+    for (int j = 0; j < kDmaPerWave; ++j) {
+      const int i = (wave + W * j) & 15;
+      const int lb = min(kb * kKB + 4 * i, kend - 1) >> a.log2_bs;  // one page for the 4 rows (block size >= 4)
+      const int raw = bt[min(lb, a.max_blocks - 1)];
+      const bool bad = lb >= a.max_blocks || uint32_t(raw) >= a.num_blocks32;
+      bad_page |= bad;
+      blk[j] = bad ? 0 : raw;
     }
   };
-
-  v16f o[kD / 32];
+  auto dma_plane = [&](const char* head_base, int kb, uint32_t m0, const int (&blk)[kDmaPerWave])
+      __attribute__((always_inline)) {
+    kb = min(kb, nkb - 1);
 #pragma unroll
-  for (int d = 0; d < kD / 32; ++d) o[d] = v16f{};
-  float m_run = -INFINITY, l_run = 0.0f;
+    for (int j = 0; j < kDmaPerWave; ++j) {
+      const int i = (wave + W * j) & 15;
+      const int row = 4 * i + (lane >> 4);
+      const int key = min(kb * kKB + row, kend - 1);
+      const uint32_t off = uint32_t(key & bs_mask) * kRowB + uint32_t((lane & 15) ^ sw(row)) * 16u;
+      dma_b128(head_base + int64_t(blk[j]) * page_stride + off, __builtin_amdgcn_readfirstlane(m0 + uint32_t(i) * 1024u));
+    }
+  };
+  auto k_slot = [&](int kb) { return k_ring + (kb % kRingK) * kPlaneB; };
+  auto v_slot = [&](int kb) { return v_ring + (kb % kRingV) * kPlaneB; };
+  // Iteration kb issues K(kb + 3) and V(kb + 2), needed two iterations
+  // later.  The page ids of block kb + 3 serve K now and V in the next
+  // iteration (carried in vblk).
+  int vblk[kDmaPerWave];
+  auto issue_step = [&](int kb) __attribute__((always_inline)) {
+    int kblk[kDmaPerWave];
+    page_ids(kb + 3, kblk);
+    dma_plane(k_head, kb + 3, k_m0 + uint32_t((kb + 3) % kRingK) * kPlaneB, kblk);
+    dma_plane(v_head, kb + 2, v_m0 + uint32_t((kb + 2) % kRingV) * kPlaneB, vblk);
+#pragma unroll
+    for (int j = 0; j < kDmaPerWave; ++j) vblk[j] = kblk[j];
+  };
 
-  if (nkb > 0) issue(0, 0);
-  for (int kb = 0; kb < nkb; ++kb) {
-    const int st = kb & 1;
-    // Block kb has landed (this wave's loads; the barrier makes it everyone's,
-    // and frees stage st^1, read at kb-1, for block kb+1).
-    asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    if (kb + 1 < nkb) issue(kb + 1, st ^ 1);
-    const char* kt = smem + st * kStageB;
-    const char* vt = kt + kPlaneB;
-
-    // ---- S^T for two 32-key tiles -------------------------------------------
-    v16f s[2];
+  // S^T of key block kb: two 32-key tiles; s[n][r] is key 64 kb + 32 n +
+  // 8 (r / 4) + 4 half + r % 4 for query col.
+  auto qk = [&](int kb, v16f (&s)[2]) __attribute__((always_inline)) {
+    const char* kt = k_slot(kb);
 #pragma unroll
     for (int n = 0; n < 2; ++n) {
       s[n] = v16f{};
@@ -167,24 +239,50 @@ void paged_prefill_kernel(PrefillArgs a) {
         s[n] = mfma<kBf16>(kk, qv[ks], s[n]);
       }
     }
-    // ---- online softmax (fp32, log2 domain) ----------------------------------
-    // s[n][r] is key 64 kb + 32 n + 8 (r / 4) + 4 half + r % 4 for query col.
+  };
+
+  v16f o[kD / 32];
+#pragma unroll
+  for (int d = 0; d < kD / 32; ++d) o[d] = v16f{};
+  // Running max (log2 domain, of the scaled scores) and sum.  The max is
+  // lazy: o and l are rescaled only when some lane's block max exceeds it
+  // by more than kLazy, so probabilities stay below 2^kLazy.
+  constexpr float kLazy = 8.0f;
+  float m_run = -INFINITY, l_run = 0.0f;
+  const float exp_in = fabsf(a.scale_log2);  // q carries the scale's sign
+  const int tr_key = 4 * (lane >> 5) + ((lane & 15) >> 2);
+  const int tr_dim = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+
+  // Softmax of block kb's scores s and O += V^T P^T.
+  auto softmax_pv = [&](int kb, v16f (&s)[2], bool masked) __attribute__((always_inline)) {
+    // Key 64 kb + 4 half + c (c a constant per register) is visible when
+    // c <= lim: the last visible key of this lane's query, block-relative.
+    const int lim = masked ? min(kend - 1, a.causal ? q_pos : kend - 1) - kb * kKB - 4 * half : kKB;
     float bmax = -INFINITY;
 #pragma unroll
     for (int n = 0; n < 2; ++n)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int key = kb * kKB + 32 * n + 8 * (r >> 2) + 4 * half + (r & 3);
-        const bool ok = key < kend && (!a.causal || key <= q_pos);
-        const float x = ok ? s[n][r] * a.scale_log2 : -INFINITY;
-        s[n][r] = x;
-        bmax = fmaxf(bmax, x);
+        const int c = 32 * n + 8 * (r >> 2) + (r & 3);
+        bmax = fmaxf(bmax, (!masked || c <= lim) ? s[n][r] : -INFINITY);
       }
-    bmax = fmaxf(bmax, swap_halves(bmax));
-    const float m_new = fmaxf(m_run, bmax);
-    const bool none = m_new == -INFINITY;
-    const float alpha = none ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
-    float bsum = 0.0f;
+    bmax = max_halves(bmax);
+    bmax = bmax == -INFINITY ? bmax : bmax * exp_in;  // no 0 * -inf when the scale is 0
+    if (__builtin_amdgcn_ballot_w64(bmax > m_run + kLazy) != 0) {  // uniform branch
+      const float m_new = fmaxf(m_run, bmax);
+      // 0 while m_run is -inf, 1 for a lane whose max stays -inf.
+      const float alpha = m_new == m_run ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int d = 0; d < kD / 32; ++d)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[d][r] *= alpha;
+      m_run = m_new;
+    }
+    // A lane that has seen no visible key keeps m_run = -inf and all its p
+    // are masked; any finite stand-in works in the exponent there.
+    const float m_use = m_run == -INFINITY ? 0.0f : m_run;
+    float bsum[2] = {0.0f, 0.0f};
     uint4 pk[2][2];  // [tile][k-step]: 8 probabilities each, packed
 #pragma unroll
     for (int n = 0; n < 2; ++n)
@@ -193,26 +291,20 @@ void paged_prefill_kernel(PrefillArgs a) {
         float p[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          p[e] = none ? 0.0f : __builtin_amdgcn_exp2f(s[n][8 * t + e] - m_new);
-          bsum += p[e];
+          const int c = 32 * n + 16 * t + 8 * (e >> 2) + (e & 3);
+          p[e] = __builtin_amdgcn_exp2f(fmaf(s[n][8 * t + e], exp_in, -m_use));
+          if (masked) p[e] = c <= lim ? p[e] : 0.0f;
+          bsum[e & 1] += p[e];
         }
         pk[n][t] = make_uint4(pack2<kBf16>(p[0], p[1]), pack2<kBf16>(p[2], p[3]), pack2<kBf16>(p[4], p[5]),
                               pack2<kBf16>(p[6], p[7]));
       }
-    l_run = l_run * alpha + bsum;
-    m_run = m_new;
-#pragma unroll
-    for (int d = 0; d < kD / 32; ++d)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[d][r] *= alpha;
-
-    // ---- O^T += V^T P^T ------------------------------------------------------
+    l_run += bsum[0] + bsum[1];
     // k-step (n, t), element e of lane half h <-> key 32 n + 16 t + 8 (e / 4)
     // + 4 h + e % 4: the keys s[n][8 t + e] holds.  Transposing load c
     // (e = 4 c + j) of lane L reads key 32 n + 16 t + 8 c + 4 (L / 32)
     // + (L % 16) / 4, dims 32 dt + 16 ((L / 16) % 2) + 4 (L % 4) + [0, 4).
-    const int tr_key = 4 * (lane >> 5) + ((lane & 15) >> 2);
-    const int tr_dim = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    const char* vt = v_slot(kb);
 #pragma unroll
     for (int n = 0; n < 2; ++n)
 #pragma unroll
@@ -225,18 +317,61 @@ void paged_prefill_kernel(PrefillArgs a) {
             const int key = 32 * n + 16 * t + 8 * c + tr_key;
             const int dim = 32 * dt + tr_dim;
             const char* ptr = vt + swz(key, dim >> 3) + ((dim & 4) << 1);
-            const v4s r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (__attribute__((address_space(3))) v4s*)(ptr));
+            const v4s r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)(ptr));
             w[2 * c] = uint32_t(uint16_t(r[0])) | (uint32_t(uint16_t(r[1])) << 16);
             w[2 * c + 1] = uint32_t(uint16_t(r[2])) | (uint32_t(uint16_t(r[3])) << 16);
           }
           o[dt] = mfma<kBf16>(make_uint4(w[0], w[1], w[2], w[3]), pk[n][t], o[dt]);
         }
+  };
+
+  // Prologue: K(0), (K(1), V(0)), (K(2), V(1)); S^T of block 0.  A
+  // workgroup with no keys (nkb uniform) skips straight to the zero output.
+  if (nkb > 0) {
+  {
+    int b0[kDmaPerWave], b1[kDmaPerWave];
+    page_ids(0, b0);
+    page_ids(1, b1);
+    page_ids(2, vblk);
+    dma_plane(k_head, 0, k_m0, b0);
+    dma_plane(k_head, 1, k_m0 + uint32_t(kPlaneB), b1);
+    dma_plane(v_head, 0, v_m0, b0);
+    dma_plane(k_head, 2, k_m0 + uint32_t(2 * kPlaneB), vblk);
+    dma_plane(v_head, 1, v_m0 + uint32_t(kPlaneB), b1);
+  }
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(4 * kDmaPerWave) : "memory");
+  v16f s_a[2], s_b[2];
+  qk(0, s_a);
+  // Iteration kb: K(kb + 1) and V(kb) have landed (only iteration kb - 1's
+  // loads may be outstanding) and every wave is done with the slots
+  // iteration kb refills; then S^T(kb + 1) on MFMA beside block kb's
+  // softmax and O update.
+  auto step = [&](int kb, v16f (&s_cur)[2], v16f (&s_nxt)[2], bool masked) __attribute__((always_inline)) {
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(2 * kDmaPerWave) : "memory");
+    issue_step(kb);
+    qk(kb + 1, s_nxt);
+    softmax_pv(kb, s_cur, masked);
+  };
+  // Blocks [kb0, kb1), scores of kb0 in s_a on entry and of kb1 on exit;
+  // unrolled by two so the score sets alternate without copies.
+  auto run = [&](int kb0, int kb1, bool masked) __attribute__((always_inline)) {
+#pragma nounroll
+    for (int kb = kb0; kb < kb1; ++kb) {
+      step(kb, s_a, s_b, masked);
+#pragma unroll
+      for (int n = 0; n < 2; ++n) s_a[n] = s_b[n];
+    }
+  };
+  run(0, n_vis, false);
+  run(n_vis, nkb, true);
+  // No ring load may still be writing LDS when the workgroup ends.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  if (bad_page && lane == 0) atomicOr(a.err, 2u);
   }
 
   // ---- normalise and store ------------------------------------------------
   // o[dt][r] is dim 32 dt + 8 (r / 4) + 4 half + r % 4 of query col.
-  const float l_tot = l_run + swap_halves(l_run);
+  const float l_tot = sum_halves(l_run);
   if (!q_ok) return;
   const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;  // flash_attn.rs:66-71
   const int64_t orow = ((int64_t(q_begin) + qi) * a.n_heads + head) * kD;
@@ -255,6 +390,30 @@ void paged_prefill_kernel(PrefillArgs a) {
             make_uint2(pack2<kBf16>(v[0], v[1]), pack2<kBf16>(v[2], v[3]));
       }
     }
+}
+
+template <bool kBf16, int W>
+hipError_t launch_prefill_w(const PrefillArgs& a, dim3 grid, hipStream_t s) {
+  static bool opted = false;  // idempotent: a race between threads setting it is harmless
+  if (!opted) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&paged_prefill_kernel<kBf16, W>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
+    if (e != hipSuccess) return e;
+    opted = true;
+  }
+  hipLaunchKernelGGL((paged_prefill_kernel<kBf16, W>), grid, dim3(64 * W), kLds, s, a);
+  return hipGetLastError();
+}
+
+template <bool kBf16>
+hipError_t launch_prefill(const PrefillArgs& a, dim3 grid, hipStream_t s) {
+  switch (a.group * a.q_tiles) {
+    case 5: return launch_prefill_w<kBf16, 5>(a, grid, s);
+    case 6: return launch_prefill_w<kBf16, 6>(a, grid, s);
+    case 7: return launch_prefill_w<kBf16, 7>(a, grid, s);
+    case 8: return launch_prefill_w<kBf16, 8>(a, grid, s);
+    default: return hipErrorInvalidValue;
+  }
 }
 }  // namespace
 
@@ -292,11 +451,12 @@ extern "C" int32_t it_paged_prefill(const it_kv_cache* c, const void* q, int32_t
   a.out = out;
   a.err = c->err_flag;
   a.page_bytes = c->page_bytes;
-  a.num_blocks = c->num_blocks;
+  a.num_blocks32 = uint32_t(c->num_blocks < INT32_MAX ? c->num_blocks : INT32_MAX);
   a.scale_log2 = scale * 1.4426950408889634f;
   a.n_heads = n_heads;
   a.n_kv_heads = c->n_kv_heads;
   a.group = group;
+  a.q_tiles = prefill_q_tiles(group);
   a.max_blocks = max_blocks;
   a.log2_bs = c->log2_bs;
   a.causal = causal ? 1 : 0;
@@ -304,18 +464,10 @@ extern "C" int32_t it_paged_prefill(const it_kv_cache* c, const void* q, int32_t
   int dev = -1;
   (void)hipGetDevice(&dev);
   if (dev != c->device) (void)hipSetDevice(c->device);
-  const dim3 grid(unsigned((max_q_len + kQB - 1) / kQB), unsigned(c->n_kv_heads), unsigned(n_seqs));
-  const size_t smem = 2 * kStageB;  // 64 KiB
-  const dim3 block(unsigned(64 * group));
-  const bool bf = c->dtype == IT_BF16;
-  if (group <= 4) {
-    if (bf) hipLaunchKernelGGL((paged_prefill_kernel<true, 4>), grid, block, smem, (hipStream_t)stream, a);
-    else hipLaunchKernelGGL((paged_prefill_kernel<false, 4>), grid, block, smem, (hipStream_t)stream, a);
-  } else {
-    if (bf) hipLaunchKernelGGL((paged_prefill_kernel<true, kMaxGroup>), grid, block, smem, (hipStream_t)stream, a);
-    else hipLaunchKernelGGL((paged_prefill_kernel<false, kMaxGroup>), grid, block, smem, (hipStream_t)stream, a);
-  }
-  hipError_t e = hipGetLastError();
+  const int wg_q = kQB * a.q_tiles;
+  const dim3 grid(unsigned((max_q_len + wg_q - 1) / wg_q), unsigned(c->n_kv_heads), unsigned(n_seqs));
+  const hipError_t e = c->dtype == IT_BF16 ? launch_prefill<true>(a, grid, (hipStream_t)stream)
+                                           : launch_prefill<false>(a, grid, (hipStream_t)stream);
   if (dev >= 0 && dev != c->device) (void)hipSetDevice(dev);
   if (e != hipSuccess) return fail(IT_DEVICE_ERROR, "%s: launch: %s", who, hipGetErrorString(e));
   return IT_OK;

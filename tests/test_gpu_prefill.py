@@ -14,9 +14,10 @@ pytestmark = pytest.mark.gpu
 RTOL, ATOL = 2e-3, 1e-2
 
 
-def _setup(dt, hq, hkv, ctx, q_lens, seed, nb=None, bs=16, D=128):
+def _setup(dt, hq, hkv, ctx, q_lens, seed, nb=None, bs=16, D=128, k_gain=None):
     """Paged cache holding every position of every sequence (cached prefix
-    and chunk), the chunk's queries, and the tables."""
+    and chunk), the chunk's queries, and the tables.  k_gain(pos) scales the
+    K row at position pos (then rounded to the cache dtype)."""
     import torch
     from infer_train_amd.kv import PagedKvCache
 
@@ -33,6 +34,10 @@ def _setup(dt, hq, hkv, ctx, q_lens, seed, nb=None, bs=16, D=128):
     slots = slots_for(tables, seqs, pos, bs)
     n = len(slots)
     k = kv_values(seed + 1, n * hkv * D, dt).reshape(n, hkv, D)
+    if k_gain is not None:
+        g = np.array([k_gain(p) for p in pos], np.float32)[:, None, None]
+        kf = widen(k, dt) * g
+        k = orc.f32_to_bf16(kf) if dt == orc.BF16 else orc.f32_to_f16(kf)
     v = kv_values(seed + 2, n * hkv * D, dt).reshape(n, hkv, D)
     ref = orc.Cache(nb, bs, hkv, D, dt)
     ref.append(k, v, slots)
@@ -44,11 +49,12 @@ def _setup(dt, hq, hkv, ctx, q_lens, seed, nb=None, bs=16, D=128):
     return dev, ref, tables, ctx, cu, q, td
 
 
-def _run(dev, tables, ctx, cu, q, td, hq, causal=True, out_f32=True):
+def _run(dev, tables, ctx, cu, q, td, hq, causal=True, out_f32=True, scale=None):
     import torch
 
     D = q.shape[2]
-    scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
+    if scale is None:
+        scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
     dq = to_dev(q.view(np.int16), td)
     max_q = int(np.max(np.diff(cu)))
     out = dev.prefill(dq, to_dev(cu), max_q, to_dev(tables), to_dev(ctx), scale=scale, causal=causal,
@@ -58,10 +64,11 @@ def _run(dev, tables, ctx, cu, q, td, hq, causal=True, out_f32=True):
 
 
 @pytest.mark.parametrize("dt", [orc.BF16, orc.F16])
-@pytest.mark.parametrize("hq,hkv", [(8, 2), (4, 4), (6, 3), (16, 2)])
+@pytest.mark.parametrize("hq,hkv", [(8, 2), (4, 4), (6, 3), (16, 2), (6, 2), (5, 1), (7, 1)])
 def test_prefill_small_causal(dt, hq, hkv):
     """Ragged chunks: partial 32-row query blocks and 64-key blocks, chunk
-    lengths 1 and whole-context, GQA groups 4, 1, 2, 8."""
+    lengths 1 and whole-context, GQA groups 4, 1, 2, 8, 3, 5, 7 (workgroups
+    of 8, 8, 8, 8, 6, 5, 7 waves)."""
     ctx = [100, 37, 64, 1, 200]
     q_lens = [45, 37, 1, 1, 70]
     dev, ref, tables, ctx, cu, q, td = _setup(dt, hq, hkv, ctx, q_lens, seed=11 + hq)
@@ -76,6 +83,31 @@ def test_prefill_non_causal_and_bf16_out():
     out, scale = _run(dev, tables, ctx, cu, q, td, hq, causal=False, out_f32=False)
     want = ref.prefill(widen(q, orc.BF16), hq, cu, tables, ctx, scale, causal=False)
     assert_close(widen(from_dev(out), orc.BF16), want, RTOL, ATOL, what="prefill non-causal bf16 out")
+
+
+@pytest.mark.parametrize("scale", [-0.0883883, 0.0, 0.25])
+def test_prefill_scale_values(scale):
+    """A negative scale (the max is taken over scaled scores), a zero scale
+    (uniform weights over the visible keys) and a large one."""
+    hq, hkv = 8, 2
+    dev, ref, tables, ctx, cu, q, td = _setup(orc.BF16, hq, hkv, [150, 70], [90, 70], seed=21)
+    out, scale = _run(dev, tables, ctx, cu, q, td, hq, scale=scale)
+    want = ref.prefill(widen(q, orc.BF16), hq, cu, tables, ctx, scale, causal=True)
+    assert_close(from_dev(out), want, RTOL, ATOL, what=f"prefill scale={scale}")
+
+
+@pytest.mark.parametrize("dt", [orc.BF16, orc.F16])
+def test_prefill_rising_scores(dt):
+    """K rows grow with position, so each 64-key block raises the running
+    max by several times the lazy-rescale threshold (2^8) and the
+    accumulators are rescaled mid-context; also a falling ramp (the max is
+    set by the first block and never rescaled)."""
+    hq, hkv = 8, 2
+    for gain in (lambda p: 1.0 + p / 24.0, lambda p: 8.0 / (1.0 + p / 24.0)):
+        dev, ref, tables, ctx, cu, q, td = _setup(dt, hq, hkv, [600, 333], [200, 333], seed=31, k_gain=gain)
+        out, scale = _run(dev, tables, ctx, cu, q, td, hq)
+        want = ref.prefill(widen(q, dt), hq, cu, tables, ctx, scale, causal=True)
+        assert_close(from_dev(out), want, RTOL, ATOL, what=f"prefill rising/falling dt={dt}")
 
 
 def test_prefill_config3_rows():
