@@ -48,6 +48,7 @@ constexpr int kPlaneB = kKB * kRowB;  // 16 KiB
 constexpr int kRingK = 4;             // K slots
 constexpr int kRingV = 3;             // V slots
 constexpr int kLds = (kRingK + kRingV) * kPlaneB;  // 112 KiB
+constexpr int kMaxLds = 160 * 1024;                // per workgroup (one per CU)
 constexpr int kMaxGroup = 8;          // query heads per KV head
 
 typedef short v4s __attribute__((ext_vector_type(4)));
@@ -108,6 +109,17 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
     return f32_to_f16_bits(lo) | (f32_to_f16_bits(hi) << 16);
   }
 }
+// acc + lo + hi of a packed bf16 / f16 pair (v_dot2c_f32_*).
+template <bool kBf16>
+__device__ __forceinline__ float dot2_ones(uint32_t w, float acc) {
+  if constexpr (kBf16) {
+    typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, w), __builtin_bit_cast(bf2, 0x3f803f80u), acc, false);
+  } else {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, w), __builtin_bit_cast(h2, 0x3c003c00u), acc, false);
+  }
+}
 // max / sum of x over this lane and lane ^ 32 (v_permlane32_swap, no LDS).
 __device__ __forceinline__ float max_halves(float x) {
   const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -119,11 +131,14 @@ __device__ __forceinline__ float sum_halves(float x) {
 }
 
 // W: waves per workgroup (G query heads x QT query tiles).
-template <bool kBf16, int W>
+// kTab: the block-table row is copied into LDS after the rings (it fits).
+template <bool kBf16, int W, bool kTab>
 __global__ __launch_bounds__(64 * W) void paged_prefill_kernel(PrefillArgs a) {
-  extern __shared__ __attribute__((aligned(16))) char smem[];  // K ring, then V ring
+  extern __shared__ __attribute__((aligned(16))) char smem[];  // K ring, V ring, [table]
   constexpr int kDmaPerWave = (16 + W - 1) / W;  // 1 KiB loads per wave per plane (16 per plane)
-  const int qb = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  // Query blocks in decreasing order: in causal attention later blocks see
+  // more keys, so the longest workgroups are dispatched first.
+  const int qb = gridDim.x - 1 - blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
   const int q_begin = a.cu_q[b];
   const int q_len = a.cu_q[b + 1] - q_begin;
   const int ctx = a.ctx_lens[b];
@@ -161,9 +176,26 @@ __global__ __launch_bounds__(64 * W) void paged_prefill_kernel(PrefillArgs a) {
       asm volatile("" : "+v"(qv[ks].x), "+v"(qv[ks].y), "+v"(qv[ks].z), "+v"(qv[ks].w));
     }
   }
-  // q must be in registers before the first ring load: the compiler's wait
-  // for it would not count the ring loads issued after it.
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  // The workgroup's block-table prefix into LDS (kTab), each entry checked
+  // once: an id outside the pool becomes page 0 and is reported.
+  int* const tab = reinterpret_cast<int*>(smem + kLds);
+  const int n_ent = min((kend + (1 << a.log2_bs) - 1) >> a.log2_bs, a.max_blocks);  // entries read
+  bool bad_tab = false;
+  if constexpr (kTab) {
+    bad_tab = kend > (a.max_blocks << a.log2_bs);  // keys past the table
+    const int32_t* row = a.bt + int64_t(b) * a.max_blocks;
+    bool lane_bad = false;
+    for (int e = threadIdx.x; e < n_ent; e += 64 * W) {
+      const int raw = row[e];
+      const bool bad = uint32_t(raw) >= a.num_blocks32;
+      lane_bad |= bad;
+      tab[e] = bad ? 0 : raw;
+    }
+    bad_tab |= __builtin_amdgcn_ballot_w64(lane_bad) != 0;
+  }
+  // q (and the table) must be in registers / LDS before the first ring
+  // load: the compiler's waits would not count the ring loads issued after.
+  asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
   const int bs_mask = (1 << a.log2_bs) - 1;
   // Block table row through scalar loads (constant address space).
@@ -185,17 +217,22 @@ __global__ __launch_bounds__(64 * W) void paged_prefill_kernel(PrefillArgs a) {
   // block past the table) is replaced by page 0 and reported once, after
   // the loop; no branch in the issue path.
   bool bad_page = false;
-  // Pool block of each of this wave's instructions for key block kb.
+  // Pool block of each of this wave's instructions for key block kb: from
+  // the LDS copy of the table row (kTab) or by scalar loads from the table.
   auto page_ids = [&](int kb, int (&blk)[kDmaPerWave]) __attribute__((always_inline)) {
     kb = min(kb, nkb - 1);
 #pragma unroll
     for (int j = 0; j < kDmaPerWave; ++j) {
       const int i = (wave + W * j) & 15;
       const int lb = min(kb * kKB + 4 * i, kend - 1) >> a.log2_bs;  // one page for the 4 rows (block size >= 4)
-      const int raw = bt[min(lb, a.max_blocks - 1)];
-      const bool bad = lb >= a.max_blocks || uint32_t(raw) >= a.num_blocks32;
-      bad_page |= bad;
-      blk[j] = bad ? 0 : raw;
+      if constexpr (kTab) {
+        blk[j] = tab[min(lb, n_ent - 1)];  // broadcast read; validated when the copy was made
+      } else {
+        const int raw = bt[min(lb, a.max_blocks - 1)];
+        const bool bad = lb >= a.max_blocks || uint32_t(raw) >= a.num_blocks32;
+        bad_page |= bad;
+        blk[j] = bad ? 0 : raw;
+      }
     }
   };
   auto dma_plane = [&](const char* head_base, int kb, uint32_t m0, const int (&blk)[kDmaPerWave])
@@ -207,22 +244,22 @@ __global__ __launch_bounds__(64 * W) void paged_prefill_kernel(PrefillArgs a) {
       const int row = 4 * i + (lane >> 4);
       const int key = min(kb * kKB + row, kend - 1);
       const uint32_t off = uint32_t(key & bs_mask) * kRowB + uint32_t((lane & 15) ^ sw(row)) * 16u;
-      dma_b128(head_base + int64_t(blk[j]) * page_stride + off, __builtin_amdgcn_readfirstlane(m0 + uint32_t(i) * 1024u));
+      const int pb = __builtin_amdgcn_readfirstlane(blk[j]);
+      dma_b128(head_base + int64_t(pb) * page_stride + off, __builtin_amdgcn_readfirstlane(m0 + uint32_t(i) * 1024u));
     }
   };
   auto k_slot = [&](int kb) { return k_ring + (kb % kRingK) * kPlaneB; };
   auto v_slot = [&](int kb) { return v_ring + (kb % kRingV) * kPlaneB; };
   // Iteration kb issues K(kb + 3) and V(kb + 2), needed two iterations
-  // later.  The page ids of block kb + 3 serve K now and V in the next
-  // iteration (carried in vblk).
-  int vblk[kDmaPerWave];
+  // later, with page ids fetched one iteration ahead: kblk holds block
+  // kb + 3's and vblk block kb + 2's (the previous iteration's kblk).
+  int vblk[kDmaPerWave], kblk[kDmaPerWave];
   auto issue_step = [&](int kb) __attribute__((always_inline)) {
-    int kblk[kDmaPerWave];
-    page_ids(kb + 3, kblk);
     dma_plane(k_head, kb + 3, k_m0 + uint32_t((kb + 3) % kRingK) * kPlaneB, kblk);
     dma_plane(v_head, kb + 2, v_m0 + uint32_t((kb + 2) % kRingV) * kPlaneB, vblk);
 #pragma unroll
     for (int j = 0; j < kDmaPerWave; ++j) vblk[j] = kblk[j];
+    page_ids(kb + 4, kblk);
   };
 
   // S^T of key block kb: two 32-key tiles; s[n][r] is key 64 kb + 32 n +
@@ -252,13 +289,15 @@ __global__ __launch_bounds__(64 * W) void paged_prefill_kernel(PrefillArgs a) {
   const float exp_in = fabsf(a.scale_log2);  // q carries the scale's sign
   const int tr_key = 4 * (lane >> 5) + ((lane & 15) >> 2);
   const int tr_dim = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  // Last visible key of this lane's query relative to block kb's first key
+  // and to this lane's half (register c of a block holds key offset
+  // 4 half + c, c = 32 n + 8 (r / 4) + r % 4).
+  const int last_vis = min(kend - 1, a.causal ? q_pos : kend - 1) - 4 * half;
+  auto lim_of = [&](int kb) { return last_vis - kb * kKB; };
 
-  // Softmax of block kb's scores s and O += V^T P^T.
-  auto softmax_pv = [&](int kb, v16f (&s)[2], bool masked) __attribute__((always_inline)) {
-    // Key 64 kb + 4 half + c (c a constant per register) is visible when
-    // c <= lim: the last visible key of this lane's query, block-relative.
-    const int lim = masked ? min(kend - 1, a.causal ? q_pos : kend - 1) - kb * kKB - 4 * half : kKB;
-    float bmax = -INFINITY;
+  // Scaled max of block kb's visible scores over the lane's query (-inf if
+  // none is visible); masked: keys past lim are not visible.
+  auto block_max = [&](const v16f (&s)[2], bool masked, int lim, float bmax) __attribute__((always_inline)) {
 #pragma unroll
     for (int n = 0; n < 2; ++n)
 #pragma unroll
@@ -267,9 +306,23 @@ __global__ __launch_bounds__(64 * W) void paged_prefill_kernel(PrefillArgs a) {
         bmax = fmaxf(bmax, (!masked || c <= lim) ? s[n][r] : -INFINITY);
       }
     bmax = max_halves(bmax);
-    bmax = bmax == -INFINITY ? bmax : bmax * exp_in;  // no 0 * -inf when the scale is 0
-    if (__builtin_amdgcn_ballot_w64(bmax > m_run + kLazy) != 0) {  // uniform branch
-      const float m_new = fmaxf(m_run, bmax);
+    return bmax == -INFINITY ? bmax : bmax * exp_in;  // no 0 * -inf when the scale is 0
+  };
+
+  v16f s[2];     // S^T of the block the next softmax phase consumes
+  uint4 pk[2][2];  // its probabilities, packed: [tile][k-step], 8 each
+
+  // Softmax phase of key block kb (VALU only): block max, lazy rescale of
+  // o and l, probabilities into pk, their sum into l.  masked: keys past
+  // lim_of(kb) are not visible (blocks below n_vis are whole).
+  // ninf: -inf, produced by the barrier the phase follows, so that the
+  // compiler keeps the phase after that barrier.
+  auto softmax_phase = [&](int kb, bool masked, float ninf) __attribute__((always_inline)) {
+    __builtin_amdgcn_sched_barrier(0);
+    const int lim = kb < n_vis ? kKB : lim_of(kb);
+    const float bm = block_max(s, masked, lim, ninf);
+    if (__builtin_amdgcn_ballot_w64(bm > m_run + kLazy) != 0) {  // uniform, rare after the first block
+      const float m_new = fmaxf(m_run, bm);
       // 0 while m_run is -inf, 1 for a lane whose max stays -inf.
       const float alpha = m_new == m_run ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
       l_run *= alpha;
@@ -283,7 +336,6 @@ __global__ __launch_bounds__(64 * W) void paged_prefill_kernel(PrefillArgs a) {
     // are masked; any finite stand-in works in the exponent there.
     const float m_use = m_run == -INFINITY ? 0.0f : m_run;
     float bsum[2] = {0.0f, 0.0f};
-    uint4 pk[2][2];  // [tile][k-step]: 8 probabilities each, packed
 #pragma unroll
     for (int n = 0; n < 2; ++n)
 #pragma unroll
@@ -294,12 +346,24 @@ __global__ __launch_bounds__(64 * W) void paged_prefill_kernel(PrefillArgs a) {
           const int c = 32 * n + 16 * t + 8 * (e >> 2) + (e & 3);
           p[e] = __builtin_amdgcn_exp2f(fmaf(s[n][8 * t + e], exp_in, -m_use));
           if (masked) p[e] = c <= lim ? p[e] : 0.0f;
-          bsum[e & 1] += p[e];
         }
-        pk[n][t] = make_uint4(pack2<kBf16>(p[0], p[1]), pack2<kBf16>(p[2], p[3]), pack2<kBf16>(p[4], p[5]),
-                              pack2<kBf16>(p[6], p[7]));
+        uint32_t w[4];
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          w[h] = pack2<kBf16>(p[2 * h], p[2 * h + 1]);
+          // The sum is taken over the rounded probabilities the MFMA uses.
+          bsum[h & 1] = dot2_ones<kBf16>(w[h], bsum[h & 1]);
+        }
+        pk[n][t] = make_uint4(w[0], w[1], w[2], w[3]);
       }
     l_run += bsum[0] + bsum[1];
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // Matrix phase of key block kb (MFMA and LDS only): O^T += V^T P^T of
+  // block kb, then S^T of block kb + 1 into s.
+  auto matrix_phase = [&](int kb) __attribute__((always_inline)) {
+    __builtin_amdgcn_sched_barrier(0);
     // k-step (n, t), element e of lane half h <-> key 32 n + 16 t + 8 (e / 4)
     // + 4 h + e % 4: the keys s[n][8 t + e] holds.  Transposing load c
     // (e = 4 c + j) of lane L reads key 32 n + 16 t + 8 c + 4 (L / 32)
@@ -323,6 +387,28 @@ __global__ __launch_bounds__(64 * W) void paged_prefill_kernel(PrefillArgs a) {
           }
           o[dt] = mfma<kBf16>(make_uint4(w[0], w[1], w[2], w[3]), pk[n][t], o[dt]);
         }
+    qk(kb + 1, s);
+    // Operand loads two MFMAs ahead: 6 transposing V reads, then per PV
+    // MFMA two more, then the K reads one per QK MFMA.
+    __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+#pragma unroll
+    for (int i = 0; i < 13; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+#pragma unroll
+    for (int i = 0; i < 13; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
+    __builtin_amdgcn_sched_barrier(0);
   };
 
   // Prologue: K(0), (K(1), V(0)), (K(2), V(1)); S^T of block 0.  A
@@ -333,6 +419,7 @@ __global__ __launch_bounds__(64 * W) void paged_prefill_kernel(PrefillArgs a) {
     page_ids(0, b0);
     page_ids(1, b1);
     page_ids(2, vblk);
+    page_ids(3, kblk);
     dma_plane(k_head, 0, k_m0, b0);
     dma_plane(k_head, 1, k_m0 + uint32_t(kPlaneB), b1);
     dma_plane(v_head, 0, v_m0, b0);
@@ -340,33 +427,87 @@ __global__ __launch_bounds__(64 * W) void paged_prefill_kernel(PrefillArgs a) {
     dma_plane(v_head, 1, v_m0 + uint32_t(kPlaneB), b1);
   }
   asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(4 * kDmaPerWave) : "memory");
-  v16f s_a[2], s_b[2];
-  qk(0, s_a);
-  // Iteration kb: K(kb + 1) and V(kb) have landed (only iteration kb - 1's
-  // loads may be outstanding) and every wave is done with the slots
-  // iteration kb refills; then S^T(kb + 1) on MFMA beside block kb's
-  // softmax and O update.
-  auto step = [&](int kb, v16f (&s_cur)[2], v16f (&s_nxt)[2], bool masked) __attribute__((always_inline)) {
-    asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(2 * kDmaPerWave) : "memory");
-    issue_step(kb);
-    qk(kb + 1, s_nxt);
-    softmax_pv(kb, s_cur, masked);
-  };
-  // Blocks [kb0, kb1), scores of kb0 in s_a on entry and of kb1 on exit;
-  // unrolled by two so the score sets alternate without copies.
-  auto run = [&](int kb0, int kb1, bool masked) __attribute__((always_inline)) {
-#pragma nounroll
-    for (int kb = kb0; kb < kb1; ++kb) {
-      step(kb, s_a, s_b, masked);
-#pragma unroll
-      for (int n = 0; n < 2; ++n) s_a[n] = s_b[n];
+  qk(0, s);
+  // Ping-pong: waves 0-3 (one per SIMD) run step kb as the matrix phase of
+  // block kb, a workgroup barrier, then the softmax phase of block kb + 1;
+  // waves 4-7 run the softmax phase of block kb, the barrier, then the
+  // matrix phase of block kb.  So the two waves sharing a SIMD keep the MFMA
+  // pipe and the VALU busy at the same time.  Waves 0-3 form block 0's
+  // probabilities first, one half step ahead.  A step's softmax phases are
+  // unmasked while blocks kb and kb + 1 are whole; the last step's block
+  // nkb has no visible key.
+  // At a step's start K(kb + 1) and V(kb) have landed (only step kb - 1's
+  // loads may be outstanding) and every wave is done with the slots step kb
+  // refills.
+  // The phases use registers only, so the compiler may move them across a
+  // barrier; each barrier therefore either consumes the probabilities the
+  // phase before it made (so that phase stays before it) or produces the
+  // -inf the phase after it starts from (so that phase stays after it).
+  auto barrier_after_softmax = [&](bool step_start) __attribute__((always_inline)) {
+    uint32_t* w = reinterpret_cast<uint32_t*>(&pk[0][0]);
+    if (step_start) {
+      asm volatile("s_waitcnt vmcnt(%16)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier"
+                   : "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]), "+v"(w[4]), "+v"(w[5]), "+v"(w[6]), "+v"(w[7]),
+                     "+v"(w[8]), "+v"(w[9]), "+v"(w[10]), "+v"(w[11]), "+v"(w[12]), "+v"(w[13]), "+v"(w[14]), "+v"(w[15])
+                   : "n"(2 * kDmaPerWave)
+                   : "memory");
+    } else {
+      asm volatile("s_barrier"
+                   : "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]), "+v"(w[4]), "+v"(w[5]), "+v"(w[6]), "+v"(w[7]),
+                     "+v"(w[8]), "+v"(w[9]), "+v"(w[10]), "+v"(w[11]), "+v"(w[12]), "+v"(w[13]), "+v"(w[14]), "+v"(w[15])
+                   :
+                   : "memory");
     }
   };
-  run(0, n_vis, false);
-  run(n_vis, nkb, true);
+  auto barrier_before_softmax = [&](bool step_start) __attribute__((always_inline)) {
+    float ninf;
+    if (step_start)
+      asm volatile("s_waitcnt vmcnt(%1)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier\n\tv_mov_b32 %0, 0xff800000"
+                   : "=v"(ninf)
+                   : "n"(2 * kDmaPerWave)
+                   : "memory");
+    else
+      asm volatile("s_barrier\n\tv_mov_b32 %0, 0xff800000" : "=v"(ninf) : : "memory");
+    return ninf;
+  };
+  const int u_end = max(n_vis - 1, 0);
+  if (wave < 4) {
+    softmax_phase(0, true, -INFINITY);
+#pragma nounroll
+    for (int kb = 0; kb < u_end; ++kb) {
+      barrier_after_softmax(true);
+      issue_step(kb);
+      matrix_phase(kb);
+      softmax_phase(kb + 1, false, barrier_before_softmax(false));
+    }
+#pragma nounroll
+    for (int kb = u_end; kb < nkb; ++kb) {
+      barrier_after_softmax(true);
+      issue_step(kb);
+      matrix_phase(kb);
+      softmax_phase(kb + 1, true, barrier_before_softmax(false));
+    }
+  } else {
+#pragma nounroll
+    for (int kb = 0; kb < u_end; ++kb) {
+      const float ninf = barrier_before_softmax(true);
+      issue_step(kb);
+      softmax_phase(kb, false, ninf);
+      barrier_after_softmax(false);
+      matrix_phase(kb);
+    }
+#pragma nounroll
+    for (int kb = u_end; kb < nkb; ++kb) {
+      const float ninf = barrier_before_softmax(true);
+      issue_step(kb);
+      softmax_phase(kb, true, ninf);
+      barrier_after_softmax(false);
+      matrix_phase(kb);
+    }
+  }
   // No ring load may still be writing LDS when the workgroup ends.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  if (bad_page && lane == 0) atomicOr(a.err, 2u);
+  if ((bad_page || bad_tab) && lane == 0) atomicOr(a.err, 2u);
   }
 
   // ---- normalise and store ------------------------------------------------
@@ -392,17 +533,25 @@ __global__ __launch_bounds__(64 * W) void paged_prefill_kernel(PrefillArgs a) {
     }
 }
 
-template <bool kBf16, int W>
-hipError_t launch_prefill_w(const PrefillArgs& a, dim3 grid, hipStream_t s) {
+template <bool kBf16, int W, bool kTab>
+hipError_t launch_prefill_t(const PrefillArgs& a, dim3 grid, size_t smem, hipStream_t s) {
   static bool opted = false;  // idempotent: a race between threads setting it is harmless
   if (!opted) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&paged_prefill_kernel<kBf16, W>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&paged_prefill_kernel<kBf16, W, kTab>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
     if (e != hipSuccess) return e;
     opted = true;
   }
-  hipLaunchKernelGGL((paged_prefill_kernel<kBf16, W>), grid, dim3(64 * W), kLds, s, a);
+  hipLaunchKernelGGL((paged_prefill_kernel<kBf16, W, kTab>), grid, dim3(64 * W), smem, s, a);
   return hipGetLastError();
+}
+
+template <bool kBf16, int W>
+hipError_t launch_prefill_w(const PrefillArgs& a, dim3 grid, hipStream_t s) {
+  // The table row fits beside the rings up to (160 - 112) KiB / 4 B entries.
+  const size_t tab = (size_t(a.max_blocks) * 4 + 15) & ~size_t(15);
+  if (kLds + tab <= size_t(kMaxLds)) return launch_prefill_t<kBf16, W, true>(a, grid, kLds + tab, s);
+  return launch_prefill_t<kBf16, W, false>(a, grid, kLds, s);
 }
 
 template <bool kBf16>
