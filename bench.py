@@ -632,6 +632,70 @@ def summarize_profile(d, args):
     print(json.dumps(traffic, indent=1))
 
 
+PREFILL_SQ = [["SQ_WAVES", "SQ_INSTS_VALU", "SQ_INSTS_MFMA", "SQ_INSTS_LDS", "SQ_INSTS_SALU",
+               "SQ_LDS_BANK_CONFLICT", "SQ_LDS_IDX_ACTIVE", "SQ_WAIT_INST_ANY"],
+              ["SQ_VALU_MFMA_BUSY_CYCLES", "SQ_BUSY_CYCLES", "SQ_WAVE_CYCLES", "SQ_ACTIVE_INST_VALU",
+               "SQ_ACTIVE_INST_LDS", "SQ_INSTS_VALU_MFMA_MOPS_BF16", "SQ_WAIT_ANY", "SQ_INSTS_VMEM_RD"]]
+
+
+def summarize_prefill_profile(d, args):
+    """Summarise rocprofv3 CSVs of `bench.py --only-prefill` runs: DIR/trace
+    (--kernel-trace --stats) and DIR/sq0, DIR/sq1 (--pmc, PREFILL_SQ) into
+    profiles/prefill_config3.md."""
+    import csv
+
+    def rows(sub, name):
+        return list(csv.DictReader(open(os.path.join(d, sub, "run_" + name + ".csv"))))
+
+    kname = "paged_prefill_kernel"
+    stats = [r for r in rows("trace", "kernel_stats") if kname in r["Name"] or "append" in r["Name"]]
+    trace = [r for r in rows("trace", "kernel_trace") if kname in r["Kernel_Name"]]
+    durs = np.array([(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in trace])
+    flops = 4.0 * 128 * 32 * 8 * sum(2048 + i + 1 for i in range(512))  # config 3, as bench_config3
+    cmd = "python3 bench.py --only-prefill --steps {s} --warmup {w}".format(s=args.steps, w=args.warmup)
+    lines = ["# paged_prefill_kernel -- config 3 (8 x 512-token chunks over 2048 cached, causal, bf16)", "",
+             "Commands (from the repository root on the GPU box; `cd /tmp && export TMPDIR=/tmp` first):", "",
+             "```",
+             f"rocprofv3 --kernel-trace --stats --output-format csv -d OUT/trace -o run -- {cmd}"]
+    for i, grp in enumerate(PREFILL_SQ):
+        lines.append(f"rocprofv3 --pmc {' '.join(grp)} --output-format csv -d OUT/sq{i} -o run -- {cmd}")
+    lines += [f"python3 bench.py --summarize-prefill-profile OUT --steps {args.steps} --warmup {args.warmup}", "```",
+              "", "## rocprofv3 --stats (kernel_stats.csv rows of the path's kernels)", "",
+              "| Name | Calls | AverageNs | MinNs | MaxNs |", "|---|---|---|---|---|"]
+    for r in stats:
+        lines.append(f"| `{r['Name'][:80]}` | {r['Calls']} | {float(r['AverageNs']):.0f} | {r['MinNs']} | {r['MaxNs']} |")
+    tf = flops / (durs.mean() * 1e-6) / 1e12
+    lines += ["", f"Prefill kernel, kernel trace: {durs.size} dispatches, mean {durs.mean():.2f} us, median "
+                  f"{np.median(durs):.2f} us -> {tf:.1f} TFLOP/s of algorithmic flops ({flops} per launch: "
+                  f"4 D Hq sum over query rows of keys attended) = {100 * tf / MFMA_BF16_PEAK_TFS:.1f}% of the "
+                  f"{MFMA_BF16_PEAK_TFS:.0f} TFLOP/s dense bf16 peak."]
+    med = {}
+    for i in range(len(PREFILL_SQ)):
+        sub = f"sq{i}"
+        if not os.path.isdir(os.path.join(d, sub)):
+            continue
+        per = {}
+        for r in rows(sub, "counter_collection"):
+            if kname in r["Kernel_Name"]:
+                per.setdefault(r["Counter_Name"], {}).setdefault(r["Dispatch_Id"], 0.0)
+                per[r["Counter_Name"]][r["Dispatch_Id"]] += float(r["Counter_Value"])
+        med.update({k: float(np.median(list(v.values()))) for k, v in per.items()})
+    if med:
+        waves = med.get("SQ_WAVES", 1.0)
+        lines += ["", "## Counters per launch (rocprofv3 --pmc, median over dispatches)", "",
+                  "| Counter | Value | Per wave |", "|---|---|---|"]
+        for grp in PREFILL_SQ:
+            for k in grp:
+                if k in med:
+                    lines.append(f"| {k} | {med[k]:.0f} | {med[k] / waves:.1f} |")
+        if "SQ_VALU_MFMA_BUSY_CYCLES" in med and "SQ_INSTS_MFMA" in med:
+            lines += ["", f"MFMA busy cycles per MFMA instruction: "
+                          f"{med['SQ_VALU_MFMA_BUSY_CYCLES'] / med['SQ_INSTS_MFMA']:.1f} "
+                          "(v_mfma_f32_32x32x16_bf16, 8 passes)."]
+    open(os.path.join(ROOT, "profiles", "prefill_config3.md"), "w").write("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -643,12 +707,19 @@ def main():
                     help="first run 4 device copies of 256 MiB (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     ap.add_argument("--only-headline", action="store_true",
                     help="run only the cold config-2 (4k) headline steps (for rocprofv3 runs)")
+    ap.add_argument("--only-prefill", action="store_true",
+                    help="run only config 3 (chunk append + causal prefill) (for rocprofv3 runs)")
+    ap.add_argument("--summarize-prefill-profile", metavar="DIR",
+                    help="CPU only: summarise rocprofv3 output of --only-prefill runs into profiles/")
     ap.add_argument("--summarize-profile", metavar="DIR",
                     help="CPU only: summarise rocprofv3 output DIR/{trace,fetch,write} of an --only-headline "
                          "--copy-probe run into profiles/")
     args = ap.parse_args()
     if args.summarize_profile:
         summarize_profile(args.summarize_profile, args)
+        return
+    if args.summarize_prefill_profile:
+        summarize_prefill_profile(args.summarize_prefill_profile, args)
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus > 1 is not supported. Decode would shard by "
@@ -668,6 +739,12 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+
+    if args.only_prefill:
+        r = bench_config3(args.steps, args.warmup, False)
+        print(json.dumps({"only_prefill": True, **{k: r[k] for k in ("prefill_us", "tflops", "pct_mfma_peak")}}),
+              flush=True)
+        return
 
     if args.only_headline:
         import infer_train_amd as it
