@@ -331,6 +331,51 @@ def bench_config2(steps, warmup, cpu):
 
 
 # ---------------------------------------------------------------------------
+# RoPE then append (survey row f4)
+# ---------------------------------------------------------------------------
+def bench_rope_append(steps, warmup):
+    """it_kv_append_rope at config 2's step (32 tokens, Hq 28 / Hkv 4) and
+    config 3's chunk (4096 tokens, Hq 32 / Hkv 8), D 128, bf16 cache, fp32
+    q/k/v in, rotated bf16 q out: mean HIP-event time and HBM bytes moved
+    (q, k, v read as fp32; q out, K, V written as bf16)."""
+    import torch
+
+    import infer_train_amd as it
+    from infer_train_amd.kv import PagedKvCache, RopeTable
+
+    dev = _dev()
+    out = {}
+    rope = RopeTable(128, 8192)
+    for name, n, hq, hkv in (("config2_step", 32, 28, 4), ("config3_chunk", 4096, 32, 8)):
+        c = PagedKvCache(4096, 16, hkv, 128, it.BF16)
+        g = torch.Generator(device=dev)
+        g.manual_seed(7)
+        q = torch.randn((n, hq, 128), generator=g, device=dev)
+        k = torch.randn((n, hkv, 128), generator=g, device=dev)
+        v = torch.randn((n, hkv, 128), generator=g, device=dev)
+        slots = torch.randperm(4096 * 16, generator=g, device=dev)[:n].to(torch.int64)
+        pos = torch.randint(0, 8192, (n,), generator=g, device=dev, dtype=torch.int32)
+        q_out = torch.empty((n, hq, 128), dtype=torch.bfloat16, device=dev)
+        for _ in range(warmup):
+            c.append_rope(rope, q, k, v, slots, pos, q_out=q_out)
+        torch.cuda.synchronize()
+        evs = [_events(2) for _ in range(steps)]
+        for e in evs:
+            e[0].record()
+            c.append_rope(rope, q, k, v, slots, pos, q_out=q_out)
+            e[1].record()
+        torch.cuda.synchronize()
+        c.check()
+        us = float(np.mean([e[0].elapsed_time(e[1]) for e in evs])) * 1e3
+        nbytes = n * 128 * ((hq + 2 * hkv) * 4 + (hq + 2 * hkv) * 2)
+        out[name] = {"tokens": n, "us": round(us, 2), "mtok_s": round(n / us, 3), "gbs": round(nbytes / us / 1e3, 1)}
+        del c
+    del rope
+    torch.cuda.empty_cache()
+    return out
+
+
+# ---------------------------------------------------------------------------
 # Config 3
 # ---------------------------------------------------------------------------
 def bench_config3(steps, warmup, cpu):
@@ -772,6 +817,8 @@ def main():
     if 5 in want:
         configs["5"] = bench_config5(small, 2, cpu)
         _progress("config 5 done")
+    configs["rope_append"] = bench_rope_append(max(10, args.steps // 2), 3)
+    _progress("rope append done")
 
     cold, warm = head["cold"], head["warm"]
     kv_bytes = head["kv_bytes"]

@@ -184,6 +184,32 @@ int32_t it_kv_cache_check(it_kv_cache* cache, void* stream);
 int32_t it_kv_append(it_kv_cache* cache, const void* k, const void* v, int32_t src_dtype,
                      const int64_t* slot_mapping, int32_t n_tokens, void* stream);
 
+/* RoPE then append (forward.rs:195-229): rope_f32 (src/backend/arm/rope.rs:
+ * 6-44) of every q and k head row at its token's position, then the rotated
+ * k and the unrotated v into the cache as it_kv_append stores them.
+ * The rotation's cos/sin come from `rope`, a table built once on the host
+ * with the C library's float32 powf/cosf/sinf in rope_f32's order
+ * (theta = (float)pos * powf(freq_base, -(float)i / n_dims) for each even
+ * i < n_dims), so device results equal rope_f32's bit for bit.  Elements
+ * past n_dims are not rotated (forward.rs passes n_dims = head_dim).
+ *   q: F32 [n_tokens][n_heads][head_dim]; k, v: F32 [n_tokens][n_kv_heads][head_dim]
+ *   positions: int32[n_tokens] in [0, max_pos) (else latched; the token writes nothing)
+ *   slot_mapping: as it_kv_append (slot < 0 = padding: q still rotated)
+ *   q_out: [n_tokens][n_heads][head_dim] of q_out_dtype: F32, or the cache
+ *          dtype for BF16/F16 caches (round to nearest even)
+ * F32 caches store the rotated fp32 values; BF16/F16 caches round them to
+ * nearest even; Q8_0 caches quantise them as quantize_row_q8_0. */
+typedef struct it_rope_table it_rope_table;
+/* n_dims: a multiple of 4 up to 4096; positions [0, max_pos); device memory
+ * max_pos * n_dims * 4 bytes. */
+int32_t it_rope_table_new(int32_t device, int32_t n_dims, float freq_base, int32_t max_pos,
+                          it_rope_table** out);
+int32_t it_rope_table_destroy(it_rope_table* rope);
+int32_t it_kv_append_rope(it_kv_cache* cache, const it_rope_table* rope, const float* q, int32_t n_heads,
+                          const float* k, const float* v, const int64_t* slot_mapping,
+                          const int32_t* positions, int32_t n_tokens, void* q_out, int32_t q_out_dtype,
+                          void* stream);
+
 /* Block-table gather: materialise the contiguous slices that
  * forward.rs:233-243 reads, through a block table.
  *   block_tables: int32[n_seqs][max_blocks] (absolute logical block index)

@@ -99,6 +99,9 @@ SIGNATURES = {
     "it_kv_gather": (i32, [P, P, i32, P, P, P, i32, i32, P, P, P]),
     "it_kv_evict": (i32, [P, P, i32, P]),
     "it_kv_copy_blocks": (i32, [P, P, P, i32, P]),
+    "it_rope_table_new": (i32, [i32, i32, f32, i32, PP]),
+    "it_rope_table_destroy": (i32, [P]),
+    "it_kv_append_rope": (i32, [P, P, P, i32, P, P, P, P, i32, P, i32, P]),
     "it_kv_sync_tables": (i32, [P, P, i32, i32, P, P, P, i32, P]),
     "it_paged_decode_workspace": (sz, [i32, i32, i32, i32, i32]),
     "it_paged_decode": (i32, [P, P, i32, i32, P, i32, P, P, i32, i32, f32, i32, P, sz, P, i32, P]),

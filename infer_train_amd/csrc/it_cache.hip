@@ -395,8 +395,9 @@ extern "C" int32_t it_kv_cache_check(it_kv_cache* c, void* stream) {
   IT_HIP(hipMemcpy(&flag, c->err_flag, 4, hipMemcpyDeviceToHost), "it_kv_cache_check: read flag");
   if (!flag) return IT_OK;
   IT_HIP(hipMemset(c->err_flag, 0, 4), "it_kv_cache_check: clear flag");
-  return fail(IT_INVALID_INPUT, "kv cache: device-side range error (%s%s%s%s)", (flag & kErrSlot) ? "slot " : "",
-              (flag & kErrBlock) ? "block-id " : "", (flag & kErrTable) ? "table-index " : "", (flag & kErrCtx) ? "ctx>max_tokens" : "");
+  return fail(IT_INVALID_INPUT, "kv cache: device-side range error (%s%s%s%s%s)", (flag & kErrSlot) ? "slot " : "",
+              (flag & kErrBlock) ? "block-id " : "", (flag & kErrTable) ? "table-index " : "",
+              (flag & kErrCtx) ? "ctx>max_tokens " : "", (flag & kErrPos) ? "rope-position" : "");
 }
 
 extern "C" int32_t it_kv_append(it_kv_cache* c, const void* k, const void* v, int32_t src_dtype,

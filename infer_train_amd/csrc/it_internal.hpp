@@ -15,6 +15,7 @@ enum : uint32_t {
   kErrBlock = 2u,       // block id (table, evict or copy list) out of range
   kErrTable = 4u,       // logical block beyond max_blocks
   kErrCtx = 8u,         // context longer than the max_tokens bound
+  kErrPos = 16u,        // RoPE position outside the table
 };
 
 inline bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }

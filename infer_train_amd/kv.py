@@ -14,7 +14,7 @@ import torch
 
 from ._lib import BF16, CacheDesc, F16, F32, Q8_0, check, lib
 
-__all__ = ["PagedKvCache", "flash_attention", "torch_dtype_id", "stream_handle"]
+__all__ = ["PagedKvCache", "RopeTable", "flash_attention", "torch_dtype_id", "stream_handle"]
 
 _TORCH_IDS = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 _ID_TORCH = {F32: torch.float32, F16: torch.float16, BF16: torch.bfloat16}
@@ -39,6 +39,25 @@ def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
     if not t.is_contiguous():
         raise ValueError("contiguous tensor expected")
     return t.data_ptr()
+
+
+class RopeTable:
+    """cos/sin of rope_f32's angles (src/backend/arm/rope.rs:30-34) for
+    positions [0, max_pos), built on the host in float32 and held on the
+    device (it_rope_table_new)."""
+
+    def __init__(self, n_dims: int, max_pos: int, freq_base: float = 10000.0, device: int = 0):
+        h = C.c_void_p()
+        check(lib.it_rope_table_new(device, n_dims, C.c_float(freq_base), max_pos, C.byref(h)))
+        self._h = h
+        self.n_dims, self.max_pos, self.freq_base, self.device = n_dims, max_pos, freq_base, device
+        self._destroy = lib.it_rope_table_destroy
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h is not None and h.value:
+            self._destroy(h)
+            self._h = None
 
 
 class PagedKvCache:
@@ -101,6 +120,23 @@ class PagedKvCache:
         n = slot_mapping.numel()
         check(lib.it_kv_append(self._h, _ptr(k), _ptr(v), torch_dtype_id(k.dtype), _ptr(slot_mapping), n,
                                stream_handle(self.device)))
+
+    def append_rope(self, rope: RopeTable, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                    slot_mapping: torch.Tensor, positions: torch.Tensor, q_out: Optional[torch.Tensor] = None,
+                    q_out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+        """RoPE then append (forward.rs:195-229): q [n_tokens, n_heads, D],
+        k, v [n_tokens, n_kv_heads, D] float32; positions int32 [n_tokens].
+        Returns the rotated q (float32, or the cache's 16-bit dtype)."""
+        if slot_mapping.dtype != torch.int64 or positions.dtype != torch.int32:
+            raise TypeError("slot_mapping must be int64 and positions int32")
+        if q.dtype != torch.float32 or k.dtype != torch.float32 or v.dtype != torch.float32:
+            raise TypeError("q, k, v must be float32")
+        if q_out is None:
+            q_out = torch.empty(q.shape, dtype=q_out_dtype or torch.float32, device=q.device)
+        check(lib.it_kv_append_rope(self._h, rope._h, _ptr(q), q.shape[1], _ptr(k), _ptr(v), _ptr(slot_mapping),
+                                    _ptr(positions), slot_mapping.numel(), _ptr(q_out),
+                                    torch_dtype_id(q_out.dtype), stream_handle(self.device)))
+        return q_out
 
     def gather(self, block_tables: torch.Tensor, ctx_lens: torch.Tensor, start_pos: Optional[torch.Tensor],
                cu_out: torch.Tensor, max_tokens: int, k_out: torch.Tensor, v_out: torch.Tensor) -> None:

@@ -56,6 +56,7 @@ def _load() -> C.CDLL:
         "orc_pool_free_list": (None, [P, P]),
         "orc_quantize_row_q8_0": (i32, [P, sz, P]),
         "orc_dequantize_row_q8_0": (None, [P, sz, P]),
+        "orc_rope_f32": (i32, [P, P, sz, i64, i32, i32, f32]),
         "orc_flash_attn_f32": (None, [P, P, P, P, P, i32, i32, f32]),
         "orc_backend_flash_attention": (i32, [P, P, P, P, P, i32, i32, i32]),
         "orc_page_bytes": (sz, [P]),
@@ -184,6 +185,26 @@ def quantize_row_q8_0(x) -> np.ndarray:
     rc = lib.orc_quantize_row_q8_0(x.ctypes.data, x.size, out.ctypes.data)
     if rc:
         raise ValueError("length not a multiple of 32")
+    return out
+
+
+def rope(x, pos: int, n_dims: int, head_dim: int, freq_base: float = 10000.0) -> np.ndarray:
+    """rope_f32 (rope.rs:6-44) of f32 x (any shape whose size is a multiple
+    of head_dim) at one position."""
+    x = _c(x, np.float32)
+    out = np.empty_like(x)
+    rc = lib.orc_rope_f32(x.ctypes.data, out.ctypes.data, x.size, int(pos), n_dims, head_dim, C.c_float(freq_base))
+    if rc:
+        raise ValueError("orc_rope_f32: invalid shape")
+    return out
+
+
+def rope_rows(x, positions, n_dims: int, head_dim: int, freq_base: float = 10000.0) -> np.ndarray:
+    """rope_f32 of x[t] at positions[t] for every leading index t."""
+    x = _c(x, np.float32)
+    out = np.empty_like(x)
+    for t, p in enumerate(np.asarray(positions).ravel()):
+        out[t] = rope(x[t], int(p), n_dims, head_dim, freq_base)
     return out
 
 

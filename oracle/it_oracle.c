@@ -250,6 +250,32 @@ void orc_dequantize_row_q8_0(const uint8_t* y, size_t n, float* x) {
 }
 
 /* ------------------------------------------------------------------------ */
+/* rope_f32 -- src/backend/arm/rope.rs:6-44                                   */
+/* ------------------------------------------------------------------------ */
+int orc_rope_f32(const float* x, float* out, size_t n, int64_t pos, int32_t n_dims, int32_t head_dim,
+                 float freq_base) {
+  if (head_dim <= 0 || n % (size_t)head_dim || n_dims % 2 || n_dims < 0 || n_dims > head_dim)
+    return ORC_INVALID_INPUT; /* rope.rs:15-16 asserts; n_dims <= head_dim as forward.rs calls it */
+  memcpy(out, x, n * sizeof(float)); /* rope.rs:18 */
+  size_t n_heads = n / (size_t)head_dim;
+  for (size_t h = 0; h < n_heads; ++h) {
+    size_t offset = h * (size_t)head_dim;
+    for (int32_t i = 0; i < n_dims; i += 2) { /* rope.rs:25 */
+      size_t idx = offset + (size_t)i;
+      if (idx + 1 >= n) break; /* rope.rs:27-29 */
+      float dim = (float)i;
+      /* rope.rs:31: `pos as f32 * freq_base.powf(-dim / n_dims as f32)` */
+      float theta = (float)pos * powf(freq_base, -dim / (float)n_dims);
+      float cos_theta = cosf(theta), sin_theta = sinf(theta);
+      float x0 = x[idx], x1 = x[idx + 1];
+      out[idx] = x0 * cos_theta - x1 * sin_theta; /* rope.rs:38-39, two roundings then one */
+      out[idx + 1] = x0 * sin_theta + x1 * cos_theta;
+    }
+  }
+  return ORC_OK;
+}
+
+/* ------------------------------------------------------------------------ */
 /* flash_attn_f32 -- src/backend/arm/flash_attn.rs:6-72                       */
 /* ------------------------------------------------------------------------ */
 void orc_flash_attn_f32(const float* q, const float* k, const float* v, const float* mask,

@@ -91,6 +91,15 @@ int orc_quantize_row_q8_0(const float* x, size_t n, uint8_t* y);
 /* Dequant semantics fp16_to_fp32(d) * q (gemv.rs:48-59, 151-160). */
 void orc_dequantize_row_q8_0(const uint8_t* y, size_t n, float* x);
 
+/* ---- RoPE (src/backend/arm/rope.rs:6-44) -------------------------------- */
+/* out = x rotated pairwise: for each head row of head_dim floats and each
+ * even i < n_dims, theta = (float)pos * powf(freq_base, -(float)i / n_dims),
+ * (x[i], x[i+1]) -> (x0 cos - x1 sin, x0 sin + x1 cos), float32 throughout,
+ * cosf/sinf/powf of the C library, no FMA.  Elements past n_dims are
+ * copied.  n = number of floats (a multiple of head_dim). */
+int orc_rope_f32(const float* x, float* out, size_t n, int64_t pos, int32_t n_dims, int32_t head_dim,
+                 float freq_base);
+
 /* ---- attention ---------------------------------------------------------- */
 /* src/backend/arm/flash_attn.rs:6-72, same operation order. mask may be NULL. */
 void orc_flash_attn_f32(const float* q, const float* k, const float* v, const float* mask,

@@ -183,3 +183,80 @@ def test_evict_and_copy_blocks():
         ref.k[d * pb:(d + 1) * pb] = ref.k[s * pb:(s + 1) * pb]
         ref.v[d * pb:(d + 1) * pb] = ref.v[s * pb:(s + 1) * pb]
     _assert_pools(dev, ref, "copy_blocks")
+
+
+def _to_cache_src(x, dt):
+    """float32 rows -> the source the oracle's append takes for a cache of dt
+    (16-bit caches: round to nearest even bits)."""
+    if dt == orc.BF16:
+        return orc.f32_to_bf16(x)
+    if dt == orc.F16:
+        return orc.f32_to_f16(x)
+    return np.ascontiguousarray(x, np.float32)
+
+
+@pytest.mark.parametrize("dt,D,bs", [(orc.BF16, 128, 16), (orc.F32, 128, 16), (orc.F16, 128, 16),
+                                     (orc.Q8_0, 256, 32)])
+def test_append_rope_bit_exact(dt, D, bs):
+    """RoPE then append (forward.rs:195-229): the cache pools and the rotated
+    q equal the oracle's rope_f32 (rope.rs:6-44) followed by its append,
+    byte for byte.  Positions span 0 (the identity angle), small values and
+    the table's last entry; one token is padding (q rotated, nothing
+    written); the first token carries special values (NaN, inf, subnormals,
+    rounding ties of the 16-bit formats)."""
+    import torch
+    from infer_train_amd.kv import RopeTable
+
+    hq, hkv, nb, n = (8, 2, 64, 40) if D == 128 else (12, 2, 48, 24)
+    max_pos = 5000
+    dev, ref = _pair(nb, bs, hkv, D, dt)
+    rope = RopeTable(D, max_pos)
+    rng = np.random.default_rng(5 + D)
+    slots = rng.permutation(nb * bs)[:n].astype(np.int64)
+    slots[7] = -1
+    pos = rng.integers(0, max_pos, n).astype(np.int32)
+    pos[:3] = [0, 1, max_pos - 1]
+    q = orc.normal(51, n * hq * D).reshape(n, hq, D)
+    k = orc.normal(52, n * hkv * D).reshape(n, hkv, D)
+    v = orc.normal(53, n * hkv * D).reshape(n, hkv, D)
+    special = np.array([np.nan, np.inf, -np.inf, 1e-41, -3e-40, 1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8,
+                        65519.0, 65520.0, 2 ** -25, 5.96e-8, -0.0], np.float32)
+    k[0, 0, :special.size] = special
+    v[0, 1, :special.size] = special
+    q[0, 0, :special.size] = special
+    q_rot = orc.rope_rows(q, pos, D, D)
+    k_rot = orc.rope_rows(k, pos, D, D)
+    ref.append(_to_cache_src(k_rot, dt), _to_cache_src(v, dt), slots)
+    td = {orc.BF16: torch.bfloat16, orc.F16: torch.float16}.get(dt, torch.float32)
+    q_out = dev.append_rope(rope, to_dev(q), to_dev(k), to_dev(v), to_dev(slots), to_dev(pos), q_out_dtype=td)
+    dev.check()
+    _assert_pools(dev, ref, f"append_rope dt={dt}")
+    got = from_dev(q_out)
+    want = q_rot if td == torch.float32 else _to_cache_src(q_rot, dt)
+    assert np.array_equal(got.reshape(-1).view(np.uint8), np.ascontiguousarray(want).reshape(-1).view(np.uint8)), \
+        "rotated q differs from rope_f32"
+    if td != torch.float32:  # the F32 output path as well
+        q32 = dev.append_rope(rope, to_dev(q), to_dev(k), to_dev(v), to_dev(slots), to_dev(pos))
+        assert np.array_equal(from_dev(q32).view(np.uint32), q_rot.view(np.uint32))
+
+
+def test_append_rope_bad_position_is_latched():
+    """A position outside the table is latched (reported by check) and its
+    token writes nothing; the other token is stored."""
+    import torch
+    from infer_train_amd import InvalidInput
+    from infer_train_amd.kv import RopeTable
+
+    dev, ref = _pair(8, 16, 1, 128, orc.F32)
+    rope = RopeTable(128, 100)
+    k = orc.normal(61, 2 * 128).reshape(2, 1, 128)
+    q = orc.normal(62, 2 * 128).reshape(2, 1, 128)
+    dev.append_rope(rope, to_dev(q), to_dev(k), to_dev(k), to_dev(np.array([3, 4], np.int64)),
+                    to_dev(np.array([5, 100], np.int32)))
+    with pytest.raises(InvalidInput):
+        dev.check()
+    torch.cuda.synchronize()
+    for pool in (dev.k_pool, dev.v_pool):
+        rows = from_dev(pool).reshape(8, 16, 128 * 4)
+        assert np.all(rows[0, 4] == SENTINEL), "a row with an out-of-table position must not be written"
+        assert not np.all(rows[0, 3] == SENTINEL)

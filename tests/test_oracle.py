@@ -404,3 +404,70 @@ def test_oracle_paged_prefill_vs_float64(orc, causal):
                 V = np.stack([vf[tables[b, p // bs], kvh, p % bs] for p in range(last + 1)])
                 np.testing.assert_allclose(got[cu[b] + i, h], _softmax_av(q[cu[b] + i, h], K, V, scale),
                                            rtol=2e-5, atol=2e-6)
+
+
+# ---- RoPE (rope.rs:6-44) ----------------------------------------------------
+def test_rope_reference_kat(orc):
+    """rope.rs:50-68: ones over 2 heads of 64, n_dims 64: position 0 keeps
+    every element within 0.1 of 1; position 100 moves element 0 by > 0.1."""
+    x = np.ones(128, np.float32)
+    out0 = orc.rope(x, 0, 64, 64)
+    assert np.all(np.abs(out0 - 1.0) < 0.1)
+    assert abs(orc.rope(x, 100, 64, 64)[0] - 1.0) > 0.1
+
+
+def test_rope_position_zero_is_identity(orc):
+    x = orc.normal(41, 4 * 128).reshape(4, 128)
+    assert np.array_equal(orc.rope(x, 0, 128, 128).view(np.uint32), x.view(np.uint32))
+
+
+@pytest.mark.parametrize("pos", [1, 7, 100, 2047, 4095, 130000])
+def test_rope_first_pair_angle_is_position(orc, pos):
+    """Pair 0 has exponent -0/n, so theta = (float)pos exactly: (1, 0) maps to
+    (cos pos, sin pos) of the float32 position."""
+    x = np.zeros(128, np.float32)
+    x[0] = 1.0
+    out = orc.rope(x, pos, 128, 128)
+    t = float(np.float32(pos))
+    assert abs(out[0] - math.cos(t)) < 2e-7 and abs(out[1] - math.sin(t)) < 2e-7
+
+
+@pytest.mark.parametrize("pos,n_dims,head_dim", [(5, 128, 128), (333, 64, 128), (4000, 256, 256)])
+def test_rope_matches_float64_rotation(orc, pos, n_dims, head_dim):
+    """Against a float64 rotation by the float32 angle of each pair (the
+    angle computed as rope.rs:31 does, in numpy float32): agreement to a few
+    float32 ulps; a swapped sign, a wrong pair or a wrong exponent would be
+    off by O(1).  Elements past n_dims are copied bit for bit."""
+    x = orc.normal(43 + pos, 3 * head_dim).reshape(3, head_dim)
+    out = orc.rope(x, pos, n_dims, head_dim)
+    i = np.arange(0, n_dims, 2)
+    e = (-i.astype(np.float32)) / np.float32(n_dims)
+    theta = (np.float32(pos) * np.power(np.float32(10000.0), e, dtype=np.float32)).astype(np.float64)
+    c, s = np.cos(theta), np.sin(theta)
+    x0, x1 = x[:, 0:n_dims:2].astype(np.float64), x[:, 1:n_dims:2].astype(np.float64)
+    want0, want1 = x0 * c - x1 * s, x0 * s + x1 * c
+    # numpy's float32 power may differ from powf by an ulp; that moves theta
+    # by up to pos * 6e-8 rad.
+    tol = 4e-6 + 2e-7 * pos * np.maximum(np.abs(x0), np.abs(x1))
+    assert np.all(np.abs(out[:, 0:n_dims:2] - want0) <= tol)
+    assert np.all(np.abs(out[:, 1:n_dims:2] - want1) <= tol)
+    assert np.array_equal(out[:, n_dims:].view(np.uint32), x[:, n_dims:].view(np.uint32))
+
+
+def test_rope_preserves_pair_norm_and_composes(orc):
+    x = orc.normal(47, 2 * 128).reshape(2, 128)
+    a = orc.rope(x, 300, 128, 128)
+    n_in = np.hypot(x[:, 0::2].astype(np.float64), x[:, 1::2].astype(np.float64))
+    n_out = np.hypot(a[:, 0::2].astype(np.float64), a[:, 1::2].astype(np.float64))
+    assert np.allclose(n_out, n_in, rtol=1e-6, atol=1e-7)
+    # theta is linear in the position: rotating by 300 then 200 = rotating by
+    # 500, up to the float32 rounding of each angle (an ulp of 500 is 3e-5).
+    b = orc.rope(a, 200, 128, 128)
+    assert np.allclose(b, orc.rope(x, 500, 128, 128), atol=1.5e-4)
+
+
+def test_rope_rejects_bad_shapes(orc):
+    with pytest.raises(ValueError):
+        orc.rope(np.ones(100, np.float32), 1, 64, 64)  # not a multiple of head_dim
+    with pytest.raises(ValueError):
+        orc.rope(np.ones(64, np.float32), 1, 63, 64)  # odd n_dims
