@@ -14,7 +14,7 @@ pytestmark = pytest.mark.gpu
 RTOL, ATOL = 2e-3, 1e-2
 
 
-def _setup(dt, hq, hkv, ctx, q_lens, seed, nb=None, bs=16, D=128, k_gain=None):
+def _setup(dt, hq, hkv, ctx, q_lens, seed, nb=None, bs=16, D=128, k_gain=None, mb=None):
     """Paged cache holding every position of every sequence (cached prefix
     and chunk), the chunk's queries, and the tables.  k_gain(pos) scales the
     K row at position pos (then rounded to the cache dtype)."""
@@ -23,7 +23,7 @@ def _setup(dt, hq, hkv, ctx, q_lens, seed, nb=None, bs=16, D=128, k_gain=None):
 
     ctx = np.asarray(ctx, np.int32)
     q_lens = np.asarray(q_lens, np.int32)
-    mb = int((ctx.max() + bs - 1) // bs)
+    mb = max(int((ctx.max() + bs - 1) // bs), mb or 0)
     need = int(sum((int(c) + bs - 1) // bs for c in ctx))
     nb = nb or need + 3
     tables = random_tables(seed, ctx, bs, nb, mb)
@@ -108,6 +108,31 @@ def test_prefill_rising_scores(dt):
         out, scale = _run(dev, tables, ctx, cu, q, td, hq)
         want = ref.prefill(widen(q, dt), hq, cu, tables, ctx, scale, causal=True)
         assert_close(from_dev(out), want, RTOL, ATOL, what=f"prefill rising/falling dt={dt}")
+
+
+@pytest.mark.parametrize("bs", [8, 32, 64])
+def test_prefill_block_sizes(bs):
+    """Pages of 8, 32 and 64 tokens: a 64-key block spans 8, 2 or 1 pages
+    (each 4-row load stays inside one page)."""
+    hq, hkv = 8, 2
+    ctx, q_lens = [333, 200], [150, 200]
+    dev, ref, tables, ctx, cu, q, td = _setup(orc.BF16, hq, hkv, ctx, q_lens, seed=71 + bs, bs=bs)
+    out, scale = _run(dev, tables, ctx, cu, q, td, hq)
+    want = ref.prefill(widen(q, orc.BF16), hq, cu, tables, ctx, scale, causal=True)
+    assert_close(from_dev(out), want, RTOL, ATOL, what=f"prefill bs={bs}")
+
+
+def test_prefill_wide_table_scalar_page_ids():
+    """A block table wider than fits beside the K/V rings in LDS (13,000
+    entries per row): page ids come from scalar loads of the table instead
+    of the workgroup's LDS copy."""
+    hq, hkv = 8, 2
+    ctx, q_lens = [400, 150], [130, 150]
+    dev, ref, tables, ctx, cu, q, td = _setup(orc.BF16, hq, hkv, ctx, q_lens, seed=81, mb=13000)
+    assert tables.shape[1] == 13000
+    out, scale = _run(dev, tables, ctx, cu, q, td, hq)
+    want = ref.prefill(widen(q, orc.BF16), hq, cu, tables, ctx, scale, causal=True)
+    assert_close(from_dev(out), want, RTOL, ATOL, what="prefill wide table")
 
 
 def test_prefill_config3_rows():
