@@ -18,15 +18,23 @@
 //       registers, lane k of each 16-lane row holding its k-th word, and every
 //       multiply-add reads its q word straight from lane k of its row through
 //       DPP row_newbcast:k (v_dot2c_f32_{bf16,f16} on packed 16-bit pairs,
-//       v_fmac_f32 for F32 and for Q8_0 after a sign-extending SDWA convert).
-//       The four quarter sums of every head are then folded with
-//       v_permlane32_swap / v_permlane16_swap (6 swaps, 6 adds for 8 heads).
-//       K rows sit in LDS with their 16-byte pieces XOR-swizzled by token,
-//       so a row of 16 lanes reads distinct bank groups.
+//       v_fmac_f32 for F32).  The four quarter sums of every head are then
+//       folded with v_permlane32_swap / v_permlane16_swap (6 swaps, 6 adds
+//       for 8 heads).  K rows sit in LDS with their 16-byte pieces
+//       XOR-swizzled by token, so a row of 16 lanes reads distinct bank
+//       groups.
 //  PV   lane l takes dims [D/64 l, D/64 (l+1)) of every token.  The
 //       probability of token t (16-bit caches: of token pair t) comes from
 //       lane t of the row through row_newbcast:t; 16-bit caches v_perm
 //       (v_t[d], v_t+1[d]) pairs for v_dot2c.
+//  Q8_0 runs both products on MFMA, exactly: int8 widens to bf16 without
+//       rounding, and the fp32 operand on the other side is split into three
+//       bf16 parts (hi + mid + lo = x), so every product is exact and only
+//       the fp32 accumulation rounds.  QK: v_mfma_f32_16x16x32_bf16 per
+//       32-group of the head dim, q heads x 16 tokens, then f32(d) of the
+//       group scales the group's sum.  PV: v_mfma_f32_16x16x16_bf16 per
+//       32-group, heads x 16 tokens x 16 dims, the A operand being p * f32(d)
+//       of the group.
 //
 // The softmax follows flash_attn_f32 (src/backend/arm/flash_attn.rs:6-72)
 // with the partition max taken first: phase 1 writes the scores (log2
@@ -256,6 +264,46 @@ __device__ __forceinline__ uint32_t i8_f32(uint32_t w) {
   return __float_as_uint(float(int32_t(w << (24 - 8 * J)) >> 24));
 }
 
+// ---- Q8_0 scores on MFMA ----------------------------------------------------
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+// Eight signed bytes as eight bf16, exactly: an integer of magnitude <= 128
+// converts to fp32 with its low 16 bits zero, so its top half is its bf16.
+__device__ __forceinline__ uint4 i8x8_bf16(uint2 w) {
+  auto pair = [](uint32_t f0, uint32_t f1) { return __builtin_amdgcn_perm(f1, f0, 0x07060302u); };
+  return make_uint4(pair(i8_f32<0>(w.x), i8_f32<1>(w.x)), pair(i8_f32<2>(w.x), i8_f32<3>(w.x)),
+                    pair(i8_f32<0>(w.y), i8_f32<1>(w.y)), pair(i8_f32<2>(w.y), i8_f32<3>(w.y)));
+}
+// x = hi + mid + lo exactly, each part a bf16 (round to nearest even): the
+// three parts carry the 24 significant bits of an fp32.  Two values per
+// packed word (lo element first).  No inline asm here: the compiler's hazard
+// checks do not look inside asm, and these words feed MFMA operands.  The
+// low element comes back to fp32 through v_perm (hi << 16 written as a shift
+// is turned into a second conversion of that element).
+__device__ __forceinline__ void split3_bf16(float x0, float x1, uint32_t& hi, uint32_t& mid, uint32_t& lo) {
+  auto rne2 = [](float a, float b) {
+    typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+    bf2 p;
+    p[0] = (__bf16)a;  // v_cvt_pk_bf16_f32
+    p[1] = (__bf16)b;
+    return __builtin_bit_cast(uint32_t, p);
+  };
+  auto lo_f = [](uint32_t w) { return __uint_as_float(__builtin_amdgcn_perm(0u, w, 0x01000C0Cu)); };
+  auto hi_f = [](uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); };
+  hi = rne2(x0, x1);
+  const float r0 = x0 - lo_f(hi), r1 = x1 - hi_f(hi);
+  mid = rne2(r0, r1);
+  const float t0 = r0 - lo_f(mid), t1 = r1 - hi_f(mid);
+  lo = rne2(t0, t1);
+}
+__device__ __forceinline__ v4f mfma16(uint4 a, uint4 b, v4f c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, a), __builtin_bit_cast(v8bf, b), c, 0, 0, 0);
+}
+typedef short v4s __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ v4f mfma16k16(uint2 a, uint2 b, v4f c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(v4s, a), __builtin_bit_cast(v4s, b), c, 0, 0, 0);
+}
+
 // (x, y) -> (x_lo + x_hi, y_lo + y_hi) across the two 32-lane halves:
 // lanes 0-31 receive x's sum, lanes 32-63 y's.
 __device__ __forceinline__ float fold32(float x, float y) {
@@ -361,7 +409,12 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
   // quarter r of the head dimension (packed 16-bit pairs, or fp32).
   const int qr_row = lane >> 4, qk_tok = lane & 15;
   uint32_t qv[GC][NQ];
-  {
+  // Q8_0: q is the A operand of v_mfma_f32_16x16x32_bf16 instead, lane
+  // (kh, h) = (lane / 16, lane % 16) holding dims 32 ks + 8 kh .. + 8 of head
+  // h (zero for h >= GC), split exactly into three bf16 parts.
+  constexpr int NK = kQ8 ? D / 32 : 1;  // 32-groups (MFMA k-steps) per row
+  uint4 qa[3][NK];
+  if constexpr (!kQ8) {
     const uint32_t* qp = static_cast<const uint32_t*>(a.q) +
                          (int64_t(b) * a.n_heads + head0) * (k16 ? D / 2 : D) + qr_row * (k16 ? D / 8 : D / 4) +
                          qk_tok;
@@ -369,14 +422,33 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
     for (int g = 0; g < GC; ++g)
 #pragma unroll
       for (int j = 0; j < NQ; ++j) qv[g][j] = qp[g * (k16 ? D / 2 : D) + 16 * j];
+    // Consume q and the block-table loads before any DMA is issued (the
+    // compiler's wait for them would not know about the ring loads), and
+    // give the DPP readers of q their wait states.
+#pragma unroll
+    for (int g = 0; g < GC; ++g)
+#pragma unroll
+      for (int j = 0; j < NQ; ++j) asm volatile("" : "+v"(qv[g][j]));
+  } else {
+    const int hq = lane & 15;
+    const float* qp = static_cast<const float*>(a.q) + (int64_t(b) * a.n_heads + head0 + (hq < GC ? hq : 0)) * D +
+                      8 * qr_row;
+#pragma unroll
+    for (int ks = 0; ks < NK; ++ks) {
+      float4 x0 = *reinterpret_cast<const float4*>(qp + 32 * ks);
+      float4 x1 = *reinterpret_cast<const float4*>(qp + 32 * ks + 4);
+      if (hq >= GC) x0 = x1 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      split3_bf16(x0.x, x0.y, qa[0][ks].x, qa[1][ks].x, qa[2][ks].x);
+      split3_bf16(x0.z, x0.w, qa[0][ks].y, qa[1][ks].y, qa[2][ks].y);
+      split3_bf16(x1.x, x1.y, qa[0][ks].z, qa[1][ks].z, qa[2][ks].z);
+      split3_bf16(x1.z, x1.w, qa[0][ks].w, qa[1][ks].w, qa[2][ks].w);
+    }
+#pragma unroll
+    for (int p = 0; p < 3; ++p)
+#pragma unroll
+      for (int ks = 0; ks < NK; ++ks)
+        asm volatile("" : "+v"(qa[p][ks].x), "+v"(qa[p][ks].y), "+v"(qa[p][ks].z), "+v"(qa[p][ks].w));
   }
-  // Consume q and the block-table loads before any DMA is issued (the
-  // compiler's wait for them would not know about the ring loads), and give
-  // the DPP readers of q their wait states.
-#pragma unroll
-  for (int g = 0; g < GC; ++g)
-#pragma unroll
-    for (int j = 0; j < NQ; ++j) asm volatile("" : "+v"(qv[g][j]));
   asm volatile("s_waitcnt vmcnt(0)\n\ts_nop 4" ::: "memory");
   lds_barrier();
 
@@ -471,10 +543,60 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
   // Head held by lane row r after the fold: {0, 2, 1, 3}[r] (+4 in s_b).
   const int h_a = ((qr_row & 1) << 1) | (qr_row >> 1);
   float m_a = -INFINITY, m_b = -INFINITY;
+  float m_q[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};  // Q8_0: heads 4 qr_row + i
   for (int s = 0; s < ns; ++s) {
     wait_item(s);
     if (s + R - 1 < S) issue(s + R - 1);
     const char* slot = my_ring + (s % R) * SLOT;
+    if constexpr (kQ8) {
+      // Scores on MFMA: S[h][t] = sum over 32-groups ks of f32(d[t][ks]) *
+      // (q[h] . qs[t]) over the group, the group dot product taken as three
+      // exact bf16 x int8 passes (hi, mid, lo parts of q) into one fp32
+      // accumulator.  Lane (kh, t) reads bytes 8 kh .. + 8 of group ks of
+      // token t and ends holding S[4 kh + i][t], i = 0..3.
+      const char* krow = slot + qk_tok * RB;
+      uint16_t dsc[NK];
+#pragma unroll
+      for (int ks = 0; ks < NK; ++ks)
+        dsc[ks] = *reinterpret_cast<const uint16_t*>(slot + GB + qk_tok * F::kScaleRow + 2 * ks);
+      // All K reads first; then the three passes of each group are software
+      // pipelined across groups, so that no MFMA waits for the one before it.
+      uint2 kr[NK];
+#pragma unroll
+      for (int ks = 0; ks < NK; ++ks) {
+        const int pc = (2 * ks + (qr_row >> 1)) ^ (qk_tok & F::kSwz);  // physical piece slot
+        kr[ks] = *reinterpret_cast<const uint2*>(krow + (pc << 4) + 8 * (qr_row & 1));
+      }
+      v4f acc[NK];
+      uint4 kb[NK];
+      Unroll<0, NK + 2>::run([&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        if constexpr (k < NK) {
+          kb[k] = i8x8_bf16(kr[k]);
+          acc[k] = mfma16(qa[0][k], kb[k], v4f{0.0f, 0.0f, 0.0f, 0.0f});
+        }
+        if constexpr (k >= 1 && k - 1 < NK) acc[k - 1] = mfma16(qa[1][k - 1], kb[k - 1], acc[k - 1]);
+        if constexpr (k >= 2) acc[k - 2] = mfma16(qa[2][k - 2], kb[k - 2], acc[k - 2]);
+      });
+      v4f sv = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int ks = 0; ks < NK; ++ks) {
+        const float d = f16_bits_to_f32(dsc[ks]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sv[i] = fmaf(d, acc[ks][i], sv[i]);
+      }
+      const int i_tok = (s * NW + wave) * kGroupTok + qk_tok;
+      if (i_tok < nt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int h = 4 * qr_row + i;
+          const float x = sv[i] * qk_mult;
+          if (h < GC) sc[h * SP + i_tok] = x;
+          m_q[i] = fmaxf(m_q[i], x);
+        }
+      }
+      continue;
+    }
     const char* row = slot + qk_tok * RB;
     float acc[8];
 #pragma unroll
@@ -482,7 +604,7 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
     uint4 kk[PQ];
 #pragma unroll
     for (int i = 0; i < PQ; ++i) kk[i] = ld16(row + (((qr_row * PQ + i) ^ (qk_tok & F::kSwz)) << 4));
-    if constexpr (!kQ8) {
+    {
       Unroll<0, PQ>::run([&](auto ic) {
         constexpr int i = decltype(ic)::value;
         constexpr int w0 = 4 * i;  // first q word of the piece (mod 16: lane; / 16: VGPR)
@@ -491,35 +613,6 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
         for (int g = 0; g < 8; ++g) qi[g] = qv[g < GC ? g : 0][w0 / 16];
         qk_words<DT, GC, w0 % 16>(acc, qi, kk[i].x, kk[i].y, kk[i].z, kk[i].w);
       });
-    } else {
-      // Each 32-group of the quarter (two pieces) has its own accumulators,
-      // scaled by the group's f32(d) once summed.
-      constexpr int NG8 = D / 128;  // 32-groups per quarter
-      float accg[NG8][8];
-#pragma unroll
-      for (int u = 0; u < NG8; ++u)
-#pragma unroll
-        for (int g = 0; g < 8; ++g) accg[u][g] = 0.0f;
-      Unroll<0, PQ>::run([&](auto ic) {
-        constexpr int i = decltype(ic)::value;  // piece: 16 int8 = q VGPR i, lanes 0..15
-        uint32_t qi[8];
-#pragma unroll
-        for (int g = 0; g < 8; ++g) qi[g] = qv[g < GC ? g : 0][i];
-        const uint32_t kw[4] = {kk[i].x, kk[i].y, kk[i].z, kk[i].w};
-        Unroll<0, 4>::run([&](auto jc) {
-          constexpr int j = decltype(jc)::value;
-          qk_words<DT, GC, 4 * j>(accg[i / 2], qi, i8_f32<0>(kw[j]), i8_f32<1>(kw[j]), i8_f32<2>(kw[j]),
-                                  i8_f32<3>(kw[j]));
-        });
-      });
-      asm volatile("s_nop 1" ::: "memory");
-      const char* srow = slot + GB + qk_tok * F::kScaleRow + qr_row * NG8 * 2;
-#pragma unroll
-      for (int u = 0; u < NG8; ++u) {
-        const float d = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(srow + 2 * u));
-#pragma unroll
-        for (int g = 0; g < 8; ++g) acc[g] = fmaf(d, accg[u][g], acc[g]);
-      }
     }
     // v_permlane*_swap must not read the accumulators within a few wait
     // states of the asm that wrote them.
@@ -543,11 +636,20 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
       m_b = fmaxf(m_b, s_b);
     }
   }
-  m_a = group_max<16>(m_a);
-  m_b = group_max<16>(m_b);
-  if (qk_tok == 0) {
-    s_mx[wave * 8 + h_a] = m_a;
-    s_mx[wave * 8 + 4 + h_a] = m_b;
+  if constexpr (kQ8) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) m_q[i] = group_max<16>(m_q[i]);
+    if (qk_tok == 0 && qr_row < 2) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s_mx[wave * 8 + 4 * qr_row + i] = m_q[i];
+    }
+  } else {
+    m_a = group_max<16>(m_a);
+    m_b = group_max<16>(m_b);
+    if (qk_tok == 0) {
+      s_mx[wave * 8 + h_a] = m_a;
+      s_mx[wave * 8 + 4 + h_a] = m_b;
+    }
   }
   lds_barrier();
 
@@ -598,7 +700,90 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
   for (int x = 0; x < DPV; ++x)
 #pragma unroll
     for (int g = 0; g < 8; ++g) acc2[x][g] = 0.0f;
-  for (int s = ns; s < S; ++s) {
+  // Q8_0: P.V on v_mfma_f32_16x16x16_bf16, per 32-group G of the head dim
+  // O[h][32 G + 2 n + c] += sum_t (p[h][t] f32(d[t][G])) qs[t][32 G + 2 n + c]
+  // (tile c = 0, 1; column n).  A = p d in fp32, split exactly into three bf16
+  // parts; B = qs widened exactly to bf16.  Lane (kq, hm) = (lane / 16,
+  // lane % 16) holds A[head hm][tokens 4 kq + j] and B[tokens 4 kq + j][column
+  // hm] (the MFMA's k index is j + 4 kq in both), and ends holding
+  // O[4 kq + i][column hm] of every tile.
+  v4f o8[kQ8 ? NK : 1][2];
+  if constexpr (kQ8) {
+    const int hm = lane & 15, kq = qr_row;
+#pragma unroll
+    for (int g = 0; g < NK; ++g) o8[g][0] = o8[g][1] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    float m_h = -INFINITY;
+    if (hm < GC) {
+#pragma unroll
+      for (int w = 0; w < NW; ++w) m_h = fmaxf(m_h, s_mx[w * 8 + hm]);
+    }
+    const bool none_h = m_h == -INFINITY;  // every key skipped, or a padding row
+    const float* const sc_h = sc + (hm < GC ? hm : 0) * SP + 4 * kq;
+    for (int s = ns; s < S; ++s) {
+      wait_item(s);
+      if (s + R - 1 < S) issue(s + R - 1);
+      const int gi = s - ns;
+      const int tb = (gi * NW + wave) * kGroupTok;
+      char* const slot = my_ring + (s % R) * SLOT;
+      if (tb + kGroupTok > nt) {
+        // Rows past the partition hold a stand-in row: each lane zeroes the
+        // bytes its own loads brought (this wave's LDS ops stay in order).
+#pragma unroll
+        for (int j = 0; j < NI; ++j) {
+          const int o = 1024 * j + 16 * lane;
+          if (tb + o / RB >= nt) *reinterpret_cast<uint4*>(slot + o) = make_uint4(0u, 0u, 0u, 0u);
+        }
+        if (s_lane && tb + s_row >= nt) *reinterpret_cast<uint32_t*>(slot + GB + 4 * lane) = 0u;
+      }
+      const float4 sv = *reinterpret_cast<const float4*>(sc_h + tb);
+      const float sj[4] = {sv.x, sv.y, sv.z, sv.w};
+      float pj[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        pj[j] = (tb + 4 * kq + j < nt && !none_h) ? __builtin_amdgcn_exp2f(sj[j] - m_h) : 0.0f;
+      lsum += (pj[0] + pj[1]) + (pj[2] + pj[3]);
+      const char* const vrow = slot + (4 * kq) * RB + 2 * hm;
+      // The scale rows of the lane's four tokens, NK fp16 each.
+      const char* const srow = slot + GB + (4 * kq) * F::kScaleRow;
+      uint32_t dw[4][NK / 2];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if constexpr (NK == 8) {
+          const uint4 t = *reinterpret_cast<const uint4*>(srow + j * F::kScaleRow);
+          dw[j][0] = t.x, dw[j][1] = t.y, dw[j][2] = t.z, dw[j][3] = t.w;
+        } else {
+          const uint2 t = *reinterpret_cast<const uint2*>(srow + j * F::kScaleRow);
+          dw[j][0] = t.x, dw[j][1] = t.y;
+        }
+      }
+      Unroll<0, NK>::run([&](auto gc) {
+        constexpr int G = decltype(gc)::value;
+        float x[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)  // p * d, one v_fma_mix_f32 each
+          x[j] = fmaf(pj[j], f16_bits_to_f32(G & 1 ? dw[j][G / 2] >> 16 : dw[j][G / 2] & 0xFFFFu), 0.0f);
+        uint2 ah, am, al;
+        split3_bf16(x[0], x[1], ah.x, am.x, al.x);
+        split3_bf16(x[2], x[3], ah.y, am.y, al.y);
+        uint32_t w[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) w[j] = *reinterpret_cast<const uint16_t*>(vrow + j * RB + 32 * G);
+        auto pair = [](uint32_t f0, uint32_t f1) { return __builtin_amdgcn_perm(f1, f0, 0x07060302u); };
+        const uint2 b0 = make_uint2(pair(i8_f32<0>(w[0]), i8_f32<0>(w[1])), pair(i8_f32<0>(w[2]), i8_f32<0>(w[3])));
+        const uint2 b1 = make_uint2(pair(i8_f32<1>(w[0]), i8_f32<1>(w[1])), pair(i8_f32<1>(w[2]), i8_f32<1>(w[3])));
+        o8[G][0] = mfma16k16(ah, b0, o8[G][0]);
+        o8[G][1] = mfma16k16(ah, b1, o8[G][1]);
+        o8[G][0] = mfma16k16(am, b0, o8[G][0]);
+        o8[G][1] = mfma16k16(am, b1, o8[G][1]);
+        o8[G][0] = mfma16k16(al, b0, o8[G][0]);
+        o8[G][1] = mfma16k16(al, b1, o8[G][1]);
+      });
+    }
+    // Sum over the four token rows kq of head hm.
+    lsum += __shfl_xor(lsum, 16);
+    lsum += __shfl_xor(lsum, 32);
+  }
+  for (int s = kQ8 ? S : ns; s < S; ++s) {
     wait_item(s);
     if (s + R - 1 < S) issue(s + R - 1);
     const int gi = s - ns;
@@ -687,15 +872,32 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
   }
 
   // ---------------- across the waves, in a fixed order -----------------------
-  lsum = group_sum<8>(lsum);  // the 8 lanes of head h_l
-  if (k_l == 0) s_l[wave * 8 + h_l] = lsum;
+  if constexpr (kQ8) {
+    if (lane < 8) s_l[wave * 8 + lane] = lsum;
+  } else {
+    lsum = group_sum<8>(lsum);  // the 8 lanes of head h_l
+    if (k_l == 0) s_l[wave * 8 + h_l] = lsum;
+  }
   lds_barrier();  // every wave is done with its ring (its last wait was vmcnt(0))
   float* const red = reinterpret_cast<float*>(smem);  // [NW][GC][D]
+  if constexpr (kQ8) {
+    const int hm = lane & 15;
 #pragma unroll
-  for (int g = 0; g < GC; ++g) {
-    float* dst = &red[(wave * GC + g) * D + DPV * lane];
-    if constexpr (DPV == 2) *reinterpret_cast<float2*>(dst) = make_float2(acc2[0][g], acc2[1][g]);
-    else *reinterpret_cast<float4*>(dst) = make_float4(acc2[0][g], acc2[1][g], acc2[2][g], acc2[3][g]);
+    for (int i = 0; i < 4; ++i) {
+      const int h = 4 * qr_row + i;
+      if (h < GC) {
+#pragma unroll
+        for (int g = 0; g < NK; ++g)
+          *reinterpret_cast<float2*>(&red[(wave * GC + h) * D + 32 * g + 2 * hm]) = make_float2(o8[g][0][i], o8[g][1][i]);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int g = 0; g < GC; ++g) {
+      float* dst = &red[(wave * GC + g) * D + DPV * lane];
+      if constexpr (DPV == 2) *reinterpret_cast<float2*>(dst) = make_float2(acc2[0][g], acc2[1][g]);
+      else *reinterpret_cast<float4*>(dst) = make_float4(acc2[0][g], acc2[1][g], acc2[2][g], acc2[3][g]);
+    }
   }
   lds_barrier();
   const int64_t part_row = (int64_t(b) * a.n_heads + head0) * a.max_parts + part;
