@@ -151,6 +151,23 @@ def test_q8_0_decode_d256():
         assert_close(got, want, *TOL[orc.Q8_0], what=f"q8_0 P={partition}")
 
 
+@pytest.mark.parametrize("D", [128, 256])
+def test_q8_0_group_sizes_and_windows(D):
+    """Q8_0 (products on MFMA) at every heads-per-workgroup count 1..8 (the
+    tiles' padding rows and the second row of four heads), contexts that end
+    inside a 16-token group and inside a page, window start positions, and two
+    partition sizes; fp32 tolerance against the oracle."""
+    bs = 32 if D == 256 else 16
+    ctx = [1, 17, 100, 333, 0]
+    start = np.array([0, 5, 37, 300, 0], np.int32)
+    for hq, hkv in ((1, 1), (2, 1), (6, 2), (4, 1), (10, 2), (18, 3), (21, 3), (8, 1)):
+        dev, ref, tables, ctx_a, q, qdt = _build(orc.Q8_0, hq, hkv, D, bs, ctx, seed=40 + hq)
+        for partition in (64, 256):
+            got, want = _run(dev, ref, tables, ctx_a, q, qdt, hq, start=start, partition=partition)
+            assert_close(got, want, *TOL[orc.Q8_0], what=f"q8_0 D={D} hq={hq} hkv={hkv} P={partition}")
+        assert np.all(got[-1] == 0)
+
+
 def test_bf16_d256_and_group_sizes():
     for hq, hkv in ((3, 1), (10, 2), (12, 12)):
         dev, ref, tables, ctx, q, qdt = _build(orc.BF16, hq, hkv, 256, 16, [333, 1029], seed=8)
