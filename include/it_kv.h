@@ -37,12 +37,15 @@ extern "C" {
 /* ---- dtype codes: QuantType (src/types.rs:106-144) ---------------------- */
 #define IT_F32 0
 #define IT_F16 1
+#define IT_Q4_0 2
 #define IT_Q8_0 8
 #define IT_BF16 30
 
 #define IT_BLOCK_SIZE 16        /* src/memory/paged.rs:9, default page size */
 #define IT_QK8_0 32             /* src/types.rs:11 */
 #define IT_BLOCK_Q8_0_BYTES 34  /* sizeof(BlockQ8_0), src/types.rs:34-41,250 */
+#define IT_QK4_0 32             /* src/types.rs:7 */
+#define IT_BLOCK_Q4_0_BYTES 18  /* sizeof(BlockQ4_0), src/types.rs:15-22 */
 
 /* ---- operator ids for it_supports (Backend::supports_op/_quant,
  *      src/backend.rs:184-186) ------------------------------------------- */
@@ -142,6 +145,9 @@ int32_t it_kv_manager_tables(const it_kv_manager* mgr, int32_t* tables, int32_t 
 /*   F32/F16/BF16 page: [block_size][head_dim] elements.                     */
 /*   Q8_0 page: int8 qs[block_size][head_dim], then fp16 d[block_size]       */
 /*   [head_dim/32] (structure of arrays of BlockQ8_0, src/types.rs:34-41).   */
+/*   Q4_0 page: u8 qs[block_size][head_dim/2] (each 32-group's 16 bytes as   */
+/*   in BlockQ4_0: low nibble = element j, high = element j+16), then fp16   */
+/*   d[block_size][head_dim/32] (src/types.rs:15-22).                        */
 /* ======================================================================== */
 typedef struct it_kv_cache it_kv_cache;
 
@@ -180,7 +186,9 @@ int32_t it_kv_cache_check(it_kv_cache* cache, void* stream);
  *   slot_mapping: int64[n_tokens], device; slot < 0 = padding, skipped.
  * F32/F16/BF16 caches take src_dtype == cache dtype (bit copy).  A Q8_0
  * cache takes F32 and quantises each 32-group exactly as
- * quantize_row_q8_0 (src/backend/arm/quant.rs:149-183). */
+ * quantize_row_q8_0 (src/backend/arm/quant.rs:149-183).  A Q4_0 cache takes
+ * F32 and quantises as ggml's quantize_row_q4_0_ref (the reference has the
+ * block and its dequantisation, vec_dot.rs:425-440, but no quantiser). */
 int32_t it_kv_append(it_kv_cache* cache, const void* k, const void* v, int32_t src_dtype,
                      const int64_t* slot_mapping, int32_t n_tokens, void* stream);
 
@@ -198,7 +206,8 @@ int32_t it_kv_append(it_kv_cache* cache, const void* k, const void* v, int32_t s
  *   q_out: [n_tokens][n_heads][head_dim] of q_out_dtype: F32, or the cache
  *          dtype for BF16/F16 caches (round to nearest even)
  * F32 caches store the rotated fp32 values; BF16/F16 caches round them to
- * nearest even; Q8_0 caches quantise them as quantize_row_q8_0. */
+ * nearest even; Q8_0 caches quantise them as quantize_row_q8_0.  (Q4_0
+ * caches: IT_NOT_IMPLEMENTED.) */
 typedef struct it_rope_table it_rope_table;
 /* n_dims: a multiple of 4 up to 4096; positions [0, max_pos); device memory
  * max_pos * n_dims * 4 bytes. */
@@ -218,7 +227,8 @@ int32_t it_kv_append_rope(it_kv_cache* cache, const it_rope_table* rope, const f
  *   max_tokens: upper bound of ctx_lens[b] - start_pos[b] (sizes the grid)
  * Output for sequence b: [n_kv_heads][ctx_b - start_b][head_dim] at token
  * offset cu_out[b] (element offset cu_out[b]*n_kv_heads*head_dim).  A Q8_0
- * cache writes packed 34-byte BlockQ8_0 records, head_dim/32 per row. */
+ * cache writes packed 34-byte BlockQ8_0 records, head_dim/32 per row; a Q4_0
+ * cache 18-byte BlockQ4_0 records. */
 int32_t it_kv_gather(const it_kv_cache* cache, const int32_t* block_tables, int32_t max_blocks,
                      const int32_t* ctx_lens, const int32_t* start_pos, const int64_t* cu_out,
                      int32_t n_seqs, int32_t max_tokens, void* k_out, void* v_out, void* stream);
@@ -253,7 +263,7 @@ size_t it_paged_decode_workspace(int32_t n_seqs, int32_t n_heads, int32_t head_d
  * and query head h the result equals flash_attn_f32 (flash_attn.rs:6-72)
  * over keys start_b..ctx_b-1 of KV head h*Hkv/Hq (forward.rs:231-254),
  * within fp32 tolerance.
- *   q: [n_seqs][n_heads][head_dim]; q_dtype F32 (F32 and Q8_0 caches),
+ *   q: [n_seqs][n_heads][head_dim]; q_dtype F32 (F32, Q8_0, Q4_0 caches),
  *      BF16 (BF16 cache) or F16 (F16 cache)
  *   block_tables/ctx_lens/start_pos: as it_kv_gather
  *   max_tokens: upper bound of ctx_b - start_b

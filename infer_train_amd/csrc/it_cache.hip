@@ -1,5 +1,5 @@
 // it_cache.hip -- the paged KV cache on gfx950: pool allocation, slot-mapped
-// append (bit copy or Q8_0 quantise), block-table gather, evict (page clear)
+// append (bit copy, Q8_0 or Q4_0 quantise), block-table gather, evict (page clear)
 // and copy-on-write page copy.
 //
 // All of these are HBM-bound data movement.  Each lane moves one 16-byte
@@ -112,6 +112,82 @@ __global__ __launch_bounds__(kThreads) void kv_append_q8_0(
 }
 
 // ---------------------------------------------------------------------------
+// Append with Q4_0 quantisation.  The reference carries the block
+// (types.rs:15-22) and its dequantisation (vec_dot.rs:425-440) but no
+// quantiser; this is ggml's quantize_row_q4_0_ref as its x86 build computes
+// it: max = the first element of largest magnitude (strict <, NaN never
+// wins), d = max / -8, id = d ? 1/d : 0, nibble = min(15, (int8_t)(x * id +
+// 8.5f)) with the product and the sum rounded separately and cvttss2si's 0
+// for NaN / out-of-range; byte j = nibble j | nibble (j + 16) << 4.
+// Eight lanes own one 32-element group, four floats each; lanes 0-3 hold
+// elements 0-15 (low nibbles), lanes 4-7 elements 16-31 (high nibbles).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t q4_byte(float x, float id) {
+  float r;
+  asm("v_mul_f32 %0, %1, %2" : "=v"(r) : "v"(x), "v"(id));  // no FMA with the add
+  r += 8.5f;
+  if (!(fabsf(r) < 2147483648.0f)) return 0u;
+  const int32_t q = min(int32_t(int8_t(int32_t(r))), 15);
+  return uint32_t(q) & 0xFFu;
+}
+
+__global__ __launch_bounds__(kThreads) void kv_append_q4_0(
+    const float4* __restrict__ k, const float4* __restrict__ v, char* __restrict__ kpool,
+    char* __restrict__ vpool, const int64_t* __restrict__ slots, int64_t total, int hkv, int d,
+    int log2_bs, int64_t page_bytes, int64_t n_slots, uint32_t* err) {
+  const int64_t gid = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  const bool is_v = blockIdx.y != 0;
+  const bool live = gid < total;
+  const float4 x = live ? (is_v ? v[gid] : k[gid]) : make_float4(0.f, 0.f, 0.f, 0.f);
+  const int l8 = int(gid & 7);
+  // (|max|, element index, max) of the lane, then of the group: larger
+  // magnitude wins, equal magnitudes go to the lower index; "none" is (0, 32).
+  float am = 0.0f, mx = 0.0f;
+  int im = 32;
+  const float xs[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float a = fabsf(xs[e]);
+    if (am < a) am = a, mx = xs[e], im = 4 * l8 + e;
+  }
+  auto step = [&](auto ctrl) {
+    constexpr int C = decltype(ctrl)::value;
+    const float a2 = dpp_f<C>(am), m2 = dpp_f<C>(mx);
+    const int i2 = __builtin_amdgcn_mov_dpp(im, C, 0xF, 0xF, true);
+    if (a2 > am || (a2 == am && i2 < im)) am = a2, mx = m2, im = i2;
+  };
+  step(std::integral_constant<int, kDppQuadXor1>{});
+  step(std::integral_constant<int, kDppQuadXor2>{});
+  step(std::integral_constant<int, kDppHalfMirror>{});
+  const float dq = mx / -8.0f;
+  const float id = dq != 0.0f ? 1.0f / dq : 0.0f;
+  const uint32_t mine = q4_byte(x.x, id) | (q4_byte(x.y, id) << 8) | (q4_byte(x.z, id) << 16) |
+                        (q4_byte(x.w, id) << 24);
+  // Lane i < 4 of the group takes lane i + 4's bytes (DPP row_shl:4).
+  const uint32_t partner = uint32_t(__builtin_amdgcn_mov_dpp(int(mine), 0x104, 0xF, 0xF, true));
+  if (!live || l8 >= 4) return;
+  const int vecs_per_row = d >> 2;
+  const int cv = int(gid % vecs_per_row);  // vector index in the row
+  const int64_t th = gid / vecs_per_row;
+  const int h = int(th % hkv);
+  const int64_t t = th / hkv;
+  const int64_t slot = slots[t];
+  if (slot < 0) return;
+  if (slot >= n_slots) {
+    if (cv == 0 && h == 0) atomicOr(err, kErrSlot);
+    return;
+  }
+  const int64_t blk = slot >> log2_bs;
+  const int64_t off = slot & ((int64_t(1) << log2_bs) - 1);
+  const int64_t bs = int64_t(1) << log2_bs;
+  const int g = cv >> 3;
+  char* page = (is_v ? vpool : kpool) + (blk * hkv + h) * page_bytes;
+  *reinterpret_cast<uint32_t*>(page + off * (d >> 1) + g * 16 + l8 * 4) = mine | ((partner & 0x0F0F0F0Fu) << 4);
+  if (l8 == 0)
+    *reinterpret_cast<uint16_t*>(page + bs * (d >> 1) + (off * (d >> 5) + g) * 2) = uint16_t(f32_to_f16_bits(dq));
+}
+
+// ---------------------------------------------------------------------------
 // Gather.  grid.y = sequence; lane = one 16-byte vector of one output row.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(kThreads) void kv_gather_vec(
@@ -195,6 +271,53 @@ __global__ __launch_bounds__(kThreads) void kv_gather_q8_0(
   }
 }
 
+// Q4_0 gather: lane = one 32-element group, written as a packed 18-byte
+// BlockQ4_0 record {u16 d; u8 qs[16]} (types.rs:15-22).
+__global__ __launch_bounds__(kThreads) void kv_gather_q4_0(
+    const char* __restrict__ kpool, const char* __restrict__ vpool, const int32_t* __restrict__ bt,
+    int max_blocks, const int32_t* __restrict__ ctx_lens, const int32_t* __restrict__ start_pos,
+    const int64_t* __restrict__ cu_out, int hkv, int d, int log2_bs, int64_t page_bytes,
+    int64_t num_blocks, char* __restrict__ kout, char* __restrict__ vout, uint32_t* err) {
+  const int b = blockIdx.y;
+  const int st = start_pos ? start_pos[b] : 0;
+  const int n = ctx_lens[b] - st;
+  if (n <= 0 || st < 0) return;
+  const int ng = d >> 5;
+  const int64_t gid = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  if (gid >= int64_t(hkv) * n * ng) return;
+  const int g = int(gid % ng);
+  const int64_t r = gid / ng;
+  const int i = int(r % n);
+  const int h = int(r / n);
+  const int pos = st + i;
+  const int lb = pos >> log2_bs;
+  if (lb >= max_blocks) {
+    atomicOr(err, kErrTable);
+    return;
+  }
+  const int blk = bt[int64_t(b) * max_blocks + lb];
+  if (blk < 0 || blk >= num_blocks) {
+    atomicOr(err, kErrBlock);
+    return;
+  }
+  const int64_t bs = int64_t(1) << log2_bs;
+  const int64_t off = pos & (bs - 1);
+  const int64_t rec = ((cu_out[b] * hkv + int64_t(h) * n + i) * ng + g) * 18;
+  for (int which = 0; which < 2; ++which) {
+    const char* page = (which ? vpool : kpool) + (int64_t(blk) * hkv + h) * page_bytes;
+    const uint4 q = ld16(page + off * (d >> 1) + g * 16);
+    const uint16_t dd = *reinterpret_cast<const uint16_t*>(page + bs * (d >> 1) + (off * ng + g) * 2);
+    uint16_t* o = reinterpret_cast<uint16_t*>((which ? vout : kout) + rec);  // 2-byte aligned
+    o[0] = dd;
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      o[1 + 2 * j] = uint16_t(w[j] & 0xFFFFu);
+      o[2 + 2 * j] = uint16_t(w[j] >> 16);
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Evict (zero pages) and copy-on-write page copy.  grid.y = list entry.
 // ---------------------------------------------------------------------------
@@ -263,11 +386,12 @@ int32_t check_shape(int64_t num_blocks, int32_t block_size, int32_t n_kv_heads, 
                 (long long)num_blocks, n_kv_heads, head_dim);
   if (!is_pow2(block_size) || block_size > 1024)
     return fail(IT_NOT_IMPLEMENTED, "kv cache: block_size %d must be a power of two <= 1024", block_size);
-  if (dtype == IT_Q8_0) {
-    if (head_dim % IT_QK8_0) return fail(IT_INVALID_INPUT, "kv cache: Q8_0 needs head_dim %% 32 == 0");
-    if (block_size < 8) return fail(IT_NOT_IMPLEMENTED, "kv cache: Q8_0 needs block_size >= 8");
+  if (dtype == IT_Q8_0 || dtype == IT_Q4_0) {
+    if (head_dim % 32) return fail(IT_INVALID_INPUT, "kv cache: Q8_0/Q4_0 need head_dim %% 32 == 0");
+    if (block_size < 8) return fail(IT_NOT_IMPLEMENTED, "kv cache: Q8_0/Q4_0 need block_size >= 8");
   } else if (dtype_bytes(dtype) == 0) {
-    return fail(IT_NOT_IMPLEMENTED, "kv cache: dtype %d not supported (F32=0, F16=1, Q8_0=8, BF16=30)", dtype);
+    return fail(IT_NOT_IMPLEMENTED, "kv cache: dtype %d not supported (F32=0, F16=1, Q4_0=2, Q8_0=8, BF16=30)",
+                dtype);
   } else if ((head_dim * dtype_bytes(dtype)) % 16) {
     return fail(IT_NOT_IMPLEMENTED, "kv cache: head_dim*elem_bytes must be a multiple of 16");
   }
@@ -318,6 +442,7 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 extern "C" int64_t it_kv_page_bytes(int32_t block_size, int32_t head_dim, int32_t dtype) {
   if (block_size <= 0 || head_dim <= 0) return -1;
   if (dtype == IT_Q8_0) return int64_t(block_size) * head_dim + int64_t(block_size) * (head_dim / IT_QK8_0) * 2;
+  if (dtype == IT_Q4_0) return int64_t(block_size) * (head_dim / 2) + int64_t(block_size) * (head_dim / IT_QK4_0) * 2;
   int64_t e = dtype_bytes(dtype);
   return e ? int64_t(block_size) * head_dim * e : -1;
 }
@@ -406,19 +531,19 @@ extern "C" int32_t it_kv_append(it_kv_cache* c, const void* k, const void* v, in
   if (n_tokens < 0) return fail(IT_INVALID_INPUT, "it_kv_append: n_tokens %d < 0", n_tokens);
   if (n_tokens == 0) return IT_OK;
   if (!k || !v || !slots) return fail(IT_INVALID_INPUT, "it_kv_append: NULL tensor");
-  const int32_t want = c->dtype == IT_Q8_0 ? IT_F32 : c->dtype;
+  const int32_t want = (c->dtype == IT_Q8_0 || c->dtype == IT_Q4_0) ? IT_F32 : c->dtype;
   if (src_dtype != want)
     return fail(IT_NOT_IMPLEMENTED, "it_kv_append: cache dtype %d takes source dtype %d, got %d", c->dtype, want, src_dtype);
   if (!aligned16(k) || !aligned16(v)) return fail(IT_INVALID_INPUT, "it_kv_append: k/v must be 16-byte aligned");
   DeviceGuard g(c->device);
   hipStream_t s = (hipStream_t)stream;
   const int64_t n_slots = c->num_blocks << c->log2_bs;
-  if (c->dtype == IT_Q8_0) {
+  if (c->dtype == IT_Q8_0 || c->dtype == IT_Q4_0) {
     const int64_t total = int64_t(n_tokens) * c->n_kv_heads * (c->head_dim / 4);
     dim3 grid(unsigned(cdiv(total, kThreads)), 2);
-    hipLaunchKernelGGL(kv_append_q8_0, grid, dim3(kThreads), 0, s, (const float4*)k, (const float4*)v,
-                       (char*)c->k_pool, (char*)c->v_pool, slots, total, c->n_kv_heads, c->head_dim,
-                       c->log2_bs, c->page_bytes, n_slots, c->err_flag);
+    hipLaunchKernelGGL(c->dtype == IT_Q8_0 ? kv_append_q8_0 : kv_append_q4_0, grid, dim3(kThreads), 0, s,
+                       (const float4*)k, (const float4*)v, (char*)c->k_pool, (char*)c->v_pool, slots, total,
+                       c->n_kv_heads, c->head_dim, c->log2_bs, c->page_bytes, n_slots, c->err_flag);
   } else {
     const int row_vecs = int(c->head_dim * dtype_bytes(c->dtype) / 16);
     const int64_t total = int64_t(n_tokens) * c->n_kv_heads * row_vecs;
@@ -442,10 +567,11 @@ extern "C" int32_t it_kv_gather(const it_kv_cache* c, const int32_t* bt, int32_t
   if (n_seqs > 65535) return fail(IT_NOT_IMPLEMENTED, "it_kv_gather: n_seqs %d > 65535", n_seqs);
   DeviceGuard g(c->device);
   hipStream_t s = (hipStream_t)stream;
-  if (c->dtype == IT_Q8_0) {
+  if (c->dtype == IT_Q8_0 || c->dtype == IT_Q4_0) {
     const int64_t per_seq = int64_t(c->n_kv_heads) * max_tokens * (c->head_dim / 32);
     dim3 grid(unsigned(cdiv(per_seq, kThreads)), unsigned(n_seqs));
-    hipLaunchKernelGGL(kv_gather_q8_0, grid, dim3(kThreads), 0, s, (const char*)c->k_pool, (const char*)c->v_pool,
+    hipLaunchKernelGGL(c->dtype == IT_Q8_0 ? kv_gather_q8_0 : kv_gather_q4_0, grid, dim3(kThreads), 0, s,
+                       (const char*)c->k_pool, (const char*)c->v_pool,
                        bt, max_blocks, ctx_lens, start_pos, cu_out, c->n_kv_heads, c->head_dim, c->log2_bs,
                        c->page_bytes, c->num_blocks, (char*)k_out, (char*)v_out, c->err_flag);
   } else {
@@ -506,7 +632,7 @@ extern "C" int32_t it_kv_copy_blocks(it_kv_cache* c, const int32_t* src, const i
 }
 
 extern "C" int32_t it_supports(int32_t op, int32_t dtype) {
-  const bool kv = dtype == IT_F32 || dtype == IT_F16 || dtype == IT_BF16 || dtype == IT_Q8_0;
+  const bool kv = dtype == IT_F32 || dtype == IT_F16 || dtype == IT_BF16 || dtype == IT_Q8_0 || dtype == IT_Q4_0;
   switch (op) {
     case IT_OP_KV_APPEND:
     case IT_OP_KV_GATHER:

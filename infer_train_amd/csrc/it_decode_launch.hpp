@@ -66,4 +66,5 @@ hipError_t launch_decode_bf16(int d, int gc, const DecodeArgs& a, dim3 grid, hip
 hipError_t launch_decode_f16(int d, int gc, const DecodeArgs& a, dim3 grid, hipStream_t s);
 hipError_t launch_decode_f32(int d, int gc, const DecodeArgs& a, dim3 grid, hipStream_t s);
 hipError_t launch_decode_q8_0(int d, int gc, const DecodeArgs& a, dim3 grid, hipStream_t s);
+hipError_t launch_decode_q4_0(int d, int gc, const DecodeArgs& a, dim3 grid, hipStream_t s);
 }  // namespace itkv

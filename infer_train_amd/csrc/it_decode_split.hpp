@@ -27,7 +27,7 @@
 //       probability of token t (16-bit caches: of token pair t) comes from
 //       lane t of the row through row_newbcast:t; 16-bit caches v_perm
 //       (v_t[d], v_t+1[d]) pairs for v_dot2c.
-//  Q8_0 runs both products on MFMA, exactly: int8 widens to bf16 without
+//  Q8_0 and Q4_0 run both products on MFMA, exactly: int8 widens to bf16 without
 //       rounding, and the fp32 operand on the other side is split into three
 //       bf16 parts (hi + mid + lo = x), so every product is exact and only
 //       the fp32 accumulation rounds.  QK: v_mfma_f32_16x16x32_bf16 per
@@ -51,6 +51,10 @@
 // Q8_0 (BlockQ8_0, src/types.rs:34-41): a page is int8 qs[bs][D] then fp16
 // d[bs][D/32]; a key dot product is sum over 32-groups of f32(d) * sum q *
 // qs, and a value element is f32(d) * qs, exact in fp32 (gemv.rs:151-160).
+// Q4_0 (BlockQ4_0, src/types.rs:15-22): a page is u8 qs[bs][D/2], each
+// group's 16 bytes holding element j in the low nibble of byte j and
+// element j + 16 in the high nibble, then fp16 d[bs][D/32]; a value element
+// is f32(d) * (nibble - 8) (vec_dot.rs:425-440), exact in fp32.
 #pragma once
 #include <hip/hip_runtime.h>
 
@@ -67,14 +71,16 @@ template <int DT, int D>
 struct SplitFmt {
   static constexpr bool k16 = DT == IT_BF16 || DT == IT_F16;
   static constexpr bool kQ8 = DT == IT_Q8_0;
-  static constexpr int kElem = DT == IT_F32 ? 4 : (kQ8 ? 1 : 2);  // bytes per main-plane element
-  static constexpr int kRow = D * kElem;                          // main-plane bytes per token
+  static constexpr bool kQ4 = DT == IT_Q4_0;
+  static constexpr bool kQuant = kQ8 || kQ4;                       // MFMA products, fp16 group scales
+  static constexpr int kElem = DT == IT_F32 ? 4 : (kQuant ? 1 : 2);  // bytes per main-plane element
+  static constexpr int kRow = kQ4 ? D / 2 : D * kElem;            // main-plane bytes per token
   static constexpr int kGroup = kGroupTok * kRow;                 // main-plane bytes per group
   static constexpr int kDma = kGroup / 1024;                      // 16-byte-per-lane loads per group
-  static constexpr int kScaleRow = kQ8 ? D / 16 : 0;              // fp16 scales per token (bytes)
+  static constexpr int kScaleRow = kQuant ? D / 16 : 0;           // fp16 scales per token (bytes)
   static constexpr int kScaleGroup = kGroupTok * kScaleRow;       // 128 or 256 B (one dword load)
   static constexpr int kSlot = kGroup + kScaleGroup;
-  static constexpr int kLoads = kDma + (kQ8 ? 1 : 0);             // vmcnt units per group
+  static constexpr int kLoads = kDma + (kQuant ? 1 : 0);          // vmcnt units per group
   static constexpr int kPieces = D / 4 * kElem / 16;              // 16-byte pieces per lane in QK
   static constexpr int kRowPieces = kRow / 16;
   static constexpr int kSwz = (kRowPieces < 16 ? kRowPieces : 16) - 1;  // piece swizzle mask
@@ -94,6 +100,7 @@ inline int split_slot_bytes(int32_t dt, int d) {
     case IT_BF16: return split_slot_bytes<IT_BF16>(d);
     case IT_F16: return split_slot_bytes<IT_F16>(d);
     case IT_F32: return split_slot_bytes<IT_F32>(d);
+    case IT_Q4_0: return split_slot_bytes<IT_Q4_0>(d);
     default: return split_slot_bytes<IT_Q8_0>(d);
   }
 }
@@ -274,6 +281,17 @@ __device__ __forceinline__ uint4 i8x8_bf16(uint2 w) {
   return make_uint4(pair(i8_f32<0>(w.x), i8_f32<1>(w.x)), pair(i8_f32<2>(w.x), i8_f32<3>(w.x)),
                     pair(i8_f32<0>(w.y), i8_f32<1>(w.y)), pair(i8_f32<2>(w.y), i8_f32<3>(w.y)));
 }
+// Four Q4_0 bytes (nibble n at element j, nibble m at element j + 16) as
+// eight bf16 values 16 (n - 8), then 16 (m - 8), exactly: n ^ 8 read as a
+// signed nibble is n - 8, and moved to the top of its byte it sign-extends
+// through the same SDWA convert as an int8.  The factor 16 goes into d.
+__device__ __forceinline__ uint4 nib8_bf16(uint32_t w) {
+  const uint32_t x = w ^ 0x88888888u;
+  const uint32_t lo = (x << 4) & 0xF0F0F0F0u, hi = x & 0xF0F0F0F0u;
+  auto pair = [](uint32_t f0, uint32_t f1) { return __builtin_amdgcn_perm(f1, f0, 0x07060302u); };
+  return make_uint4(pair(i8_f32<0>(lo), i8_f32<1>(lo)), pair(i8_f32<2>(lo), i8_f32<3>(lo)),
+                    pair(i8_f32<0>(hi), i8_f32<1>(hi)), pair(i8_f32<2>(hi), i8_f32<3>(hi)));
+}
 // x = hi + mid + lo exactly, each part a bf16 (round to nearest even): the
 // three parts carry the 24 significant bits of an fp32.  Two values per
 // packed word (lo element first).  No inline asm here: the compiler's hazard
@@ -346,7 +364,7 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
   using F = SplitFmt<DT, D>;
   constexpr int RB = F::kRow, GB = F::kGroup, SLOT = F::kSlot, NI = F::kDma, NL = F::kLoads;
   constexpr int PQ = F::kPieces, NQ = F::kQRegs, DPV = F::kDpv;
-  constexpr bool k16 = F::k16, kQ8 = F::kQ8;
+  constexpr bool k16 = F::k16, kQ = F::kQuant, kQ4 = F::kQ4;
   constexpr int NT = 64 * NW;  // threads
   static_assert(GC >= 1 && GC <= 8, "1..8 heads per workgroup");
   static_assert(NW == 2 || NW == 4, "2 or 4 waves");
@@ -409,12 +427,14 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
   // quarter r of the head dimension (packed 16-bit pairs, or fp32).
   const int qr_row = lane >> 4, qk_tok = lane & 15;
   uint32_t qv[GC][NQ];
-  // Q8_0: q is the A operand of v_mfma_f32_16x16x32_bf16 instead, lane
-  // (kh, h) = (lane / 16, lane % 16) holding dims 32 ks + 8 kh .. + 8 of head
-  // h (zero for h >= GC), split exactly into three bf16 parts.
-  constexpr int NK = kQ8 ? D / 32 : 1;  // 32-groups (MFMA k-steps) per row
+  // Q8_0 / Q4_0: q is the A operand of v_mfma_f32_16x16x32_bf16 instead,
+  // lane (kh, h) = (lane / 16, lane % 16) holding eight dims of group ks of
+  // head h (zero for h >= GC), split exactly into three bf16 parts: Q8_0
+  // dims 32 ks + 8 kh .. + 8; Q4_0 dims 32 ks + 4 kh .. + 4 and 32 ks + 16 +
+  // 4 kh .. + 4 (the low and high nibbles of bytes 4 kh .. + 4 of the group).
+  constexpr int NK = kQ ? D / 32 : 1;  // 32-groups (MFMA k-steps) per row
   uint4 qa[3][NK];
-  if constexpr (!kQ8) {
+  if constexpr (!kQ) {
     const uint32_t* qp = static_cast<const uint32_t*>(a.q) +
                          (int64_t(b) * a.n_heads + head0) * (k16 ? D / 2 : D) + qr_row * (k16 ? D / 8 : D / 4) +
                          qk_tok;
@@ -432,11 +452,11 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
   } else {
     const int hq = lane & 15;
     const float* qp = static_cast<const float*>(a.q) + (int64_t(b) * a.n_heads + head0 + (hq < GC ? hq : 0)) * D +
-                      8 * qr_row;
+                      (kQ4 ? 4 : 8) * qr_row;
 #pragma unroll
     for (int ks = 0; ks < NK; ++ks) {
       float4 x0 = *reinterpret_cast<const float4*>(qp + 32 * ks);
-      float4 x1 = *reinterpret_cast<const float4*>(qp + 32 * ks + 4);
+      float4 x1 = *reinterpret_cast<const float4*>(qp + 32 * ks + (kQ4 ? 16 : 4));
       if (hq >= GC) x0 = x1 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
       split3_bf16(x0.x, x0.y, qa[0][ks].x, qa[1][ks].x, qa[2][ks].x);
       split3_bf16(x0.z, x0.w, qa[0][ks].y, qa[1][ks].y, qa[2][ks].y);
@@ -475,7 +495,7 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
     lane_off_k[j] = tt * RB + ((ps ^ (tt & F::kSwz)) << 4);
     lane_off_v[j] = tt * RB + (ps << 4);
   }
-  const int s_row = kQ8 ? (4 * lane) / (F::kScaleRow > 0 ? F::kScaleRow : 1) : 0;  // scale row of this lane
+  const int s_row = kQ ? (4 * lane) / (F::kScaleRow > 0 ? F::kScaleRow : 1) : 0;  // scale row of this lane
   const bool s_lane = 4 * lane < F::kScaleGroup;
   auto issue = [&](int s) {
     const bool is_v = s >= ns;
@@ -497,10 +517,10 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
         if (!full && tb + lane_row[j] >= nt) off -= lane_row[j] * RB;
         dma_b128(base + off, __builtin_amdgcn_readfirstlane(m0 + 1024u * j));
       }
-      if constexpr (kQ8) {
+      if constexpr (kQ) {
         int row = s_row;
         if (!full && tb + row >= nt) row = 0;
-        const char* g = pbase + uint32_t(bs * D + (in_page + row) * F::kScaleRow + (4 * lane) % F::kScaleRow);
+        const char* g = pbase + uint32_t(bs * RB + (in_page + row) * F::kScaleRow + (4 * lane) % F::kScaleRow);
         if (s_lane) dma_b32(g, __builtin_amdgcn_readfirstlane(m0 + uint32_t(GB)));
       }
     } else {
@@ -515,13 +535,13 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
         const char* g = pool + (uint64_t(page) * page_bytes + uint32_t((t & bs_mask) * RB + off));
         dma_b128(g, __builtin_amdgcn_readfirstlane(m0 + 1024u * j));
       }
-      if constexpr (kQ8) {
+      if constexpr (kQ) {
         int tr = tb + s_row;
         if (tr >= nt) tr = tb;
         const int t = tok0 + tr;
         const uint32_t page = uint32_t(s_pages[(t >> a.log2_bs) - lb0]);
         const char* g = pool + (uint64_t(page) * page_bytes +
-                                uint32_t(bs * D + (t & bs_mask) * F::kScaleRow + (4 * lane) % F::kScaleRow));
+                                uint32_t(bs * RB + (t & bs_mask) * F::kScaleRow + (4 * lane) % F::kScaleRow));
         if (s_lane) dma_b32(g, __builtin_amdgcn_readfirstlane(m0 + uint32_t(GB)));
       }
     }
@@ -548,12 +568,13 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
     wait_item(s);
     if (s + R - 1 < S) issue(s + R - 1);
     const char* slot = my_ring + (s % R) * SLOT;
-    if constexpr (kQ8) {
+    if constexpr (kQ) {
       // Scores on MFMA: S[h][t] = sum over 32-groups ks of f32(d[t][ks]) *
       // (q[h] . qs[t]) over the group, the group dot product taken as three
       // exact bf16 x int8 passes (hi, mid, lo parts of q) into one fp32
       // accumulator.  Lane (kh, t) reads bytes 8 kh .. + 8 of group ks of
-      // token t and ends holding S[4 kh + i][t], i = 0..3.
+      // token t (Q4_0: bytes 4 kh .. + 4 of the group's 16, as 16 (n - 8))
+      // and ends holding S[4 kh + i][t], i = 0..3.
       const char* krow = slot + qk_tok * RB;
       uint16_t dsc[NK];
 #pragma unroll
@@ -564,15 +585,20 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
       uint2 kr[NK];
 #pragma unroll
       for (int ks = 0; ks < NK; ++ks) {
-        const int pc = (2 * ks + (qr_row >> 1)) ^ (qk_tok & F::kSwz);  // physical piece slot
-        kr[ks] = *reinterpret_cast<const uint2*>(krow + (pc << 4) + 8 * (qr_row & 1));
+        if constexpr (kQ4) {
+          const int pc = ks ^ (qk_tok & F::kSwz);  // a Q4_0 group is one 16-byte piece
+          kr[ks] = make_uint2(*reinterpret_cast<const uint32_t*>(krow + (pc << 4) + 4 * qr_row), 0u);
+        } else {
+          const int pc = (2 * ks + (qr_row >> 1)) ^ (qk_tok & F::kSwz);  // physical piece slot
+          kr[ks] = *reinterpret_cast<const uint2*>(krow + (pc << 4) + 8 * (qr_row & 1));
+        }
       }
       v4f acc[NK];
       uint4 kb[NK];
       Unroll<0, NK + 2>::run([&](auto kc) {
         constexpr int k = decltype(kc)::value;
         if constexpr (k < NK) {
-          kb[k] = i8x8_bf16(kr[k]);
+          kb[k] = kQ4 ? nib8_bf16(kr[k].x) : i8x8_bf16(kr[k]);
           acc[k] = mfma16(qa[0][k], kb[k], v4f{0.0f, 0.0f, 0.0f, 0.0f});
         }
         if constexpr (k >= 1 && k - 1 < NK) acc[k - 1] = mfma16(qa[1][k - 1], kb[k - 1], acc[k - 1]);
@@ -581,7 +607,7 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
       v4f sv = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int ks = 0; ks < NK; ++ks) {
-        const float d = f16_bits_to_f32(dsc[ks]);
+        const float d = f16_bits_to_f32(dsc[ks]) * (kQ4 ? 0.0625f : 1.0f);  // exact
 #pragma unroll
         for (int i = 0; i < 4; ++i) sv[i] = fmaf(d, acc[ks][i], sv[i]);
       }
@@ -636,7 +662,7 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
       m_b = fmaxf(m_b, s_b);
     }
   }
-  if constexpr (kQ8) {
+  if constexpr (kQ) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) m_q[i] = group_max<16>(m_q[i]);
     if (qk_tok == 0 && qr_row < 2) {
@@ -700,15 +726,17 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
   for (int x = 0; x < DPV; ++x)
 #pragma unroll
     for (int g = 0; g < 8; ++g) acc2[x][g] = 0.0f;
-  // Q8_0: P.V on v_mfma_f32_16x16x16_bf16, per 32-group G of the head dim
-  // O[h][32 G + 2 n + c] += sum_t (p[h][t] f32(d[t][G])) qs[t][32 G + 2 n + c]
-  // (tile c = 0, 1; column n).  A = p d in fp32, split exactly into three bf16
-  // parts; B = qs widened exactly to bf16.  Lane (kq, hm) = (lane / 16,
+  // Q8_0 / Q4_0: P.V on v_mfma_f32_16x16x16_bf16, per 32-group G of the head
+  // dim O[h][dim(G, c, n)] += sum_t (p[h][t] f32(d[t][G])) v[t][dim(G, c, n)]
+  // (tile c = 0, 1; column n; Q8_0 dim 32 G + 2 n + c from a 2-byte read,
+  // Q4_0 dim 32 G + 16 c + n, the two nibbles of byte n of the group).
+  // A = p d in fp32 (Q4_0: p d / 16), split exactly into three bf16 parts;
+  // B = qs (Q4_0: 16 (nibble - 8)) widened exactly to bf16.  Lane (kq, hm) = (lane / 16,
   // lane % 16) holds A[head hm][tokens 4 kq + j] and B[tokens 4 kq + j][column
   // hm] (the MFMA's k index is j + 4 kq in both), and ends holding
   // O[4 kq + i][column hm] of every tile.
-  v4f o8[kQ8 ? NK : 1][2];
-  if constexpr (kQ8) {
+  v4f o8[kQ ? NK : 1][2];
+  if constexpr (kQ) {
     const int hm = lane & 15, kq = qr_row;
 #pragma unroll
     for (int g = 0; g < NK; ++g) o8[g][0] = o8[g][1] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
@@ -742,7 +770,11 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
       for (int j = 0; j < 4; ++j)
         pj[j] = (tb + 4 * kq + j < nt && !none_h) ? __builtin_amdgcn_exp2f(sj[j] - m_h) : 0.0f;
       lsum += (pj[0] + pj[1]) + (pj[2] + pj[3]);
-      const char* const vrow = slot + (4 * kq) * RB + 2 * hm;
+      if constexpr (kQ4) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) pj[j] *= 0.0625f;  // exact; undoes B's factor 16
+      }
+      const char* const vrow = slot + (4 * kq) * RB + (kQ4 ? 1 : 2) * hm;
       // The scale rows of the lane's four tokens, NK fp16 each.
       const char* const srow = slot + GB + (4 * kq) * F::kScaleRow;
       uint32_t dw[4][NK / 2];
@@ -765,12 +797,22 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
         uint2 ah, am, al;
         split3_bf16(x[0], x[1], ah.x, am.x, al.x);
         split3_bf16(x[2], x[3], ah.y, am.y, al.y);
-        uint32_t w[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) w[j] = *reinterpret_cast<const uint16_t*>(vrow + j * RB + 32 * G);
         auto pair = [](uint32_t f0, uint32_t f1) { return __builtin_amdgcn_perm(f1, f0, 0x07060302u); };
-        const uint2 b0 = make_uint2(pair(i8_f32<0>(w[0]), i8_f32<0>(w[1])), pair(i8_f32<0>(w[2]), i8_f32<0>(w[3])));
-        const uint2 b1 = make_uint2(pair(i8_f32<1>(w[0]), i8_f32<1>(w[1])), pair(i8_f32<1>(w[2]), i8_f32<1>(w[3])));
+        uint2 b0, b1;
+        if constexpr (kQ4) {
+          uint32_t w = 0;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) w |= uint32_t(*reinterpret_cast<const uint8_t*>(vrow + j * RB + 16 * G)) << (8 * j);
+          const uint4 t = nib8_bf16(w);  // tokens 4 kq + j: low nibbles (tile 0), then high (tile 1)
+          b0 = make_uint2(t.x, t.y);
+          b1 = make_uint2(t.z, t.w);
+        } else {
+          uint32_t w[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) w[j] = *reinterpret_cast<const uint16_t*>(vrow + j * RB + 32 * G);
+          b0 = make_uint2(pair(i8_f32<0>(w[0]), i8_f32<0>(w[1])), pair(i8_f32<0>(w[2]), i8_f32<0>(w[3])));
+          b1 = make_uint2(pair(i8_f32<1>(w[0]), i8_f32<1>(w[1])), pair(i8_f32<1>(w[2]), i8_f32<1>(w[3])));
+        }
         o8[G][0] = mfma16k16(ah, b0, o8[G][0]);
         o8[G][1] = mfma16k16(ah, b1, o8[G][1]);
         o8[G][0] = mfma16k16(am, b0, o8[G][0]);
@@ -783,96 +825,77 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
     lsum += __shfl_xor(lsum, 16);
     lsum += __shfl_xor(lsum, 32);
   }
-  for (int s = kQ8 ? S : ns; s < S; ++s) {
-    wait_item(s);
-    if (s + R - 1 < S) issue(s + R - 1);
-    const int gi = s - ns;
-    const int tb = (gi * NW + wave) * kGroupTok;
-    char* const slot = my_ring + (s % R) * SLOT;
-    if (tb + kGroupTok > nt) {
-      // Rows past the partition hold a stand-in row: each lane zeroes the
-      // bytes its own loads brought (this wave's LDS ops stay in order).
+  if constexpr (!kQ) {
+    for (int s = ns; s < S; ++s) {
+      wait_item(s);
+      if (s + R - 1 < S) issue(s + R - 1);
+      const int gi = s - ns;
+      const int tb = (gi * NW + wave) * kGroupTok;
+      char* const slot = my_ring + (s % R) * SLOT;
+      if (tb + kGroupTok > nt) {
+        // Rows past the partition hold a stand-in row: each lane zeroes the
+        // bytes its own loads brought (this wave's LDS ops stay in order).
 #pragma unroll
-      for (int j = 0; j < NI; ++j) {
-        const int o = 1024 * j + 16 * lane;
-        if (tb + o / RB >= nt) *reinterpret_cast<uint4*>(slot + o) = make_uint4(0u, 0u, 0u, 0u);
+        for (int j = 0; j < NI; ++j) {
+          const int o = 1024 * j + 16 * lane;
+          if (tb + o / RB >= nt) *reinterpret_cast<uint4*>(slot + o) = make_uint4(0u, 0u, 0u, 0u);
+        }
       }
-      if constexpr (kQ8) {
-        if (s_lane && tb + s_row >= nt) *reinterpret_cast<uint32_t*>(slot + GB + 4 * lane) = 0u;
+      // Probabilities of the group: computed per lane, then read back with
+      // token (pair) t in lane t of every row (same-wave LDS ops stay in order).
+      uint32_t pv[8];
+      {
+        const int i0 = tb + 2 * k_l;
+        const float2 sv = *reinterpret_cast<const float2*>(sc_l + i0);
+        const float p0 = (i0 < nt && !none_l) ? __builtin_amdgcn_exp2f(sv.x - m_l) : 0.0f;
+        const float p1 = (i0 + 1 < nt && !none_l) ? __builtin_amdgcn_exp2f(sv.y - m_l) : 0.0f;
+        if constexpr (k16) {
+          const uint32_t pp = pack16<DT>(p0, p1);
+          lsum += lo16<DT>(pp) + hi16<DT>(pp);
+          pp_w[lane] = pp;
+        } else {
+          lsum += p0 + p1;
+          *reinterpret_cast<float2*>(pp_w + 2 * lane) = make_float2(p0, p1);
+        }
+#pragma unroll
+        for (int g = 0; g < 8; ++g)
+          pv[g] = k16 ? pp_w[(g < GC ? g : 0) * 8 + (qk_tok & 7)] : pp_w[(g < GC ? g : 0) * 16 + qk_tok];
       }
-    }
-    // Probabilities of the group: computed per lane, then read back with
-    // token (pair) t in lane t of every row (same-wave LDS ops stay in order).
-    uint32_t pv[8];
-    {
-      const int i0 = tb + 2 * k_l;
-      const float2 sv = *reinterpret_cast<const float2*>(sc_l + i0);
-      const float p0 = (i0 < nt && !none_l) ? __builtin_amdgcn_exp2f(sv.x - m_l) : 0.0f;
-      const float p1 = (i0 + 1 < nt && !none_l) ? __builtin_amdgcn_exp2f(sv.y - m_l) : 0.0f;
       if constexpr (k16) {
-        const uint32_t pp = pack16<DT>(p0, p1);
-        lsum += lo16<DT>(pp) + hi16<DT>(pp);
-        pp_w[lane] = pp;
+        Unroll<0, kGroupTok / 2>::run([&](auto jc) {
+          constexpr int j = decltype(jc)::value;  // token pair
+          if constexpr (DPV == 2) {
+            const uint32_t w0 = *reinterpret_cast<const uint32_t*>(slot + (2 * j) * RB + 4 * lane);
+            const uint32_t w1 = *reinterpret_cast<const uint32_t*>(slot + (2 * j + 1) * RB + 4 * lane);
+            pv_words<DT, GC, j>(acc2[0], acc2[1], pv, __builtin_amdgcn_perm(w1, w0, 0x05040100u),
+                                __builtin_amdgcn_perm(w1, w0, 0x07060302u));
+          } else {
+            const uint2 w0 = *reinterpret_cast<const uint2*>(slot + (2 * j) * RB + 8 * lane);
+            const uint2 w1 = *reinterpret_cast<const uint2*>(slot + (2 * j + 1) * RB + 8 * lane);
+            pv_words<DT, GC, j>(acc2[0], acc2[1], pv, __builtin_amdgcn_perm(w1.x, w0.x, 0x05040100u),
+                                __builtin_amdgcn_perm(w1.x, w0.x, 0x07060302u));
+            pv_words<DT, GC, j>(acc2[2], acc2[3], pv, __builtin_amdgcn_perm(w1.y, w0.y, 0x05040100u),
+                                __builtin_amdgcn_perm(w1.y, w0.y, 0x07060302u));
+          }
+        });
       } else {
-        lsum += p0 + p1;
-        *reinterpret_cast<float2*>(pp_w + 2 * lane) = make_float2(p0, p1);
+        Unroll<0, kGroupTok>::run([&](auto tc) {
+          constexpr int t = decltype(tc)::value;  // token
+          if constexpr (DPV == 2) {
+            const uint2 w = *reinterpret_cast<const uint2*>(slot + t * RB + 8 * lane);
+            pv_words<DT, GC, t>(acc2[0], acc2[1], pv, w.x, w.y);
+          } else {
+            const uint4 w = *reinterpret_cast<const uint4*>(slot + t * RB + 16 * lane);
+            pv_words<DT, GC, t>(acc2[0], acc2[1], pv, w.x, w.y);
+            pv_words<DT, GC, t>(acc2[2], acc2[3], pv, w.z, w.w);
+          }
+        });
       }
-#pragma unroll
-      for (int g = 0; g < 8; ++g)
-        pv[g] = k16 ? pp_w[(g < GC ? g : 0) * 8 + (qk_tok & 7)] : pp_w[(g < GC ? g : 0) * 16 + qk_tok];
-    }
-    if constexpr (k16) {
-      Unroll<0, kGroupTok / 2>::run([&](auto jc) {
-        constexpr int j = decltype(jc)::value;  // token pair
-        if constexpr (DPV == 2) {
-          const uint32_t w0 = *reinterpret_cast<const uint32_t*>(slot + (2 * j) * RB + 4 * lane);
-          const uint32_t w1 = *reinterpret_cast<const uint32_t*>(slot + (2 * j + 1) * RB + 4 * lane);
-          pv_words<DT, GC, j>(acc2[0], acc2[1], pv, __builtin_amdgcn_perm(w1, w0, 0x05040100u),
-                              __builtin_amdgcn_perm(w1, w0, 0x07060302u));
-        } else {
-          const uint2 w0 = *reinterpret_cast<const uint2*>(slot + (2 * j) * RB + 8 * lane);
-          const uint2 w1 = *reinterpret_cast<const uint2*>(slot + (2 * j + 1) * RB + 8 * lane);
-          pv_words<DT, GC, j>(acc2[0], acc2[1], pv, __builtin_amdgcn_perm(w1.x, w0.x, 0x05040100u),
-                              __builtin_amdgcn_perm(w1.x, w0.x, 0x07060302u));
-          pv_words<DT, GC, j>(acc2[2], acc2[3], pv, __builtin_amdgcn_perm(w1.y, w0.y, 0x05040100u),
-                              __builtin_amdgcn_perm(w1.y, w0.y, 0x07060302u));
-        }
-      });
-    } else if constexpr (DT == IT_F32) {
-      Unroll<0, kGroupTok>::run([&](auto tc) {
-        constexpr int t = decltype(tc)::value;  // token
-        if constexpr (DPV == 2) {
-          const uint2 w = *reinterpret_cast<const uint2*>(slot + t * RB + 8 * lane);
-          pv_words<DT, GC, t>(acc2[0], acc2[1], pv, w.x, w.y);
-        } else {
-          const uint4 w = *reinterpret_cast<const uint4*>(slot + t * RB + 16 * lane);
-          pv_words<DT, GC, t>(acc2[0], acc2[1], pv, w.x, w.y);
-          pv_words<DT, GC, t>(acc2[2], acc2[3], pv, w.z, w.w);
-        }
-      });
-    } else {
-      // Q8_0: v = f32(d) * qs, d of the lane's 32-group of token t.
-      const char* sbase = slot + GB + ((DPV * lane) / 32) * 2;
-      Unroll<0, kGroupTok>::run([&](auto tc) {
-        constexpr int t = decltype(tc)::value;
-        const float d = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(sbase + t * F::kScaleRow));
-        if constexpr (DPV == 2) {
-          const uint32_t w = *reinterpret_cast<const uint16_t*>(slot + t * RB + 2 * lane);
-          pv_words<DT, GC, t>(acc2[0], acc2[1], pv, __float_as_uint(d * __uint_as_float(i8_f32<0>(w))),
-                              __float_as_uint(d * __uint_as_float(i8_f32<1>(w))));
-        } else {
-          const uint32_t w = *reinterpret_cast<const uint32_t*>(slot + t * RB + 4 * lane);
-          pv_words<DT, GC, t>(acc2[0], acc2[1], pv, __float_as_uint(d * __uint_as_float(i8_f32<0>(w))),
-                              __float_as_uint(d * __uint_as_float(i8_f32<1>(w))));
-          pv_words<DT, GC, t>(acc2[2], acc2[3], pv, __float_as_uint(d * __uint_as_float(i8_f32<2>(w))),
-                              __float_as_uint(d * __uint_as_float(i8_f32<3>(w))));
-        }
-      });
     }
   }
 
   // ---------------- across the waves, in a fixed order -----------------------
-  if constexpr (kQ8) {
+  if constexpr (kQ) {
     if (lane < 8) s_l[wave * 8 + lane] = lsum;
   } else {
     lsum = group_sum<8>(lsum);  // the 8 lanes of head h_l
@@ -880,15 +903,22 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
   }
   lds_barrier();  // every wave is done with its ring (its last wait was vmcnt(0))
   float* const red = reinterpret_cast<float*>(smem);  // [NW][GC][D]
-  if constexpr (kQ8) {
+  if constexpr (kQ) {
     const int hm = lane & 15;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int h = 4 * qr_row + i;
       if (h < GC) {
 #pragma unroll
-        for (int g = 0; g < NK; ++g)
-          *reinterpret_cast<float2*>(&red[(wave * GC + h) * D + 32 * g + 2 * hm]) = make_float2(o8[g][0][i], o8[g][1][i]);
+        for (int g = 0; g < NK; ++g) {
+          float* const row = &red[(wave * GC + h) * D + 32 * g];
+          if constexpr (kQ4) {
+            row[hm] = o8[g][0][i];
+            row[16 + hm] = o8[g][1][i];
+          } else {
+            *reinterpret_cast<float2*>(row + 2 * hm) = make_float2(o8[g][0][i], o8[g][1][i]);
+          }
+        }
       }
     }
   } else {

@@ -12,7 +12,7 @@ from typing import Optional, Tuple
 
 import torch
 
-from ._lib import BF16, CacheDesc, F16, F32, Q8_0, check, lib
+from ._lib import BF16, CacheDesc, F16, F32, Q4_0, Q8_0, check, lib
 
 __all__ = ["PagedKvCache", "RopeTable", "flash_attention", "torch_dtype_id", "stream_handle"]
 
@@ -62,7 +62,8 @@ class RopeTable:
 
 class PagedKvCache:
     """Paged K/V pools in HBM, [num_blocks][n_kv_heads] pages of block_size
-    token rows (Q8_0 pages: int8 rows then fp16 group scales)."""
+    token rows (Q8_0 pages: int8 rows then fp16 group scales; Q4_0 pages:
+    rows of BlockQ4_0 nibble bytes then fp16 group scales)."""
 
     def __init__(self, num_blocks: int, block_size: int, n_kv_heads: int, head_dim: int, dtype: int = BF16,
                  device: int = 0):
@@ -98,6 +99,8 @@ class PagedKvCache:
         pool = self.k_pool if which == "k" else self.v_pool
         if self.dtype == Q8_0:
             raise TypeError("use q8_planes() for a Q8_0 cache")
+        if self.dtype == Q4_0:
+            raise TypeError("use q4_planes() for a Q4_0 cache")
         return pool.view(_ID_TORCH[self.dtype]).view(self.num_blocks, self.n_kv_heads, self.block_size, self.head_dim)
 
     def q8_planes(self, which: str = "k") -> Tuple[torch.Tensor, torch.Tensor]:
@@ -106,6 +109,15 @@ class PagedKvCache:
         bs, D = self.block_size, self.head_dim
         qs = pool[:, :, : bs * D].view(torch.int8).reshape(self.num_blocks, self.n_kv_heads, bs, D)
         d = pool[:, :, bs * D:].contiguous().view(torch.int16).reshape(self.num_blocks, self.n_kv_heads, bs, D // 32)
+        return qs, d
+
+    def q4_planes(self, which: str = "k") -> Tuple[torch.Tensor, torch.Tensor]:
+        """(qs uint8 [nb, H, bs, D/2], d fp16 bits int16 [nb, H, bs, D/32]) of a Q4_0 cache."""
+        pool = (self.k_pool if which == "k" else self.v_pool).view(self.num_blocks, self.n_kv_heads, self.page_bytes)
+        bs, D = self.block_size, self.head_dim
+        qs = pool[:, :, : bs * D // 2].reshape(self.num_blocks, self.n_kv_heads, bs, D // 2)
+        d = pool[:, :, bs * D // 2:].contiguous().view(torch.int16).reshape(self.num_blocks, self.n_kv_heads, bs,
+                                                                              D // 32)
         return qs, d
 
     def check(self) -> None:

@@ -250,6 +250,62 @@ void orc_dequantize_row_q8_0(const uint8_t* y, size_t n, float* x) {
 }
 
 /* ------------------------------------------------------------------------ */
+/* Q4_0 -- block types.rs:15-22, dequantisation vec_dot.rs:425-440; the     */
+/* quantiser restates ggml's quantize_row_q4_0_ref (none in the reference)  */
+/* ------------------------------------------------------------------------ */
+/* ggml's (int8_t)(float) as the x86 build computes it: cvttss2si truncates
+ * toward zero and returns 0x80000000 (low byte 0) for NaN and out-of-range
+ * values; the cast keeps the low byte.  For finite x with a finite 1/d the
+ * argument x * id + 8.5 lies in [0, 16.5]; it is NaN or infinite only when
+ * x or 1/d is (an infinite element, or |d| below 2^-128). */
+static int32_t q4_trunc_i8(float f) {
+  if (f != f || fabsf(f) >= 2147483648.0f) return 0;
+  return (int32_t)(int8_t)(int32_t)f;
+}
+
+int orc_quantize_row_q4_0(const float* x, size_t n, uint8_t* y) {
+  if (n % ORC_QK4_0) return ORC_INVALID_INPUT;
+  size_t nb = n / ORC_QK4_0;
+  for (size_t i = 0; i < nb; ++i) {
+    const float* xb = x + i * ORC_QK4_0;
+    uint8_t* rec = y + i * ORC_BLOCK_Q4_0_BYTES;
+    float amax = 0.0f, max = 0.0f;
+    for (int j = 0; j < ORC_QK4_0; ++j) { /* strict <: the first of equal magnitudes; NaN never wins */
+      float a = fabsf(xb[j]);
+      if (amax < a) {
+        amax = a;
+        max = xb[j];
+      }
+    }
+    const float d = max / -8.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    uint16_t dh = orc_f32_to_f16(d);
+    rec[0] = (uint8_t)(dh & 0xFF);
+    rec[1] = (uint8_t)(dh >> 8);
+    for (int j = 0; j < ORC_QK4_0 / 2; ++j) {
+      int32_t q0 = q4_trunc_i8(xb[j] * id + 8.5f);
+      int32_t q1 = q4_trunc_i8(xb[j + ORC_QK4_0 / 2] * id + 8.5f);
+      if (q0 > 15) q0 = 15;
+      if (q1 > 15) q1 = 15;
+      rec[2 + j] = (uint8_t)(q0 | (q1 << 4));
+    }
+  }
+  return ORC_OK;
+}
+
+void orc_dequantize_row_q4_0(const uint8_t* y, size_t n, float* x) {
+  size_t nb = n / ORC_QK4_0;
+  for (size_t i = 0; i < nb; ++i) {
+    const uint8_t* rec = y + i * ORC_BLOCK_Q4_0_BYTES;
+    float d = orc_f16_to_f32((uint16_t)(rec[0] | (rec[1] << 8)));
+    for (int j = 0; j < ORC_QK4_0 / 2; ++j) {
+      x[i * ORC_QK4_0 + j] = d * (float)((int32_t)(rec[2 + j] & 0xF) - 8);
+      x[i * ORC_QK4_0 + j + ORC_QK4_0 / 2] = d * (float)((int32_t)(rec[2 + j] >> 4) - 8);
+    }
+  }
+}
+
+/* ------------------------------------------------------------------------ */
 /* rope_f32 -- src/backend/arm/rope.rs:6-44                                   */
 /* ------------------------------------------------------------------------ */
 int orc_rope_f32(const float* x, float* out, size_t n, int64_t pos, int32_t n_dims, int32_t head_dim,
@@ -338,12 +394,14 @@ static size_t elem_bytes(int32_t dtype) {
 static int desc_ok(const orc_cache_desc* c) {
   if (c->num_blocks <= 0 || c->block_size <= 0 || c->n_kv_heads <= 0 || c->head_dim <= 0) return 0;
   if (c->dtype == ORC_Q8_0) return c->head_dim % ORC_QK8_0 == 0;
+  if (c->dtype == ORC_Q4_0) return c->head_dim % ORC_QK4_0 == 0;
   return elem_bytes(c->dtype) != 0;
 }
 
 size_t orc_page_bytes(const orc_cache_desc* c) {
   size_t bs = (size_t)c->block_size, d = (size_t)c->head_dim;
   if (c->dtype == ORC_Q8_0) return bs * d + bs * (d / ORC_QK8_0) * 2;
+  if (c->dtype == ORC_Q4_0) return bs * (d / 2) + bs * (d / ORC_QK4_0) * 2;
   return bs * d * elem_bytes(c->dtype);
 }
 
@@ -365,6 +423,19 @@ static void put_row(const orc_cache_desc* c, uint8_t* page, int32_t slot, const 
       sc[g * 2] = rec[0];
       sc[g * 2 + 1] = rec[1];
     }
+  } else if (c->dtype == ORC_Q4_0) {
+    /* qs plane [block_size][d / 2] (each group's 16 bytes as in the block),
+     * then the d plane [block_size][d / 32] fp16. */
+    size_t ng = d / ORC_QK4_0;
+    uint8_t rec[ORC_BLOCK_Q4_0_BYTES];
+    uint8_t* qs = page + (size_t)slot * (d / 2);
+    uint8_t* sc = page + (size_t)c->block_size * (d / 2) + (size_t)slot * ng * 2;
+    for (size_t g = 0; g < ng; ++g) {
+      orc_quantize_row_q4_0((const float*)src_row + g * ORC_QK4_0, ORC_QK4_0, rec);
+      memcpy(qs + g * 16, rec + 2, 16);
+      sc[g * 2] = rec[0];
+      sc[g * 2 + 1] = rec[1];
+    }
   } else {
     size_t rb = d * elem_bytes(c->dtype);
     memcpy(page + (size_t)slot * rb, src_row, rb);
@@ -374,7 +445,7 @@ static void put_row(const orc_cache_desc* c, uint8_t* page, int32_t slot, const 
 int orc_kv_append(const orc_cache_desc* c, uint8_t* k_pool, uint8_t* v_pool,
                   const void* k, const void* v, const int64_t* slots, int32_t n_tokens) {
   if (!desc_ok(c) || n_tokens < 0) return ORC_INVALID_INPUT;
-  size_t src_eb = c->dtype == ORC_Q8_0 ? 4 : elem_bytes(c->dtype);
+  size_t src_eb = (c->dtype == ORC_Q8_0 || c->dtype == ORC_Q4_0) ? 4 : elem_bytes(c->dtype);
   size_t row = (size_t)c->head_dim * src_eb;
   int64_t n_slots = c->num_blocks * c->block_size;
   for (int32_t t = 0; t < n_tokens; ++t) {
@@ -406,6 +477,16 @@ static void get_row_raw(const orc_cache_desc* c, const uint8_t* page, int32_t sl
       rec[1] = sc[g * 2 + 1];
       memcpy(rec + 2, qs + g * ORC_QK8_0, ORC_QK8_0);
     }
+  } else if (c->dtype == ORC_Q4_0) {
+    size_t ng = d / ORC_QK4_0;
+    const uint8_t* qs = page + (size_t)slot * (d / 2);
+    const uint8_t* sc = page + (size_t)c->block_size * (d / 2) + (size_t)slot * ng * 2;
+    for (size_t g = 0; g < ng; ++g) {
+      uint8_t* rec = dst + g * ORC_BLOCK_Q4_0_BYTES;
+      rec[0] = sc[g * 2];
+      rec[1] = sc[g * 2 + 1];
+      memcpy(rec + 2, qs + g * 16, 16);
+    }
   } else {
     size_t rb = d * elem_bytes(c->dtype);
     memcpy(dst, page + (size_t)slot * rb, rb);
@@ -414,10 +495,12 @@ static void get_row_raw(const orc_cache_desc* c, const uint8_t* page, int32_t sl
 
 static size_t row_out_bytes(const orc_cache_desc* c) {
   if (c->dtype == ORC_Q8_0) return (size_t)(c->head_dim / ORC_QK8_0) * ORC_BLOCK_Q8_0_BYTES;
+  if (c->dtype == ORC_Q4_0) return (size_t)(c->head_dim / ORC_QK4_0) * ORC_BLOCK_Q4_0_BYTES;
   return (size_t)c->head_dim * elem_bytes(c->dtype);
 }
 
-/* Widen one stored row to f32 (bf16/f16 exact, Q8_0 = f32(d)*q). */
+/* Widen one stored row to f32 (bf16/f16 exact, Q8_0 = f32(d)*q, Q4_0 =
+ * f32(d)*(nibble-8)). */
 static void get_row_f32(const orc_cache_desc* c, const uint8_t* page, int32_t slot, float* dst) {
   size_t d = (size_t)c->head_dim;
   switch (c->dtype) {
@@ -430,6 +513,15 @@ static void get_row_f32(const orc_cache_desc* c, const uint8_t* page, int32_t sl
       uint8_t* buf = ng * ORC_BLOCK_Q8_0_BYTES <= sizeof(rec) ? rec : (uint8_t*)malloc(ng * ORC_BLOCK_Q8_0_BYTES);
       get_row_raw(c, page, slot, buf);
       orc_dequantize_row_q8_0(buf, d, dst);
+      if (buf != rec) free(buf);
+      break;
+    }
+    case ORC_Q4_0: {
+      uint8_t rec[8 * ORC_BLOCK_Q4_0_BYTES * 4];
+      size_t ng = d / ORC_QK4_0;
+      uint8_t* buf = ng * ORC_BLOCK_Q4_0_BYTES <= sizeof(rec) ? rec : (uint8_t*)malloc(ng * ORC_BLOCK_Q4_0_BYTES);
+      get_row_raw(c, page, slot, buf);
+      orc_dequantize_row_q4_0(buf, d, dst);
       if (buf != rec) free(buf);
       break;
     }

@@ -34,11 +34,14 @@ extern "C" {
 /* dtype codes = ggml QuantType ids (types.rs:106-144). */
 #define ORC_F32 0
 #define ORC_F16 1
+#define ORC_Q4_0 2
 #define ORC_Q8_0 8
 #define ORC_BF16 30
 
 #define ORC_QK8_0 32          /* types.rs:11 */
 #define ORC_BLOCK_Q8_0_BYTES 34 /* types.rs:34-41: repr(C) {u16 d; i8 qs[32]} */
+#define ORC_QK4_0 32          /* types.rs:7 */
+#define ORC_BLOCK_Q4_0_BYTES 18 /* types.rs:15-22: repr(C) {u16 d; u8 qs[16]} */
 
 /* ---- seeded synthetic inputs (not a reference function: test plumbing) -- */
 uint64_t orc_splitmix64(uint64_t* state);
@@ -91,6 +94,18 @@ int orc_quantize_row_q8_0(const float* x, size_t n, uint8_t* y);
 /* Dequant semantics fp16_to_fp32(d) * q (gemv.rs:48-59, 151-160). */
 void orc_dequantize_row_q8_0(const uint8_t* y, size_t n, float* x);
 
+/* ---- Q4_0 ---------------------------------------------------------------- */
+/* The reference fixes the block (types.rs:15-22) and its dequantisation
+ * (vec_dot.rs:425-440): element j of a group is the low nibble of qs[j],
+ * element j + 16 the high nibble, value fp16_to_fp32(d) * (nibble - 8).  It
+ * has no Q4_0 quantiser; orc_quantize_row_q4_0 restates ggml's
+ * quantize_row_q4_0_ref (ggml-quants.c, the library whose block_q4_0 the
+ * reference's BlockQ4_0 mirrors; not vendored): max = the first element of
+ * largest magnitude, d = max / -8, id = d ? 1/d : 0, nibble =
+ * min(15, (int8_t)(x * id + 8.5f)), d stored as fp16 (RNE). */
+int orc_quantize_row_q4_0(const float* x, size_t n, uint8_t* y);
+void orc_dequantize_row_q4_0(const uint8_t* y, size_t n, float* x);
+
 /* ---- RoPE (src/backend/arm/rope.rs:6-44) -------------------------------- */
 /* out = x rotated pairwise: for each head row of head_dim floats and each
  * even i < n_dims, theta = (float)pos * powf(freq_base, -(float)i / n_dims),
@@ -115,7 +130,9 @@ int orc_backend_flash_attention(const float* q, const float* k, const float* v,
 /* Pool layout: [num_blocks][n_kv_heads][block_size][head_dim] elements of
  * elem_bytes each, one pool for K and one for V.  For Q8_0 each
  * (block, head) page holds block_size*head_dim int8 values followed by
- * block_size*head_dim/32 fp16 scales (slot-major). */
+ * block_size*head_dim/32 fp16 scales (slot-major).  Q4_0 likewise:
+ * block_size*head_dim/2 bytes of nibbles (each 32-group's 16 bytes in
+ * BlockQ4_0 order), then block_size*head_dim/32 fp16 scales. */
 typedef struct {
   int64_t num_blocks;
   int32_t block_size;
@@ -128,15 +145,15 @@ size_t orc_page_bytes(const orc_cache_desc* c);
 
 /* KV append (forward.rs:219-229 generalised from `seq_pos` to a slot):
  * k_cache[slot/bs][h][slot%bs][:] = k[t][h][:].  Negative slots are skipped.
- * F32/F16/BF16: bit copy (src dtype == cache dtype).  Q8_0: src is f32 and
- * each 32-group is quantised with orc_quantize_row_q8_0. */
+ * F32/F16/BF16: bit copy (src dtype == cache dtype).  Q8_0 / Q4_0: src is
+ * f32 and each 32-group is quantised with orc_quantize_row_q8_0 / _q4_0. */
 int orc_kv_append(const orc_cache_desc* c, uint8_t* k_pool, uint8_t* v_pool,
                   const void* k, const void* v, const int64_t* slots, int32_t n_tokens);
 
 /* Block-table gather: the contiguous slice k_cache[kv][start..ctx] of
  * forward.rs:233-243 read through a block table.  Output per sequence b is
  * [n_kv_heads][ctx_b - start_b][head_dim] at token offset cu_out[b].  Q8_0
- * outputs packed 34-byte BlockQ8_0 records. */
+ * outputs packed 34-byte BlockQ8_0 records, Q4_0 18-byte BlockQ4_0 ones. */
 int orc_kv_gather(const orc_cache_desc* c, const uint8_t* k_pool, const uint8_t* v_pool,
                   const int32_t* block_tables, int32_t max_blocks, const int32_t* ctx_lens,
                   const int32_t* start_pos, const int64_t* cu_out, int32_t n_seqs,
@@ -147,7 +164,8 @@ int orc_kv_evict(const orc_cache_desc* c, uint8_t* k_pool, uint8_t* v_pool,
                  const int32_t* blocks, int32_t n);
 
 /* Paged decode: for each seq b and q-head h, flash_attn_f32 over the
- * widened (bf16/f16 -> f32, Q8_0 -> f32(d)*q) keys start_b..ctx_b-1 of KV
+ * widened (bf16/f16 -> f32, Q8_0 -> f32(d)*q, Q4_0 -> f32(d)*(n-8)) keys
+ * start_b..ctx_b-1 of KV
  * head h*Hkv/Hq (forward.rs:231-254).  q: [n_seqs][n_heads][D] f32,
  * out: [n_seqs][n_heads][D] f32.  start_pos may be NULL (all zero). */
 int orc_paged_decode(const orc_cache_desc* c, const uint8_t* k_pool, const uint8_t* v_pool,

@@ -75,3 +75,72 @@ def assert_close(got: np.ndarray, want: np.ndarray, rtol: float, atol: float, wh
         i = np.flatnonzero(bad.ravel())[0]
         raise AssertionError(f"{what}: {bad.sum()} of {bad.size} outside |d| <= {atol} + {rtol}|ref|; first at {i}: "
                              f"got {got.ravel()[i]!r} want {want.ravel()[i]!r}; max err {err.max():.3g}")
+
+
+def exact_decode(ref, q, hq: int, tables, ctx, start, scale: float) -> np.ndarray:
+    """float64 softmax(q K^T * scale) V over the rows the oracle cache `ref`
+    holds (its stored values widened exactly: bf16/f16, Q8_0 f32(d)*q, Q4_0
+    f32(d)*(n-8)), keys start_b..ctx_b-1 of KV head h*Hkv/Hq.  The rounding-
+    free answer both fp32 implementations approximate."""
+    ctx = np.asarray(ctx, np.int32)
+    st = np.zeros_like(ctx) if start is None else np.asarray(start, np.int32)
+    n = ctx - st
+    cu = np.concatenate([[0], np.cumsum(n)[:-1]]).astype(np.int64)
+    hkv, D, dt = ref.desc.n_kv_heads, ref.desc.head_dim, ref.desc.dtype
+    gk, gv = ref.gather(tables, ctx, st, cu, int(n.sum()))
+    rb = ref.row_out_bytes()
+
+    def rows(g, b):
+        raw = g[int(cu[b]) * hkv * rb:(int(cu[b]) + int(n[b])) * hkv * rb].reshape(hkv, int(n[b]), rb)
+        if dt == orc.Q8_0:
+            return orc.dequantize_row_q8_0(raw).reshape(hkv, int(n[b]), D)
+        if dt == orc.Q4_0:
+            return orc.dequantize_row_q4_0(raw).reshape(hkv, int(n[b]), D)
+        if dt == orc.F32:
+            return raw.view(np.float32).reshape(hkv, int(n[b]), D)
+        return widen(raw.view(np.uint16), dt).reshape(hkv, int(n[b]), D)
+
+    out = np.zeros((len(ctx), hq, D), np.float64)
+    for b in range(len(ctx)):
+        if n[b] <= 0:
+            continue
+        K, V = rows(gk, b).astype(np.float64), rows(gv, b).astype(np.float64)
+        for h in range(hq):
+            kv = h * hkv // hq
+            s = K[kv] @ q[b, h].astype(np.float64) * scale
+            p = np.exp(s - s.max())
+            out[b, h] = p @ V[kv] / p.sum()
+    return out
+
+
+def lazy(fn):
+    """fn() computed on the first call only."""
+    box = []
+
+    def get():
+        if not box:
+            box.append(fn())
+        return box[0]
+
+    return get
+
+
+def assert_close_or_closer(got, want, exact_fn, rtol: float, atol: float, what: str = "") -> None:
+    """assert_close, except that an element outside the tolerance of the fp32
+    oracle `want` passes when `got` is no farther from the float64 answer
+    (exact_fn()) than the oracle is, plus atol: two fp32 summation orders
+    cannot agree to atol on an element whose terms cancel (an output of 0.009
+    from terms of total magnitude ~2), and there the oracle's own error can
+    exceed atol."""
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    bad = np.abs(got - want) > atol + rtol * np.abs(want)
+    if not bad.any():
+        return
+    exact = np.asarray(exact_fn(), np.float64).reshape(got.shape)
+    worse = bad & (np.abs(got - exact) > np.abs(want - exact) + atol)
+    if worse.any():
+        i = np.flatnonzero(worse.ravel())[0]
+        raise AssertionError(f"{what}: {worse.sum()} of {worse.size} outside |d| <= {atol} + {rtol}|ref| and farther "
+                             f"from the float64 answer than the oracle; first at {i}: got {got.ravel()[i]!r} "
+                             f"want {want.ravel()[i]!r} exact {exact.ravel()[i]!r}")

@@ -1,5 +1,5 @@
-"""GPU parity of the data-movement kernels: slot-mapped append (bit copy and
-Q8_0 quantise), block-table gather, evict and copy-on-write page copy.  Every
+"""GPU parity of the data-movement kernels: slot-mapped append (bit copy,
+Q8_0 and Q4_0 quantise), block-table gather, evict and copy-on-write page copy.  Every
 result is compared byte for byte with the oracle on the same seeded inputs;
 pools start filled with a sentinel so stray writes show up."""
 import numpy as np
@@ -28,7 +28,7 @@ def _pair(num_blocks, bs, hkv, D, dt):
 
 
 def _src(seed, n_tokens, hkv, D, dt):
-    if dt == orc.Q8_0:
+    if dt in (orc.Q8_0, orc.Q4_0):
         k = kv_values(seed, n_tokens * hkv * D, orc.F32, outliers=True)
         v = kv_values(seed + 1, n_tokens * hkv * D, orc.F32, outliers=True)
     else:
@@ -40,7 +40,7 @@ def _src(seed, n_tokens, hkv, D, dt):
 def _dev_src(a, dt):
     import torch
 
-    if dt in (orc.F32, orc.Q8_0):
+    if dt in (orc.F32, orc.Q8_0, orc.Q4_0):
         return to_dev(a)
     return to_dev(a.view(np.int16), torch.bfloat16 if dt == orc.BF16 else torch.float16)
 
@@ -56,7 +56,8 @@ def _assert_pools(dev, ref, what):
 
 
 @pytest.mark.parametrize("dt,D,bs", [(orc.BF16, 128, 16), (orc.F32, 128, 16), (orc.F16, 128, 16),
-                                     (orc.BF16, 256, 32), (orc.Q8_0, 256, 32), (orc.Q8_0, 128, 16)])
+                                     (orc.BF16, 256, 32), (orc.Q8_0, 256, 32), (orc.Q8_0, 128, 16),
+                                     (orc.Q4_0, 256, 32), (orc.Q4_0, 128, 16), (orc.Q4_0, 64, 8)])
 def test_append_bit_exact(dt, D, bs):
     hkv, nb, n = 4, 64, 300
     dev, ref = _pair(nb, bs, hkv, D, dt)
@@ -97,6 +98,33 @@ def test_append_q8_special_groups():
     _assert_pools(dev, ref, "append q8 special")
 
 
+def test_append_q4_special_groups():
+    """Q4_0 (ggml's quantiser; the reference has none): equal magnitudes of
+    both signs, all-zero, -0, constant, subnormal, NaN, inf and a
+    group whose 1/d overflows."""
+    hkv, D, bs, nb = 1, 256, 32, 4
+    dev, ref = _pair(nb, bs, hkv, D, orc.Q4_0)
+    g = np.zeros((8, 32), np.float32)
+    g[0, [2, 7, 20]] = [-4.0, 4.0, 4.0]  # first of equal magnitudes: max = -4
+    g[0, [3, 4, 5]] = [1.25, -1.75, 3.0]  # x * id + 8.5 on .5 boundaries
+    g[1] = -0.0
+    g[2] = 0.75
+    g[3] = orc.normal(3, 32) * np.float32(1e-30)
+    g[4] = orc.normal(4, 32) * np.float32(1e-40)  # d underflows to 0 (or 1/d overflows)
+    g[5] = orc.normal(5, 32)
+    g[5, 9] = np.nan
+    g[6] = orc.normal(6, 32)
+    g[6, 2] = -np.inf
+    g[7] = orc.normal(7, 32) * np.float32(6e4)
+    rows = [np.roll(g.reshape(-1), 32 * s) for s in range(8)]
+    k = np.stack(rows).reshape(8, hkv, D)
+    v = -k
+    slots = np.array([0, 5, 31, 32, 63, 64, 100, 127], np.int64)
+    ref.append(k, v, slots)
+    dev.append(to_dev(k), to_dev(v), to_dev(slots))
+    _assert_pools(dev, ref, "append q4 special")
+
+
 def test_append_config1_full_step():
     # Config 1: fp32, Hkv 2, D 128, bs 16, 64 blocks, identity table; 1023
     # cached tokens then the token at position 1023.
@@ -125,7 +153,8 @@ def test_append_bad_slot_is_latched_not_written():
     _assert_pools(dev, ref, "bad slot")  # nothing else written; flag cleared
 
 
-@pytest.mark.parametrize("dt,D,bs", [(orc.BF16, 128, 16), (orc.F32, 128, 16), (orc.Q8_0, 256, 32)])
+@pytest.mark.parametrize("dt,D,bs", [(orc.BF16, 128, 16), (orc.F32, 128, 16), (orc.Q8_0, 256, 32),
+                                     (orc.Q4_0, 128, 16)])
 def test_gather_bit_exact(dt, D, bs):
     import torch
 
@@ -163,6 +192,16 @@ def test_gather_bit_exact(dt, D, bs):
         want = np.concatenate(rows).ravel()
         off = int(cu[b]) * hkv * (D // 32) * 34
         np.testing.assert_array_equal(from_dev(ko)[off:off + want.size], want)
+    if dt == orc.Q4_0:  # AoS records equal quantize_row_q4_0 of the source rows
+        b = 3
+        rows = []
+        for h in range(hkv):
+            for i in range(n[b]):
+                t = int(sum(ctx[:b])) + int(start[b]) + i
+                rows.append(orc.quantize_row_q4_0(v[t, h]))
+        want = np.concatenate(rows).ravel()
+        off = int(cu[b]) * hkv * (D // 32) * 18
+        np.testing.assert_array_equal(from_dev(vo)[off:off + want.size], want)
 
 
 def test_evict_and_copy_blocks():

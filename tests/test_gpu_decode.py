@@ -9,11 +9,14 @@ import numpy as np
 import pytest
 
 import oracle as orc
-from kvutil import assert_close, from_dev, kv_values, random_tables, slots_for, to_dev, widen
+from kvutil import (assert_close, assert_close_or_closer, exact_decode, from_dev, kv_values, lazy, random_tables,
+                    slots_for, to_dev, widen)
 
 pytestmark = pytest.mark.gpu
 
-TOL = {orc.F32: (1e-5, 1e-6), orc.Q8_0: (1e-5, 1e-6), orc.BF16: (2e-3, 1e-2), orc.F16: (2e-3, 1e-2)}
+TOL = {orc.F32: (1e-5, 1e-6), orc.Q8_0: (1e-5, 1e-6), orc.Q4_0: (1e-5, 1e-6), orc.BF16: (2e-3, 1e-2),
+       orc.F16: (2e-3, 1e-2)}
+QUANT = (orc.Q8_0, orc.Q4_0)
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 
 
@@ -33,9 +36,9 @@ def _build(dt, hq, hkv, D, bs, ctx, start=None, nb=None, seed=1, mb=None):
         pos += list(range(int(c)))
     slots = slots_for(tables, seqs, pos, bs)
     n = len(slots)
-    src_dt = orc.F32 if dt == orc.Q8_0 else dt
-    k = kv_values(seed + 10, n * hkv * D, src_dt, outliers=dt == orc.Q8_0).reshape(n, hkv, D)
-    v = kv_values(seed + 11, n * hkv * D, src_dt, outliers=dt == orc.Q8_0).reshape(n, hkv, D)
+    src_dt = orc.F32 if dt in QUANT else dt
+    k = kv_values(seed + 10, n * hkv * D, src_dt, outliers=dt in QUANT).reshape(n, hkv, D)
+    v = kv_values(seed + 11, n * hkv * D, src_dt, outliers=dt in QUANT).reshape(n, hkv, D)
     ref = orc.Cache(nb, bs, hkv, D, dt)
     ref.append(k, v, slots)
     dev = PagedKvCache(nb, bs, hkv, D, dt)
@@ -46,7 +49,7 @@ def _build(dt, hq, hkv, D, bs, ctx, start=None, nb=None, seed=1, mb=None):
             td = torch.bfloat16 if dt == orc.BF16 else torch.float16
             dk, dv = to_dev(k.view(np.int16), td), to_dev(v.view(np.int16), td)
         dev.append(dk, dv, to_dev(slots))
-    qdt = orc.F32 if dt in (orc.F32, orc.Q8_0) else dt
+    qdt = orc.F32 if dt in (orc.F32,) + QUANT else dt
     q = kv_values(seed + 12, len(ctx) * hq * D, qdt).reshape(len(ctx), hq, D)
     return dev, ref, tables, ctx, q, qdt
 
@@ -146,26 +149,42 @@ def test_q8_0_decode_d256():
     fp32 tolerance against the oracle on the same quantised cache."""
     hq, hkv, D, bs = 24, 4, 256, 32
     dev, ref, tables, ctx, q, qdt = _build(orc.Q8_0, hq, hkv, D, bs, [3000, 1025, 33], seed=7)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
+    exact = lazy(lambda: exact_decode(ref, q, hq, tables, ctx, None, scale))
     for partition in (512, 1024, 2048):
         got, want = _run(dev, ref, tables, ctx, q, qdt, hq, partition=partition)
-        assert_close(got, want, *TOL[orc.Q8_0], what=f"q8_0 P={partition}")
+        assert_close_or_closer(got, want, exact, *TOL[orc.Q8_0], what=f"q8_0 P={partition}")
 
 
+@pytest.mark.parametrize("dt", QUANT)
 @pytest.mark.parametrize("D", [128, 256])
-def test_q8_0_group_sizes_and_windows(D):
-    """Q8_0 (products on MFMA) at every heads-per-workgroup count 1..8 (the
-    tiles' padding rows and the second row of four heads), contexts that end
-    inside a 16-token group and inside a page, window start positions, and two
-    partition sizes; fp32 tolerance against the oracle."""
+def test_quant_group_sizes_and_windows(dt, D):
+    """Q8_0 and Q4_0 (products on MFMA) at every heads-per-workgroup count
+    1..8 (the tiles' padding rows and the second row of four heads), contexts
+    that end inside a 16-token group and inside a page, window start
+    positions, and two partition sizes; fp32 tolerance against the oracle."""
     bs = 32 if D == 256 else 16
     ctx = [1, 17, 100, 333, 0]
     start = np.array([0, 5, 37, 300, 0], np.int32)
     for hq, hkv in ((1, 1), (2, 1), (6, 2), (4, 1), (10, 2), (18, 3), (21, 3), (8, 1)):
-        dev, ref, tables, ctx_a, q, qdt = _build(orc.Q8_0, hq, hkv, D, bs, ctx, seed=40 + hq)
+        dev, ref, tables, ctx_a, q, qdt = _build(dt, hq, hkv, D, bs, ctx, seed=40 + hq)
         for partition in (64, 256):
             got, want = _run(dev, ref, tables, ctx_a, q, qdt, hq, start=start, partition=partition)
-            assert_close(got, want, *TOL[orc.Q8_0], what=f"q8_0 D={D} hq={hq} hkv={hkv} P={partition}")
+            scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
+            assert_close_or_closer(got, want, lambda: exact_decode(ref, q, hq, tables, ctx_a, start, scale), *TOL[dt],
+                                   what=f"dt={dt} D={D} hq={hq} hkv={hkv} P={partition}")
         assert np.all(got[-1] == 0)
+
+
+def test_q4_0_decode_config5_heads():
+    """Config-5 heads (Hq 24, Hkv 4, D 256, bs 32) on a Q4_0 cache."""
+    hq, hkv, D, bs = 24, 4, 256, 32
+    dev, ref, tables, ctx, q, qdt = _build(orc.Q4_0, hq, hkv, D, bs, [3000, 1025, 33], seed=9)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
+    exact = lazy(lambda: exact_decode(ref, q, hq, tables, ctx, None, scale))
+    for partition in (512, 1024):
+        got, want = _run(dev, ref, tables, ctx, q, qdt, hq, partition=partition)
+        assert_close_or_closer(got, want, exact, *TOL[orc.Q4_0], what=f"q4_0 P={partition}")
 
 
 def test_bf16_d256_and_group_sizes():

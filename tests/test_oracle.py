@@ -152,6 +152,144 @@ def test_q8_dequant_is_d_times_q(orc):
     assert np.max(np.abs(deq - x.reshape(-1, 32))) <= np.max(d) * 0.5 * (1 + 1e-3) + 1e-7
 
 
+# ---------------- Q4_0 ------------------------------------------------------
+# The reference fixes the block (types.rs:15-22) and its dequantisation
+# (vec_dot.rs:425-440, and the NEON path :97-137 agrees); it has no Q4_0
+# quantiser, so the quantiser is pinned to ggml's quantize_row_q4_0_ref by
+# hand-worked cases below, not to reference output.
+def _f16_bits(x) -> int:
+    return int(np.float16(x).view(np.uint16))
+
+
+def _q4_d(rec) -> np.ndarray:
+    return (rec[:, 0].astype(np.uint16) | (rec[:, 1].astype(np.uint16) << 8)).view(np.float16)
+
+
+def test_q4_dequant_layout(orc):
+    rec = np.zeros((1, 18), np.uint8)
+    rec[0, :2] = np.frombuffer(np.float16(0.1).tobytes(), np.uint8)
+    rec[0, 2:] = 0x88  # the reference's own KAT input (gemv.rs:186-204): all zero
+    assert np.all(orc.dequantize_row_q4_0(rec) == 0)
+    rec[0, 2:] = [j | ((15 - j) << 4) for j in range(16)]  # low nibble j, high nibble 15 - j
+    out = orc.dequantize_row_q4_0(rec)
+    d = np.float32(np.float16(0.1))
+    np.testing.assert_array_equal(out[:16], d * np.arange(-8, 8, dtype=np.float32))
+    np.testing.assert_array_equal(out[16:], d * np.arange(7, -9, -1, dtype=np.float32))
+
+
+def test_q4_zero_group(orc):
+    for z in (np.zeros(32, np.float32), -np.zeros(32, np.float32)):
+        rec = orc.quantize_row_q4_0(z)
+        assert _q4_d(rec)[0] == 0 and np.all(rec[0, 2:] == 0x88)
+
+
+def test_q4_hand_worked_group(orc):
+    # max = 8.0 (index 5; the -8.0 at index 20 has the same magnitude and
+    # comes later), so d = -1 and id = -1: nibble = min(15, trunc(8.5 - x)).
+    x = np.zeros(32, np.float32)
+    vals = {0: 3.0, 1: -3.0, 2: 2.5, 3: -2.5, 4: 0.49, 5: 8.0, 6: 0.51, 7: 7.9, 8: -7.9, 20: -8.0, 21: 1.0}
+    for i, v in vals.items():
+        x[i] = v
+    rec = orc.quantize_row_q4_0(x)
+    assert int(rec[0, 0]) | (int(rec[0, 1]) << 8) == _f16_bits(-1.0)
+    want = np.full(32, 8)
+    for i, q in {0: 5, 1: 11, 2: 6, 3: 11, 4: 8, 5: 0, 6: 7, 7: 0, 8: 15, 20: 15, 21: 7}.items():
+        want[i] = q
+    got = np.concatenate([rec[0, 2:] & 0xF, rec[0, 2:] >> 4])
+    np.testing.assert_array_equal(got, want)
+
+
+def test_q4_first_of_equal_magnitudes(orc):
+    x = np.zeros(32, np.float32)
+    x[2], x[7] = -4.0, 4.0  # max = -4: d = 0.5, id = 2
+    rec = orc.quantize_row_q4_0(x)
+    assert int(rec[0, 0]) | (int(rec[0, 1]) << 8) == _f16_bits(0.5)
+    assert rec[0, 2 + 2] & 0xF == 0 and rec[0, 2 + 7] & 0xF == 15  # -8 + 8.5 -> 0; 8 + 8.5 -> 16 -> 15
+    x[2], x[7] = 4.0, -4.0  # max = 4: d = -0.5
+    rec = orc.quantize_row_q4_0(x)
+    assert int(rec[0, 0]) | (int(rec[0, 1]) << 8) == _f16_bits(-0.5)
+
+
+def test_q4_nan_inf(orc):
+    x = np.linspace(-1, 1, 32).astype(np.float32)
+    x[3] = np.nan  # never the max; its nibble is trunc(NaN) -> 0
+    rec = orc.quantize_row_q4_0(x)
+    assert _q4_d(rec)[0] == np.float16(0.125)  # max = x[0] = -1, the first of |-1| = |1|
+    assert rec[0, 2 + 3] & 0xF == 0
+    x[3] = -np.inf  # d = inf, id = 0: finite x -> 8; the inf element -> NaN -> 0
+    rec = orc.quantize_row_q4_0(x)
+    assert int(rec[0, 0]) | (int(rec[0, 1]) << 8) == 0x7C00
+    nib = np.concatenate([rec[0, 2:] & 0xF, rec[0, 2:] >> 4])
+    assert nib[3] == 0 and np.all(np.delete(nib, 3) == 8)
+
+
+def test_q4_round_trip_bound(orc):
+    x = orc.normal(22, 32 * 2048)
+    rng = np.random.default_rng(1)
+    x[rng.random(x.size) < 0.01] *= 8
+    x[:32] *= 1e-3
+    x[32:64] *= 3e3
+    rec = orc.quantize_row_q4_0(x)
+    deq = orc.dequantize_row_q4_0(rec).reshape(-1, 32)
+    xg = x.reshape(-1, 32)
+    d = np.abs(_q4_d(rec).astype(np.float32))[:, None]
+    err = np.abs(deq - xg)
+    # round half up onto the grid d * (-8..7): at most d / 2, except the +8
+    # end (the opposite sign of max, clamped to nibble 15) at most d; slack for
+    # the fp16 rounding of d (2^-11 relative, times 8 steps)
+    assert np.all(err <= d * (1 + 8 * 2 ** -10) + 1e-30)
+    inner = np.abs(xg) < 7.5 * d
+    assert np.all(err[inner] <= (d * 0.5 * (1 + 16 * 2 ** -10))[np.nonzero(inner)[0]].ravel() + 1e-30)
+    # the element of largest magnitude comes back as -8 d
+    imax = np.argmax(np.abs(xg), axis=1)
+    np.testing.assert_array_equal(deq[np.arange(len(xg)), imax], -8 * _q4_d(rec).astype(np.float32))
+
+
+def test_oracle_q4_gather_records_equal_quantize_row(orc):
+    nb, bs, hkv, D = 4, 16, 2, 64
+    c = orc.Cache(nb, bs, hkv, D, orc.Q4_0)
+    n = nb * bs
+    x = (orc.normal(14, n * hkv * D) * np.float32(3)).reshape(n, hkv, D)
+    c.append(x, -x, np.arange(n, dtype=np.int64))
+    tables = np.arange(nb, dtype=np.int32)[None, :]
+    gk, gv = c.gather(tables, np.array([n], np.int32), None, np.array([0], np.int64), n)
+    rk, rv = gk.reshape(hkv, n, D // 32 * 18), gv.reshape(hkv, n, D // 32 * 18)
+    for h in range(hkv):
+        for t in (0, 1, 37, n - 1):
+            assert bytes(rk[h, t]) == bytes(orc.quantize_row_q4_0(x[t, h]))
+            assert bytes(rv[h, t]) == bytes(orc.quantize_row_q4_0(-x[t, h]))
+
+
+def test_exact_decode_helper_and_closer_check(orc):
+    """The float64 tie-break the GPU decode tests use for fp32 tolerance:
+    exact_decode agrees with the oracle's decode, and a result perturbed by
+    1e-4 is rejected even though the tie-break is consulted."""
+    from kvutil import assert_close_or_closer, exact_decode, random_tables, slots_for
+
+    hq, hkv, D, bs = 6, 2, 128, 16
+    ctx = np.array([40, 77], np.int32)
+    start = np.array([0, 9], np.int32)
+    nb = 8
+    tables = random_tables(3, ctx, bs, nb, 5)
+    seqs = [0] * 40 + [1] * 77
+    pos = list(range(40)) + list(range(77))
+    slots = slots_for(tables, seqs, pos, bs)
+    c = orc.Cache(nb, bs, hkv, D, orc.Q4_0)
+    c.append(orc.normal(5, len(slots) * hkv * D).reshape(-1, hkv, D),
+             orc.normal(6, len(slots) * hkv * D).reshape(-1, hkv, D), slots)
+    q = orc.normal(7, 2 * hq * D).reshape(2, hq, D)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
+    want = c.decode(q, hq, tables, ctx, start, scale)
+    exact = exact_decode(c, q, hq, tables, ctx, start, scale)
+    assert np.max(np.abs(want - exact)) < 1e-5
+    fn = lambda: exact  # noqa: E731
+    assert_close_or_closer(want, want, fn, 1e-5, 1e-6)
+    bad = want.copy()
+    bad[1, 3, 17] += 1e-4
+    with pytest.raises(AssertionError):
+        assert_close_or_closer(bad, want, fn, 1e-5, 1e-6)
+
+
 # ---------------- conversions --------------------------------------------
 def test_f16_bf16_converters_exhaustive():
     exe = os.path.join(ROOT, "oracle", "check_f16")
