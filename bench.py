@@ -763,6 +763,68 @@ def summarize_prefill_profile(d, args):
     print("\n".join(lines))
 
 
+def summarize_config5_profile(d, args):
+    """Summarise rocprofv3 CSVs of `bench.py --only-config5` runs: DIR/trace
+    (--kernel-trace --stats) and DIR/sq0, DIR/sq1 (--pmc, PREFILL_SQ) into
+    profiles/decode_split_config5.md (the Q8_0 split kernel, D 256)."""
+    import csv
+
+    def rows(sub, name):
+        return list(csv.DictReader(open(os.path.join(d, sub, "run_" + name + ".csv"))))
+
+    kname = "paged_decode_split<8, 256"  # Q8_0 (dtype id 8), head_dim 256
+    stats = [r for r in rows("trace", "kernel_stats") if "decode" in r["Name"] or "append" in r["Name"]]
+    trace = [r for r in rows("trace", "kernel_trace") if kname in r["Kernel_Name"]]
+    durs = np.array([(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in trace])
+    rng = np.random.default_rng(5)  # the config-5 contexts, as bench_config5
+    kv_bytes = float(rng.integers(32768, 131073, 16).astype(np.int64).sum()) * 4 * 2 * 256 * 34 / 32
+    cmd = "python3 bench.py --only-config5 --steps {s} --warmup {w}".format(s=args.steps, w=args.warmup)
+    lines = ["# paged_decode_split (Q8_0, D 256) -- config 5 (batch 16, ctx U[32768, 131072], "
+             "Hq 24 / Hkv 4, 1024-token partitions)", "",
+             "Commands (from the repository root on the GPU box; `cd /tmp && export TMPDIR=/tmp` first):", "",
+             "```",
+             f"rocprofv3 --kernel-trace --stats --output-format csv -d OUT/trace -o run -- {cmd}"]
+    for i, grp in enumerate(PREFILL_SQ):
+        lines.append(f"rocprofv3 --pmc {' '.join(grp)} --output-format csv -d OUT/sq{i} -o run -- {cmd}")
+    lines += [f"python3 bench.py --summarize-config5-profile OUT --steps {args.steps} --warmup {args.warmup}", "```",
+              "", "## rocprofv3 --stats (kernel_stats.csv rows of the path's kernels)", "",
+              "| Name | Calls | AverageNs | MinNs | MaxNs |", "|---|---|---|---|---|"]
+    for r in stats:
+        lines.append(f"| `{r['Name'][:80]}` | {r['Calls']} | {float(r['AverageNs']):.0f} | {r['MinNs']} | {r['MaxNs']} |")
+    gbs = kv_bytes / (durs.mean() * 1e-6) / 1e9
+    lines += ["", f"Split kernel, kernel trace: {durs.size} dispatches, mean {durs.mean():.2f} us, median "
+                  f"{np.median(durs):.2f} us -> {gbs:.0f} GB/s of KV bytes ({kv_bytes:.0f} per launch) = "
+                  f"{100 * gbs / HBM_PEAK_GBS:.1f}% of {HBM_PEAK_GBS:.0f} GB/s."]
+    med = {}
+    for i in range(len(PREFILL_SQ)):
+        sub = f"sq{i}"
+        if not os.path.isdir(os.path.join(d, sub)):
+            continue
+        per = {}
+        for r in rows(sub, "counter_collection"):
+            if kname in r["Kernel_Name"]:
+                per.setdefault(r["Counter_Name"], {}).setdefault(r["Dispatch_Id"], 0.0)
+                per[r["Counter_Name"]][r["Dispatch_Id"]] += float(r["Counter_Value"])
+        med.update({k: float(np.median(list(v.values()))) for k, v in per.items()})
+    if med:
+        waves = med.get("SQ_WAVES", 1.0)
+        lines += ["", "## Counters per launch (rocprofv3 --pmc, median over dispatches)", "",
+                  "| Counter | Value | Per wave |", "|---|---|---|"]
+        for grp in PREFILL_SQ:
+            for k in grp:
+                if k in med:
+                    lines.append(f"| {k} | {med[k]:.0f} | {med[k] / waves:.1f} |")
+        if "SQ_VALU_MFMA_BUSY_CYCLES" in med and "SQ_BUSY_CYCLES" in med:
+            # SQ_BUSY_CYCLES sums 32 shader engines of 8 CUs (32 SIMDs) each;
+            # the MFMA busy count sums all 1024 SIMDs.
+            frac = med["SQ_VALU_MFMA_BUSY_CYCLES"] / (med["SQ_BUSY_CYCLES"] * 32)
+            lines += ["", f"MFMA pipe busy {100 * frac:.1f}% of SIMD cycles (SQ_VALU_MFMA_BUSY_CYCLES over "
+                          "SQ_BUSY_CYCLES x 32 SIMDs per shader engine). The kernel is bound by VALU and MFMA "
+                          "issue, not HBM: fp32-exact Q8_0 products run on MFMA as three exact bf16 passes."]
+    open(os.path.join(ROOT, "profiles", "decode_split_config5.md"), "w").write("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -774,6 +836,10 @@ def main():
                     help="first run 4 device copies of 256 MiB (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     ap.add_argument("--only-headline", action="store_true",
                     help="run only the cold config-2 (4k) headline steps (for rocprofv3 runs)")
+    ap.add_argument("--only-config5", action="store_true",
+                    help="time only config 5 (Q8_0 decode), for profiling")
+    ap.add_argument("--summarize-config5-profile", metavar="DIR",
+                    help="summarise rocprofv3 CSVs of --only-config5 runs into profiles/decode_split_config5.md")
     ap.add_argument("--only-prefill", action="store_true",
                     help="run only config 3 (chunk append + causal prefill) (for rocprofv3 runs)")
     ap.add_argument("--summarize-prefill-profile", metavar="DIR",
@@ -787,6 +853,9 @@ def main():
         return
     if args.summarize_prefill_profile:
         summarize_prefill_profile(args.summarize_prefill_profile, args)
+        return
+    if args.summarize_config5_profile:
+        summarize_config5_profile(args.summarize_config5_profile, args)
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus > 1 is not supported. Decode would shard by "
@@ -806,6 +875,12 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+
+    if args.only_config5:
+        r = bench_config5(args.steps, args.warmup, False)
+        print(json.dumps({"only_config5": True, **{k: r[k] for k in ("decode_us", "split_us", "pct_hbm_peak")}}),
+              flush=True)
+        return
 
     if args.only_prefill:
         r = bench_config3(args.steps, args.warmup, False)
