@@ -103,7 +103,7 @@ class DecodeWorkload:
         self.caches = []
         for _ in range(replicas):
             c = PagedKvCache(pool_blocks, bs, hkv, D, dtype)
-            if dtype in (it.Q8_0, it.Q4_0):
+            if dtype in (it.Q8_0, it.Q4_0, it.Q4_1):
                 # Only the pages the tables name are filled, through the
                 # quantising append (N(0,1) with 1% of elements x8).
                 used = np.concatenate([t[b, : (int(cc) + bs - 1) // bs] for b, cc in enumerate(self.ctx)])
@@ -122,19 +122,20 @@ class DecodeWorkload:
                 c.view("k").copy_(torch.randn(c.view("k").shape, generator=g, device=dev).to(td))
                 c.view("v").copy_(torch.randn(c.view("v").shape, generator=g, device=dev).to(td))
             self.caches.append(c)
-        qd = {it.Q8_0: torch.float32, it.Q4_0: torch.float32, it.F32: torch.float32, it.BF16: torch.bfloat16,
-              it.F16: torch.float16}[dtype]
+        qd = {it.Q8_0: torch.float32, it.Q4_0: torch.float32, it.Q4_1: torch.float32, it.F32: torch.float32,
+              it.BF16: torch.bfloat16, it.F16: torch.float16}[dtype]
         self.q = torch.randn((B, hq, D), generator=g, device=dev).to(qd)
-        src_t = torch.float32 if dtype in (it.Q8_0, it.Q4_0, it.F32) else qd
+        src_t = torch.float32 if dtype in (it.Q8_0, it.Q4_0, it.Q4_1, it.F32) else qd
         self.k_new = torch.randn((B, hkv, D), generator=g, device=dev).to(src_t)
         self.v_new = torch.randn((B, hkv, D), generator=g, device=dev).to(src_t)
         self.out = torch.empty((B, hq, D), dtype=qd, device=dev)
         self.max_tokens = int(self.ctx.max())
         self.ws = self.caches[0].decode_workspace(B, hq, self.max_tokens, partition)
         self.scale = 1.0 / math.sqrt(D)
-        elem = {it.BF16: 2.0, it.F16: 2.0, it.F32: 4.0, it.Q8_0: 34.0 / 32.0, it.Q4_0: 18.0 / 32.0}[dtype]
+        elem = {it.BF16: 2.0, it.F16: 2.0, it.F32: 4.0, it.Q8_0: 34.0 / 32.0, it.Q4_0: 18.0 / 32.0,
+                it.Q4_1: 20.0 / 32.0}[dtype]
         self.kv_bytes = float(self.ctx.astype(np.int64).sum()) * hkv * 2 * D * elem
-        src_elem = 4.0 if dtype in (it.Q8_0, it.Q4_0, it.F32) else 2.0
+        src_elem = 4.0 if dtype in (it.Q8_0, it.Q4_0, it.Q4_1, it.F32) else 2.0
         self.append_bytes = B * hkv * 2 * D * (src_elem + elem)
 
     def _split(self, c):
@@ -591,18 +592,20 @@ def bench_config5(steps, warmup, cpu):
     return res
 
 
-def bench_q4_0(steps, warmup):
-    """Q4_0 KV (a format beyond the five configs) on the config-5 shape: Hq 24
-    / Hkv 4 / D 256, block 32, batch 16, ctx U[32768, 131072], 1024-token
-    partitions; quantise-append 1 token per sequence + split-K decode."""
+def bench_q4(dtype, steps, warmup):
+    """Q4_0 / Q4_1 KV (formats beyond the five configs) on the config-5 shape:
+    Hq 24 / Hkv 4 / D 256, block 32, batch 16, ctx U[32768, 131072],
+    1024-token partitions; quantise-append 1 token per sequence + split-K
+    decode."""
     import infer_train_amd as it
 
     rng = np.random.default_rng(5)
     ctx = rng.integers(32768, 131073, 16).astype(np.int32)
     pool_blocks = int(sum((int(c) + 31) // 32 for c in ctx)) + 16
-    w = DecodeWorkload(it.Q4_0, 24, 4, 256, 32, ctx, pool_blocks, 1024, seed=5, replicas=1)
+    w = DecodeWorkload(dtype, 24, 4, 256, 32, ctx, pool_blocks, 1024, seed=5, replicas=1)
     r = w.time(steps, warmup, rotate=False)
-    res = {"workload": "Q4_0 KV on the config-5 shape (Hq 24 / Hkv 4 / D 256, block 32, batch 16, "
+    name = {it.Q4_0: "Q4_0", it.Q4_1: "Q4_1"}[dtype]
+    res = {"workload": f"{name} KV on the config-5 shape (Hq 24 / Hkv 4 / D 256, block 32, batch 16, "
                        "ctx U[32768, 131072], 1024-token partitions), dequantising in registers",
            "kv_bytes": int(w.kv_bytes), "decode_us": round(r["decode"] * 1e3, 2), "split_us": round(r["split"] * 1e3, 2),
            "kv_gbs": round(w.kv_bytes / (r["decode"] * 1e-3) / 1e9, 1),
@@ -917,8 +920,11 @@ def main():
     configs["rope_append"] = bench_rope_append(max(10, args.steps // 2), 3)
     _progress("rope append done")
     if 5 in want:
-        configs["q4_0_config5_shape"] = bench_q4_0(small, 2)
-        _progress("q4_0 done")
+        import infer_train_amd as it
+
+        configs["q4_0_config5_shape"] = bench_q4(it.Q4_0, small, 2)
+        configs["q4_1_config5_shape"] = bench_q4(it.Q4_1, small, 2)
+        _progress("q4_0 / q4_1 done")
 
     cold, warm = head["cold"], head["warm"]
     kv_bytes = head["kv_bytes"]

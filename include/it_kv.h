@@ -38,6 +38,7 @@ extern "C" {
 #define IT_F32 0
 #define IT_F16 1
 #define IT_Q4_0 2
+#define IT_Q4_1 3
 #define IT_Q8_0 8
 #define IT_BF16 30
 
@@ -46,6 +47,8 @@ extern "C" {
 #define IT_BLOCK_Q8_0_BYTES 34  /* sizeof(BlockQ8_0), src/types.rs:34-41,250 */
 #define IT_QK4_0 32             /* src/types.rs:7 */
 #define IT_BLOCK_Q4_0_BYTES 18  /* sizeof(BlockQ4_0), src/types.rs:15-22 */
+#define IT_QK4_1 32             /* src/types.rs:8 */
+#define IT_BLOCK_Q4_1_BYTES 20  /* sizeof(BlockQ4_1), src/types.rs:24-32,249 */
 
 /* ---- operator ids for it_supports (Backend::supports_op/_quant,
  *      src/backend.rs:184-186) ------------------------------------------- */
@@ -148,6 +151,8 @@ int32_t it_kv_manager_tables(const it_kv_manager* mgr, int32_t* tables, int32_t 
 /*   Q4_0 page: u8 qs[block_size][head_dim/2] (each 32-group's 16 bytes as   */
 /*   in BlockQ4_0: low nibble = element j, high = element j+16), then fp16   */
 /*   d[block_size][head_dim/32] (src/types.rs:15-22).                        */
+/*   Q4_1 page: the Q4_0 nibble plane, then fp16 (d, m) pairs                */
+/*   [block_size][head_dim/32] (BlockQ4_1, src/types.rs:24-32).              */
 /* ======================================================================== */
 typedef struct it_kv_cache it_kv_cache;
 
@@ -188,7 +193,9 @@ int32_t it_kv_cache_check(it_kv_cache* cache, void* stream);
  * cache takes F32 and quantises each 32-group exactly as
  * quantize_row_q8_0 (src/backend/arm/quant.rs:149-183).  A Q4_0 cache takes
  * F32 and quantises as ggml's quantize_row_q4_0_ref (the reference has the
- * block and its dequantisation, vec_dot.rs:425-440, but no quantiser). */
+ * block and its dequantisation, vec_dot.rs:425-440, but no quantiser).  A
+ * Q4_1 cache takes F32 and quantises as ggml's quantize_row_q4_1_ref (the
+ * reference has only the block). */
 int32_t it_kv_append(it_kv_cache* cache, const void* k, const void* v, int32_t src_dtype,
                      const int64_t* slot_mapping, int32_t n_tokens, void* stream);
 
@@ -206,8 +213,8 @@ int32_t it_kv_append(it_kv_cache* cache, const void* k, const void* v, int32_t s
  *   q_out: [n_tokens][n_heads][head_dim] of q_out_dtype: F32, or the cache
  *          dtype for BF16/F16 caches (round to nearest even)
  * F32 caches store the rotated fp32 values; BF16/F16 caches round them to
- * nearest even; Q8_0 caches quantise them as quantize_row_q8_0.  (Q4_0
- * caches: IT_NOT_IMPLEMENTED.) */
+ * nearest even; Q8_0 caches quantise them as quantize_row_q8_0.  (Q4_0 and
+ * Q4_1 caches: IT_NOT_IMPLEMENTED.) */
 typedef struct it_rope_table it_rope_table;
 /* n_dims: a multiple of 4 up to 4096; positions [0, max_pos); device memory
  * max_pos * n_dims * 4 bytes. */
@@ -228,7 +235,7 @@ int32_t it_kv_append_rope(it_kv_cache* cache, const it_rope_table* rope, const f
  * Output for sequence b: [n_kv_heads][ctx_b - start_b][head_dim] at token
  * offset cu_out[b] (element offset cu_out[b]*n_kv_heads*head_dim).  A Q8_0
  * cache writes packed 34-byte BlockQ8_0 records, head_dim/32 per row; a Q4_0
- * cache 18-byte BlockQ4_0 records. */
+ * cache 18-byte BlockQ4_0 records, a Q4_1 cache 20-byte BlockQ4_1 ones. */
 int32_t it_kv_gather(const it_kv_cache* cache, const int32_t* block_tables, int32_t max_blocks,
                      const int32_t* ctx_lens, const int32_t* start_pos, const int64_t* cu_out,
                      int32_t n_seqs, int32_t max_tokens, void* k_out, void* v_out, void* stream);
@@ -263,7 +270,7 @@ size_t it_paged_decode_workspace(int32_t n_seqs, int32_t n_heads, int32_t head_d
  * and query head h the result equals flash_attn_f32 (flash_attn.rs:6-72)
  * over keys start_b..ctx_b-1 of KV head h*Hkv/Hq (forward.rs:231-254),
  * within fp32 tolerance.
- *   q: [n_seqs][n_heads][head_dim]; q_dtype F32 (F32, Q8_0, Q4_0 caches),
+ *   q: [n_seqs][n_heads][head_dim]; q_dtype F32 (F32, Q8_0, Q4_0, Q4_1 caches),
  *      BF16 (BF16 cache) or F16 (F16 cache)
  *   block_tables/ctx_lens/start_pos: as it_kv_gather
  *   max_tokens: upper bound of ctx_b - start_b

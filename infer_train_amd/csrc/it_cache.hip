@@ -8,6 +8,7 @@
 // 128-byte lines of both source and destination.
 #include <hip/hip_runtime.h>
 
+#include <cfloat>
 #include <cstring>
 
 #include "it_device.hpp"
@@ -188,6 +189,83 @@ __global__ __launch_bounds__(kThreads) void kv_append_q4_0(
 }
 
 // ---------------------------------------------------------------------------
+// Append with Q4_1 quantisation.  The reference carries only the block
+// (types.rs:24-32); this is ggml's quantize_row_q4_1_ref as its x86 build
+// computes it: min / max of the group (strict compares, so NaN never wins
+// and of equal values -- +0 and -0 -- the first stays), d = (max - min) /
+// 15, id = d ? 1/d : 0, nibble = min(15, (int8_t)((x - min) * id + 0.5f))
+// with each operation rounded, d and m = min stored as fp16.  Lanes as in
+// kv_append_q4_0.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t q41_byte(float x, float mn, float id) {
+  float r;
+  const float t = x - mn;
+  asm("v_mul_f32 %0, %1, %2" : "=v"(r) : "v"(t), "v"(id));  // no FMA with the add
+  r += 0.5f;
+  if (!(fabsf(r) < 2147483648.0f)) return 0u;
+  const int32_t q = min(int32_t(int8_t(int32_t(r))), 15);
+  return uint32_t(q) & 0xFFu;
+}
+
+__global__ __launch_bounds__(kThreads) void kv_append_q4_1(
+    const float4* __restrict__ k, const float4* __restrict__ v, char* __restrict__ kpool,
+    char* __restrict__ vpool, const int64_t* __restrict__ slots, int64_t total, int hkv, int d,
+    int log2_bs, int64_t page_bytes, int64_t n_slots, uint32_t* err) {
+  const int64_t gid = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  const bool is_v = blockIdx.y != 0;
+  const bool live = gid < total;
+  const float4 x = live ? (is_v ? v[gid] : k[gid]) : make_float4(0.f, 0.f, 0.f, 0.f);
+  const int l8 = int(gid & 7);
+  // (value, element index) of the group's min and max; on equal values the
+  // lower index wins, as the sequential scan keeps the first.
+  float mn = FLT_MAX, mx = -FLT_MAX;
+  int imn = 32, imx = 32;
+  const float xs[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    if (xs[e] < mn) mn = xs[e], imn = 4 * l8 + e;
+    if (xs[e] > mx) mx = xs[e], imx = 4 * l8 + e;
+  }
+  auto step = [&](auto ctrl) {
+    constexpr int C = decltype(ctrl)::value;
+    const float mn2 = dpp_f<C>(mn), mx2 = dpp_f<C>(mx);
+    const int imn2 = __builtin_amdgcn_mov_dpp(imn, C, 0xF, 0xF, true);
+    const int imx2 = __builtin_amdgcn_mov_dpp(imx, C, 0xF, 0xF, true);
+    if (mn2 < mn || (mn2 == mn && imn2 < imn)) mn = mn2, imn = imn2;
+    if (mx2 > mx || (mx2 == mx && imx2 < imx)) mx = mx2, imx = imx2;
+  };
+  step(std::integral_constant<int, kDppQuadXor1>{});
+  step(std::integral_constant<int, kDppQuadXor2>{});
+  step(std::integral_constant<int, kDppHalfMirror>{});
+  const float dq = (mx - mn) / 15.0f;
+  const float id = dq != 0.0f ? 1.0f / dq : 0.0f;
+  const uint32_t mine = q41_byte(x.x, mn, id) | (q41_byte(x.y, mn, id) << 8) | (q41_byte(x.z, mn, id) << 16) |
+                        (q41_byte(x.w, mn, id) << 24);
+  const uint32_t partner = uint32_t(__builtin_amdgcn_mov_dpp(int(mine), 0x104, 0xF, 0xF, true));
+  if (!live || l8 >= 4) return;
+  const int vecs_per_row = d >> 2;
+  const int cv = int(gid % vecs_per_row);
+  const int64_t th = gid / vecs_per_row;
+  const int h = int(th % hkv);
+  const int64_t t = th / hkv;
+  const int64_t slot = slots[t];
+  if (slot < 0) return;
+  if (slot >= n_slots) {
+    if (cv == 0 && h == 0) atomicOr(err, kErrSlot);
+    return;
+  }
+  const int64_t blk = slot >> log2_bs;
+  const int64_t off = slot & ((int64_t(1) << log2_bs) - 1);
+  const int64_t bs = int64_t(1) << log2_bs;
+  const int g = cv >> 3;
+  char* page = (is_v ? vpool : kpool) + (blk * hkv + h) * page_bytes;
+  *reinterpret_cast<uint32_t*>(page + off * (d >> 1) + g * 16 + l8 * 4) = mine | ((partner & 0x0F0F0F0Fu) << 4);
+  if (l8 == 0)
+    *reinterpret_cast<uint32_t*>(page + bs * (d >> 1) + (off * (d >> 5) + g) * 4) =
+        f32_to_f16_bits(dq) | (f32_to_f16_bits(mn) << 16);
+}
+
+// ---------------------------------------------------------------------------
 // Gather.  grid.y = sequence; lane = one 16-byte vector of one output row.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(kThreads) void kv_gather_vec(
@@ -318,6 +396,51 @@ __global__ __launch_bounds__(kThreads) void kv_gather_q4_0(
   }
 }
 
+// Q4_1 gather: lane = one 32-element group, written as a packed 20-byte
+// BlockQ4_1 record {u16 d; u16 m; u8 qs[16]} (types.rs:24-32).
+__global__ __launch_bounds__(kThreads) void kv_gather_q4_1(
+    const char* __restrict__ kpool, const char* __restrict__ vpool, const int32_t* __restrict__ bt,
+    int max_blocks, const int32_t* __restrict__ ctx_lens, const int32_t* __restrict__ start_pos,
+    const int64_t* __restrict__ cu_out, int hkv, int d, int log2_bs, int64_t page_bytes,
+    int64_t num_blocks, char* __restrict__ kout, char* __restrict__ vout, uint32_t* err) {
+  const int b = blockIdx.y;
+  const int st = start_pos ? start_pos[b] : 0;
+  const int n = ctx_lens[b] - st;
+  if (n <= 0 || st < 0) return;
+  const int ng = d >> 5;
+  const int64_t gid = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  if (gid >= int64_t(hkv) * n * ng) return;
+  const int g = int(gid % ng);
+  const int64_t r = gid / ng;
+  const int i = int(r % n);
+  const int h = int(r / n);
+  const int pos = st + i;
+  const int lb = pos >> log2_bs;
+  if (lb >= max_blocks) {
+    atomicOr(err, kErrTable);
+    return;
+  }
+  const int blk = bt[int64_t(b) * max_blocks + lb];
+  if (blk < 0 || blk >= num_blocks) {
+    atomicOr(err, kErrBlock);
+    return;
+  }
+  const int64_t bs = int64_t(1) << log2_bs;
+  const int64_t off = pos & (bs - 1);
+  const int64_t rec = ((cu_out[b] * hkv + int64_t(h) * n + i) * ng + g) * 20;
+  for (int which = 0; which < 2; ++which) {
+    const char* page = (which ? vpool : kpool) + (int64_t(blk) * hkv + h) * page_bytes;
+    const uint4 q = ld16(page + off * (d >> 1) + g * 16);
+    const uint32_t dm = *reinterpret_cast<const uint32_t*>(page + bs * (d >> 1) + (off * ng + g) * 4);
+    uint32_t* o = reinterpret_cast<uint32_t*>((which ? vout : kout) + rec);  // 4-byte aligned
+    o[0] = dm;
+    o[1] = q.x;
+    o[2] = q.y;
+    o[3] = q.z;
+    o[4] = q.w;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Evict (zero pages) and copy-on-write page copy.  grid.y = list entry.
 // ---------------------------------------------------------------------------
@@ -386,12 +509,12 @@ int32_t check_shape(int64_t num_blocks, int32_t block_size, int32_t n_kv_heads, 
                 (long long)num_blocks, n_kv_heads, head_dim);
   if (!is_pow2(block_size) || block_size > 1024)
     return fail(IT_NOT_IMPLEMENTED, "kv cache: block_size %d must be a power of two <= 1024", block_size);
-  if (dtype == IT_Q8_0 || dtype == IT_Q4_0) {
-    if (head_dim % 32) return fail(IT_INVALID_INPUT, "kv cache: Q8_0/Q4_0 need head_dim %% 32 == 0");
-    if (block_size < 8) return fail(IT_NOT_IMPLEMENTED, "kv cache: Q8_0/Q4_0 need block_size >= 8");
+  if (dtype == IT_Q8_0 || dtype == IT_Q4_0 || dtype == IT_Q4_1) {
+    if (head_dim % 32) return fail(IT_INVALID_INPUT, "kv cache: Q8_0/Q4_0/Q4_1 need head_dim %% 32 == 0");
+    if (block_size < 8) return fail(IT_NOT_IMPLEMENTED, "kv cache: Q8_0/Q4_0/Q4_1 need block_size >= 8");
   } else if (dtype_bytes(dtype) == 0) {
-    return fail(IT_NOT_IMPLEMENTED, "kv cache: dtype %d not supported (F32=0, F16=1, Q4_0=2, Q8_0=8, BF16=30)",
-                dtype);
+    return fail(IT_NOT_IMPLEMENTED,
+                "kv cache: dtype %d not supported (F32=0, F16=1, Q4_0=2, Q4_1=3, Q8_0=8, BF16=30)", dtype);
   } else if ((head_dim * dtype_bytes(dtype)) % 16) {
     return fail(IT_NOT_IMPLEMENTED, "kv cache: head_dim*elem_bytes must be a multiple of 16");
   }
@@ -443,6 +566,7 @@ extern "C" int64_t it_kv_page_bytes(int32_t block_size, int32_t head_dim, int32_
   if (block_size <= 0 || head_dim <= 0) return -1;
   if (dtype == IT_Q8_0) return int64_t(block_size) * head_dim + int64_t(block_size) * (head_dim / IT_QK8_0) * 2;
   if (dtype == IT_Q4_0) return int64_t(block_size) * (head_dim / 2) + int64_t(block_size) * (head_dim / IT_QK4_0) * 2;
+  if (dtype == IT_Q4_1) return int64_t(block_size) * (head_dim / 2) + int64_t(block_size) * (head_dim / IT_QK4_1) * 4;
   int64_t e = dtype_bytes(dtype);
   return e ? int64_t(block_size) * head_dim * e : -1;
 }
@@ -531,17 +655,19 @@ extern "C" int32_t it_kv_append(it_kv_cache* c, const void* k, const void* v, in
   if (n_tokens < 0) return fail(IT_INVALID_INPUT, "it_kv_append: n_tokens %d < 0", n_tokens);
   if (n_tokens == 0) return IT_OK;
   if (!k || !v || !slots) return fail(IT_INVALID_INPUT, "it_kv_append: NULL tensor");
-  const int32_t want = (c->dtype == IT_Q8_0 || c->dtype == IT_Q4_0) ? IT_F32 : c->dtype;
+  const bool quant = c->dtype == IT_Q8_0 || c->dtype == IT_Q4_0 || c->dtype == IT_Q4_1;
+  const int32_t want = quant ? IT_F32 : c->dtype;
   if (src_dtype != want)
     return fail(IT_NOT_IMPLEMENTED, "it_kv_append: cache dtype %d takes source dtype %d, got %d", c->dtype, want, src_dtype);
   if (!aligned16(k) || !aligned16(v)) return fail(IT_INVALID_INPUT, "it_kv_append: k/v must be 16-byte aligned");
   DeviceGuard g(c->device);
   hipStream_t s = (hipStream_t)stream;
   const int64_t n_slots = c->num_blocks << c->log2_bs;
-  if (c->dtype == IT_Q8_0 || c->dtype == IT_Q4_0) {
+  if (quant) {
     const int64_t total = int64_t(n_tokens) * c->n_kv_heads * (c->head_dim / 4);
     dim3 grid(unsigned(cdiv(total, kThreads)), 2);
-    hipLaunchKernelGGL(c->dtype == IT_Q8_0 ? kv_append_q8_0 : kv_append_q4_0, grid, dim3(kThreads), 0, s,
+    auto* kern = c->dtype == IT_Q8_0 ? kv_append_q8_0 : (c->dtype == IT_Q4_0 ? kv_append_q4_0 : kv_append_q4_1);
+    hipLaunchKernelGGL(kern, grid, dim3(kThreads), 0, s,
                        (const float4*)k, (const float4*)v, (char*)c->k_pool, (char*)c->v_pool, slots, total,
                        c->n_kv_heads, c->head_dim, c->log2_bs, c->page_bytes, n_slots, c->err_flag);
   } else {
@@ -567,10 +693,11 @@ extern "C" int32_t it_kv_gather(const it_kv_cache* c, const int32_t* bt, int32_t
   if (n_seqs > 65535) return fail(IT_NOT_IMPLEMENTED, "it_kv_gather: n_seqs %d > 65535", n_seqs);
   DeviceGuard g(c->device);
   hipStream_t s = (hipStream_t)stream;
-  if (c->dtype == IT_Q8_0 || c->dtype == IT_Q4_0) {
+  if (c->dtype == IT_Q8_0 || c->dtype == IT_Q4_0 || c->dtype == IT_Q4_1) {
     const int64_t per_seq = int64_t(c->n_kv_heads) * max_tokens * (c->head_dim / 32);
     dim3 grid(unsigned(cdiv(per_seq, kThreads)), unsigned(n_seqs));
-    hipLaunchKernelGGL(c->dtype == IT_Q8_0 ? kv_gather_q8_0 : kv_gather_q4_0, grid, dim3(kThreads), 0, s,
+    auto* kern = c->dtype == IT_Q8_0 ? kv_gather_q8_0 : (c->dtype == IT_Q4_0 ? kv_gather_q4_0 : kv_gather_q4_1);
+    hipLaunchKernelGGL(kern, grid, dim3(kThreads), 0, s,
                        (const char*)c->k_pool, (const char*)c->v_pool,
                        bt, max_blocks, ctx_lens, start_pos, cu_out, c->n_kv_heads, c->head_dim, c->log2_bs,
                        c->page_bytes, c->num_blocks, (char*)k_out, (char*)v_out, c->err_flag);
@@ -632,7 +759,8 @@ extern "C" int32_t it_kv_copy_blocks(it_kv_cache* c, const int32_t* src, const i
 }
 
 extern "C" int32_t it_supports(int32_t op, int32_t dtype) {
-  const bool kv = dtype == IT_F32 || dtype == IT_F16 || dtype == IT_BF16 || dtype == IT_Q8_0 || dtype == IT_Q4_0;
+  const bool kv = dtype == IT_F32 || dtype == IT_F16 || dtype == IT_BF16 || dtype == IT_Q8_0 || dtype == IT_Q4_0 ||
+                  dtype == IT_Q4_1;
   switch (op) {
     case IT_OP_KV_APPEND:
     case IT_OP_KV_GATHER:

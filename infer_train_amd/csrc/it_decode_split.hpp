@@ -54,7 +54,10 @@
 // Q4_0 (BlockQ4_0, src/types.rs:15-22): a page is u8 qs[bs][D/2], each
 // group's 16 bytes holding element j in the low nibble of byte j and
 // element j + 16 in the high nibble, then fp16 d[bs][D/32]; a value element
-// is f32(d) * (nibble - 8) (vec_dot.rs:425-440), exact in fp32.
+// is f32(d) * (nibble - 8) (vec_dot.rs:425-440), exact in fp32.  Q4_1
+// (BlockQ4_1, src/types.rs:24-32): the same nibbles, then fp16 (d, m) pairs;
+// a value is f32(d) * nibble + f32(m) (ggml), taken here as f32(d) (nibble -
+// 8) + m' with m' = m + 8 d, the offset term a further small MFMA product.
 #pragma once
 #include <hip/hip_runtime.h>
 
@@ -71,16 +74,18 @@ template <int DT, int D>
 struct SplitFmt {
   static constexpr bool k16 = DT == IT_BF16 || DT == IT_F16;
   static constexpr bool kQ8 = DT == IT_Q8_0;
-  static constexpr bool kQ4 = DT == IT_Q4_0;
+  static constexpr bool kQ41 = DT == IT_Q4_1;                      // Q4_1: (d, m) per group
+  static constexpr bool kQ4 = DT == IT_Q4_0 || kQ41;               // nibble planes
   static constexpr bool kQuant = kQ8 || kQ4;                       // MFMA products, fp16 group scales
   static constexpr int kElem = DT == IT_F32 ? 4 : (kQuant ? 1 : 2);  // bytes per main-plane element
   static constexpr int kRow = kQ4 ? D / 2 : D * kElem;            // main-plane bytes per token
   static constexpr int kGroup = kGroupTok * kRow;                 // main-plane bytes per group
   static constexpr int kDma = kGroup / 1024;                      // 16-byte-per-lane loads per group
-  static constexpr int kScaleRow = kQuant ? D / 16 : 0;           // fp16 scales per token (bytes)
-  static constexpr int kScaleGroup = kGroupTok * kScaleRow;       // 128 or 256 B (one dword load)
+  static constexpr int kScaleRow = kQuant ? (kQ41 ? D / 8 : D / 16) : 0;  // group scales per token (bytes)
+  static constexpr int kScaleGroup = kGroupTok * kScaleRow;       // 128..512 B
+  static constexpr int kScaleLoads = (kScaleGroup + 255) / 256;   // dword loads (64 lanes x 4 B) per group
   static constexpr int kSlot = kGroup + kScaleGroup;
-  static constexpr int kLoads = kDma + (kQuant ? 1 : 0);          // vmcnt units per group
+  static constexpr int kLoads = kDma + kScaleLoads;               // vmcnt units per group
   static constexpr int kPieces = D / 4 * kElem / 16;              // 16-byte pieces per lane in QK
   static constexpr int kRowPieces = kRow / 16;
   static constexpr int kSwz = (kRowPieces < 16 ? kRowPieces : 16) - 1;  // piece swizzle mask
@@ -88,7 +93,7 @@ struct SplitFmt {
   static constexpr int kDpv = D / 64;                             // PV dims per lane
   static constexpr int kScratch = k16 ? 256 : 512;                // probability scratch per wave (B)
   static_assert(D == 128 || D == 256, "head_dim 128 or 256");
-  static_assert(kGroup % 1024 == 0 && kScaleGroup <= 256, "group geometry");
+  static_assert(kGroup % 1024 == 0 && kScaleGroup <= 512, "group geometry");
 };
 
 template <int DT>
@@ -101,6 +106,7 @@ inline int split_slot_bytes(int32_t dt, int d) {
     case IT_F16: return split_slot_bytes<IT_F16>(d);
     case IT_F32: return split_slot_bytes<IT_F32>(d);
     case IT_Q4_0: return split_slot_bytes<IT_Q4_0>(d);
+    case IT_Q4_1: return split_slot_bytes<IT_Q4_1>(d);
     default: return split_slot_bytes<IT_Q8_0>(d);
   }
 }
@@ -292,6 +298,12 @@ __device__ __forceinline__ uint4 nib8_bf16(uint32_t w) {
   return make_uint4(pair(i8_f32<0>(lo), i8_f32<1>(lo)), pair(i8_f32<2>(lo), i8_f32<3>(lo)),
                     pair(i8_f32<0>(hi), i8_f32<1>(hi)), pair(i8_f32<2>(hi), i8_f32<3>(hi)));
 }
+// Q4_1 value d n + m taken as d (n - 8) + m', m' = m + 8 d: the nibble part
+// is Q4_0's, and m' sits near the group's mean, so neither part is much
+// larger than the value (with m the group minimum the two would cancel).
+__device__ __forceinline__ float q41_offset(uint32_t dm) {
+  return fmaf(8.0f, f16_bits_to_f32(dm & 0xFFFFu), f16_bits_to_f32(dm >> 16));
+}
 // x = hi + mid + lo exactly, each part a bf16 (round to nearest even): the
 // three parts carry the 24 significant bits of an fp32.  Two values per
 // packed word (lo element first).  No inline asm here: the compiler's hazard
@@ -364,7 +376,7 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
   using F = SplitFmt<DT, D>;
   constexpr int RB = F::kRow, GB = F::kGroup, SLOT = F::kSlot, NI = F::kDma, NL = F::kLoads;
   constexpr int PQ = F::kPieces, NQ = F::kQRegs, DPV = F::kDpv;
-  constexpr bool k16 = F::k16, kQ = F::kQuant, kQ4 = F::kQ4;
+  constexpr bool k16 = F::k16, kQ = F::kQuant, kQ4 = F::kQ4, kQ41 = F::kQ41;
   constexpr int NT = 64 * NW;  // threads
   static_assert(GC >= 1 && GC <= 8, "1..8 heads per workgroup");
   static_assert(NW == 2 || NW == 4, "2 or 4 waves");
@@ -434,6 +446,10 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
   // 4 kh .. + 4 (the low and high nibbles of bytes 4 kh .. + 4 of the group).
   constexpr int NK = kQ ? D / 32 : 1;  // 32-groups (MFMA k-steps) per row
   uint4 qa[3][NK];
+  // Q4_1: sum of q over each 32-group, the A operand of the offset-term MFMA
+  // (v_mfma_f32_16x16x16_bf16, k = group): lane (kh, h) holds groups
+  // 4 kh .. + 4 of head h, split exactly into three bf16 parts.
+  uint2 qs_a[3];
   if constexpr (!kQ) {
     const uint32_t* qp = static_cast<const uint32_t*>(a.q) +
                          (int64_t(b) * a.n_heads + head0) * (k16 ? D / 2 : D) + qr_row * (k16 ? D / 8 : D / 4) +
@@ -453,15 +469,32 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
     const int hq = lane & 15;
     const float* qp = static_cast<const float*>(a.q) + (int64_t(b) * a.n_heads + head0 + (hq < GC ? hq : 0)) * D +
                       (kQ4 ? 4 : 8) * qr_row;
+    float qsum[NK];
 #pragma unroll
     for (int ks = 0; ks < NK; ++ks) {
       float4 x0 = *reinterpret_cast<const float4*>(qp + 32 * ks);
       float4 x1 = *reinterpret_cast<const float4*>(qp + 32 * ks + (kQ4 ? 16 : 4));
       if (hq >= GC) x0 = x1 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if constexpr (kQ41) qsum[ks] = ((x0.x + x0.y) + (x0.z + x0.w)) + ((x1.x + x1.y) + (x1.z + x1.w));
       split3_bf16(x0.x, x0.y, qa[0][ks].x, qa[1][ks].x, qa[2][ks].x);
       split3_bf16(x0.z, x0.w, qa[0][ks].y, qa[1][ks].y, qa[2][ks].y);
       split3_bf16(x1.x, x1.y, qa[0][ks].z, qa[1][ks].z, qa[2][ks].z);
       split3_bf16(x1.z, x1.w, qa[0][ks].w, qa[1][ks].w, qa[2][ks].w);
+    }
+    if constexpr (kQ41) {
+      float qg[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int ks = 0; ks < NK; ++ks) {
+        qsum[ks] += __shfl_xor(qsum[ks], 16);  // the four lanes of head hq
+        qsum[ks] += __shfl_xor(qsum[ks], 32);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (ks == 4 * qr_row + j) qg[j] = qsum[ks];
+      }
+      uint2 p0, p1, p2;
+      split3_bf16(qg[0], qg[1], p0.x, p1.x, p2.x);
+      split3_bf16(qg[2], qg[3], p0.y, p1.y, p2.y);
+      qs_a[0] = p0, qs_a[1] = p1, qs_a[2] = p2;
     }
 #pragma unroll
     for (int p = 0; p < 3; ++p)
@@ -495,8 +528,18 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
     lane_off_k[j] = tt * RB + ((ps ^ (tt & F::kSwz)) << 4);
     lane_off_v[j] = tt * RB + (ps << 4);
   }
-  const int s_row = kQ ? (4 * lane) / (F::kScaleRow > 0 ? F::kScaleRow : 1) : 0;  // scale row of this lane
-  const bool s_lane = 4 * lane < F::kScaleGroup;
+  // Scale loads: load u moves bytes [256 u + 4 lane, +4) of the group's
+  // scale rows (row s_row[u], byte s_col[u]) when that is inside them.
+  constexpr int NS = F::kScaleLoads > 0 ? F::kScaleLoads : 1;
+  int s_row[NS], s_col[NS];
+  bool s_lane[NS];
+#pragma unroll
+  for (int u = 0; u < NS; ++u) {
+    const int sb = 256 * u + 4 * lane;
+    s_lane[u] = sb < F::kScaleGroup;
+    s_row[u] = kQ ? sb / (F::kScaleRow > 0 ? F::kScaleRow : 1) : 0;
+    s_col[u] = kQ ? sb % (F::kScaleRow > 0 ? F::kScaleRow : 1) : 0;
+  }
   auto issue = [&](int s) {
     const bool is_v = s >= ns;
     const int gi = is_v ? s - ns : s;
@@ -518,10 +561,13 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
         dma_b128(base + off, __builtin_amdgcn_readfirstlane(m0 + 1024u * j));
       }
       if constexpr (kQ) {
-        int row = s_row;
-        if (!full && tb + row >= nt) row = 0;
-        const char* g = pbase + uint32_t(bs * RB + (in_page + row) * F::kScaleRow + (4 * lane) % F::kScaleRow);
-        if (s_lane) dma_b32(g, __builtin_amdgcn_readfirstlane(m0 + uint32_t(GB)));
+#pragma unroll
+        for (int u = 0; u < F::kScaleLoads; ++u) {
+          int row = s_row[u];
+          if (!full && tb + row >= nt) row = 0;
+          const char* g = pbase + uint32_t(bs * RB + (in_page + row) * F::kScaleRow + s_col[u]);
+          if (s_lane[u]) dma_b32(g, __builtin_amdgcn_readfirstlane(m0 + uint32_t(GB + 256 * u)));
+        }
       }
     } else {
 #pragma unroll
@@ -536,13 +582,16 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
         dma_b128(g, __builtin_amdgcn_readfirstlane(m0 + 1024u * j));
       }
       if constexpr (kQ) {
-        int tr = tb + s_row;
-        if (tr >= nt) tr = tb;
-        const int t = tok0 + tr;
-        const uint32_t page = uint32_t(s_pages[(t >> a.log2_bs) - lb0]);
-        const char* g = pool + (uint64_t(page) * page_bytes +
-                                uint32_t(bs * RB + (t & bs_mask) * F::kScaleRow + (4 * lane) % F::kScaleRow));
-        if (s_lane) dma_b32(g, __builtin_amdgcn_readfirstlane(m0 + uint32_t(GB)));
+#pragma unroll
+        for (int u = 0; u < F::kScaleLoads; ++u) {
+          int tr = tb + s_row[u];
+          if (tr >= nt) tr = tb;
+          const int t = tok0 + tr;
+          const uint32_t page = uint32_t(s_pages[(t >> a.log2_bs) - lb0]);
+          const char* g =
+              pool + (uint64_t(page) * page_bytes + uint32_t(bs * RB + (t & bs_mask) * F::kScaleRow + s_col[u]));
+          if (s_lane[u]) dma_b32(g, __builtin_amdgcn_readfirstlane(m0 + uint32_t(GB + 256 * u)));
+        }
       }
     }
   };
@@ -579,7 +628,7 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
       uint16_t dsc[NK];
 #pragma unroll
       for (int ks = 0; ks < NK; ++ks)
-        dsc[ks] = *reinterpret_cast<const uint16_t*>(slot + GB + qk_tok * F::kScaleRow + 2 * ks);
+        dsc[ks] = *reinterpret_cast<const uint16_t*>(slot + GB + qk_tok * F::kScaleRow + (kQ41 ? 4 : 2) * ks);
       // All K reads first; then the three passes of each group are software
       // pipelined across groups, so that no MFMA waits for the one before it.
       uint2 kr[NK];
@@ -610,6 +659,26 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
         const float d = f16_bits_to_f32(dsc[ks]) * (kQ4 ? 0.0625f : 1.0f);  // exact
 #pragma unroll
         for (int i = 0; i < 4; ++i) sv[i] = fmaf(d, acc[ks][i], sv[i]);
+      }
+      if constexpr (kQ41) {
+        // + sum over groups G of m'_G(t) qsum[h][G]: lane (kh, t) holds
+        // B[G = 4 kh + j][t] = m'_G(t), zero past the groups; both operands
+        // in three exact bf16 parts.
+        float mv[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int G = 4 * qr_row + j;
+          mv[j] = G < NK ? q41_offset(*reinterpret_cast<const uint32_t*>(slot + GB + qk_tok * F::kScaleRow +
+                                                                          4 * (G < NK ? G : 0)))
+                         : 0.0f;
+        }
+        uint2 mb[3];
+        split3_bf16(mv[0], mv[1], mb[0].x, mb[1].x, mb[2].x);
+        split3_bf16(mv[2], mv[3], mb[0].y, mb[1].y, mb[2].y);
+#pragma unroll
+        for (int p = 0; p < 3; ++p)
+#pragma unroll
+          for (int r = 0; r < 3; ++r) sv = mfma16k16(qs_a[p], mb[r], sv);
       }
       const int i_tok = (s * NW + wave) * kGroupTok + qk_tok;
       if (i_tok < nt) {
@@ -736,6 +805,7 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
   // hm] (the MFMA's k index is j + 4 kq in both), and ends holding
   // O[4 kq + i][column hm] of every tile.
   v4f o8[kQ ? NK : 1][2];
+  v4f mo = {0.0f, 0.0f, 0.0f, 0.0f};  // Q4_1: sum_t p[4 kq + i][t] m'_hm(t)
   if constexpr (kQ) {
     const int hm = lane & 15, kq = qr_row;
 #pragma unroll
@@ -761,7 +831,9 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
           const int o = 1024 * j + 16 * lane;
           if (tb + o / RB >= nt) *reinterpret_cast<uint4*>(slot + o) = make_uint4(0u, 0u, 0u, 0u);
         }
-        if (s_lane && tb + s_row >= nt) *reinterpret_cast<uint32_t*>(slot + GB + 4 * lane) = 0u;
+#pragma unroll
+        for (int u = 0; u < F::kScaleLoads; ++u)
+          if (s_lane[u] && tb + s_row[u] >= nt) *reinterpret_cast<uint32_t*>(slot + GB + 256 * u + 4 * lane) = 0u;
       }
       const float4 sv = *reinterpret_cast<const float4*>(sc_h + tb);
       const float sj[4] = {sv.x, sv.y, sv.z, sv.w};
@@ -770,6 +842,26 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
       for (int j = 0; j < 4; ++j)
         pj[j] = (tb + 4 * kq + j < nt && !none_h) ? __builtin_amdgcn_exp2f(sj[j] - m_h) : 0.0f;
       lsum += (pj[0] + pj[1]) + (pj[2] + pj[3]);
+      if constexpr (kQ41) {
+        // The offset term: M[h][G] += sum over the item's tokens of p[h][t]
+        // m'_G(t); B[t][G = hm] for the lane's four tokens, zero past the
+        // groups; both operands in three exact bf16 parts.
+        float mv[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          mv[j] = hm < NK ? q41_offset(*reinterpret_cast<const uint32_t*>(slot + GB + (4 * kq + j) * F::kScaleRow +
+                                                                           4 * (hm < NK ? hm : 0)))
+                          : 0.0f;
+        uint2 mb[3], pa[3];
+        split3_bf16(mv[0], mv[1], mb[0].x, mb[1].x, mb[2].x);
+        split3_bf16(mv[2], mv[3], mb[0].y, mb[1].y, mb[2].y);
+        split3_bf16(pj[0], pj[1], pa[0].x, pa[1].x, pa[2].x);
+        split3_bf16(pj[2], pj[3], pa[0].y, pa[1].y, pa[2].y);
+#pragma unroll
+        for (int p = 0; p < 3; ++p)
+#pragma unroll
+          for (int r = 0; r < 3; ++r) mo = mfma16k16(pa[p], mb[r], mo);
+      }
       if constexpr (kQ4) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) pj[j] *= 0.0625f;  // exact; undoes B's factor 16
@@ -777,23 +869,33 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
       const char* const vrow = slot + (4 * kq) * RB + (kQ4 ? 1 : 2) * hm;
       // The scale rows of the lane's four tokens, NK fp16 each.
       const char* const srow = slot + GB + (4 * kq) * F::kScaleRow;
-      uint32_t dw[4][NK / 2];
+      constexpr int SW = (F::kScaleRow > 0 ? F::kScaleRow : 4) / 4;  // dwords per token row
+      uint32_t dw[4][SW];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        if constexpr (NK == 8) {
-          const uint4 t = *reinterpret_cast<const uint4*>(srow + j * F::kScaleRow);
-          dw[j][0] = t.x, dw[j][1] = t.y, dw[j][2] = t.z, dw[j][3] = t.w;
+        if constexpr (SW % 4 == 0) {
+#pragma unroll
+          for (int c = 0; c < SW / 4; ++c) {
+            const uint4 t = *reinterpret_cast<const uint4*>(srow + j * F::kScaleRow + 16 * c);
+            dw[j][4 * c] = t.x, dw[j][4 * c + 1] = t.y, dw[j][4 * c + 2] = t.z, dw[j][4 * c + 3] = t.w;
+          }
         } else {
           const uint2 t = *reinterpret_cast<const uint2*>(srow + j * F::kScaleRow);
           dw[j][0] = t.x, dw[j][1] = t.y;
         }
       }
+      // fp16 d of group G for token 4 kq + j (Q4_1 rows hold (d, m) pairs).
+      auto dbits = [&](int j, auto gc) -> uint32_t {
+        constexpr int G = decltype(gc)::value;
+        if constexpr (kQ41) return dw[j][G] & 0xFFFFu;
+        else return G & 1 ? dw[j][G / 2] >> 16 : dw[j][G / 2] & 0xFFFFu;
+      };
       Unroll<0, NK>::run([&](auto gc) {
         constexpr int G = decltype(gc)::value;
         float x[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j)  // p * d, one v_fma_mix_f32 each
-          x[j] = fmaf(pj[j], f16_bits_to_f32(G & 1 ? dw[j][G / 2] >> 16 : dw[j][G / 2] & 0xFFFFu), 0.0f);
+          x[j] = fmaf(pj[j], f16_bits_to_f32(dbits(j, gc)), 0.0f);
         uint2 ah, am, al;
         split3_bf16(x[0], x[1], ah.x, am.x, al.x);
         split3_bf16(x[2], x[3], ah.y, am.y, al.y);
@@ -905,6 +1007,14 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
   float* const red = reinterpret_cast<float*>(smem);  // [NW][GC][D]
   if constexpr (kQ) {
     const int hm = lane & 15;
+    if constexpr (kQ41) {
+      // M[h][G] of this wave into its probability scratch (unused on this
+      // path): [8 heads][8 groups] fp32.
+      float* const s_mo = reinterpret_cast<float*>(s_pp + wave * (F::kScratch / 4));
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (4 * qr_row + i < GC && hm < NK) s_mo[(4 * qr_row + i) * 8 + hm] = mo[i];
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int h = 4 * qr_row + i;
@@ -947,6 +1057,11 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
     if constexpr (NW == 2) o = red[i] + red[GC * D + i];
     else o = (red[i] + red[GC * D + i]) + (red[2 * GC * D + i] + red[3 * GC * D + i]);
     const int g = i / D, d = i - g * D;
+    if constexpr (kQ41) {  // + the offset term of dim d's group, from every wave
+      const float* const s_mo = reinterpret_cast<const float*>(s_pp);
+#pragma unroll
+      for (int w = 0; w < NW; ++w) o += s_mo[w * (F::kScratch / 4) + g * 8 + d / 32];
+    }
     a.ws_o[(part_row + int64_t(g) * a.max_parts) * D + d] = o;
   }
 }

@@ -12,7 +12,7 @@ from typing import Optional, Tuple
 
 import torch
 
-from ._lib import BF16, CacheDesc, F16, F32, Q4_0, Q8_0, check, lib
+from ._lib import BF16, CacheDesc, F16, F32, Q4_0, Q4_1, Q8_0, check, lib
 
 __all__ = ["PagedKvCache", "RopeTable", "flash_attention", "torch_dtype_id", "stream_handle"]
 
@@ -99,8 +99,8 @@ class PagedKvCache:
         pool = self.k_pool if which == "k" else self.v_pool
         if self.dtype == Q8_0:
             raise TypeError("use q8_planes() for a Q8_0 cache")
-        if self.dtype == Q4_0:
-            raise TypeError("use q4_planes() for a Q4_0 cache")
+        if self.dtype in (Q4_0, Q4_1):
+            raise TypeError("use q4_planes() for a Q4_0 / Q4_1 cache")
         return pool.view(_ID_TORCH[self.dtype]).view(self.num_blocks, self.n_kv_heads, self.block_size, self.head_dim)
 
     def q8_planes(self, which: str = "k") -> Tuple[torch.Tensor, torch.Tensor]:
@@ -112,12 +112,13 @@ class PagedKvCache:
         return qs, d
 
     def q4_planes(self, which: str = "k") -> Tuple[torch.Tensor, torch.Tensor]:
-        """(qs uint8 [nb, H, bs, D/2], d fp16 bits int16 [nb, H, bs, D/32]) of a Q4_0 cache."""
+        """(qs uint8 [nb, H, bs, D/2], scales fp16 bits int16 [nb, H, bs, D/32] (Q4_0: d) or
+        [nb, H, bs, D/32, 2] (Q4_1: d, m)) of a Q4_0 / Q4_1 cache."""
         pool = (self.k_pool if which == "k" else self.v_pool).view(self.num_blocks, self.n_kv_heads, self.page_bytes)
         bs, D = self.block_size, self.head_dim
         qs = pool[:, :, : bs * D // 2].reshape(self.num_blocks, self.n_kv_heads, bs, D // 2)
-        d = pool[:, :, bs * D // 2:].contiguous().view(torch.int16).reshape(self.num_blocks, self.n_kv_heads, bs,
-                                                                              D // 32)
+        shape = (self.num_blocks, self.n_kv_heads, bs, D // 32) + ((2,) if self.dtype == Q4_1 else ())
+        d = pool[:, :, bs * D // 2:].contiguous().view(torch.int16).reshape(shape)
         return qs, d
 
     def check(self) -> None:

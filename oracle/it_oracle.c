@@ -10,6 +10,7 @@
  */
 #include "it_oracle.h"
 
+#include <float.h>
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
@@ -306,6 +307,52 @@ void orc_dequantize_row_q4_0(const uint8_t* y, size_t n, float* x) {
 }
 
 /* ------------------------------------------------------------------------ */
+/* Q4_1 -- block types.rs:24-32; quantiser and dequantiser restate ggml's    */
+/* (the reference has no code for Q4_1)                                     */
+/* ------------------------------------------------------------------------ */
+int orc_quantize_row_q4_1(const float* x, size_t n, uint8_t* y) {
+  if (n % ORC_QK4_1) return ORC_INVALID_INPUT;
+  size_t nb = n / ORC_QK4_1;
+  for (size_t i = 0; i < nb; ++i) {
+    const float* xb = x + i * ORC_QK4_1;
+    uint8_t* rec = y + i * ORC_BLOCK_Q4_1_BYTES;
+    float mn = FLT_MAX, mx = -FLT_MAX;
+    for (int j = 0; j < ORC_QK4_1; ++j) {
+      if (xb[j] < mn) mn = xb[j];
+      if (xb[j] > mx) mx = xb[j];
+    }
+    const float d = (mx - mn) / 15.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    uint16_t dh = orc_f32_to_f16(d), mh = orc_f32_to_f16(mn);
+    rec[0] = (uint8_t)(dh & 0xFF);
+    rec[1] = (uint8_t)(dh >> 8);
+    rec[2] = (uint8_t)(mh & 0xFF);
+    rec[3] = (uint8_t)(mh >> 8);
+    for (int j = 0; j < ORC_QK4_1 / 2; ++j) {
+      int32_t q0 = q4_trunc_i8((xb[j] - mn) * id + 0.5f);
+      int32_t q1 = q4_trunc_i8((xb[j + ORC_QK4_1 / 2] - mn) * id + 0.5f);
+      if (q0 > 15) q0 = 15;
+      if (q1 > 15) q1 = 15;
+      rec[4 + j] = (uint8_t)(q0 | (q1 << 4));
+    }
+  }
+  return ORC_OK;
+}
+
+void orc_dequantize_row_q4_1(const uint8_t* y, size_t n, float* x) {
+  size_t nb = n / ORC_QK4_1;
+  for (size_t i = 0; i < nb; ++i) {
+    const uint8_t* rec = y + i * ORC_BLOCK_Q4_1_BYTES;
+    float d = orc_f16_to_f32((uint16_t)(rec[0] | (rec[1] << 8)));
+    float m = orc_f16_to_f32((uint16_t)(rec[2] | (rec[3] << 8)));
+    for (int j = 0; j < ORC_QK4_1 / 2; ++j) {
+      x[i * ORC_QK4_1 + j] = d * (float)(rec[4 + j] & 0xF) + m;
+      x[i * ORC_QK4_1 + j + ORC_QK4_1 / 2] = d * (float)(rec[4 + j] >> 4) + m;
+    }
+  }
+}
+
+/* ------------------------------------------------------------------------ */
 /* rope_f32 -- src/backend/arm/rope.rs:6-44                                   */
 /* ------------------------------------------------------------------------ */
 int orc_rope_f32(const float* x, float* out, size_t n, int64_t pos, int32_t n_dims, int32_t head_dim,
@@ -395,6 +442,7 @@ static int desc_ok(const orc_cache_desc* c) {
   if (c->num_blocks <= 0 || c->block_size <= 0 || c->n_kv_heads <= 0 || c->head_dim <= 0) return 0;
   if (c->dtype == ORC_Q8_0) return c->head_dim % ORC_QK8_0 == 0;
   if (c->dtype == ORC_Q4_0) return c->head_dim % ORC_QK4_0 == 0;
+  if (c->dtype == ORC_Q4_1) return c->head_dim % ORC_QK4_1 == 0;
   return elem_bytes(c->dtype) != 0;
 }
 
@@ -402,6 +450,7 @@ size_t orc_page_bytes(const orc_cache_desc* c) {
   size_t bs = (size_t)c->block_size, d = (size_t)c->head_dim;
   if (c->dtype == ORC_Q8_0) return bs * d + bs * (d / ORC_QK8_0) * 2;
   if (c->dtype == ORC_Q4_0) return bs * (d / 2) + bs * (d / ORC_QK4_0) * 2;
+  if (c->dtype == ORC_Q4_1) return bs * (d / 2) + bs * (d / ORC_QK4_1) * 4;
   return bs * d * elem_bytes(c->dtype);
 }
 
@@ -422,6 +471,17 @@ static void put_row(const orc_cache_desc* c, uint8_t* page, int32_t slot, const 
       memcpy(qs + g * ORC_QK8_0, rec + 2, ORC_QK8_0);
       sc[g * 2] = rec[0];
       sc[g * 2 + 1] = rec[1];
+    }
+  } else if (c->dtype == ORC_Q4_1) {
+    /* qs plane [block_size][d / 2], then [block_size][d / 32] (d, m) fp16 pairs. */
+    size_t ng = d / ORC_QK4_1;
+    uint8_t rec[ORC_BLOCK_Q4_1_BYTES];
+    uint8_t* qs = page + (size_t)slot * (d / 2);
+    uint8_t* sc = page + (size_t)c->block_size * (d / 2) + (size_t)slot * ng * 4;
+    for (size_t g = 0; g < ng; ++g) {
+      orc_quantize_row_q4_1((const float*)src_row + g * ORC_QK4_1, ORC_QK4_1, rec);
+      memcpy(qs + g * 16, rec + 4, 16);
+      memcpy(sc + g * 4, rec, 4);
     }
   } else if (c->dtype == ORC_Q4_0) {
     /* qs plane [block_size][d / 2] (each group's 16 bytes as in the block),
@@ -445,7 +505,7 @@ static void put_row(const orc_cache_desc* c, uint8_t* page, int32_t slot, const 
 int orc_kv_append(const orc_cache_desc* c, uint8_t* k_pool, uint8_t* v_pool,
                   const void* k, const void* v, const int64_t* slots, int32_t n_tokens) {
   if (!desc_ok(c) || n_tokens < 0) return ORC_INVALID_INPUT;
-  size_t src_eb = (c->dtype == ORC_Q8_0 || c->dtype == ORC_Q4_0) ? 4 : elem_bytes(c->dtype);
+  size_t src_eb = (c->dtype == ORC_Q8_0 || c->dtype == ORC_Q4_0 || c->dtype == ORC_Q4_1) ? 4 : elem_bytes(c->dtype);
   size_t row = (size_t)c->head_dim * src_eb;
   int64_t n_slots = c->num_blocks * c->block_size;
   for (int32_t t = 0; t < n_tokens; ++t) {
@@ -477,6 +537,15 @@ static void get_row_raw(const orc_cache_desc* c, const uint8_t* page, int32_t sl
       rec[1] = sc[g * 2 + 1];
       memcpy(rec + 2, qs + g * ORC_QK8_0, ORC_QK8_0);
     }
+  } else if (c->dtype == ORC_Q4_1) {
+    size_t ng = d / ORC_QK4_1;
+    const uint8_t* qs = page + (size_t)slot * (d / 2);
+    const uint8_t* sc = page + (size_t)c->block_size * (d / 2) + (size_t)slot * ng * 4;
+    for (size_t g = 0; g < ng; ++g) {
+      uint8_t* rec = dst + g * ORC_BLOCK_Q4_1_BYTES;
+      memcpy(rec, sc + g * 4, 4);
+      memcpy(rec + 4, qs + g * 16, 16);
+    }
   } else if (c->dtype == ORC_Q4_0) {
     size_t ng = d / ORC_QK4_0;
     const uint8_t* qs = page + (size_t)slot * (d / 2);
@@ -496,6 +565,7 @@ static void get_row_raw(const orc_cache_desc* c, const uint8_t* page, int32_t sl
 static size_t row_out_bytes(const orc_cache_desc* c) {
   if (c->dtype == ORC_Q8_0) return (size_t)(c->head_dim / ORC_QK8_0) * ORC_BLOCK_Q8_0_BYTES;
   if (c->dtype == ORC_Q4_0) return (size_t)(c->head_dim / ORC_QK4_0) * ORC_BLOCK_Q4_0_BYTES;
+  if (c->dtype == ORC_Q4_1) return (size_t)(c->head_dim / ORC_QK4_1) * ORC_BLOCK_Q4_1_BYTES;
   return (size_t)c->head_dim * elem_bytes(c->dtype);
 }
 
@@ -513,6 +583,15 @@ static void get_row_f32(const orc_cache_desc* c, const uint8_t* page, int32_t sl
       uint8_t* buf = ng * ORC_BLOCK_Q8_0_BYTES <= sizeof(rec) ? rec : (uint8_t*)malloc(ng * ORC_BLOCK_Q8_0_BYTES);
       get_row_raw(c, page, slot, buf);
       orc_dequantize_row_q8_0(buf, d, dst);
+      if (buf != rec) free(buf);
+      break;
+    }
+    case ORC_Q4_1: {
+      uint8_t rec[8 * ORC_BLOCK_Q4_1_BYTES * 4];
+      size_t ng = d / ORC_QK4_1;
+      uint8_t* buf = ng * ORC_BLOCK_Q4_1_BYTES <= sizeof(rec) ? rec : (uint8_t*)malloc(ng * ORC_BLOCK_Q4_1_BYTES);
+      get_row_raw(c, page, slot, buf);
+      orc_dequantize_row_q4_1(buf, d, dst);
       if (buf != rec) free(buf);
       break;
     }

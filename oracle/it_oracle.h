@@ -35,6 +35,7 @@ extern "C" {
 #define ORC_F32 0
 #define ORC_F16 1
 #define ORC_Q4_0 2
+#define ORC_Q4_1 3
 #define ORC_Q8_0 8
 #define ORC_BF16 30
 
@@ -42,6 +43,8 @@ extern "C" {
 #define ORC_BLOCK_Q8_0_BYTES 34 /* types.rs:34-41: repr(C) {u16 d; i8 qs[32]} */
 #define ORC_QK4_0 32          /* types.rs:7 */
 #define ORC_BLOCK_Q4_0_BYTES 18 /* types.rs:15-22: repr(C) {u16 d; u8 qs[16]} */
+#define ORC_QK4_1 32          /* types.rs:8 */
+#define ORC_BLOCK_Q4_1_BYTES 20 /* types.rs:24-32, size asserted at :249: {u16 d; u16 m; u8 qs[16]} */
 
 /* ---- seeded synthetic inputs (not a reference function: test plumbing) -- */
 uint64_t orc_splitmix64(uint64_t* state);
@@ -106,6 +109,17 @@ void orc_dequantize_row_q8_0(const uint8_t* y, size_t n, float* x);
 int orc_quantize_row_q4_0(const float* x, size_t n, uint8_t* y);
 void orc_dequantize_row_q4_0(const uint8_t* y, size_t n, float* x);
 
+/* ---- Q4_1 ---------------------------------------------------------------- */
+/* The reference fixes only the block (types.rs:24-32, 20 bytes, :249); no
+ * code in it reads or writes one.  Restated from ggml (ggml-quants.c, not
+ * vendored): quantize_row_q4_1_ref -- min / max of the group (NaN never
+ * wins), d = (max - min) / 15, id = d ? 1/d : 0, nibble = min(15,
+ * (int8_t)((x - min) * id + 0.5f)), d and m = min stored as fp16 (RNE), the
+ * nibble order of Q4_0; dequantize_row_q4_1 -- value = f32(d) * nibble +
+ * f32(m), product and sum rounded separately. */
+int orc_quantize_row_q4_1(const float* x, size_t n, uint8_t* y);
+void orc_dequantize_row_q4_1(const uint8_t* y, size_t n, float* x);
+
 /* ---- RoPE (src/backend/arm/rope.rs:6-44) -------------------------------- */
 /* out = x rotated pairwise: for each head row of head_dim floats and each
  * even i < n_dims, theta = (float)pos * powf(freq_base, -(float)i / n_dims),
@@ -132,7 +146,8 @@ int orc_backend_flash_attention(const float* q, const float* k, const float* v,
  * (block, head) page holds block_size*head_dim int8 values followed by
  * block_size*head_dim/32 fp16 scales (slot-major).  Q4_0 likewise:
  * block_size*head_dim/2 bytes of nibbles (each 32-group's 16 bytes in
- * BlockQ4_0 order), then block_size*head_dim/32 fp16 scales. */
+ * BlockQ4_0 order), then block_size*head_dim/32 fp16 scales.  Q4_1: the
+ * nibbles, then per token and group the fp16 pair (d, m). */
 typedef struct {
   int64_t num_blocks;
   int32_t block_size;

@@ -44,7 +44,9 @@ def test_status_codes_and_pure_queries():
     assert lib.it_abi_version() == 1
     assert lib.it_supports(L.OP_PAGED_DECODE, L.BF16) == 1
     assert lib.it_supports(L.OP_PAGED_DECODE, L.Q4_0) == 1
-    assert lib.it_supports(L.OP_PAGED_DECODE, 3) == 0  # Q4_1 caches are not implemented
+    assert lib.it_supports(L.OP_PAGED_DECODE, L.Q4_1) == 1
+    assert lib.it_supports(L.OP_PAGED_DECODE, 6) == 0  # Q5_0 caches are not implemented
+    assert lib.it_kv_page_bytes(32, 256, L.Q4_1) == 32 * 128 + 32 * 8 * 4  # 5120
     assert lib.it_supports(L.OP_PAGED_PREFILL, L.Q4_0) == 0
     assert lib.it_kv_page_bytes(32, 256, L.Q4_0) == 32 * 128 + 32 * 8 * 2  # 4608
     assert lib.it_kv_page_bytes(16, 128, L.BF16) == 4096
@@ -67,7 +69,7 @@ def test_invalid_input_before_device():
     h = C.c_void_p()
     assert lib.it_kv_cache_new(0, 16, 12, 2, 128, L.BF16, C.byref(h)) == L.NOT_IMPLEMENTED  # bs not 2^k
     assert lib.it_kv_cache_new(0, 16, 16, 2, 100, L.Q8_0, C.byref(h)) == L.INVALID_INPUT  # D % 32
-    assert lib.it_kv_cache_new(0, 16, 16, 2, 128, 3, C.byref(h)) == L.NOT_IMPLEMENTED  # Q4_1
+    assert lib.it_kv_cache_new(0, 16, 16, 2, 128, 6, C.byref(h)) == L.NOT_IMPLEMENTED  # Q5_0
     assert lib.it_kv_cache_new(0, 16, 16, 2, 96 + 8, L.Q4_0, C.byref(h)) == L.INVALID_INPUT  # D % 32
 
 

@@ -28,7 +28,7 @@ def _pair(num_blocks, bs, hkv, D, dt):
 
 
 def _src(seed, n_tokens, hkv, D, dt):
-    if dt in (orc.Q8_0, orc.Q4_0):
+    if dt in (orc.Q8_0, orc.Q4_0, orc.Q4_1):
         k = kv_values(seed, n_tokens * hkv * D, orc.F32, outliers=True)
         v = kv_values(seed + 1, n_tokens * hkv * D, orc.F32, outliers=True)
     else:
@@ -40,7 +40,7 @@ def _src(seed, n_tokens, hkv, D, dt):
 def _dev_src(a, dt):
     import torch
 
-    if dt in (orc.F32, orc.Q8_0, orc.Q4_0):
+    if dt in (orc.F32, orc.Q8_0, orc.Q4_0, orc.Q4_1):
         return to_dev(a)
     return to_dev(a.view(np.int16), torch.bfloat16 if dt == orc.BF16 else torch.float16)
 
@@ -57,7 +57,8 @@ def _assert_pools(dev, ref, what):
 
 @pytest.mark.parametrize("dt,D,bs", [(orc.BF16, 128, 16), (orc.F32, 128, 16), (orc.F16, 128, 16),
                                      (orc.BF16, 256, 32), (orc.Q8_0, 256, 32), (orc.Q8_0, 128, 16),
-                                     (orc.Q4_0, 256, 32), (orc.Q4_0, 128, 16), (orc.Q4_0, 64, 8)])
+                                     (orc.Q4_0, 256, 32), (orc.Q4_0, 128, 16), (orc.Q4_0, 64, 8),
+                                     (orc.Q4_1, 256, 32), (orc.Q4_1, 128, 16), (orc.Q4_1, 64, 8)])
 def test_append_bit_exact(dt, D, bs):
     hkv, nb, n = 4, 64, 300
     dev, ref = _pair(nb, bs, hkv, D, dt)
@@ -98,12 +99,13 @@ def test_append_q8_special_groups():
     _assert_pools(dev, ref, "append q8 special")
 
 
-def test_append_q4_special_groups():
-    """Q4_0 (ggml's quantiser; the reference has none): equal magnitudes of
-    both signs, all-zero, -0, constant, subnormal, NaN, inf and a
-    group whose 1/d overflows."""
+@pytest.mark.parametrize("dt", [orc.Q4_0, orc.Q4_1])
+def test_append_q4_special_groups(dt):
+    """Q4_0 / Q4_1 (ggml's quantisers; the reference has none): equal
+    magnitudes of both signs, all-zero, -0, constant, subnormal, NaN, inf and
+    a group whose 1/d overflows."""
     hkv, D, bs, nb = 1, 256, 32, 4
-    dev, ref = _pair(nb, bs, hkv, D, orc.Q4_0)
+    dev, ref = _pair(nb, bs, hkv, D, dt)
     g = np.zeros((8, 32), np.float32)
     g[0, [2, 7, 20]] = [-4.0, 4.0, 4.0]  # first of equal magnitudes: max = -4
     g[0, [3, 4, 5]] = [1.25, -1.75, 3.0]  # x * id + 8.5 on .5 boundaries
@@ -116,13 +118,16 @@ def test_append_q4_special_groups():
     g[6] = orc.normal(6, 32)
     g[6, 2] = -np.inf
     g[7] = orc.normal(7, 32) * np.float32(6e4)
+    if dt == orc.Q4_1:  # min over +0 and -0: the first stays
+        g[1, :16] = 1.0
+        g[1, [3, 9]] = [0.0, -0.0]
     rows = [np.roll(g.reshape(-1), 32 * s) for s in range(8)]
     k = np.stack(rows).reshape(8, hkv, D)
     v = -k
     slots = np.array([0, 5, 31, 32, 63, 64, 100, 127], np.int64)
     ref.append(k, v, slots)
     dev.append(to_dev(k), to_dev(v), to_dev(slots))
-    _assert_pools(dev, ref, "append q4 special")
+    _assert_pools(dev, ref, f"append q4 special dt={dt}")
 
 
 def test_append_config1_full_step():
@@ -154,7 +159,7 @@ def test_append_bad_slot_is_latched_not_written():
 
 
 @pytest.mark.parametrize("dt,D,bs", [(orc.BF16, 128, 16), (orc.F32, 128, 16), (orc.Q8_0, 256, 32),
-                                     (orc.Q4_0, 128, 16)])
+                                     (orc.Q4_0, 128, 16), (orc.Q4_1, 256, 32)])
 def test_gather_bit_exact(dt, D, bs):
     import torch
 

@@ -260,6 +260,70 @@ def test_oracle_q4_gather_records_equal_quantize_row(orc):
             assert bytes(rv[h, t]) == bytes(orc.quantize_row_q4_0(-x[t, h]))
 
 
+# ---------------- Q4_1 ------------------------------------------------------
+# The reference fixes only the block (types.rs:24-32, 20 bytes asserted at
+# :249); quantiser and dequantiser follow ggml and are pinned here by
+# hand-worked cases, not by reference output.
+def test_q4_1_layout_and_hand_worked_group(orc):
+    x = np.zeros(32, np.float32)
+    x[:16] = np.arange(16)  # min 0, max 15: d = 1, id = 1, nibble = trunc(x + 0.5)
+    x[16:24] = [7.4, 7.5, 7.6, 0.49, 0.5, 14.5, 14.51, 3.0]
+    rec = orc.quantize_row_q4_1(x)
+    assert rec.shape == (1, 20)
+    assert int(rec[0, 0]) | (int(rec[0, 1]) << 8) == _f16_bits(1.0)  # d
+    assert int(rec[0, 2]) | (int(rec[0, 3]) << 8) == _f16_bits(0.0)  # m = min
+    lo, hi = rec[0, 4:] & 0xF, rec[0, 4:] >> 4
+    np.testing.assert_array_equal(lo, np.arange(16))
+    np.testing.assert_array_equal(hi, [7, 8, 8, 0, 1, 15, 15, 3] + [0] * 8)
+    deq = orc.dequantize_row_q4_1(rec)
+    np.testing.assert_array_equal(deq[:16], np.arange(16, dtype=np.float32))
+    np.testing.assert_array_equal(deq[16:24], np.array([7, 8, 8, 0, 1, 15, 15, 3], np.float32))
+
+
+def test_q4_1_offset_and_nan(orc):
+    x = np.linspace(-1, 2, 32).astype(np.float32)  # d = 3/15, m = -1
+    x[5] = np.nan  # never the min or the max; its nibble is trunc(NaN) -> 0
+    rec = orc.quantize_row_q4_1(x)
+    assert int(rec[0, 0]) | (int(rec[0, 1]) << 8) == _f16_bits(np.float32(3.0) / np.float32(15.0))
+    assert int(rec[0, 2]) | (int(rec[0, 3]) << 8) == _f16_bits(-1.0)
+    assert rec[0, 4 + 5] & 0xF == 0
+    deq = orc.dequantize_row_q4_1(rec)
+    d = np.float32(np.float16(np.float32(3.0) / np.float32(15.0)))
+    nib = np.concatenate([rec[0, 4:] & 0xF, rec[0, 4:] >> 4]).astype(np.float32)
+    np.testing.assert_array_equal(deq, d * nib + np.float32(-1.0))
+
+
+def test_q4_1_round_trip_bound(orc):
+    x = orc.normal(23, 32 * 2048)
+    rng = np.random.default_rng(2)
+    x[rng.random(x.size) < 0.01] *= 8
+    x[:32] += 5.0  # all-positive group: m far from 0
+    rec = orc.quantize_row_q4_1(x)
+    deq = orc.dequantize_row_q4_1(rec).reshape(-1, 32)
+    xg = x.reshape(-1, 32)
+    d = (rec[:, 0].astype(np.uint16) | (rec[:, 1].astype(np.uint16) << 8)).view(np.float16).astype(np.float32)
+    m = (rec[:, 2].astype(np.uint16) | (rec[:, 3].astype(np.uint16) << 8)).view(np.float16).astype(np.float32)
+    # round half up onto min + d * (0..15), then fp16 rounding of d (15 steps)
+    # and of m move the grid by at most 15 |d| 2^-11 + |m| 2^-11
+    bound = d * 0.5 + (15 * d + np.abs(m)) * 2.0 ** -11 * 1.01 + 1e-30
+    assert np.all(np.abs(deq - xg) <= bound[:, None])
+
+
+def test_oracle_q4_1_gather_records_equal_quantize_row(orc):
+    nb, bs, hkv, D = 4, 16, 2, 64
+    c = orc.Cache(nb, bs, hkv, D, orc.Q4_1)
+    n = nb * bs
+    x = (orc.normal(15, n * hkv * D) * np.float32(3)).reshape(n, hkv, D)
+    c.append(x, -x, np.arange(n, dtype=np.int64))
+    tables = np.arange(nb, dtype=np.int32)[None, :]
+    gk, gv = c.gather(tables, np.array([n], np.int32), None, np.array([0], np.int64), n)
+    rk, rv = gk.reshape(hkv, n, D // 32 * 20), gv.reshape(hkv, n, D // 32 * 20)
+    for h in range(hkv):
+        for t in (0, 1, 37, n - 1):
+            assert bytes(rk[h, t]) == bytes(orc.quantize_row_q4_1(x[t, h]))
+            assert bytes(rv[h, t]) == bytes(orc.quantize_row_q4_1(-x[t, h]))
+
+
 def test_exact_decode_helper_and_closer_check(orc):
     """The float64 tie-break the GPU decode tests use for fp32 tolerance:
     exact_decode agrees with the oracle's decode, and a result perturbed by
