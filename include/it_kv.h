@@ -213,8 +213,8 @@ int32_t it_kv_append(it_kv_cache* cache, const void* k, const void* v, int32_t s
  *   q_out: [n_tokens][n_heads][head_dim] of q_out_dtype: F32, or the cache
  *          dtype for BF16/F16 caches (round to nearest even)
  * F32 caches store the rotated fp32 values; BF16/F16 caches round them to
- * nearest even; Q8_0 caches quantise them as quantize_row_q8_0.  (Q4_0 and
- * Q4_1 caches: IT_NOT_IMPLEMENTED.) */
+ * nearest even; Q8_0 / Q4_0 / Q4_1 caches quantise them as it_kv_append
+ * does. */
 typedef struct it_rope_table it_rope_table;
 /* n_dims: a multiple of 4 up to 4096; positions [0, max_pos); device memory
  * max_pos * n_dims * 4 bytes. */

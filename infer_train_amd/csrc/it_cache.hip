@@ -8,11 +8,11 @@
 // 128-byte lines of both source and destination.
 #include <hip/hip_runtime.h>
 
-#include <cfloat>
 #include <cstring>
 
 #include "it_device.hpp"
 #include "it_internal.hpp"
+#include "it_quant.hpp"
 
 using namespace itkv;
 
@@ -55,21 +55,12 @@ __global__ __launch_bounds__(kThreads) void kv_append_copy(
 }
 
 // ---------------------------------------------------------------------------
-// Append with Q8_0 quantisation (quantize_row_q8_0, quant.rs:149-183).
-// Eight lanes own one 32-element group, four floats each (one 16-byte load).
-// blockIdx.y selects K (0) or V (1).
+// Append with quantisation (Q8_0, Q4_0, Q4_1: the quantisers of
+// it_quant.hpp).  Eight lanes own one 32-element group, four floats each (one
+// 16-byte load); blockIdx.y selects K (0) or V (1).
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ int32_t q8_round(float x, float scale) {
-  // quant.rs:176-178: (x / scale).round() as i32, then clamp to [-128, 127].
-  // IEEE division (v_div_scale/fmas/fixup), round half away from zero; NaN
-  // -> 0 as Rust's saturating `as` does.
-  float r = roundf(x / scale);
-  if (r != r) return 0;
-  r = fminf(fmaxf(r, -128.0f), 127.0f);
-  return int32_t(r);
-}
-
-__global__ __launch_bounds__(kThreads) void kv_append_q8_0(
+template <int DT>
+__global__ __launch_bounds__(kThreads) void kv_append_quant(
     const float4* __restrict__ k, const float4* __restrict__ v, char* __restrict__ kpool,
     char* __restrict__ vpool, const int64_t* __restrict__ slots, int64_t total, int hkv, int d,
     int log2_bs, int64_t page_bytes, int64_t n_slots, uint32_t* err) {
@@ -77,96 +68,8 @@ __global__ __launch_bounds__(kThreads) void kv_append_q8_0(
   const bool is_v = blockIdx.y != 0;
   const bool live = gid < total;
   const float4 x = live ? (is_v ? v[gid] : k[gid]) : make_float4(0.f, 0.f, 0.f, 0.f);
-  // amax with NaN ignored (quant.rs:157-163 compares with `>`).
-  auto absn = [](float f) { return f == f ? fabsf(f) : 0.0f; };
-  float amax = fmaxf(fmaxf(absn(x.x), absn(x.y)), fmaxf(absn(x.z), absn(x.w)));
-  amax = group_max<8>(amax);  // the 8 lanes of the group are lane-aligned
+  const QuantGroup q = quant_group<DT>(x, int(gid & 7));  // the 8 lanes of a group are lane-aligned
   if (!live) return;
-  const int vecs_per_row = d >> 2;
-  const int cv = int(gid % vecs_per_row);   // vector index in the row
-  const int64_t th = gid / vecs_per_row;
-  const int h = int(th % hkv);
-  const int64_t t = th / hkv;
-  const int64_t slot = slots[t];
-  if (slot < 0) return;
-  if (slot >= n_slots) {
-    if (cv == 0 && h == 0) atomicOr(err, kErrSlot);
-    return;
-  }
-  uint32_t packed = 0;
-  uint32_t dbits = 0;
-  if (amax != 0.0f) {  // quant.rs:166-170: an all-zero group stores d=0, qs=0
-    const float scale = amax / 127.0f;  // quant.rs:173
-    packed = (uint32_t(q8_round(x.x, scale)) & 0xFFu) | ((uint32_t(q8_round(x.y, scale)) & 0xFFu) << 8) |
-             ((uint32_t(q8_round(x.z, scale)) & 0xFFu) << 16) | ((uint32_t(q8_round(x.w, scale)) & 0xFFu) << 24);
-    dbits = f32_to_f16_bits(scale);  // quant.rs:181 (fp16 of the unrounded scale)
-  }
-  const int64_t blk = slot >> log2_bs;
-  const int64_t off = slot & ((int64_t(1) << log2_bs) - 1);
-  const int64_t bs = int64_t(1) << log2_bs;
-  char* page = (is_v ? vpool : kpool) + (blk * hkv + h) * page_bytes;
-  *reinterpret_cast<uint32_t*>(page + off * d + cv * 4) = packed;
-  if ((cv & 7) == 0) {
-    const int g = cv >> 3;
-    *reinterpret_cast<uint16_t*>(page + bs * d + (off * (d >> 5) + g) * 2) = uint16_t(dbits);
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Append with Q4_0 quantisation.  The reference carries the block
-// (types.rs:15-22) and its dequantisation (vec_dot.rs:425-440) but no
-// quantiser; this is ggml's quantize_row_q4_0_ref as its x86 build computes
-// it: max = the first element of largest magnitude (strict <, NaN never
-// wins), d = max / -8, id = d ? 1/d : 0, nibble = min(15, (int8_t)(x * id +
-// 8.5f)) with the product and the sum rounded separately and cvttss2si's 0
-// for NaN / out-of-range; byte j = nibble j | nibble (j + 16) << 4.
-// Eight lanes own one 32-element group, four floats each; lanes 0-3 hold
-// elements 0-15 (low nibbles), lanes 4-7 elements 16-31 (high nibbles).
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ uint32_t q4_byte(float x, float id) {
-  float r;
-  asm("v_mul_f32 %0, %1, %2" : "=v"(r) : "v"(x), "v"(id));  // no FMA with the add
-  r += 8.5f;
-  if (!(fabsf(r) < 2147483648.0f)) return 0u;
-  const int32_t q = min(int32_t(int8_t(int32_t(r))), 15);
-  return uint32_t(q) & 0xFFu;
-}
-
-__global__ __launch_bounds__(kThreads) void kv_append_q4_0(
-    const float4* __restrict__ k, const float4* __restrict__ v, char* __restrict__ kpool,
-    char* __restrict__ vpool, const int64_t* __restrict__ slots, int64_t total, int hkv, int d,
-    int log2_bs, int64_t page_bytes, int64_t n_slots, uint32_t* err) {
-  const int64_t gid = int64_t(blockIdx.x) * kThreads + threadIdx.x;
-  const bool is_v = blockIdx.y != 0;
-  const bool live = gid < total;
-  const float4 x = live ? (is_v ? v[gid] : k[gid]) : make_float4(0.f, 0.f, 0.f, 0.f);
-  const int l8 = int(gid & 7);
-  // (|max|, element index, max) of the lane, then of the group: larger
-  // magnitude wins, equal magnitudes go to the lower index; "none" is (0, 32).
-  float am = 0.0f, mx = 0.0f;
-  int im = 32;
-  const float xs[4] = {x.x, x.y, x.z, x.w};
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const float a = fabsf(xs[e]);
-    if (am < a) am = a, mx = xs[e], im = 4 * l8 + e;
-  }
-  auto step = [&](auto ctrl) {
-    constexpr int C = decltype(ctrl)::value;
-    const float a2 = dpp_f<C>(am), m2 = dpp_f<C>(mx);
-    const int i2 = __builtin_amdgcn_mov_dpp(im, C, 0xF, 0xF, true);
-    if (a2 > am || (a2 == am && i2 < im)) am = a2, mx = m2, im = i2;
-  };
-  step(std::integral_constant<int, kDppQuadXor1>{});
-  step(std::integral_constant<int, kDppQuadXor2>{});
-  step(std::integral_constant<int, kDppHalfMirror>{});
-  const float dq = mx / -8.0f;
-  const float id = dq != 0.0f ? 1.0f / dq : 0.0f;
-  const uint32_t mine = q4_byte(x.x, id) | (q4_byte(x.y, id) << 8) | (q4_byte(x.z, id) << 16) |
-                        (q4_byte(x.w, id) << 24);
-  // Lane i < 4 of the group takes lane i + 4's bytes (DPP row_shl:4).
-  const uint32_t partner = uint32_t(__builtin_amdgcn_mov_dpp(int(mine), 0x104, 0xF, 0xF, true));
-  if (!live || l8 >= 4) return;
   const int vecs_per_row = d >> 2;
   const int cv = int(gid % vecs_per_row);  // vector index in the row
   const int64_t th = gid / vecs_per_row;
@@ -180,89 +83,8 @@ __global__ __launch_bounds__(kThreads) void kv_append_q4_0(
   }
   const int64_t blk = slot >> log2_bs;
   const int64_t off = slot & ((int64_t(1) << log2_bs) - 1);
-  const int64_t bs = int64_t(1) << log2_bs;
-  const int g = cv >> 3;
   char* page = (is_v ? vpool : kpool) + (blk * hkv + h) * page_bytes;
-  *reinterpret_cast<uint32_t*>(page + off * (d >> 1) + g * 16 + l8 * 4) = mine | ((partner & 0x0F0F0F0Fu) << 4);
-  if (l8 == 0)
-    *reinterpret_cast<uint16_t*>(page + bs * (d >> 1) + (off * (d >> 5) + g) * 2) = uint16_t(f32_to_f16_bits(dq));
-}
-
-// ---------------------------------------------------------------------------
-// Append with Q4_1 quantisation.  The reference carries only the block
-// (types.rs:24-32); this is ggml's quantize_row_q4_1_ref as its x86 build
-// computes it: min / max of the group (strict compares, so NaN never wins
-// and of equal values -- +0 and -0 -- the first stays), d = (max - min) /
-// 15, id = d ? 1/d : 0, nibble = min(15, (int8_t)((x - min) * id + 0.5f))
-// with each operation rounded, d and m = min stored as fp16.  Lanes as in
-// kv_append_q4_0.
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ uint32_t q41_byte(float x, float mn, float id) {
-  float r;
-  const float t = x - mn;
-  asm("v_mul_f32 %0, %1, %2" : "=v"(r) : "v"(t), "v"(id));  // no FMA with the add
-  r += 0.5f;
-  if (!(fabsf(r) < 2147483648.0f)) return 0u;
-  const int32_t q = min(int32_t(int8_t(int32_t(r))), 15);
-  return uint32_t(q) & 0xFFu;
-}
-
-__global__ __launch_bounds__(kThreads) void kv_append_q4_1(
-    const float4* __restrict__ k, const float4* __restrict__ v, char* __restrict__ kpool,
-    char* __restrict__ vpool, const int64_t* __restrict__ slots, int64_t total, int hkv, int d,
-    int log2_bs, int64_t page_bytes, int64_t n_slots, uint32_t* err) {
-  const int64_t gid = int64_t(blockIdx.x) * kThreads + threadIdx.x;
-  const bool is_v = blockIdx.y != 0;
-  const bool live = gid < total;
-  const float4 x = live ? (is_v ? v[gid] : k[gid]) : make_float4(0.f, 0.f, 0.f, 0.f);
-  const int l8 = int(gid & 7);
-  // (value, element index) of the group's min and max; on equal values the
-  // lower index wins, as the sequential scan keeps the first.
-  float mn = FLT_MAX, mx = -FLT_MAX;
-  int imn = 32, imx = 32;
-  const float xs[4] = {x.x, x.y, x.z, x.w};
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    if (xs[e] < mn) mn = xs[e], imn = 4 * l8 + e;
-    if (xs[e] > mx) mx = xs[e], imx = 4 * l8 + e;
-  }
-  auto step = [&](auto ctrl) {
-    constexpr int C = decltype(ctrl)::value;
-    const float mn2 = dpp_f<C>(mn), mx2 = dpp_f<C>(mx);
-    const int imn2 = __builtin_amdgcn_mov_dpp(imn, C, 0xF, 0xF, true);
-    const int imx2 = __builtin_amdgcn_mov_dpp(imx, C, 0xF, 0xF, true);
-    if (mn2 < mn || (mn2 == mn && imn2 < imn)) mn = mn2, imn = imn2;
-    if (mx2 > mx || (mx2 == mx && imx2 < imx)) mx = mx2, imx = imx2;
-  };
-  step(std::integral_constant<int, kDppQuadXor1>{});
-  step(std::integral_constant<int, kDppQuadXor2>{});
-  step(std::integral_constant<int, kDppHalfMirror>{});
-  const float dq = (mx - mn) / 15.0f;
-  const float id = dq != 0.0f ? 1.0f / dq : 0.0f;
-  const uint32_t mine = q41_byte(x.x, mn, id) | (q41_byte(x.y, mn, id) << 8) | (q41_byte(x.z, mn, id) << 16) |
-                        (q41_byte(x.w, mn, id) << 24);
-  const uint32_t partner = uint32_t(__builtin_amdgcn_mov_dpp(int(mine), 0x104, 0xF, 0xF, true));
-  if (!live || l8 >= 4) return;
-  const int vecs_per_row = d >> 2;
-  const int cv = int(gid % vecs_per_row);
-  const int64_t th = gid / vecs_per_row;
-  const int h = int(th % hkv);
-  const int64_t t = th / hkv;
-  const int64_t slot = slots[t];
-  if (slot < 0) return;
-  if (slot >= n_slots) {
-    if (cv == 0 && h == 0) atomicOr(err, kErrSlot);
-    return;
-  }
-  const int64_t blk = slot >> log2_bs;
-  const int64_t off = slot & ((int64_t(1) << log2_bs) - 1);
-  const int64_t bs = int64_t(1) << log2_bs;
-  const int g = cv >> 3;
-  char* page = (is_v ? vpool : kpool) + (blk * hkv + h) * page_bytes;
-  *reinterpret_cast<uint32_t*>(page + off * (d >> 1) + g * 16 + l8 * 4) = mine | ((partner & 0x0F0F0F0Fu) << 4);
-  if (l8 == 0)
-    *reinterpret_cast<uint32_t*>(page + bs * (d >> 1) + (off * (d >> 5) + g) * 4) =
-        f32_to_f16_bits(dq) | (f32_to_f16_bits(mn) << 16);
+  store_group<DT>(page, off, int64_t(1) << log2_bs, d, cv, q);
 }
 
 // ---------------------------------------------------------------------------
@@ -666,7 +488,8 @@ extern "C" int32_t it_kv_append(it_kv_cache* c, const void* k, const void* v, in
   if (quant) {
     const int64_t total = int64_t(n_tokens) * c->n_kv_heads * (c->head_dim / 4);
     dim3 grid(unsigned(cdiv(total, kThreads)), 2);
-    auto* kern = c->dtype == IT_Q8_0 ? kv_append_q8_0 : (c->dtype == IT_Q4_0 ? kv_append_q4_0 : kv_append_q4_1);
+    auto* kern = c->dtype == IT_Q8_0 ? kv_append_quant<IT_Q8_0>
+                 : (c->dtype == IT_Q4_0 ? kv_append_quant<IT_Q4_0> : kv_append_quant<IT_Q4_1>);
     hipLaunchKernelGGL(kern, grid, dim3(kThreads), 0, s,
                        (const float4*)k, (const float4*)v, (char*)c->k_pool, (char*)c->v_pool, slots, total,
                        c->n_kv_heads, c->head_dim, c->log2_bs, c->page_bytes, n_slots, c->err_flag);

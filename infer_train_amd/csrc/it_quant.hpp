@@ -1,0 +1,163 @@
+// it_quant.hpp -- the per-group KV quantisers shared by the append kernels
+// (slot-mapped append and RoPE-then-append), device code.
+//
+// Eight consecutive lanes own one 32-element group of a token row, four
+// floats each (lane l8 holds elements 4 l8 .. 4 l8 + 3).  Every lane of the
+// group must make the call, live or not: the group reductions are DPP moves.
+//
+//  Q8_0  quantize_row_q8_0 (src/backend/arm/quant.rs:149-183, x86 path):
+//        amax ignoring NaN, scale = amax / 127 (IEEE division), q =
+//        roundf(x / scale) saturated to int8 (NaN -> 0), d = fp16(scale).
+//  Q4_0  ggml's quantize_row_q4_0_ref (the reference carries the block,
+//        types.rs:15-22, and its dequantisation, vec_dot.rs:425-440, but no
+//        quantiser): max = the first element of largest magnitude, d =
+//        max / -8, id = d ? 1/d : 0, nibble = min(15, (int8_t)(x id + 8.5f)).
+//  Q4_1  ggml's quantize_row_q4_1_ref (the reference has only the block,
+//        types.rs:24-32): min / max (strict compares: NaN never wins, the
+//        first of equal values stays), d = (max - min) / 15, nibble =
+//        min(15, (int8_t)((x - min) id + 0.5f)), d and m = min as fp16.
+// Q4 products and sums are rounded separately (no FMA: this library builds
+// with -ffp-contract=fast), and (int8_t) of NaN or an out-of-range value is
+// 0, as x86's cvttss2si gives; byte j = nibble j | nibble (j + 16) << 4.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cfloat>
+#include <type_traits>
+
+#include "it_device.hpp"
+#include "it_kv.h"
+
+namespace itkv {
+
+// fp32 -> fp16 bits as the oracle's (and the `half` crate's) from_f32:
+// round to nearest even, subnormals kept, NaN quieted with its top payload.
+__device__ __forceinline__ uint32_t f16_bits_rne(float f) {
+  const uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return ((u >> 16) & 0x8000u) | 0x7E00u | ((u & 0x7FFFFFu) >> 13);
+  return f32_to_f16_bits(f);
+}
+
+// A rounded float32 product the compiler cannot fuse into an FMA.
+__device__ __forceinline__ float mul_rn(float a, float b) {
+  float r;
+  asm("v_mul_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+
+// What a lane stores: `qs` at its place in the group's main-plane bytes
+// (Q8_0: four int8 at byte 4 l8; Q4_0 / Q4_1: four bytes at byte 4 l8, lanes
+// 0-3 only) and, from lane 0, the group's scale word `meta` (Q8_0 / Q4_0:
+// fp16 d; Q4_1: fp16 d | fp16 m << 16).
+struct QuantGroup {
+  uint32_t qs, meta;
+};
+
+__device__ __forceinline__ int32_t q8_round(float x, float scale) {
+  // quant.rs:176-178: (x / scale).round() as i32, clamped to [-128, 127];
+  // IEEE division, round half away from zero, NaN -> 0 (Rust's saturating as).
+  float r = roundf(x / scale);
+  if (r != r) return 0;
+  r = fminf(fmaxf(r, -128.0f), 127.0f);
+  return int32_t(r);
+}
+
+// (int8_t)(r) as ggml's x86 build computes it, then min(15, .), low byte.
+__device__ __forceinline__ uint32_t q4_nibble(float r) {
+  if (!(fabsf(r) < 2147483648.0f)) return 0u;
+  return uint32_t(min(int32_t(int8_t(int32_t(r))), 15)) & 0xFFu;
+}
+
+template <int DT>
+__device__ __forceinline__ QuantGroup quant_group(float4 x, int l8) {
+  const float xs[4] = {x.x, x.y, x.z, x.w};
+  QuantGroup out{0u, 0u};
+  if constexpr (DT == IT_Q8_0) {
+    auto absn = [](float f) { return f == f ? fabsf(f) : 0.0f; };
+    float amax = fmaxf(fmaxf(absn(x.x), absn(x.y)), fmaxf(absn(x.z), absn(x.w)));
+    amax = group_max<8>(amax);
+    if (amax != 0.0f) {  // quant.rs:166-170: an all-zero group stores d = 0, qs = 0
+      const float scale = amax / 127.0f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) out.qs |= (uint32_t(q8_round(xs[e], scale)) & 0xFFu) << (8 * e);
+      out.meta = f16_bits_rne(scale);
+    }
+  } else if constexpr (DT == IT_Q4_0) {
+    // (|max|, element index, max): larger magnitude wins, equal magnitudes go
+    // to the lower index; "none" is (0, 32).
+    float am = 0.0f, mx = 0.0f;
+    int im = 32;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float a = fabsf(xs[e]);
+      if (am < a) am = a, mx = xs[e], im = 4 * l8 + e;
+    }
+    auto step = [&](auto ctrl) {
+      constexpr int C = decltype(ctrl)::value;
+      const float a2 = dpp_f<C>(am), m2 = dpp_f<C>(mx);
+      const int i2 = __builtin_amdgcn_mov_dpp(im, C, 0xF, 0xF, true);
+      if (a2 > am || (a2 == am && i2 < im)) am = a2, mx = m2, im = i2;
+    };
+    step(std::integral_constant<int, kDppQuadXor1>{});
+    step(std::integral_constant<int, kDppQuadXor2>{});
+    step(std::integral_constant<int, kDppHalfMirror>{});
+    const float d = mx / -8.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) out.qs |= q4_nibble(mul_rn(xs[e], id) + 8.5f) << (8 * e);
+    out.meta = f16_bits_rne(d);
+  } else {
+    static_assert(DT == IT_Q4_1, "Q8_0, Q4_0 or Q4_1");
+    float mn = FLT_MAX, mx = -FLT_MAX;
+    int imn = 32, imx = 32;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (xs[e] < mn) mn = xs[e], imn = 4 * l8 + e;
+      if (xs[e] > mx) mx = xs[e], imx = 4 * l8 + e;
+    }
+    auto step = [&](auto ctrl) {
+      constexpr int C = decltype(ctrl)::value;
+      const float mn2 = dpp_f<C>(mn), mx2 = dpp_f<C>(mx);
+      const int imn2 = __builtin_amdgcn_mov_dpp(imn, C, 0xF, 0xF, true);
+      const int imx2 = __builtin_amdgcn_mov_dpp(imx, C, 0xF, 0xF, true);
+      if (mn2 < mn || (mn2 == mn && imn2 < imn)) mn = mn2, imn = imn2;
+      if (mx2 > mx || (mx2 == mx && imx2 < imx)) mx = mx2, imx = imx2;
+    };
+    step(std::integral_constant<int, kDppQuadXor1>{});
+    step(std::integral_constant<int, kDppQuadXor2>{});
+    step(std::integral_constant<int, kDppHalfMirror>{});
+    const float d = (mx - mn) / 15.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) out.qs |= q4_nibble(mul_rn(xs[e] - mn, id) + 0.5f) << (8 * e);
+    out.meta = f16_bits_rne(d) | (f16_bits_rne(mn) << 16);
+  }
+  if constexpr (DT != IT_Q8_0) {
+    // Lane i < 4 of the group takes lane i + 4's bytes (DPP row_shl:4):
+    // byte j of the group = nibble j | nibble (j + 16) << 4.
+    const uint32_t partner = uint32_t(__builtin_amdgcn_mov_dpp(int(out.qs), 0x104, 0xF, 0xF, true));
+    out.qs |= (partner & 0x0F0F0F0Fu) << 4;
+  }
+  return out;
+}
+
+// Store a lane's part of a group into its page: token row `off` of a page of
+// bs rows, head_dim d, vector cv of the row (group cv / 8, lane cv % 8).
+template <int DT>
+__device__ __forceinline__ void store_group(char* page, int64_t off, int64_t bs, int d, int cv, QuantGroup q) {
+  const int g = cv >> 3, l8 = cv & 7;
+  if constexpr (DT == IT_Q8_0) {
+    *reinterpret_cast<uint32_t*>(page + off * d + cv * 4) = q.qs;
+    if (l8 == 0) *reinterpret_cast<uint16_t*>(page + bs * d + (off * (d >> 5) + g) * 2) = uint16_t(q.meta);
+  } else {
+    if (l8 < 4) *reinterpret_cast<uint32_t*>(page + off * (d >> 1) + g * 16 + l8 * 4) = q.qs;
+    if (l8 == 0) {
+      if constexpr (DT == IT_Q4_1)
+        *reinterpret_cast<uint32_t*>(page + bs * (d >> 1) + (off * (d >> 5) + g) * 4) = q.meta;
+      else
+        *reinterpret_cast<uint16_t*>(page + bs * (d >> 1) + (off * (d >> 5) + g) * 2) = uint16_t(q.meta);
+    }
+  }
+}
+
+}  // namespace itkv

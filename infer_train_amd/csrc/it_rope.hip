@@ -7,8 +7,8 @@
 // library's float32 powf/cosf/sinf, in rope_f32's operation order, and held
 // on the device: the device only multiplies and adds, so its results equal
 // the CPU's bit for bit.  One lane rotates one 16-byte vector (two pairs) of
-// one (token, head) row; K and V lanes then convert (or Q8_0-quantise) and
-// store like the plain append, Q lanes write the rotated query.
+// one (token, head) row; K and V lanes then convert (or quantise: Q8_0,
+// Q4_0, Q4_1) and store like the plain append, Q lanes write the rotated query.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -16,6 +16,7 @@
 
 #include "it_device.hpp"
 #include "it_internal.hpp"
+#include "it_quant.hpp"
 
 using namespace itkv;
 
@@ -47,13 +48,6 @@ struct RopeAppendArgs {
   int hq, hkv, d, n_dims, max_pos, log2_bs, q_out_dtype;
 };
 
-// fp32 -> fp16 bits as the oracle's (and the `half` crate's) from_f32:
-// round to nearest even, subnormals kept, NaN quieted with its top payload.
-__device__ __forceinline__ uint32_t f16_bits_rne(float f) {
-  const uint32_t u = __float_as_uint(f);
-  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return ((u >> 16) & 0x8000u) | 0x7E00u | ((u & 0x7FFFFFu) >> 13);
-  return f32_to_f16_bits(f);
-}
 
 // Four floats to the 16-bit format DT16 (IT_BF16 or IT_F16), packed.
 template <int DT16>
@@ -62,21 +56,6 @@ __device__ __forceinline__ uint2 pack4(const float4& x) {
   return make_uint2(cv(x.x) | (cv(x.y) << 16), cv(x.z) | (cv(x.w) << 16));
 }
 
-__device__ __forceinline__ int32_t q8_round(float x, float scale) {
-  // quant.rs:176-178 (as kv_append_q8_0): round half away from zero, NaN -> 0.
-  float r = roundf(x / scale);
-  if (r != r) return 0;
-  r = fminf(fmaxf(r, -128.0f), 127.0f);
-  return int32_t(r);
-}
-
-// A rounded float32 product the compiler cannot fuse into an FMA (this
-// library builds with -ffp-contract=fast, which ignores contract pragmas).
-__device__ __forceinline__ float mul_rn(float a, float b) {
-  float r;
-  asm("v_mul_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
-  return r;
-}
 
 // rope.rs:38-39 on the pairs (x, y) and (z, w) with the table's (cos, sin):
 // two products, each rounded, then their difference / sum -- no FMA.
@@ -132,12 +111,10 @@ __global__ __launch_bounds__(kThreads) void kv_append_rope(RopeAppendArgs a) {
     else static_cast<uint2*>(a.q_out)[gid] = pack4<IT_F16>(x);
     return;
   }
-  if constexpr (DT == IT_Q8_0) {
-    // Eight lanes own one 32-element group (rows of d/4 vectors, d % 32 == 0):
-    // the group's amax before any lane leaves (kv_append_q8_0).
-    auto absn = [](float f) { return f == f ? fabsf(f) : 0.0f; };
-    float amax = fmaxf(fmaxf(absn(x.x), absn(x.y)), fmaxf(absn(x.z), absn(x.w)));
-    amax = group_max<8>(amax);
+  if constexpr (DT == IT_Q8_0 || DT == IT_Q4_0 || DT == IT_Q4_1) {
+    // Eight lanes own one 32-element group (rows of d/4 vectors, d % 32 ==
+    // 0): the group's reductions run before any lane leaves.
+    const QuantGroup qg = quant_group<DT>(x, cv & 7);
     if (!live || !pos_ok) return;
     const int64_t slot = a.slots[t];
     if (slot < 0) return;
@@ -145,19 +122,10 @@ __global__ __launch_bounds__(kThreads) void kv_append_rope(RopeAppendArgs a) {
       if (cv == 0 && h == 0) atomicOr(a.err, kErrSlot);
       return;
     }
-    uint32_t packed = 0, dbits = 0;
-    if (amax != 0.0f) {
-      const float scale = amax / 127.0f;
-      packed = (uint32_t(q8_round(x.x, scale)) & 0xFFu) | ((uint32_t(q8_round(x.y, scale)) & 0xFFu) << 8) |
-               ((uint32_t(q8_round(x.z, scale)) & 0xFFu) << 16) | ((uint32_t(q8_round(x.w, scale)) & 0xFFu) << 24);
-      dbits = f16_bits_rne(scale);
-    }
     const int64_t blk = slot >> a.log2_bs;
     const int64_t off = slot & ((int64_t(1) << a.log2_bs) - 1);
-    const int64_t bs = int64_t(1) << a.log2_bs;
     char* page = (part == 1 ? a.vpool : a.kpool) + (blk * a.hkv + h) * a.page_bytes;
-    *reinterpret_cast<uint32_t*>(page + off * a.d + cv * 4) = packed;
-    if ((cv & 7) == 0) *reinterpret_cast<uint16_t*>(page + bs * a.d + (off * (a.d >> 5) + (cv >> 3)) * 2) = uint16_t(dbits);
+    store_group<DT>(page, off, int64_t(1) << a.log2_bs, a.d, cv, qg);
   } else {
     if (!live || !pos_ok) return;
     const int64_t slot = a.slots[t];
@@ -239,12 +207,12 @@ extern "C" int32_t it_kv_append_rope(it_kv_cache* c, const it_rope_table* rope, 
   if (rope->n_dims > c->head_dim)
     return fail(IT_INVALID_INPUT, "%s: table n_dims %d > head_dim %d", who, rope->n_dims, c->head_dim);
   if (rope->device != c->device) return fail(IT_INVALID_INPUT, "%s: table and cache on different devices", who);
-  const bool q8 = c->dtype == IT_Q8_0;
-  if (c->dtype != IT_F32 && c->dtype != IT_BF16 && c->dtype != IT_F16 && !q8)
+  const bool quant = c->dtype == IT_Q8_0 || c->dtype == IT_Q4_0 || c->dtype == IT_Q4_1;
+  if (c->dtype != IT_F32 && c->dtype != IT_BF16 && c->dtype != IT_F16 && !quant)
     return fail(IT_NOT_IMPLEMENTED, "%s: cache dtype %d", who, c->dtype);
   const bool q_ok = q_out_dtype == IT_F32 || ((c->dtype == IT_BF16 || c->dtype == IT_F16) && q_out_dtype == c->dtype);
   if (!q_ok) return fail(IT_NOT_IMPLEMENTED, "%s: q_out dtype %d for cache dtype %d", who, q_out_dtype, c->dtype);
-  if (c->head_dim % 4 || (q8 && c->head_dim % 32))
+  if (c->head_dim % 4 || (quant && c->head_dim % 32))
     return fail(IT_NOT_IMPLEMENTED, "%s: head_dim %d", who, c->head_dim);
   if (n_tokens == 0) return IT_OK;
   if (!q || !k || !v || !slot_mapping || !positions || !q_out) return fail(IT_INVALID_INPUT, "%s: NULL tensor", who);
@@ -283,6 +251,8 @@ extern "C" int32_t it_kv_append_rope(it_kv_cache* c, const it_rope_table* rope, 
     case IT_F32: hipLaunchKernelGGL(kv_append_rope<IT_F32>, grid, dim3(kThreads), 0, s, a); break;
     case IT_BF16: hipLaunchKernelGGL(kv_append_rope<IT_BF16>, grid, dim3(kThreads), 0, s, a); break;
     case IT_F16: hipLaunchKernelGGL(kv_append_rope<IT_F16>, grid, dim3(kThreads), 0, s, a); break;
+    case IT_Q4_0: hipLaunchKernelGGL(kv_append_rope<IT_Q4_0>, grid, dim3(kThreads), 0, s, a); break;
+    case IT_Q4_1: hipLaunchKernelGGL(kv_append_rope<IT_Q4_1>, grid, dim3(kThreads), 0, s, a); break;
     default: hipLaunchKernelGGL(kv_append_rope<IT_Q8_0>, grid, dim3(kThreads), 0, s, a); break;
   }
   const hipError_t e = hipGetLastError();

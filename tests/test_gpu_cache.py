@@ -240,7 +240,7 @@ def _to_cache_src(x, dt):
 
 
 @pytest.mark.parametrize("dt,D,bs", [(orc.BF16, 128, 16), (orc.F32, 128, 16), (orc.F16, 128, 16),
-                                     (orc.Q8_0, 256, 32)])
+                                     (orc.Q8_0, 256, 32), (orc.Q4_0, 128, 16), (orc.Q4_1, 256, 32)])
 def test_append_rope_bit_exact(dt, D, bs):
     """RoPE then append (forward.rs:195-229): the cache pools and the rotated
     q equal the oracle's rope_f32 (rope.rs:6-44) followed by its append,
