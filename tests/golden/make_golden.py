@@ -5,6 +5,9 @@ ships no fixtures of its own).  Run from the repo root:
 Fixtures:
   config1_decode_out.npy  oracle flash_attn_f32 output of config 1 (12x128 f32)
   q8_cases.json           explicit Q8_0 inputs/records incl. .5 ties, NaN, inf
+  q4_cases.json           explicit Q4_0 / Q4_1 inputs/records (ggml's quantisers,
+                          which the reference does not carry): hand-worked
+                          groups, equal magnitudes, -0, NaN, inf
   manifest.json           seeds, shapes and SHA-256 digests of larger results
 """
 import hashlib
@@ -58,6 +61,38 @@ def q8_cases():
     return out
 
 
+def q4_cases():
+    cases = []
+    x = np.zeros(32, np.float32)
+    vals = {0: 3.0, 1: -3.0, 2: 2.5, 3: -2.5, 4: 0.49, 5: 8.0, 6: 0.51, 7: 7.9, 8: -7.9, 20: -8.0, 21: 1.0}
+    for i, v in vals.items():
+        x[i] = v
+    cases.append(("hand_d_minus_1", x))
+    e = np.zeros(32, np.float32)
+    e[[2, 7]] = [-4.0, 4.0]
+    cases.append(("equal_magnitudes", e))
+    cases.append(("zeros", np.zeros(32, np.float32)))
+    cases.append(("neg_zeros", -np.zeros(32, np.float32)))
+    m = np.zeros(32, np.float32)
+    m[:16] = np.arange(16)
+    m[16:24] = [7.4, 7.5, 7.6, 0.49, 0.5, 14.5, 14.51, 3.0]
+    cases.append(("ramp", m))
+    y = np.linspace(-1, 2, 32).astype(np.float32)
+    y[5] = np.nan
+    cases.append(("nan_ignored", y))
+    z = y.copy()
+    z[9] = -np.inf
+    cases.append(("inf", z))
+    cases.append(("normal", orc.normal(46, 32)))
+    cases.append(("tiny", orc.normal(47, 32) * np.float32(1e-30)))
+    out = []
+    for name, a in cases:
+        out.append({"name": name, "x_bits": [int(u) for u in a.view(np.uint32)],
+                    "q4_0": [int(b) for b in orc.quantize_row_q4_0(a)[0]],
+                    "q4_1": [int(b) for b in orc.quantize_row_q4_1(a)[0]]})
+    return out
+
+
 def c4_log(n_steps=2768):
     cap, bs, W, start = 16512, 16, 4096, 30000
     pool = orc.Pool(cap, order=orc.permutation(4, cap))
@@ -78,6 +113,8 @@ def main():
     np.save(os.path.join(HERE, "config1_decode_out.npy"), out)
     with open(os.path.join(HERE, "q8_cases.json"), "w") as f:
         json.dump(q8_cases(), f, indent=0)
+    with open(os.path.join(HERE, "q4_cases.json"), "w") as f:
+        json.dump(q4_cases(), f, indent=0)
     slots, evs, tables = c4_log()
     x = orc.normal(20, 32 * 4096)
     u = orc.uniform_i32(20 ^ 0x5A5A, 0, 99, x.size)
@@ -89,6 +126,8 @@ def main():
                              "evicted_sha256": sha(evs), "tables_sha256": sha(tables),
                              "first_evicted": [int(e) for e in evs[:64]], "first_slots": [int(s) for s in slots[:64]]},
         "q8_0_outliers": {"seed": 20, "n": int(x.size), "records_sha256": sha(orc.quantize_row_q8_0(x))},
+        "q4_0_outliers": {"seed": 20, "n": int(x.size), "records_sha256": sha(orc.quantize_row_q4_0(x))},
+        "q4_1_outliers": {"seed": 20, "n": int(x.size), "records_sha256": sha(orc.quantize_row_q4_1(x))},
     }
     with open(os.path.join(HERE, "manifest.json"), "w") as f:
         json.dump(manifest, f, indent=1)

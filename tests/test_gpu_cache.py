@@ -130,6 +130,36 @@ def test_append_q4_special_groups(dt):
     _assert_pools(dev, ref, f"append q4 special dt={dt}")
 
 
+@pytest.mark.parametrize("dt", [orc.Q8_0, orc.Q4_0, orc.Q4_1])
+def test_append_golden_cases(dt):
+    """The committed quantiser fixtures (tests/golden/q8_cases.json,
+    q4_cases.json): each case is one 32-element token row of a D = 32 cache;
+    append, then gather the records and compare them with the fixture bytes."""
+    import json
+    import os
+
+    import torch
+
+    golden = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+    name = "q8_cases.json" if dt == orc.Q8_0 else "q4_cases.json"
+    key = {orc.Q8_0: "record", orc.Q4_0: "q4_0", orc.Q4_1: "q4_1"}[dt]
+    cases = json.load(open(os.path.join(golden, name)))
+    x = np.stack([np.array(c["x_bits"], np.uint32).view(np.float32) for c in cases]).reshape(-1, 1, 32)
+    n = len(cases)
+    dev, _ = _pair(4, 8, 1, 32, dt)
+    slots = np.arange(n, dtype=np.int64)
+    dev.append(to_dev(x), to_dev(-x), to_dev(slots))
+    rb = {orc.Q8_0: 34, orc.Q4_0: 18, orc.Q4_1: 20}[dt]
+    ko = torch.zeros(n * rb, dtype=torch.uint8, device="cuda:0")
+    vo = torch.zeros(n * rb, dtype=torch.uint8, device="cuda:0")
+    tables = np.arange(4, dtype=np.int32)[None, :]
+    dev.gather(to_dev(tables), to_dev(np.array([n], np.int32)), None, to_dev(np.array([0], np.int64)), n, ko, vo)
+    dev.check()
+    got = from_dev(ko).reshape(n, rb)
+    for i, c in enumerate(cases):
+        assert list(got[i]) == c[key], c["name"]
+
+
 def test_append_config1_full_step():
     # Config 1: fp32, Hkv 2, D 128, bs 16, 64 blocks, identity table; 1023
     # cached tokens then the token at position 1023.

@@ -354,6 +354,49 @@ def test_exact_decode_helper_and_closer_check(orc):
         assert_close_or_closer(bad, want, fn, 1e-5, 1e-6)
 
 
+# ---------------- committed fixtures (tests/golden, written by make_golden.py) --
+GOLDEN = os.path.join(ROOT, "tests", "golden")
+
+
+def _golden_x(case) -> np.ndarray:
+    return np.array(case["x_bits"], np.uint32).view(np.float32)
+
+
+def test_golden_quant_cases(orc):
+    import json
+
+    for case in json.load(open(os.path.join(GOLDEN, "q8_cases.json"))):
+        assert list(orc.quantize_row_q8_0(_golden_x(case))[0]) == case["record"], case["name"]
+    for case in json.load(open(os.path.join(GOLDEN, "q4_cases.json"))):
+        assert list(orc.quantize_row_q4_0(_golden_x(case))[0]) == case["q4_0"], case["name"]
+        assert list(orc.quantize_row_q4_1(_golden_x(case))[0]) == case["q4_1"], case["name"]
+
+
+def test_golden_digests(orc):
+    import hashlib
+    import json
+
+    man = json.load(open(os.path.join(GOLDEN, "manifest.json")))
+
+    def sha(a):
+        return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+    x = orc.normal(20, 32 * 4096)
+    u = orc.uniform_i32(20 ^ 0x5A5A, 0, 99, x.size)
+    x = np.where(u == 0, x * np.float32(8), x).astype(np.float32)
+    assert sha(orc.quantize_row_q8_0(x)) == man["q8_0_outliers"]["records_sha256"]
+    assert sha(orc.quantize_row_q4_0(x)) == man["q4_0_outliers"]["records_sha256"]
+    assert sha(orc.quantize_row_q4_1(x)) == man["q4_1_outliers"]["records_sha256"]
+    c1 = man["config1"]
+    k = orc.normal(c1["seeds"]["k"], 1024 * 2 * 128).reshape(1024, 2, 128)
+    v = orc.normal(c1["seeds"]["v"], 1024 * 2 * 128).reshape(1024, 2, 128)
+    c = orc.Cache(64, 16, 2, 128, orc.F32)
+    c.append(k, v, np.arange(1024, dtype=np.int64))
+    assert sha(c.k) == c1["k_pool_sha256"] and sha(c.v) == c1["v_pool_sha256"]
+    out = np.load(os.path.join(GOLDEN, "config1_decode_out.npy"))
+    assert sha(out) == c1["out_sha256"]
+
+
 # ---------------- conversions --------------------------------------------
 def test_f16_bf16_converters_exhaustive():
     exe = os.path.join(ROOT, "oracle", "check_f16")
