@@ -176,6 +176,21 @@ def test_quant_group_sizes_and_windows(dt, D):
         assert np.all(got[-1] == 0)
 
 
+@pytest.mark.parametrize("dt", QUANT)
+def test_quant_block_size_8(dt):
+    """8-token pages: every 16-token group straddles two pages, so each lane
+    looks up its own page for the main rows and the scale rows."""
+    hq, hkv, D, bs = 12, 2, 128, 8
+    ctx = [9, 300, 1037]
+    start = np.array([0, 3, 500], np.int32)
+    dev, ref, tables, ctx_a, q, qdt = _build(dt, hq, hkv, D, bs, ctx, seed=71)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
+    exact = lazy(lambda: exact_decode(ref, q, hq, tables, ctx_a, start, scale))
+    for partition in (64, 512):
+        got, want = _run(dev, ref, tables, ctx_a, q, qdt, hq, start=start, partition=partition)
+        assert_close_or_closer(got, want, exact, *TOL[dt], what=f"dt={dt} bs=8 P={partition}")
+
+
 @pytest.mark.parametrize("dt", [orc.Q4_0, orc.Q4_1])
 def test_q4_decode_config5_heads(dt):
     """Config-5 heads (Hq 24, Hkv 4, D 256, bs 32) on a Q4_0 / Q4_1 cache."""
