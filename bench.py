@@ -3,7 +3,7 @@
 Headline (`value`): config 2 at its 4k target -- batched paged decode,
 bf16, Hq 28 / Hkv 4 / D 128, block size 16, batch 32 with every sequence at
 4096 tokens after the step's append, pages a seeded permutation of a
-16384-block pool, split-K over 512-token partitions.  One step = slot-mapped
+16384-block pool, split-K over 512-token partitions (the host planner's choice).  One step = slot-mapped
 append of 1 token per sequence + split-K decode + combine; value = KV bytes
 read per step / mean(split + combine time), the algorithmic bytes
 sum_b ctx_b * Hkv * 2 * D * 2.  Three pool replicas are rotated so the 256 MB
@@ -304,16 +304,25 @@ def bench_config2(steps, warmup, cpu):
 
     import infer_train_amd as it
 
-    w = DecodeWorkload(it.BF16, 28, 4, 128, 16, np.full(32, 4096), 16384, 512, seed=2)
+    from infer_train_amd.kv import decode_partition
+
+    # Partitions from the library's host planner, as a batcher that knows
+    # its contexts would call it: 512 tokens at 4k, 256 for the ragged batch.
+    ctx4k = np.full(32, 4096)
+    p4k = decode_partition(it.BF16, 128, 16, 28, 4, ctx4k)
+    w = DecodeWorkload(it.BF16, 28, 4, 128, 16, ctx4k, 16384, p4k, seed=2)
     cold = w.time(steps, warmup, rotate=True)
     warm = w.time(steps, warmup, rotate=False)
-    head = {"kv_bytes": int(w.kv_bytes), "append_bytes": int(w.append_bytes), "B": w.B, "cold": cold, "warm": warm}
+    head = {"kv_bytes": int(w.kv_bytes), "append_bytes": int(w.append_bytes), "B": w.B, "cold": cold, "warm": warm,
+            "partition": p4k}
     w.release()
     rng = np.random.default_rng(22)
     ctx2 = rng.integers(256, 4097, 32) + 1
-    w2 = DecodeWorkload(it.BF16, 28, 4, 128, 16, ctx2, 16384, 512, seed=3)
+    p2 = decode_partition(it.BF16, 128, 16, 28, 4, ctx2)
+    w2 = DecodeWorkload(it.BF16, 28, 4, 128, 16, ctx2, 16384, p2, seed=3)
     r2 = w2.time(steps, warmup, rotate=True)
-    ragged = {"workload": "config 2 as specified: ctx U[256, 4096] + 1 appended, batch 32",
+    ragged = {"workload": f"config 2 as specified: ctx U[256, 4096] + 1 appended, batch 32, {p2}-token partitions "
+                          "(host planner)",
               "kv_gbs": round(w2.kv_bytes / (r2["decode"] * 1e-3) / 1e9, 1), "decode_us": round(r2["decode"] * 1e3, 2),
               "split_us": round(r2["split"] * 1e3, 2), "kv_bytes": int(w2.kv_bytes),
               "append_us": round(r2["append"] * 1e3, 2),
@@ -893,8 +902,11 @@ def main():
 
     if args.only_headline:
         import infer_train_amd as it
+        from infer_train_amd.kv import decode_partition
 
-        w = DecodeWorkload(it.BF16, 28, 4, 128, 16, np.full(32, 4096), 16384, 512, seed=2)
+        ctx4k = np.full(32, 4096)
+        w = DecodeWorkload(it.BF16, 28, 4, 128, 16, ctx4k, 16384, decode_partition(it.BF16, 128, 16, 28, 4, ctx4k),
+                           seed=2)
         r = w.time(args.steps, args.warmup, rotate=True)
         print(json.dumps({"only_headline": True, "split_us": round(r["split"] * 1e3, 2),
                           "decode_us": round(r["decode"] * 1e3, 2),
@@ -948,7 +960,8 @@ def main():
         "data": "synthetic N(0,1) K/V/Q of each config's shape, seeded; pages a seeded permutation of the pool",
         "config": {"workload": "config 2 at its 4k target: batched paged decode, Hq 28 / Hkv 4 / D 128, block 16, "
                                "batch 32, ctx 4096 each (4095 cached + 1 appended), 16384-block pool, split-K "
-                               "512-token partitions + combine; cold (3 pool replicas rotated)",
+                               f"{head['partition']}-token partitions (host planner) + combine; cold (3 pool "
+                               "replicas rotated)",
                    "global_batch": 32, "seq_len": 4096, "parallelism": "none (1 GPU)"},
         "pct_hbm_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2),
         "decode_us": round(cold["decode"] * 1e3, 2),

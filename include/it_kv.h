@@ -266,6 +266,21 @@ int32_t it_kv_copy_blocks(it_kv_cache* cache, const int32_t* src, const int32_t*
 size_t it_paged_decode_workspace(int32_t n_seqs, int32_t n_heads, int32_t head_dim,
                                  int32_t max_tokens, int32_t partition);
 
+/* Partition (tokens per split) for it_paged_decode over contexts the caller
+ * knows on the host, as a batcher does: the smallest multiple of 64 in
+ * [64, 2048] whose non-empty (sequence, KV head, partition) units run in the
+ * fewest rounds of four resident workgroups per compute unit.  Short
+ * partitions keep each workgroup's chain of dependent page loads short;
+ * units beyond the resident slots would run a second round.
+ *   ctx_lens, start_pos: host int32[n_seqs] (start_pos may be NULL)
+ *   n_cu: compute units of the device (0 = ask the current HIP device)
+ * No counterpart in the reference: flash_attn_f32 (flash_attn.rs:6-72) does
+ * not split keys.  Its caller is the batcher's step (continuous.rs:28-74),
+ * which holds the lengths. */
+int32_t it_paged_decode_partition(int32_t dtype, int32_t head_dim, int32_t block_size, int32_t n_heads,
+                                  int32_t n_kv_heads, const int32_t* ctx_lens, const int32_t* start_pos,
+                                  int32_t n_seqs, int32_t n_cu, int32_t* partition);
+
 /* Paged split-K flash-decode, one query per sequence.  For each sequence b
  * and query head h the result equals flash_attn_f32 (flash_attn.rs:6-72)
  * over keys start_b..ctx_b-1 of KV head h*Hkv/Hq (forward.rs:231-254),
@@ -274,7 +289,8 @@ size_t it_paged_decode_workspace(int32_t n_seqs, int32_t n_heads, int32_t head_d
  *      BF16 (BF16 cache) or F16 (F16 cache)
  *   block_tables/ctx_lens/start_pos: as it_kv_gather
  *   max_tokens: upper bound of ctx_b - start_b
- *   partition: tokens per split (256, 512 or 1024)
+ *   partition: tokens per split, a multiple of 64 in [64, 2048]
+ *              (it_paged_decode_partition picks one for a batch)
  *   ws: it_paged_decode_workspace(...) bytes, device
  *   out: [n_seqs][n_heads][head_dim] of out_dtype (F32 or q_dtype)
  * Two kernels: the split pass writes (m, l, O) per partition, the combine

@@ -108,6 +108,7 @@ SIGNATURES = {
     "it_kv_append_rope": (i32, [P, P, P, i32, P, P, P, P, i32, P, i32, P]),
     "it_kv_sync_tables": (i32, [P, P, i32, i32, P, P, P, i32, P]),
     "it_paged_decode_workspace": (sz, [i32, i32, i32, i32, i32]),
+    "it_paged_decode_partition": (i32, [i32, i32, i32, i32, i32, P, P, i32, i32, P]),
     "it_paged_decode": (i32, [P, P, i32, i32, P, i32, P, P, i32, i32, f32, i32, P, sz, P, i32, P]),
     "it_paged_decode_split": (i32, [P, P, i32, i32, P, i32, P, P, i32, i32, f32, i32, P, sz, P, i32, P]),
     "it_paged_decode_combine": (i32, [P, P, i32, i32, P, i32, P, P, i32, i32, f32, i32, P, sz, P, i32, P]),

@@ -2,6 +2,7 @@
 // (+ combine) and the Backend FlashAttention operator over contiguous K/V.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 
 #include "it_decode.hpp"
@@ -12,6 +13,7 @@ using namespace itkv;
 
 namespace {
 constexpr int kMaxParts = 4096;
+constexpr int kCompactSeqs = 512;
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
@@ -90,8 +92,11 @@ int32_t run_decode(const char* who, int32_t cache_dt, int32_t q_dtype, int32_t o
   a.chunks = a.group / gc;
   if (int64_t(a.n_kv_heads) * a.chunks > 65535) return fail(IT_NOT_IMPLEMENTED, "%s: too many head chunks", who);
   a.max_pages = (a.partition >> a.log2_bs) + 2;
-  const size_t smem = decode_smem_bytes(cache_dt, gc, d, a.partition, a.max_pages,
-                                        int64_t(a.max_parts) * a.n_kv_heads * a.chunks * n_seqs);
+  const int64_t n_wg = int64_t(a.max_parts) * a.n_kv_heads * a.chunks * n_seqs;
+  // Per-sequence contexts: map workgroups to the non-empty units in order
+  // (every wave scans the n_seqs context lengths once, so only up to 512).
+  a.compact = (a.ctx_lens != nullptr && n_seqs <= kCompactSeqs && n_wg < (int64_t(1) << 31)) ? 1 : 0;
+  const size_t smem = decode_smem_bytes(cache_dt, gc, d, a.partition, a.max_pages, n_wg);
   if (smem > kMaxDecodeLds) return fail(IT_INVALID_INPUT, "%s: partition %d needs %zu bytes of LDS", who, a.partition, smem);
   if (max_tokens > 0 && (phases & 1)) {
     dim3 grid(unsigned(a.max_parts), unsigned(a.n_kv_heads * a.chunks), unsigned(n_seqs));
@@ -111,6 +116,60 @@ extern "C" size_t it_paged_decode_workspace(int32_t n_seqs, int32_t n_heads, int
   if (n_seqs <= 0 || n_heads <= 0 || head_dim <= 0 || partition <= 0 || max_tokens < 0) return 0;
   const int64_t parts = max_tokens > 0 ? (int64_t(max_tokens) + partition - 1) / partition : 1;
   return ws_layout(n_seqs, n_heads, head_dim, parts).total;
+}
+
+extern "C" int32_t it_paged_decode_partition(int32_t dtype, int32_t head_dim, int32_t block_size, int32_t n_heads,
+                                             int32_t n_kv_heads, const int32_t* ctx_lens, const int32_t* start_pos,
+                                             int32_t n_seqs, int32_t n_cu, int32_t* partition) {
+  constexpr const char* who = "it_paged_decode_partition";
+  if (!ctx_lens || !partition) return fail(IT_INVALID_INPUT, "%s: NULL argument", who);
+  if (n_seqs <= 0) return fail(IT_INVALID_INPUT, "%s: n_seqs %d <= 0", who, n_seqs);
+  if (n_kv_heads <= 0 || n_heads <= 0 || n_heads % n_kv_heads)
+    return fail(IT_INVALID_INPUT, "%s: n_heads %d must be a positive multiple of n_kv_heads %d", who, n_heads,
+                n_kv_heads);
+  if (block_size < 8 || (block_size & (block_size - 1)))
+    return fail(IT_INVALID_INPUT, "%s: block_size %d must be a power of two >= 8", who, block_size);
+  if (head_dim != 128 && head_dim != 256) return fail(IT_NOT_IMPLEMENTED, "%s: head_dim %d", who, head_dim);
+  if (n_cu <= 0) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n_cu <= 0)
+      return fail(IT_DEVICE_ERROR, "%s: cannot read the device's compute-unit count", who);
+  }
+  int log2_bs = 0;
+  while ((1 << log2_bs) < block_size) ++log2_bs;
+  const int group = n_heads / n_kv_heads, gc = pick_chunk(group);
+  const int64_t hc = int64_t(n_kv_heads) * (group / gc);
+  int64_t max_n = 0;
+  for (int b = 0; b < n_seqs; ++b) {
+    const int64_t n = int64_t(ctx_lens[b]) - (start_pos ? start_pos[b] : 0);
+    if (n > max_n) max_n = n;
+  }
+  // Resident slots of one round: four workgroups per compute unit, fewer
+  // where the LDS does not hold four.
+  int best = 0;
+  int64_t best_rounds = 0;
+  for (int p = 64; p <= 2048; p += 64) {
+    const int64_t parts = max_n > 0 ? (max_n + p - 1) / p : 1;
+    if (parts > kMaxParts) continue;
+    const size_t smem =
+        decode_smem_bytes(dtype, gc, head_dim, p, (p >> log2_bs) + 2, parts * hc * n_seqs);
+    if (smem > kMaxDecodeLds) continue;
+    const int64_t per_cu = std::min<int64_t>(4, int64_t(kMaxDecodeLds / smem));
+    int64_t units = 0;
+    for (int b = 0; b < n_seqs; ++b) {
+      const int64_t n = int64_t(ctx_lens[b]) - (start_pos ? start_pos[b] : 0);
+      if (n > 0) units += (n + p - 1) / p;
+    }
+    const int64_t rounds = (units * hc + per_cu * n_cu - 1) / (per_cu * n_cu);
+    if (!best || rounds < best_rounds) {
+      best = p;
+      best_rounds = rounds;
+    }
+  }
+  if (!best) return fail(IT_NOT_IMPLEMENTED, "%s: no partition fits (max context %lld)", who, (long long)max_n);
+  *partition = best;
+  return IT_OK;
 }
 
 namespace {

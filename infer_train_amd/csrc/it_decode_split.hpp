@@ -371,6 +371,21 @@ __device__ __forceinline__ void fold8(const float (&x)[8], float& ra, float& rb)
   }
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave (DPP: row shifts within
+// each 16-lane row, then row broadcasts of lanes 15 and 31).  Lanes a DPP
+// source does not reach add 0 (bound_ctrl, or the disabled banks and rows,
+// which return the old operand 0).
+__device__ __forceinline__ int wave_inclusive_sum(int x) {
+  int v = x + __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, true);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, true);          // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, x, 0x113, 0xf, 0xf, true);          // row_shr:3
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xe, false);         // row_shr:4, banks 1-3
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xc, false);         // row_shr:8, banks 2-3
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);         // row_bcast:15, rows 1, 3
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);         // row_bcast:31, rows 2-3
+  return v;
+}
+
 template <int DT, int D, int GC, int NW, int R>
 __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
   using F = SplitFmt<DT, D>;
@@ -395,16 +410,61 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
   int32_t* const s_pages = reinterpret_cast<int32_t*>(s_pp + NW * (F::kScratch / 4));
   // Score of head h, token i (partition-relative): sc[h * SP + i].
 
-  const int part = blockIdx.x;
-  const int kvh = blockIdx.y / a.chunks;
-  const int chunk = blockIdx.y - kvh * a.chunks;
-  const int b = blockIdx.z;
-  const int head0 = kvh * a.group + chunk * GC;
-
-  const int ctx = a.ctx_lens ? a.ctx_lens[b] : a.ctx_const;
-  const int st = a.start_pos ? a.start_pos[b] : 0;
-  const int n = ctx - st;
   const int P = a.partition;
+  int part, yc, b, ctx, st;
+  if (a.compact) {
+    // Workgroup L takes the L-th non-empty (sequence, head chunk, partition)
+    // unit, counted sequence by sequence.  The non-empty units are then the
+    // grid's first workgroups, and consecutive ones go to different XCDs
+    // (the dispatcher deals workgroups to the XCDs round-robin), so ragged
+    // contexts spread evenly over the XCDs.  Every wave finds the unit
+    // itself: a 64-wide prefix sum of the sequences' unit counts.
+    const int L = int(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z));
+    const int n_seqs = int(gridDim.z), hc = int(gridDim.y);
+    const int ln = int(threadIdx.x & 63);
+    int base = 0;
+    b = -1;
+    part = yc = ctx = st = 0;
+    for (int s0 = 0; s0 < n_seqs; s0 += 64) {
+      const int s = s0 + ln;
+      int cnt = 0, c = 0, t = 0;
+      if (s < n_seqs) {
+        c = a.ctx_lens[s];
+        t = a.start_pos ? a.start_pos[s] : 0;
+        const int nn = c - t;
+        cnt = nn > 0 ? min((nn + P - 1) / P, a.max_parts) * hc : 0;
+      }
+      const int incl = wave_inclusive_sum(cnt);
+      const int total = __builtin_amdgcn_readlane(incl, 63);
+      if (L < base + total) {
+        // Inclusive prefixes do not decrease, so the lanes at or below L
+        // are a prefix of the wave; the unit's sequence is the next lane.
+        const int idx = int(__popcll(__builtin_amdgcn_ballot_w64(base + incl <= L)));
+        const int r = L - base - __builtin_amdgcn_readlane(incl - cnt, idx);
+        const int np = max(1, __builtin_amdgcn_readlane(cnt, idx) / hc);
+        b = s0 + idx;
+        ctx = __builtin_amdgcn_readlane(c, idx);
+        st = __builtin_amdgcn_readlane(t, idx);
+        yc = r / np;
+        part = r - yc * np;
+        break;
+      }
+      base += total;
+    }
+    // Past the last unit (uniform for the workgroup); the range checks keep
+    // every index in bounds whatever the counts.
+    if (b < 0 || b >= n_seqs || yc < 0 || yc >= hc || part < 0 || part >= a.max_parts) return;
+  } else {
+    part = blockIdx.x;
+    yc = blockIdx.y;
+    b = blockIdx.z;
+    ctx = a.ctx_lens ? a.ctx_lens[b] : a.ctx_const;
+    st = a.start_pos ? a.start_pos[b] : 0;
+  }
+  const int kvh = yc / a.chunks;
+  const int chunk = yc - kvh * a.chunks;
+  const int head0 = kvh * a.group + chunk * GC;
+  const int n = ctx - st;
   if (n <= 0 || part * P >= n) return;  // uniform for the workgroup
   if (part == a.max_parts - 1 && n > a.max_parts * P && threadIdx.x == 0)
     atomicOr(a.err, 8u);  // context longer than the caller's max_tokens: tail ignored

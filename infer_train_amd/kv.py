@@ -173,6 +173,12 @@ class PagedKvCache:
         nbytes = lib.it_paged_decode_workspace(n_seqs, n_heads, self.head_dim, max_tokens, partition)
         return torch.empty(nbytes, dtype=torch.uint8, device=self.device)
 
+    def decode_partition(self, n_heads: int, ctx_lens, start_pos=None, n_cu: int = 0) -> int:
+        """Partition for a decode over these host-side contexts
+        (it_paged_decode_partition)."""
+        return decode_partition(self.dtype, self.head_dim, self.block_size, n_heads, self.n_kv_heads, ctx_lens,
+                                start_pos, n_cu)
+
     def decode(self, q: torch.Tensor, block_tables: torch.Tensor, ctx_lens: torch.Tensor,
                start_pos: Optional[torch.Tensor], max_tokens: int, scale: Optional[float] = None,
                partition: int = 512, out: Optional[torch.Tensor] = None, ws: Optional[torch.Tensor] = None,
@@ -215,6 +221,24 @@ class PagedKvCache:
         if h is not None and h.value and destroy is not None:
             destroy(h)
             self._h = C.c_void_p()
+
+
+def decode_partition(dtype: int, head_dim: int, block_size: int, n_heads: int, n_kv_heads: int, ctx_lens,
+                     start_pos=None, n_cu: int = 0) -> int:
+    """Tokens per split for a paged decode over contexts known on the host
+    (it_paged_decode_partition): the smallest multiple of 64 whose non-empty
+    units run in the fewest rounds of resident workgroups.  n_cu 0 asks the
+    current device."""
+    import numpy as np
+
+    ctx = np.ascontiguousarray(np.asarray(ctx_lens, dtype=np.int32))
+    st = None if start_pos is None else np.ascontiguousarray(np.asarray(start_pos, dtype=np.int32))
+    if st is not None and st.shape != ctx.shape:
+        raise ValueError("start_pos must match ctx_lens")
+    out = C.c_int32()
+    check(lib.it_paged_decode_partition(dtype, head_dim, block_size, n_heads, n_kv_heads, ctx.ctypes.data,
+                                        None if st is None else st.ctypes.data, ctx.size, n_cu, C.byref(out)))
+    return out.value
 
 
 def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask: Optional[torch.Tensor] = None,

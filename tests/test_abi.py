@@ -56,6 +56,42 @@ def test_status_codes_and_pure_queries():
     assert ws >= 32 * 28 * 9 * (128 + 2) * 4
 
 
+def test_decode_partition_planner():
+    """it_paged_decode_partition: the smallest multiple of 64 whose
+    non-empty units run in the fewest rounds of four resident workgroups per
+    compute unit (host arithmetic, no device with n_cu given)."""
+    import numpy as np
+
+    from infer_train_amd import _lib as L
+    from infer_train_amd.kv import decode_partition
+
+    def plan(ctx, start=None, hq=28, hkv=4, dt=L.BF16, D=128, bs=16, n_cu=256):
+        return decode_partition(dt, D, bs, hq, hkv, ctx, start, n_cu)
+
+    # Config 2 at 4k: 32 x 4 heads x 8 partitions of 512 = 1024 = 4 x 256.
+    assert plan(np.full(32, 4096)) == 512
+    # Config 2 as specified (ragged): 256-token partitions give 1024 units.
+    ctx = np.random.default_rng(22).integers(256, 4097, 32) + 1
+    assert plan(ctx) == 256
+    units = lambda p: int(sum((c + p - 1) // p for c in ctx)) * 4
+    assert units(256) <= 1024 < units(192)
+    # One 1024-token sequence (config 1 heads): the shortest partition.
+    assert plan([1024], hq=12, hkv=2, dt=L.F32) == 64
+    # Windows count only [start, ctx); empty batches take the shortest.
+    assert plan(np.full(32, 8192), np.full(32, 8192 - 4096)) == 512
+    assert plan([0, 5], [0, 5]) == 64
+    # Half the compute units: 512-token partitions take 2 rounds of 512
+    # slots; 1024-token ones also 2 (their LDS leaves 2 per CU); shorter
+    # ones 3 or more.
+    assert plan(np.full(32, 4096), n_cu=128) == 512
+    with pytest.raises(L.InvalidInput):
+        plan([5], hq=7, hkv=2)
+    with pytest.raises(L.NotImplementedOp):
+        plan([5], D=96)
+    with pytest.raises(ValueError):
+        plan([5, 6], [1])
+
+
 def test_invalid_input_before_device():
     from infer_train_amd import _lib as L
 

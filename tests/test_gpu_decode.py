@@ -126,6 +126,33 @@ def test_config2_full_size_bf16():
     assert_close(got, want, *TOL[orc.BF16], what="config2 full")
 
 
+def test_many_sequences_unit_mapping():
+    """Workgroups run the non-empty (sequence, head, partition) units in
+    order, found by a prefix sum over the context lengths 64 sequences at a
+    time: 130 sequences (three scan steps) with empty ones (ctx 0, and a
+    window start equal to ctx), windows, and 64-token partitions; the
+    partition the host planner picks for the batch; and 600 sequences, past
+    the 512 the scan takes, where workgroups map to units by grid index."""
+    hq, hkv, D, bs = 8, 2, 128, 16
+    rng = np.random.default_rng(41)
+    ctx = rng.integers(0, 300, 130).astype(np.int32)
+    ctx[[0, 63, 64, 127, 129]] = 0
+    start = np.minimum(rng.integers(0, 100, 130), ctx).astype(np.int32)
+    start[[5, 70, 128]] = ctx[[5, 70, 128]]
+    dev, ref, tables, ctx, q, qdt = _build(orc.BF16, hq, hkv, D, bs, ctx, seed=41)
+    p_host = dev.decode_partition(hq, ctx, start)
+    assert 64 <= p_host <= 2048 and p_host % 64 == 0
+    for partition in (64, 128, p_host):
+        got, want = _run(dev, ref, tables, ctx, q, qdt, hq, start=start, partition=partition)
+        assert_close(got, want, *TOL[orc.BF16], what=f"130 seqs P={partition}")
+        n = ctx - start
+        assert np.all(got[n <= 0] == 0)
+    ctx2 = rng.integers(0, 40, 600).astype(np.int32)
+    dev, ref, tables, ctx2, q, qdt = _build(orc.BF16, hq, hkv, D, bs, ctx2, seed=42)
+    got, want = _run(dev, ref, tables, ctx2, q, qdt, hq, partition=64)
+    assert_close(got, want, *TOL[orc.BF16], what="600 seqs")
+
+
 @pytest.mark.parametrize("dt", [orc.F16, orc.F32])
 def test_other_dtypes(dt):
     hq, hkv, D, bs = 8, 2, 128, 16
