@@ -504,7 +504,12 @@ def bench_config4(steps, warmup, cpu):
     kn = torch.randn((n_seqs, hkv, D), generator=g, device=dev).to(torch.bfloat16)
     vn = torch.randn((n_seqs, hkv, D), generator=g, device=dev).to(torch.bfloat16)
     out = torch.empty_like(q)
-    ws = c.decode_workspace(n_seqs, hq, W, 512)
+    from infer_train_amd.kv import decode_partition
+
+    # Every sequence reads a full window each step: the planner's partition
+    # for 64 windows of W tokens.
+    P = decode_partition(it.BF16, D, bs, hq, hkv, np.full(n_seqs, W))
+    ws = c.decode_workspace(n_seqs, hq, W, P)
     scale = 1.0 / math.sqrt(D)
     seqs = list(range(n_seqs))
 
@@ -528,7 +533,7 @@ def bench_config4(steps, warmup, cpu):
         c.sync_tables(tables, tseq, tpos, slots)
         if ev is not None:
             ev[1].record()
-        c.decode(q, tables, ctx_d, st_d, W, scale=scale, partition=512, out=out, ws=ws)
+        c.decode(q, tables, ctx_d, st_d, W, scale=scale, partition=P, out=out, ws=ws)
         if ev is not None:
             ev[2].record()
         return host_s, int(plan.evicted.size)
@@ -579,13 +584,17 @@ def bench_config5(steps, warmup, cpu):
     rng = np.random.default_rng(5)
     ctx = rng.integers(32768, 131073, 16).astype(np.int32)
     pool_blocks = int(sum((int(c) + 31) // 32 for c in ctx)) + 16
-    # 1024-token partitions (the config leaves the split to the builder): half the
-    # (m, l, O) partials of 512, and still two workgroups per CU.
-    w = DecodeWorkload(it.Q8_0, 24, 4, 256, 32, ctx, pool_blocks, 1024, seed=5, replicas=1)
+    # The config leaves the split to the builder: the host planner's partition
+    # (the batch fills the machine many times over at any size, so the longest
+    # that keeps two workgroups per CU: 1792 tokens).
+    from infer_train_amd.kv import decode_partition
+
+    P = decode_partition(it.Q8_0, 256, 32, 24, 4, ctx)
+    w = DecodeWorkload(it.Q8_0, 24, 4, 256, 32, ctx, pool_blocks, P, seed=5, replicas=1)
     r = w.time(steps, warmup, rotate=False)
     res = {"workload": "config 5: Q8_0 KV, Hq 24 / Hkv 4 / D 256, block 32, batch 16, ctx U[32768, 131072], "
-                       "quantise-append 1 token per sequence + split-K decode (1024-token partitions) dequantising "
-                       "in registers",
+                       f"quantise-append 1 token per sequence + split-K decode ({P}-token partitions from the host "
+                       "planner) dequantising in registers",
            "kv_bytes": int(w.kv_bytes), "decode_us": round(r["decode"] * 1e3, 2), "split_us": round(r["split"] * 1e3, 2),
            "kv_gbs": round(w.kv_bytes / (r["decode"] * 1e-3) / 1e9, 1),
            "pct_hbm_peak": round(100 * w.kv_bytes / (r["decode"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
@@ -604,18 +613,20 @@ def bench_config5(steps, warmup, cpu):
 def bench_q4(dtype, steps, warmup):
     """Q4_0 / Q4_1 KV (formats beyond the five configs) on the config-5 shape:
     Hq 24 / Hkv 4 / D 256, block 32, batch 16, ctx U[32768, 131072],
-    1024-token partitions; quantise-append 1 token per sequence + split-K
+    partitions from the host planner; quantise-append 1 token per sequence + split-K
     decode."""
     import infer_train_amd as it
+    from infer_train_amd.kv import decode_partition
 
     rng = np.random.default_rng(5)
     ctx = rng.integers(32768, 131073, 16).astype(np.int32)
     pool_blocks = int(sum((int(c) + 31) // 32 for c in ctx)) + 16
-    w = DecodeWorkload(dtype, 24, 4, 256, 32, ctx, pool_blocks, 1024, seed=5, replicas=1)
+    P = decode_partition(dtype, 256, 32, 24, 4, ctx)
+    w = DecodeWorkload(dtype, 24, 4, 256, 32, ctx, pool_blocks, P, seed=5, replicas=1)
     r = w.time(steps, warmup, rotate=False)
     name = {it.Q4_0: "Q4_0", it.Q4_1: "Q4_1"}[dtype]
     res = {"workload": f"{name} KV on the config-5 shape (Hq 24 / Hkv 4 / D 256, block 32, batch 16, "
-                       "ctx U[32768, 131072], 1024-token partitions), dequantising in registers",
+                       f"ctx U[32768, 131072], {P}-token partitions from the host planner), dequantising in registers",
            "kv_bytes": int(w.kv_bytes), "decode_us": round(r["decode"] * 1e3, 2), "split_us": round(r["split"] * 1e3, 2),
            "kv_gbs": round(w.kv_bytes / (r["decode"] * 1e-3) / 1e9, 1),
            "pct_hbm_peak": round(100 * w.kv_bytes / (r["decode"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
@@ -788,11 +799,16 @@ def summarize_config5_profile(d, args):
     stats = [r for r in rows("trace", "kernel_stats") if "decode" in r["Name"] or "append" in r["Name"]]
     trace = [r for r in rows("trace", "kernel_trace") if kname in r["Kernel_Name"]]
     durs = np.array([(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in trace])
+    import infer_train_amd as it
+    from infer_train_amd.kv import decode_partition
+
     rng = np.random.default_rng(5)  # the config-5 contexts, as bench_config5
-    kv_bytes = float(rng.integers(32768, 131073, 16).astype(np.int64).sum()) * 4 * 2 * 256 * 34 / 32
+    ctx = rng.integers(32768, 131073, 16)
+    kv_bytes = float(ctx.astype(np.int64).sum()) * 4 * 2 * 256 * 34 / 32
+    part = decode_partition(it.Q8_0, 256, 32, 24, 4, ctx, None, 256)
     cmd = "python3 bench.py --only-config5 --steps {s} --warmup {w}".format(s=args.steps, w=args.warmup)
     lines = ["# paged_decode_split (Q8_0, D 256) -- config 5 (batch 16, ctx U[32768, 131072], "
-             "Hq 24 / Hkv 4, 1024-token partitions)", "",
+             f"Hq 24 / Hkv 4, {part}-token partitions)", "",
              "Commands (from the repository root on the GPU box; `cd /tmp && export TMPDIR=/tmp` first):", "",
              "```",
              f"rocprofv3 --kernel-trace --stats --output-format csv -d OUT/trace -o run -- {cmd}"]
@@ -927,15 +943,15 @@ def main():
         configs["4"] = bench_config4(max(16, args.steps // 2), 4, cpu)
         _progress("config 4 done")
     if 5 in want:
-        configs["5"] = bench_config5(small, 2, cpu)
+        configs["5"] = bench_config5(small, 10, cpu)
         _progress("config 5 done")
     configs["rope_append"] = bench_rope_append(max(10, args.steps // 2), 3)
     _progress("rope append done")
     if 5 in want:
         import infer_train_amd as it
 
-        configs["q4_0_config5_shape"] = bench_q4(it.Q4_0, small, 2)
-        configs["q4_1_config5_shape"] = bench_q4(it.Q4_1, small, 2)
+        configs["q4_0_config5_shape"] = bench_q4(it.Q4_0, small, 10)
+        configs["q4_1_config5_shape"] = bench_q4(it.Q4_1, small, 10)
         _progress("q4_0 / q4_1 done")
 
     cold, warm = head["cold"], head["warm"]

@@ -271,7 +271,9 @@ size_t it_paged_decode_workspace(int32_t n_seqs, int32_t n_heads, int32_t head_d
  * [64, 2048] whose non-empty (sequence, KV head, partition) units run in the
  * fewest rounds of four resident workgroups per compute unit.  Short
  * partitions keep each workgroup's chain of dependent page loads short;
- * units beyond the resident slots would run a second round.
+ * units beyond the resident slots would run a second round.  A batch that
+ * needs more than two rounds at any size takes the longest partition that
+ * keeps two workgroups per compute unit instead (fewest partials).
  *   ctx_lens, start_pos: host int32[n_seqs] (start_pos may be NULL)
  *   n_cu: compute units of the device (0 = ask the current HIP device)
  * No counterpart in the reference: flash_attn_f32 (flash_attn.rs:6-72) does

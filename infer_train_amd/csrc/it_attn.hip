@@ -147,7 +147,7 @@ extern "C" int32_t it_paged_decode_partition(int32_t dtype, int32_t head_dim, in
   }
   // Resident slots of one round: four workgroups per compute unit, fewer
   // where the LDS does not hold four.
-  int best = 0;
+  int best = 0, longest_two = 0;
   int64_t best_rounds = 0;
   for (int p = 64; p <= 2048; p += 64) {
     const int64_t parts = max_n > 0 ? (max_n + p - 1) / p : 1;
@@ -166,9 +166,14 @@ extern "C" int32_t it_paged_decode_partition(int32_t dtype, int32_t head_dim, in
       best = p;
       best_rounds = rounds;
     }
+    if (per_cu >= 2) longest_two = p;
   }
   if (!best) return fail(IT_NOT_IMPLEMENTED, "%s: no partition fits (max context %lld)", who, (long long)max_n);
-  *partition = best;
+  // Beyond two rounds the workgroups stream back to back and the machine
+  // stays full whatever the size: then the longest partition that still
+  // keeps two workgroups per CU writes the fewest partials and starts the
+  // fewest workgroups.
+  *partition = (best_rounds > 2 && longest_two) ? longest_two : best;
   return IT_OK;
 }
 

@@ -84,6 +84,10 @@ def test_decode_partition_planner():
     # slots; 1024-token ones also 2 (their LDS leaves 2 per CU); shorter
     # ones 3 or more.
     assert plan(np.full(32, 4096), n_cu=128) == 512
+    # Config 5 (Q8_0, D 256, block 32, 16 x U[32k, 128k]) needs many rounds
+    # at any size: the longest partition with two workgroups per CU.
+    c5 = np.random.default_rng(5).integers(32768, 131073, 16)
+    assert plan(c5, hq=24, hkv=4, dt=L.Q8_0, D=256, bs=32) == 1536
     with pytest.raises(L.InvalidInput):
         plan([5], hq=7, hkv=2)
     with pytest.raises(L.NotImplementedOp):
