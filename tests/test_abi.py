@@ -85,9 +85,12 @@ def test_decode_partition_planner():
     # ones 3 or more.
     assert plan(np.full(32, 4096), n_cu=128) == 512
     # Config 5 (Q8_0, D 256, block 32, 16 x U[32k, 128k]) needs many rounds
-    # at any size: the longest partition with two workgroups per CU.
+    # at any size: the longest partition with two workgroups per CU (at
+    # 1792 tokens a 4-wave workgroup takes just under 80 KiB of LDS; at
+    # 1856 it would not fit twice).
     c5 = np.random.default_rng(5).integers(32768, 131073, 16)
-    assert plan(c5, hq=24, hkv=4, dt=L.Q8_0, D=256, bs=32) == 1536
+    assert plan(c5, hq=24, hkv=4, dt=L.Q8_0, D=256, bs=32) == 1792
+    assert plan(c5, hq=24, hkv=4, dt=L.Q4_0, D=256, bs=32) == 1920
     with pytest.raises(L.InvalidInput):
         plan([5], hq=7, hkv=2)
     with pytest.raises(L.NotImplementedOp):
