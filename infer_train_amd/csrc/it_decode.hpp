@@ -56,6 +56,14 @@ __device__ __forceinline__ void dma_b32(const void* g, uint32_t m0) {
 }
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// One merged output element in the caller's dtype.  The value is o / l when
+// l > 0, else zero (flash_attn.rs:66-71: multiply by 1/s when s > 0).
+__device__ __forceinline__ void store_combined(void* out, int out_dtype, int64_t idx, float v) {
+  if (out_dtype == IT_F32) static_cast<float*>(out)[idx] = v;
+  else if (out_dtype == IT_BF16) static_cast<uint16_t*>(out)[idx] = uint16_t(f32_to_bf16_bits(v));
+  else static_cast<uint16_t*>(out)[idx] = uint16_t(f32_to_f16_bits(v));
+}
+
 // Merge the partitions of one (sequence, head) over a 64-dim slice (grid z):
 // M = max m_p, L = sum l_p 2^(m_p - M), O = sum O_p 2^(m_p - M) / L (the
 // split-K form of flash_attn_f32's rescaling, flash_attn.rs:42-71).  Lane d
@@ -75,14 +83,46 @@ __global__ __launch_bounds__(64) void paged_decode_combine(const float* __restri
   // the error); only the computed ones are merged.
   constexpr int kChunk = 16;
   const int h = blockIdx.x, b = blockIdx.y, d = 64 * blockIdx.z + threadIdx.x, lane = threadIdx.x;
+  const int64_t row = int64_t(b) * n_heads + h;
+  const float2* ml = reinterpret_cast<const float2*>(ws_ml) + row * max_parts;
+  const float* op = ws_o + row * max_parts * D + d;
+  // With at most kChunk partitions the loads of all max_parts slots go out
+  // before the context length arrives (the addresses do not depend on it);
+  // slots past this sequence's count hold stale bytes and are replaced by
+  // (-inf, 0) and 0 once the count is known.
+  float2 pre_ml[kChunk];
+  float pre_o[kChunk];
+  if (max_parts <= kChunk) {
+#pragma unroll
+    for (int c = 0; c < kChunk; ++c) {
+      if (c < max_parts) {
+        pre_ml[c] = ml[c];
+        pre_o[c] = op[int64_t(c) * D];
+      }
+    }
+  }
   const int ctx = ctx_lens ? ctx_lens[b] : ctx_const;
   const int st = start_pos ? start_pos[b] : 0;
   const int n = ctx - st;
   const int np = n > 0 ? min((n + partition - 1) / partition, max_parts) : 0;
-  const int64_t row = int64_t(b) * n_heads + h;
-  const float2* ml = reinterpret_cast<const float2*>(ws_ml) + row * max_parts;
-  const float* op = ws_o + row * max_parts * D + d;
   float mx = -INFINITY;
+  if (max_parts <= kChunk) {
+    float l = 0.0f, o = 0.0f;
+#pragma unroll
+    for (int c = 0; c < kChunk; ++c) {
+      if (c < np) mx = fmaxf(mx, pre_ml[c].x);
+    }
+#pragma unroll
+    for (int c = 0; c < kChunk; ++c) {
+      if (c < np) {
+        const float w = (pre_ml[c].x == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(pre_ml[c].x - mx);
+        l = fmaf(pre_ml[c].y, w, l);
+        o = fmaf(pre_o[c], w, o);
+      }
+    }
+    store_combined(out, out_dtype, row * D + d, l > 0.0f ? o * (1.0f / l) : 0.0f);
+    return;
+  }
   if (np > kChunk) {
     for (int p = lane; p < np; p += 64) mx = fmaxf(mx, ml[p].x);
     mx = group_max<64>(mx);
@@ -108,12 +148,7 @@ __global__ __launch_bounds__(64) void paged_decode_combine(const float* __restri
       o = fmaf(oc[c], w, o);
     }
   }
-  // flash_attn.rs:66-71: multiply by 1/s when s > 0, else zeros.
-  const float v = l > 0.0f ? o * (1.0f / l) : 0.0f;
-  const int64_t idx = row * D + d;
-  if (out_dtype == IT_F32) static_cast<float*>(out)[idx] = v;
-  else if (out_dtype == IT_BF16) static_cast<uint16_t*>(out)[idx] = uint16_t(f32_to_bf16_bits(v));
-  else static_cast<uint16_t*>(out)[idx] = uint16_t(f32_to_f16_bits(v));
+  store_combined(out, out_dtype, row * D + d, l > 0.0f ? o * (1.0f / l) : 0.0f);
 }
 
 }  // namespace itkv
