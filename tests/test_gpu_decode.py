@@ -153,6 +153,63 @@ def test_many_sequences_unit_mapping():
     assert_close(got, want, *TOL[orc.BF16], what="600 seqs")
 
 
+def test_config5_full_size_q8_0():
+    """Config 5 at full size: Q8_0, Hq 24 / Hkv 4 / D 256, block 32, 16
+    sequences of U[32768, 131072] tokens over a seeded permutation of the
+    pool, the planner's partition (1792 tokens: up to 74 partials merged per
+    row).  The oracle decodes the two shortest sequences over the same pages
+    (their bytes copied from the device pools into an oracle cache); a
+    second decode at 1024-token partitions agrees with the first."""
+    import torch
+    from infer_train_amd.kv import PagedKvCache
+
+    hq, hkv, D, bs = 24, 4, 256, 32
+    ctx = np.random.default_rng(5).integers(32768, 131073, 16).astype(np.int32)
+    nblk = (ctx + bs - 1) // bs
+    nb, mb = int(nblk.sum()), int(nblk.max())
+    tables = random_tables(55, ctx, bs, nb, mb)
+    dev = PagedKvCache(nb, bs, hkv, D, orc.Q8_0)
+    seqs = np.repeat(np.arange(16), ctx)
+    pos = np.concatenate([np.arange(c) for c in ctx])
+    slots = tables[seqs, pos // bs].astype(np.int64) * bs + pos % bs
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(55)
+    step = 1 << 16
+    for s0 in range(0, slots.size, step):
+        n = min(step, slots.size - s0)
+        k = torch.randn((n, hkv, D), generator=g, device="cuda:0")
+        v = torch.randn((n, hkv, D), generator=g, device="cuda:0")
+        dev.append(k, v, to_dev(slots[s0:s0 + n]))
+    dev.check()
+    q = kv_values(56, 16 * hq * D, orc.F32).reshape(16, hq, D)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
+    p_plan = dev.decode_partition(hq, ctx)
+    assert p_plan == 1792
+    outs = {}
+    for partition in (p_plan, 1024):
+        out = dev.decode(to_dev(q), to_dev(tables), to_dev(ctx), None, int(ctx.max()), scale=scale,
+                         partition=partition)
+        dev.check()
+        outs[partition] = from_dev(out)
+    assert_close(outs[1024], outs[p_plan], *TOL[orc.Q8_0], what="config5 1024 vs planner partition")
+
+    # Oracle over the two shortest sequences' pages, renumbered 0..n-1.
+    pick = np.argsort(ctx)[:2]
+    blocks = np.concatenate([tables[b, :nblk[b]] for b in pick])
+    t2 = np.full((2, int(nblk[pick].max())), -1, np.int32)
+    t2[0, :nblk[pick[0]]] = np.arange(nblk[pick[0]])
+    t2[1, :nblk[pick[1]]] = nblk[pick[0]] + np.arange(nblk[pick[1]])
+    ref = orc.Cache(blocks.size, bs, hkv, D, orc.Q8_0)
+    row = hkv * dev.page_bytes
+    idx = torch.from_numpy(blocks.astype(np.int64)).to("cuda:0")
+    ref.k[:] = from_dev(dev.k_pool.view(nb, row).index_select(0, idx)).reshape(-1)
+    ref.v[:] = from_dev(dev.v_pool.view(nb, row).index_select(0, idx)).reshape(-1)
+    want = ref.decode(q[pick], hq, t2, ctx[pick], None, scale)
+    exact = lazy(lambda: exact_decode(ref, q[pick], hq, t2, ctx[pick], None, scale))
+    got = outs[p_plan][pick].reshape(want.shape)
+    assert_close_or_closer(got, want, exact, *TOL[orc.Q8_0], what="config5 full, two shortest sequences")
+
+
 @pytest.mark.parametrize("dt", [orc.F16, orc.F32])
 def test_other_dtypes(dt):
     hq, hkv, D, bs = 8, 2, 128, 16
