@@ -1,0 +1,148 @@
+// Randomised exercise of the host allocator and slot manager (it_host.cpp),
+// built with AddressSanitizer and UndefinedBehaviorSanitizer by
+// test_host.py::test_host_code_under_sanitizers.  Every operation's
+// outputs are checked against the pool's own counters:
+//   - num_free + (distinct blocks some sequence holds) == capacity;
+//   - every table entry is held (ref_count >= 1), and a block's ref_count is
+//     the number of table entries naming it;
+//   - each returned slot lies in the block the table names for its position;
+//   - error paths (pool exhausted, table full, bad ids) return a status and
+//     leave no memory error behind.
+// Exit status 0 = all checks held; 1 = a check failed (message on stderr).
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <map>
+#include <random>
+#include <vector>
+
+#include "it_kv.h"
+
+namespace {
+long g_errors = 0, g_cows = 0, g_forks = 0, g_evicted = 0;
+
+int fail(const char* what, long a = 0, long b = 0) {
+  std::fprintf(stderr, "check failed: %s (%ld, %ld)\n", what, a, b);
+  std::exit(1);
+}
+
+struct Ctx {
+  it_block_pool* pool;
+  it_kv_manager* mgr;
+  int bs, seqs, mb;
+};
+
+// Tables, contexts and window starts, checked against the pool's counters.
+void check_state(const Ctx& c) {
+  std::vector<int32_t> t(size_t(c.seqs) * c.mb), ctx(c.seqs), st(c.seqs);
+  if (it_kv_manager_tables(c.mgr, t.data(), c.mb, ctx.data(), st.data()) != IT_OK) fail("tables");
+  std::map<int64_t, int64_t> refs;
+  for (int s = 0; s < c.seqs; ++s) {
+    if (st[s] < 0 || st[s] > ctx[s]) fail("window start", st[s], ctx[s]);
+    for (int j = 0; j < c.mb; ++j) {
+      const int32_t blk = t[size_t(s) * c.mb + j];
+      if (blk < 0) continue;
+      if (blk >= it_block_pool_capacity(c.pool)) fail("table entry range", blk);
+      ++refs[blk];
+    }
+  }
+  for (const auto& kv : refs)
+    if (it_block_pool_ref_count(c.pool, kv.first) != kv.second)
+      fail("ref count", kv.first, it_block_pool_ref_count(c.pool, kv.first));
+  if (it_block_pool_num_free(c.pool) + int64_t(refs.size()) != it_block_pool_capacity(c.pool))
+    fail("free + held != capacity", it_block_pool_num_free(c.pool), long(refs.size()));
+}
+
+void check_slots(const Ctx& c, const std::vector<int32_t>& seqs, const std::vector<int32_t>& ntok,
+                 const std::vector<int32_t>& ctx_before, const std::vector<int64_t>& slots) {
+  std::vector<int32_t> t(size_t(c.seqs) * c.mb);
+  if (it_kv_manager_tables(c.mgr, t.data(), c.mb, nullptr, nullptr) != IT_OK) fail("tables");
+  size_t k = 0;
+  for (size_t i = 0; i < seqs.size(); ++i)
+    for (int j = 0; j < ntok[i]; ++j, ++k) {
+      const int64_t pos = int64_t(ctx_before[i]) + j;
+      const int32_t blk = t[size_t(seqs[i]) * c.mb + pos / c.bs];
+      if (blk < 0 || slots[k] != int64_t(blk) * c.bs + pos % c.bs) fail("slot", long(slots[k]), long(blk));
+    }
+}
+
+int run(int window, uint32_t seed) {
+  Ctx c{nullptr, nullptr, 16, 8, 64};
+  const int64_t cap = 300;
+  if (it_block_pool_new(cap, IT_BF16, &c.pool) != IT_OK) fail("pool");
+  if (it_kv_manager_new(c.pool, c.bs, c.seqs, c.mb, window, &c.mgr) != IT_OK) fail("manager");
+  std::mt19937 rng(seed);
+  std::vector<int32_t> ev(4096), cs(64), cd(64);
+  std::vector<int64_t> slots(4096);
+  for (int step = 0; step < 3000; ++step) {
+    const int op = int(rng() % 100);
+    std::vector<int32_t> ctx(c.seqs);
+    if (it_kv_manager_tables(c.mgr, nullptr, c.mb, ctx.data(), nullptr) != IT_OK) fail("ctx");
+    if (op < 80) {  // append to a random subset, 1..40 tokens each
+      std::vector<int32_t> seqs, ntok, before;
+      for (int s = 0; s < c.seqs; ++s)
+        if (rng() % 2) {
+          seqs.push_back(s);
+          ntok.push_back(1 + int(rng() % 40));
+          before.push_back(ctx[s]);
+        }
+      if (seqs.empty()) continue;
+      int32_t n_ev = 0, n_cow = 0;
+      const int32_t rc =
+          (op < 40) ? it_kv_manager_append(c.mgr, seqs.data(), ntok.data(), int32_t(seqs.size()), slots.data(),
+                                           ev.data(), int32_t(ev.size()), &n_ev)
+                    : it_kv_manager_append_cow(c.mgr, seqs.data(), ntok.data(), int32_t(seqs.size()), slots.data(),
+                                               ev.data(), int32_t(ev.size()), &n_ev, cs.data(), cd.data(),
+                                               int32_t(cs.size()), &n_cow);
+      g_evicted += n_ev;
+      if (rc != IT_OK) {
+        ++g_errors;
+        // Table full or pool exhausted: the state is unspecified, so start
+        // every sequence over (releasing what each holds) and go on.
+        for (int s = 0; s < c.seqs; ++s)
+          if (it_kv_manager_release_seq(c.mgr, s, ev.data(), int32_t(ev.size()), &n_ev) != IT_OK)
+            fail("release after error", s);
+      } else {
+        check_slots(c, seqs, ntok, before, slots);
+        g_cows += n_cow;
+        for (int i = 0; i < n_cow; ++i)
+          if (cs[i] < 0 || cd[i] < 0 || cs[i] == cd[i]) fail("cow pair", cs[i], cd[i]);
+      }
+    } else if (op < 90) {  // release one sequence
+      int32_t n_ev = 0;
+      if (it_kv_manager_release_seq(c.mgr, int32_t(rng() % c.seqs), ev.data(), int32_t(ev.size()), &n_ev) != IT_OK)
+        fail("release");
+    } else {  // fork into an empty sequence, if there is one
+      int dst = -1;
+      for (int s = 0; s < c.seqs; ++s)
+        if (ctx[s] == 0) dst = s;
+      const int src = int(rng() % c.seqs);
+      if (dst >= 0 && src != dst) {
+        if (it_kv_manager_fork(c.mgr, src, dst) != IT_OK) fail("fork", src, dst);
+        ++g_forks;
+      }
+    }
+    check_state(c);
+  }
+  // Bad ids and arguments: statuses, never memory errors.
+  int32_t n_ev = 0;
+  if (it_kv_manager_release_seq(c.mgr, c.seqs, ev.data(), 4, &n_ev) == IT_OK) fail("release out of range");
+  if (it_block_pool_free(c.pool, cap) == IT_OK) fail("free out of range");
+  if (it_block_pool_share(c.pool, -1) == IT_OK) fail("share out of range");
+  it_kv_manager_destroy(c.mgr);
+  it_block_pool_destroy(c.pool);
+  return 0;
+}
+}  // namespace
+
+int main() {
+  for (uint32_t seed = 1; seed <= 4; ++seed) {
+    run(0, seed);
+    run(100, seed);
+  }
+  std::printf("host sanitize driver: ok (%ld error recoveries, %ld forks, %ld copy-on-write pairs, %ld evictions)\n",
+              g_errors, g_forks, g_cows, g_evicted);
+  // Each path must have been taken, or the run proves little.
+  if (!g_errors || !g_forks || !g_cows || !g_evicted) return 1;
+  return 0;
+}
