@@ -160,7 +160,7 @@ def test_batcher_fifo_admission_and_plans():
 def test_host_code_under_sanitizers(tmp_path):
     """The host allocator and slot manager (csrc/it_host.cpp, plain C++)
     built with AddressSanitizer and UndefinedBehaviorSanitizer and driven by
-    tests/host_sanitize_driver.cpp: 24,000 random appends (plain and
+    tests/host_sanitize_driver.cpp: 24,000 random steps of appends (plain and
     copy-on-write), releases and forks with and without a window, the error
     paths of a full table and an exhausted pool, and the pool's counters
     checked after every operation."""
