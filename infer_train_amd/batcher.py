@@ -64,7 +64,16 @@ class KvManager:
         total = int(nt.sum())
         before = self.positions()
         token_seq = np.repeat(seqs_a, nt).astype(np.int32)
-        token_pos = (before[token_seq] + (np.arange(total) - np.repeat(np.cumsum(nt) - nt, nt))).astype(np.int32)
+        # Each token's position: its sequence's position before the call plus
+        # the tokens of that sequence listed before it (a sequence may be
+        # listed more than once, as the native manager allows).
+        token_pos = np.empty(total, dtype=np.int32)
+        run = before.astype(np.int64)
+        off = 0
+        for sq, k in zip(seqs_a.tolist(), nt.tolist()):
+            token_pos[off:off + k] = run[sq] + np.arange(k)
+            run[sq] += k
+            off += k
         slots = np.empty(max(total, 1), dtype=np.int64)
         # Upper bound of frees: every block of every listed sequence.
         cap = int(seqs_a.size * self.max_blocks + 1)

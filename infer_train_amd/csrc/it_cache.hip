@@ -98,7 +98,11 @@ __global__ __launch_bounds__(kThreads) void kv_gather_vec(
   const int b = blockIdx.y;
   const int st = start_pos ? start_pos[b] : 0;
   const int n = ctx_lens[b] - st;
-  if (n <= 0 || st < 0) return;
+  if (st < 0) {  // skipped and latched
+    if (blockIdx.x == 0 && threadIdx.x == 0) atomicOr(err, kErrStart);
+    return;
+  }
+  if (n <= 0) return;
   const int64_t gid = int64_t(blockIdx.x) * kThreads + threadIdx.x;
   if (gid >= int64_t(hkv) * n * row_vecs) return;
   const int c = int(gid % row_vecs);
@@ -133,7 +137,11 @@ __global__ __launch_bounds__(kThreads) void kv_gather_q8_0(
   const int b = blockIdx.y;
   const int st = start_pos ? start_pos[b] : 0;
   const int n = ctx_lens[b] - st;
-  if (n <= 0 || st < 0) return;
+  if (st < 0) {  // skipped and latched
+    if (blockIdx.x == 0 && threadIdx.x == 0) atomicOr(err, kErrStart);
+    return;
+  }
+  if (n <= 0) return;
   const int ng = d >> 5;
   const int64_t gid = int64_t(blockIdx.x) * kThreads + threadIdx.x;
   if (gid >= int64_t(hkv) * n * ng) return;
@@ -181,7 +189,11 @@ __global__ __launch_bounds__(kThreads) void kv_gather_q4_0(
   const int b = blockIdx.y;
   const int st = start_pos ? start_pos[b] : 0;
   const int n = ctx_lens[b] - st;
-  if (n <= 0 || st < 0) return;
+  if (st < 0) {  // skipped and latched
+    if (blockIdx.x == 0 && threadIdx.x == 0) atomicOr(err, kErrStart);
+    return;
+  }
+  if (n <= 0) return;
   const int ng = d >> 5;
   const int64_t gid = int64_t(blockIdx.x) * kThreads + threadIdx.x;
   if (gid >= int64_t(hkv) * n * ng) return;
@@ -228,7 +240,11 @@ __global__ __launch_bounds__(kThreads) void kv_gather_q4_1(
   const int b = blockIdx.y;
   const int st = start_pos ? start_pos[b] : 0;
   const int n = ctx_lens[b] - st;
-  if (n <= 0 || st < 0) return;
+  if (st < 0) {  // skipped and latched
+    if (blockIdx.x == 0 && threadIdx.x == 0) atomicOr(err, kErrStart);
+    return;
+  }
+  if (n <= 0) return;
   const int ng = d >> 5;
   const int64_t gid = int64_t(blockIdx.x) * kThreads + threadIdx.x;
   if (gid >= int64_t(hkv) * n * ng) return;
@@ -466,9 +482,10 @@ extern "C" int32_t it_kv_cache_check(it_kv_cache* c, void* stream) {
   IT_HIP(hipMemcpy(&flag, c->err_flag, 4, hipMemcpyDeviceToHost), "it_kv_cache_check: read flag");
   if (!flag) return IT_OK;
   IT_HIP(hipMemset(c->err_flag, 0, 4), "it_kv_cache_check: clear flag");
-  return fail(IT_INVALID_INPUT, "kv cache: device-side range error (%s%s%s%s%s)", (flag & kErrSlot) ? "slot " : "",
+  return fail(IT_INVALID_INPUT, "kv cache: device-side range error (%s%s%s%s%s%s)", (flag & kErrSlot) ? "slot " : "",
               (flag & kErrBlock) ? "block-id " : "", (flag & kErrTable) ? "table-index " : "",
-              (flag & kErrCtx) ? "ctx>max_tokens " : "", (flag & kErrPos) ? "rope-position" : "");
+              (flag & kErrCtx) ? "ctx>max_tokens " : "", (flag & kErrPos) ? "rope-position " : "",
+              (flag & kErrStart) ? "negative-start" : "");
 }
 
 extern "C" int32_t it_kv_append(it_kv_cache* c, const void* k, const void* v, int32_t src_dtype,
@@ -590,7 +607,7 @@ extern "C" int32_t it_supports(int32_t op, int32_t dtype) {
     case IT_OP_KV_EVICT:
     case IT_OP_KV_COPY_BLOCKS:
     case IT_OP_PAGED_DECODE: return kv ? 1 : 0;
-    case IT_OP_PAGED_PREFILL: return dtype == IT_BF16 ? 1 : 0;
+    case IT_OP_PAGED_PREFILL: return (dtype == IT_BF16 || dtype == IT_F16) ? 1 : 0;
     case IT_OP_FLASH_ATTENTION: return dtype == IT_F32 ? 1 : 0;
     default: return 0;
   }

@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 
 #include "it_device.hpp"
+#include "it_internal.hpp"
 #include "it_kv.h"
 
 namespace itkv {
@@ -47,12 +48,15 @@ __device__ __forceinline__ uint32_t lds_offset(const void* p) {
 }
 // 64 lanes x 16 B from per-lane global addresses into LDS [m0, m0 + 1 KiB).
 // One wait state between the SALU write of M0 and the LDS-DMA read of it.
+// The loads carry the non-temporal hint: cache pages are streamed once per
+// step, and with `nt` the paged read pattern of config 2 runs at 6.65 TB/s
+// instead of 5.9 TB/s (measured with a DMA-only kernel of the same pattern).
 __device__ __forceinline__ void dma_b128(const void* g, uint32_t m0) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(m0), "v"(g) : "memory", "m0");
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off nt" ::"s"(m0), "v"(g) : "memory", "m0");
 }
-// Active lanes x 4 B into LDS [m0 + 4 lane].
+// Active lanes x 4 B into LDS [m0 + 4 lane], non-temporal like dma_b128.
 __device__ __forceinline__ void dma_b32(const void* g, uint32_t m0) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off" ::"s"(m0), "v"(g) : "memory", "m0");
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off nt" ::"s"(m0), "v"(g) : "memory", "m0");
 }
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
@@ -104,7 +108,9 @@ __global__ __launch_bounds__(64) void paged_decode_combine(const float* __restri
   const int ctx = ctx_lens ? ctx_lens[b] : ctx_const;
   const int st = start_pos ? start_pos[b] : 0;
   const int n = ctx - st;
-  const int np = n > 0 ? min((n + partition - 1) / partition, max_parts) : 0;
+  // A negative start position was skipped by the split pass (and latched):
+  // no partitions, zeros.
+  const int np = (n > 0 && st >= 0) ? min((n + partition - 1) / partition, max_parts) : 0;
   float mx = -INFINITY;
   if (max_parts <= kChunk) {
     float l = 0.0f, o = 0.0f;

@@ -411,6 +411,12 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
   // Score of head h, token i (partition-relative): sc[h * SP + i].
 
   const int P = a.partition;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int bs_mask = (1 << a.log2_bs) - 1;
+  const int bs = bs_mask + 1;
+  const int n_seqs = int(gridDim.z), hc = int(gridDim.y);
+  const int L = int(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z));
+
   int part, yc, b, ctx, st;
   if (a.compact) {
     // Workgroup L takes the L-th non-empty (sequence, head chunk, partition)
@@ -418,9 +424,8 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
     // grid's first workgroups, and consecutive ones go to different XCDs
     // (the dispatcher deals workgroups to the XCDs round-robin), so ragged
     // contexts spread evenly over the XCDs.  Every wave finds the unit
-    // itself: a 64-wide prefix sum of the sequences' unit counts.
-    const int L = int(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z));
-    const int n_seqs = int(gridDim.z), hc = int(gridDim.y);
+    // itself: a 64-wide prefix sum of the sequences' unit counts.  A
+    // sequence whose start position is negative has no units (latched).
     const int ln = int(threadIdx.x & 63);
     int base = 0;
     b = -1;
@@ -432,7 +437,8 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
         c = a.ctx_lens[s];
         t = a.start_pos ? a.start_pos[s] : 0;
         const int nn = c - t;
-        cnt = nn > 0 ? min((nn + P - 1) / P, a.max_parts) * hc : 0;
+        cnt = (nn > 0 && t >= 0) ? min((nn + P - 1) / P, a.max_parts) * hc : 0;
+        if (t < 0 && L == 0) atomicOr(a.err, kErrStart);
       }
       const int incl = wave_inclusive_sum(cnt);
       const int total = __builtin_amdgcn_readlane(incl, 63);
@@ -460,6 +466,10 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
     b = blockIdx.z;
     ctx = a.ctx_lens ? a.ctx_lens[b] : a.ctx_const;
     st = a.start_pos ? a.start_pos[b] : 0;
+    if (st < 0) {  // skipped, as the gather skips it (uniform for the workgroup)
+      if (tid == 0) atomicOr(a.err, kErrStart);
+      return;
+    }
   }
   const int kvh = yc / a.chunks;
   const int chunk = yc - kvh * a.chunks;
@@ -467,12 +477,9 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
   const int n = ctx - st;
   if (n <= 0 || part * P >= n) return;  // uniform for the workgroup
   if (part == a.max_parts - 1 && n > a.max_parts * P && threadIdx.x == 0)
-    atomicOr(a.err, 8u);  // context longer than the caller's max_tokens: tail ignored
+    atomicOr(a.err, kErrCtx);  // context longer than the caller's max_tokens: tail ignored
   const int tok0 = st + part * P;
   const int nt = min(P, n - part * P);
-  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int bs_mask = (1 << a.log2_bs) - 1;
-  const int bs = bs_mask + 1;
 
   // Page indices (block * n_kv_heads + kvh) of the partition, via LDS.
   const int lb0 = tok0 >> a.log2_bs;
@@ -482,14 +489,14 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
     int blk = lb;
     if (a.bt) {
       if (lb >= a.max_blocks) {
-        atomicOr(a.err, 4u);
+        atomicOr(a.err, kErrTable);
         blk = 0;
       } else {
         blk = a.bt[int64_t(b) * a.max_blocks + lb];
       }
     }
     if (blk < 0 || blk >= a.num_blocks) {
-      atomicOr(a.err, 2u);
+      atomicOr(a.err, kErrBlock);
       blk = 0;
     }
     s_pages[i] = blk * a.n_kv_heads + kvh;

@@ -202,9 +202,12 @@ int32_t append_impl(it_kv_manager* m, const int32_t* seqs, const int32_t* n_toke
           const int64_t j = m->first[size_t(s)];
           if (j >= m->max_blocks) break;
           if (row[j] >= 0) {
-            if (it_block_pool_free(m->pool, row[j]) != IT_OK) return IT_INVALID_INPUT;
-            if (ne >= evicted_cap)
+            // Capacity first: a block is freed only together with clearing
+            // its table entry, so an error leaves no table naming a freed
+            // block.
+            if (!evicted_out || ne >= evicted_cap)
               return fail(IT_INVALID_INPUT, "it_kv_manager_append: evicted_out capacity %d exceeded", evicted_cap);
+            if (it_block_pool_free(m->pool, row[j]) != IT_OK) return IT_INVALID_INPUT;
             evicted_out[ne++] = row[j];
             row[j] = -1;
           }
@@ -224,9 +227,10 @@ int32_t append_impl(it_kv_manager* m, const int32_t* seqs, const int32_t* n_toke
                     (long long)p);
       } else if (cow_src && it_block_pool_ref_count(m->pool, row[lb]) > 1) {
         // Copy-on-write: a shared partial block is about to be written.
+        // Capacity before allocating, so an error leaks no block.
+        if (nc >= cow_cap) return fail(IT_INVALID_INPUT, "it_kv_manager_append: cow capacity %d exceeded", cow_cap);
         const int64_t id = it_block_pool_allocate(m->pool);
         if (id < 0) return fail(IT_INVALID_INPUT, "it_kv_manager_append: block pool exhausted (CoW)");
-        if (nc >= cow_cap) return fail(IT_INVALID_INPUT, "it_kv_manager_append: cow capacity %d exceeded", cow_cap);
         cow_src[nc] = row[lb];
         cow_dst[nc] = int32_t(id);
         ++nc;

@@ -16,6 +16,7 @@ enum : uint32_t {
   kErrTable = 4u,       // logical block beyond max_blocks
   kErrCtx = 8u,         // context longer than the max_tokens bound
   kErrPos = 16u,        // RoPE position outside the table
+  kErrStart = 32u,      // negative start position (the sequence is skipped)
 };
 
 inline bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }

@@ -12,6 +12,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
+#include <cstring>
 #include <map>
 #include <random>
 #include <vector>
@@ -19,7 +20,7 @@
 #include "it_kv.h"
 
 namespace {
-long g_errors = 0, g_cows = 0, g_forks = 0, g_evicted = 0;
+long g_errors = 0, g_cows = 0, g_forks = 0, g_evicted = 0, g_ev_cap = 0, g_cow_cap = 0;
 
 int fail(const char* what, long a = 0, long b = 0) {
   std::fprintf(stderr, "check failed: %s (%ld, %ld)\n", what, a, b);
@@ -88,15 +89,23 @@ int run(int window, uint32_t seed) {
         }
       if (seqs.empty()) continue;
       int32_t n_ev = 0, n_cow = 0;
+      // Now and then the eviction and copy-on-write outputs are too small,
+      // so their capacity errors are taken too.
+      const int32_t ev_cap = (rng() % 6 == 0) ? int32_t(rng() % 3) : int32_t(ev.size());
+      const int32_t cow_cap = (rng() % 6 == 0) ? int32_t(rng() % 2) : int32_t(cs.size());
       const int32_t rc =
           (op < 40) ? it_kv_manager_append(c.mgr, seqs.data(), ntok.data(), int32_t(seqs.size()), slots.data(),
-                                           ev.data(), int32_t(ev.size()), &n_ev)
+                                           ev.data(), ev_cap, &n_ev)
                     : it_kv_manager_append_cow(c.mgr, seqs.data(), ntok.data(), int32_t(seqs.size()), slots.data(),
-                                               ev.data(), int32_t(ev.size()), &n_ev, cs.data(), cd.data(),
-                                               int32_t(cs.size()), &n_cow);
-      g_evicted += n_ev;
+                                               ev.data(), ev_cap, &n_ev, cs.data(), cd.data(), cow_cap, &n_cow);
+      if (rc == IT_OK) g_evicted += n_ev;
       if (rc != IT_OK) {
         ++g_errors;
+        if (std::strstr(it_last_error(), "evicted_out capacity")) ++g_ev_cap;
+        if (std::strstr(it_last_error(), "cow capacity")) ++g_cow_cap;
+        // Whatever the error, no table names a freed block and no block is
+        // lost: the counters hold before the recovery too.
+        check_state(c);
         // Table full or pool exhausted: the state is unspecified, so start
         // every sequence over (releasing what each holds) and go on.
         for (int s = 0; s < c.seqs; ++s)
@@ -135,14 +144,53 @@ int run(int window, uint32_t seed) {
 }
 }  // namespace
 
+// The case of a window eviction past evicted_cap: bs 16, window 16, 31
+// tokens, then one more with no room for the freed id.  The call fails, the
+// table no longer names the block, and releasing the sequence afterwards
+// frees nothing twice (another sequence's block stays allocated).
+void evict_capacity_case() {
+  it_block_pool* pool = nullptr;
+  it_kv_manager* mgr = nullptr;
+  if (it_block_pool_new(8, IT_BF16, &pool) != IT_OK || it_kv_manager_new(pool, 16, 2, 4, 16, &mgr) != IT_OK)
+    fail("evict case setup");
+  Ctx c{pool, mgr, 16, 2, 4};
+  std::vector<int64_t> slots(64);
+  std::vector<int32_t> ev(8);
+  int32_t seq = 0, n = 31, n_ev = 0;
+  if (it_kv_manager_append(mgr, &seq, &n, 1, slots.data(), ev.data(), 8, &n_ev) != IT_OK) fail("evict case 31");
+  n = 1;
+  if (it_kv_manager_append(mgr, &seq, &n, 1, slots.data(), ev.data(), 0, &n_ev) == IT_OK) fail("evict cap 0 accepted");
+  check_state(c);
+  seq = 1;
+  n = 20;
+  if (it_kv_manager_append(mgr, &seq, &n, 1, slots.data(), ev.data(), 8, &n_ev) != IT_OK) fail("evict case seq 1");
+  if (it_kv_manager_release_seq(mgr, 0, ev.data(), 8, &n_ev) != IT_OK) fail("evict case release");
+  check_state(c);
+  // Copy-on-write with no room for the pair: no block leaks.
+  if (it_kv_manager_fork(mgr, 1, 0) != IT_OK) fail("cow case fork");
+  int32_t cs = -1, cd = -1, n_cow = 0;
+  seq = 0;
+  n = 1;
+  if (it_kv_manager_append_cow(mgr, &seq, &n, 1, slots.data(), ev.data(), 8, &n_ev, &cs, &cd, 0, &n_cow) == IT_OK)
+    fail("cow cap 0 accepted");
+  check_state(c);
+  for (int s = 0; s < 2; ++s)
+    if (it_kv_manager_release_seq(mgr, s, ev.data(), 8, &n_ev) != IT_OK) fail("cow case release", s);
+  if (it_block_pool_num_free(pool) != 8) fail("blocks lost", long(it_block_pool_num_free(pool)));
+  it_kv_manager_destroy(mgr);
+  it_block_pool_destroy(pool);
+}
+
 int main() {
+  evict_capacity_case();
   for (uint32_t seed = 1; seed <= 4; ++seed) {
     run(0, seed);
     run(100, seed);
   }
-  std::printf("host sanitize driver: ok (%ld error recoveries, %ld forks, %ld copy-on-write pairs, %ld evictions)\n",
-              g_errors, g_forks, g_cows, g_evicted);
+  std::printf("host sanitize driver: ok (%ld error recoveries, %ld of them evicted_out capacity, %ld cow capacity; "
+              "%ld forks, %ld copy-on-write pairs, %ld evictions)\n",
+              g_errors, g_ev_cap, g_cow_cap, g_forks, g_cows, g_evicted);
   // Each path must have been taken, or the run proves little.
-  if (!g_errors || !g_forks || !g_cows || !g_evicted) return 1;
+  if (!g_errors || !g_ev_cap || !g_cow_cap || !g_forks || !g_cows || !g_evicted) return 1;
   return 0;
 }

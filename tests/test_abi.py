@@ -48,6 +48,8 @@ def test_status_codes_and_pure_queries():
     assert lib.it_supports(L.OP_PAGED_DECODE, 6) == 0  # Q5_0 caches are not implemented
     assert lib.it_kv_page_bytes(32, 256, L.Q4_1) == 32 * 128 + 32 * 8 * 4  # 5120
     assert lib.it_supports(L.OP_PAGED_PREFILL, L.Q4_0) == 0
+    assert lib.it_supports(L.OP_PAGED_PREFILL, L.BF16) == 1
+    assert lib.it_supports(L.OP_PAGED_PREFILL, L.F16) == 1  # F16 caches run the same MFMA kernel
     assert lib.it_kv_page_bytes(32, 256, L.Q4_0) == 32 * 128 + 32 * 8 * 2  # 4608
     assert lib.it_kv_page_bytes(16, 128, L.BF16) == 4096
     assert lib.it_kv_page_bytes(32, 256, L.Q8_0) == 32 * 256 + 32 * 8 * 2  # 8704

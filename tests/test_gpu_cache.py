@@ -239,6 +239,37 @@ def test_gather_bit_exact(dt, D, bs):
         np.testing.assert_array_equal(from_dev(vo)[off:off + want.size], want)
 
 
+def test_gather_negative_start_is_latched():
+    """A negative start position: the gather writes nothing for that
+    sequence, the others are exact, and it_kv_cache_check reports it."""
+    import torch
+    from infer_train_amd import InvalidInput
+
+    dt, D, bs, hkv, nb = orc.BF16, 128, 16, 2, 64
+    ctx = np.array([40, 70], np.int32)
+    tables = random_tables(9, ctx, bs, nb, 8)
+    dev, ref = _pair(nb, bs, hkv, D, dt)
+    seqs = [0] * 40 + [1] * 70
+    pos = list(range(40)) + list(range(70))
+    slots = slots_for(tables, seqs, pos, bs)
+    k, v = _src(4, len(slots), hkv, D, dt)
+    ref.append(k, v, slots)
+    dev.append(_dev_src(k, dt), _dev_src(v, dt), to_dev(slots))
+    start = np.array([-2, 3], np.int32)
+    n = np.array([40, 67], np.int64)
+    cu = np.array([0, 40], np.int64)
+    rk, rv = ref.gather(tables, ctx, np.array([0, 3], np.int32), cu, int(n.sum()))
+    ko = torch.zeros(rk.size, dtype=torch.uint8, device="cuda:0")
+    vo = torch.zeros(rv.size, dtype=torch.uint8, device="cuda:0")
+    dev.gather(to_dev(tables), to_dev(ctx), to_dev(start), to_dev(cu), 70, ko, vo)
+    with pytest.raises(InvalidInput, match="negative-start"):
+        dev.check()
+    row = hkv * D * 2  # bytes per token (both heads), bf16
+    np.testing.assert_array_equal(from_dev(ko)[:40 * row], 0)
+    np.testing.assert_array_equal(from_dev(ko)[40 * row:], rk[40 * row:])
+    np.testing.assert_array_equal(from_dev(vo)[40 * row:], rv[40 * row:])
+
+
 def test_evict_and_copy_blocks():
     hkv, D, bs, nb = 2, 128, 16, 32
     dev, ref = _pair(nb, bs, hkv, D, orc.BF16)

@@ -153,6 +153,51 @@ def test_many_sequences_unit_mapping():
     assert_close(got, want, *TOL[orc.BF16], what="600 seqs")
 
 
+def test_uniform_lengths():
+    """Equal lengths without start positions (the headline's shape at a
+    smaller batch): full and partial last partitions, 64- and 512-token
+    partitions, and one sequence shorter than the rest, which shifts the
+    unit order of every workgroup after it."""
+    hq, hkv, D, bs = 28, 4, 128, 16
+    for ctx in ([2048] * 12, [1000] * 9, [1536] * 5 + [700] + [1536] * 4):
+        dev, ref, tables, c, q, qdt = _build(orc.BF16, hq, hkv, D, bs, ctx, seed=12)
+        for partition in (512, 64):
+            got, want = _run(dev, ref, tables, c, q, qdt, hq, partition=partition)
+            assert_close(got, want, *TOL[orc.BF16], what=f"uniform {ctx[0]} x {len(ctx)} P={partition}")
+
+
+@pytest.mark.parametrize("n_seqs", [3, 600])
+def test_negative_start_is_skipped_and_latched(n_seqs):
+    """A negative start position is skipped, as the gather skips it: that
+    sequence's output is zeros, the others are unaffected, and
+    it_kv_cache_check reports the condition.  3 sequences take the compact
+    unit scan, 600 the grid mapping."""
+    import torch
+    from infer_train_amd import InvalidInput
+
+    hq, hkv, D, bs = 8, 2, 128, 16
+    rng = np.random.default_rng(7)
+    ctx = np.array([300, 200, 500], np.int32) if n_seqs == 3 else rng.integers(1, 40, n_seqs).astype(np.int32)
+    dev, ref, tables, ctx, q, qdt = _build(orc.BF16, hq, hkv, D, bs, ctx, seed=8)
+    start = np.zeros(n_seqs, np.int32)
+    start[-1] = min(5, int(ctx[-1]) - 1)
+    bad = 1
+    start[bad] = -3
+    ok_start = start.copy()
+    ok_start[bad] = 0
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
+    want = ref.decode(widen(q, qdt), hq, tables, ctx, ok_start, scale)
+    out = dev.decode(to_dev(q.view(np.int16), torch.bfloat16), to_dev(tables), to_dev(ctx), to_dev(start),
+                     int(ctx.max()), scale=scale, partition=64, out_dtype=torch.float32)
+    with pytest.raises(InvalidInput, match="negative-start"):
+        dev.check()
+    got = from_dev(out).reshape(want.shape)
+    assert np.all(got[bad] == 0)
+    keep = np.arange(n_seqs) != bad
+    assert_close(got[keep], want[keep], *TOL[orc.BF16], what=f"negative start, {n_seqs} seqs")
+    dev.check()  # the flag was cleared
+
+
 def test_config5_full_size_q8_0():
     """Config 5 at full size: Q8_0, Hq 24 / Hkv 4 / D 256, block 32, 16
     sequences of U[32768, 131072] tokens over a seeded permutation of the

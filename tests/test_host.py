@@ -139,6 +139,26 @@ def test_fork_copy_on_write():
     assert plan0.cow_src.size == 0 and plan0.slots[0] == 14 * 16 + 4
 
 
+def test_repeated_sequence_positions_match_slots():
+    """A sequence listed twice in one append gets consecutive positions, in
+    the order the native manager assigns its slots: the plan's positions
+    and slots agree (slot = table[pos / bs] * bs + pos % bs), also across a
+    block boundary."""
+    from infer_train_amd import BF16, BlockPool, KvManager
+
+    bs = 16
+    pool = BlockPool(32, BF16)
+    mgr = KvManager(pool, bs, 4, 8)
+    mgr.append([0], [15])
+    plan = mgr.append([0, 1, 0, 0], [1, 3, 1, 2])
+    tables, ctx, _ = mgr.tables()
+    assert list(plan.token_pos[plan.token_seq == 0]) == [15, 16, 17, 18]
+    assert list(plan.token_pos[plan.token_seq == 1]) == [0, 1, 2]
+    want = tables[plan.token_seq, plan.token_pos // bs].astype(np.int64) * bs + plan.token_pos % bs
+    np.testing.assert_array_equal(plan.slots, want)
+    assert ctx[0] == 19 and ctx[1] == 3
+
+
 def test_batcher_fifo_admission_and_plans():
     pool = BlockPool(64)
     m = KvManager(pool, 16, 4, 16)
