@@ -317,6 +317,21 @@ int32_t it_paged_decode_combine(const it_kv_cache* cache, const void* q, int32_t
                                 int32_t partition, void* ws, size_t ws_bytes, void* out, int32_t out_dtype,
                                 void* stream);
 
+/* it_paged_decode without a workspace argument.  No counterpart in the
+ * reference: it is for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  The
+ * partials live in a 32 MiB device array of the library (one per GPU, held
+ * until the process ends); a call that needs more than that
+ * (it_paged_decode_workspace > 32 MiB) is IT_INVALID_INPUT.  It allocates
+ * nothing: the array's device address is looked up once per device, on the
+ * first call there.  Calls on one GPU share the array, so calls that
+ * overlap in time on one GPU (different streams) race.  Other arguments and
+ * results as it_paged_decode. */
+int32_t it_paged_decode_noalloc(const it_kv_cache* cache, const void* q, int32_t q_dtype, int32_t n_heads,
+                                const int32_t* block_tables, int32_t max_blocks, const int32_t* ctx_lens,
+                                const int32_t* start_pos, int32_t n_seqs, int32_t max_tokens, float scale,
+                                int32_t partition, void* out, int32_t out_dtype, void* stream);
+
 /* Chunked prefill attention over the cache (the chunk's K/V already
  * appended).  Sequence b has q_len_b = cu_q[b+1]-cu_q[b] query rows at
  * positions ctx_b - q_len_b + i; with causal != 0 row i attends keys

@@ -112,6 +112,7 @@ SIGNATURES = {
     "it_paged_decode": (i32, [P, P, i32, i32, P, i32, P, P, i32, i32, f32, i32, P, sz, P, i32, P]),
     "it_paged_decode_split": (i32, [P, P, i32, i32, P, i32, P, P, i32, i32, f32, i32, P, sz, P, i32, P]),
     "it_paged_decode_combine": (i32, [P, P, i32, i32, P, i32, P, P, i32, i32, f32, i32, P, sz, P, i32, P]),
+    "it_paged_decode_noalloc": (i32, [P, P, i32, i32, P, i32, P, P, i32, i32, f32, i32, P, i32, P]),
     "it_paged_prefill": (i32, [P, P, i32, i32, P, i32, P, i32, P, i32, f32, i32, P, i32, P]),
     "it_flash_attention_workspace": (sz, [i32, i32, i32]),
     "it_flash_attention": (i32, [P, P, P, P, P, i32, i32, i32, P, sz, P]),

@@ -4,6 +4,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 
 #include "it_decode.hpp"
 #include "it_decode_launch.hpp"
@@ -232,6 +233,64 @@ extern "C" int32_t it_paged_decode_split(IT_DECODE_ARGS) {
 }
 extern "C" int32_t it_paged_decode_combine(IT_DECODE_ARGS) {
   return paged_decode_phases("it_paged_decode_combine", IT_DECODE_PASS, 2);
+}
+
+// ---- it_paged_decode_noalloc: the decode without a caller workspace ------
+// For callers that cannot allocate (code under HIP graph capture, serving
+// loops, harnesses that forbid hipMalloc): the (m, l, O) partials live in
+// `scratch`, a file-scope device array of kNoAllocScratch bytes that every
+// GPU the library runs on holds until the process ends.  In host code the
+// array's name is only a host-side stand-in, so its device address is
+// looked up once per device (hipGetSymbolAddress, with that device current)
+// and only that address is used.  Calls on one GPU share the array: calls
+// that overlap in time on one GPU (two streams) race.
+namespace {
+constexpr size_t kNoAllocScratch = size_t(32) << 20;  // 32 MiB
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) char scratch[kNoAllocScratch];
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of `scratch` on `device` (current), or NULL with the
+// thread's message set.
+void* scratch_address(int device) {
+  if (device < 0 || device >= kMaxDevices) {
+    fail(IT_DEVICE_ERROR, "it_paged_decode_noalloc: device %d outside [0, %d)", device, kMaxDevices);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[device]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      fail(IT_DEVICE_ERROR, "it_paged_decode_noalloc: hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_ptr[device] = ptr;
+  }
+  return g_scratch_ptr[device];
+}
+}  // namespace
+
+extern "C" int32_t it_paged_decode_noalloc(const it_kv_cache* c, const void* q, int32_t q_dtype, int32_t n_heads,
+                                           const int32_t* block_tables, int32_t max_blocks, const int32_t* ctx_lens,
+                                           const int32_t* start_pos, int32_t n_seqs, int32_t max_tokens, float scale,
+                                           int32_t partition, void* out, int32_t out_dtype, void* stream) {
+  constexpr const char* who = "it_paged_decode_noalloc";
+  if (!c) return fail(IT_INVALID_INPUT, "%s: cache is NULL", who);
+  const size_t need = it_paged_decode_workspace(n_seqs, n_heads, c->head_dim, max_tokens, partition);
+  if (need == 0) return fail(IT_INVALID_INPUT, "%s: invalid sizes", who);
+  if (need > kNoAllocScratch)
+    return fail(IT_INVALID_INPUT, "%s: the partials need %zu bytes, more than the %zu-byte scratch (fewer sequences, "
+                "fewer heads or longer partitions fit)", who, need, kNoAllocScratch);
+  int dev = -1;
+  (void)hipGetDevice(&dev);
+  if (dev != c->device) (void)hipSetDevice(c->device);
+  void* ws = scratch_address(c->device);
+  if (dev >= 0 && dev != c->device) (void)hipSetDevice(dev);
+  if (!ws) return IT_DEVICE_ERROR;
+  return paged_decode_phases(who, c, q, q_dtype, n_heads, block_tables, max_blocks, ctx_lens, start_pos, n_seqs,
+                             max_tokens, scale, partition, ws, kNoAllocScratch, out, out_dtype, stream, 3);
 }
 
 // The Backend FlashAttention operator (src/backend/arm.rs:304-370) runs the
