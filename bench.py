@@ -1,22 +1,27 @@
-"""Benchmark of the MI355X KV-cache hot path (BASELINE.json's five configs).
+"""Benchmark of the MI355X KV-cache hot path (the five configurations of the
+KV-cache north star: decode, chunked prefill, sliding window, Q8_0).
 
 Headline (`value`): config 2 at its 4k target -- batched paged decode,
 bf16, Hq 28 / Hkv 4 / D 128, block size 16, batch 32 with every sequence at
 4096 tokens after the step's append, pages a seeded permutation of a
 16384-block pool, split-K over 512-token partitions (the host planner's choice).  One step = slot-mapped
 append of 1 token per sequence + split-K decode + combine; value = KV bytes
-read per step / mean(split + combine time), the algorithmic bytes
-sum_b ctx_b * Hkv * 2 * D * 2.  Three pool replicas are rotated so the 256 MB
-last-level cache does not hold the previous step's pages (cold); warm numbers
-(one replica) are reported beside it.  Kernel times are HIP events recorded
-on the stream the kernels run on (torch's current stream).
+read per step / median(split + combine time) over the timed steps, the
+algorithmic bytes sum_b ctx_b * Hkv * 2 * D * 2.  Three pool replicas are
+rotated so the 256 MB last-level cache does not hold the previous step's
+pages (cold); warm numbers (one replica) and the decode captured in a HIP
+graph are reported beside it.  Kernel times are HIP events recorded on the
+stream the kernels run on (torch's current stream); the roofline's kernel
+time is the mean of back-to-back split launches between two events.
 
 The other configs run at their full shapes and are reported under
 "configs": config 1 (fp32 single-sequence step), config 2 as specified
 (ragged contexts), config 3 (chunk append + MFMA causal prefill), config 4
 (sliding-window steps with eviction and block reuse) and config 5 (Q8_0
 quantise-append + long-context decode).  Each carries a bounded CPU sample
-of the oracle (the C restatement of the reference's arithmetic, 1 thread).
+of the oracle (the C restatement of the reference's arithmetic): on 1 host
+thread, as the reference runs, and on all of the process's host threads
+(OpenMP over sequences and KV heads, or over prefill rows).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 1,2,3,4,5]
                     [--no-cpu] [--copy-probe]
@@ -61,7 +66,28 @@ def _progress(msg):
 
 
 def _cpu_threads():
-    return 1  # the oracle is scalar C, run on one host thread
+    return 1  # the oracle is scalar C, run on one host thread (the reference is single-threaded)
+
+
+def _cpu_all_threads():
+    """Host threads of the all-cores baseline: the process's CPU share (its
+    affinity mask), capped by OMP_NUM_THREADS when that is set."""
+    n = len(os.sched_getaffinity(0))
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        n = min(n, int(env))
+    return max(1, n)
+
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 # ---------------------------------------------------------------------------
@@ -192,22 +218,77 @@ class DecodeWorkload:
             self.step_split_timed(i % n_rep, evs2[i])
         torch.cuda.synchronize()
         split = np.array([e[0].elapsed_time(e[1]) for e in evs2])
+        # The split kernel alone, `steps` launches back to back between two
+        # events (replicas rotated): its mean launch duration, without the
+        # per-bracket event overhead of single launches.
+        e0, e1 = _events(2)
+        e0.record()
+        for i in range(steps):
+            self._split(self.caches[i % n_rep])
+        e1.record()
+        torch.cuda.synchronize()
+        split_b2b = e0.elapsed_time(e1) / steps
         for c in self.caches:
             c.check()
-        return {"append": float(app.mean()), "decode": float(dec.mean()), "decode_median": float(np.median(dec)),
-                "split": float(split.mean()), "step_wall": wall * 1e3 / steps}
+        return {"append": float(app.mean()), "append_median": float(np.median(app)), "decode": float(dec.mean()),
+                "decode_median": float(np.median(dec)), "split": float(split.mean()),
+                "split_median": float(np.median(split)), "split_b2b": float(split_b2b),
+                "step_wall": wall * 1e3 / steps}
+
+    def time_graph(self, replays, rotate=True):
+        """split + combine captured in one HIP graph per pool replica, as a
+        serving loop that captures its decode would run them; `replays`
+        back-to-back replays (replicas rotated) between two events, 5 times:
+        the median per-replay time.  The first replay's output must equal the
+        eager decode's."""
+        torch = self.torch
+        n_rep = len(self.caches) if rotate else 1
+        self._split(self.caches[0])
+        self._combine(self.caches[0])
+        torch.cuda.synchronize()
+        eager = self.out.clone()
+        graphs = []
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            self._split(self.caches[0])
+            self._combine(self.caches[0])
+        torch.cuda.current_stream().wait_stream(side)
+        for i in range(n_rep):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                self._split(self.caches[i])
+                self._combine(self.caches[i])
+            graphs.append(g)
+        graphs[0].replay()
+        torch.cuda.synchronize()
+        assert torch.equal(self.out, eager), "graph replay differs from the eager decode"
+        for i in range(3):
+            graphs[i % n_rep].replay()
+        t = []
+        for _ in range(5):
+            e0, e1 = _events(2)
+            e0.record()
+            for i in range(replays):
+                graphs[i % n_rep].replay()
+            e1.record()
+            torch.cuda.synchronize()
+            t.append(e0.elapsed_time(e1) / replays)
+        del graphs
+        return {"decode_graph": float(np.median(t))}
 
     def release(self):
         self.caches = []
         self.torch.cuda.empty_cache()
 
 
-def cpu_decode_sample(dtype, hq, hkv, D, bs, ctx, budget_s=8.0, seqs_per_call=2):
+def cpu_decode_sample(dtype, hq, hkv, D, bs, ctx, budget_s=8.0, seqs_per_call=2, threads=1):
     """The oracle's paged decode (flash_attn_f32 per head) on `seqs_per_call`
-    sequences of context `ctx`, repeated for about budget_s; KV GB/s."""
+    sequences of context `ctx` (more with threads > 1, so every thread has a
+    (sequence, KV head) pair), repeated for about budget_s; KV GB/s."""
     import oracle as orc
 
-    B = seqs_per_call
+    B = max(seqs_per_call, -(-threads // hkv)) if threads > 1 else seqs_per_call
     nb = B * ((ctx + bs - 1) // bs)
     c = orc.Cache(nb, bs, hkv, D, dtype)
     if dtype == orc.Q8_0:
@@ -230,7 +311,7 @@ def cpu_decode_sample(dtype, hq, hkv, D, bs, ctx, budget_s=8.0, seqs_per_call=2)
     q = orc.normal(3, B * hq * D)
     done, t0 = 0, time.perf_counter()
     while True:
-        c.decode(q, hq, t, cl, None, 1.0 / math.sqrt(D))
+        c.decode(q, hq, t, cl, None, 1.0 / math.sqrt(D), threads=threads)
         done += B
         el = time.perf_counter() - t0
         if el >= budget_s:
@@ -243,11 +324,14 @@ def cpu_decode_sample(dtype, hq, hkv, D, bs, ctx, budget_s=8.0, seqs_per_call=2)
 # ---------------------------------------------------------------------------
 def bench_config1(steps, warmup, cpu):
     """Config 1 is one short sequence, so a step is bound by launch latency,
-    not by the 2 MB of KV.  A serving loop captures such a step in a HIP
-    graph; so does this benchmark: append + split + combine are captured once
-    and the step time is the mean of graph replays (checked equal to the
-    eager step's output).  Event times of the eager kernels are reported
-    beside it."""
+    not by the 2 MB of KV.  A serving loop captures its step in a HIP graph
+    (with the rest of the model's layers, so one graph launch covers many
+    kernels); so does this benchmark: append + split + combine of one step
+    are captured 16 times into one graph, and the step time is the graph's
+    replay time / 16 (the median of 5 timings of back-to-back replays).  A
+    graph of a single step, replayed with events around each replay, is
+    reported beside it; there the host's graph launch, not the GPU, sets the
+    pace.  Every replay's output is checked equal to the eager step's."""
     import torch
 
     import infer_train_amd as it
@@ -265,27 +349,48 @@ def bench_config1(steps, warmup, cpu):
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         w.step(0)
+    per_graph = 16
+    graph16 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph16):
+        for _ in range(per_graph):
+            w.step(0)
     for _ in range(warmup):
         graph.replay()
+        graph16.replay()
     torch.cuda.synchronize()
     assert torch.equal(w.out, eager), "graph replay differs from the eager step"
-    e0, e1 = _events(2)
-    e0.record()
-    for _ in range(steps):
+    reps = max(4, steps // 4)
+    t16 = []
+    for _ in range(5):
+        e0, e1 = _events(2)
+        e0.record()
+        for _ in range(reps):
+            graph16.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        assert torch.equal(w.out, eager), "graph replay differs from the eager step"
+        t16.append(e0.elapsed_time(e1) / (reps * per_graph))
+    step_ms = float(np.median(t16))
+    evs = [_events(2) for _ in range(steps)]
+    for i in range(steps):
+        evs[i][0].record()
         graph.replay()
-    e1.record()
+        evs[i][1].record()
     torch.cuda.synchronize()
     assert torch.equal(w.out, eager), "graph replay differs from the eager step"
-    step_ms = e0.elapsed_time(e1) / steps
+    one = float(np.median([e[0].elapsed_time(e[1]) for e in evs]))
     out = {"workload": "config 1: fp32 GQA decode step, Hq 12 / Hkv 2 / D 128, block 16, 1023 cached + 1 "
                        "appended, identity table over 64 blocks, 64-token partitions",
            "step_us": round(step_ms * 1e3, 2), "steps_per_s": round(1e3 / step_ms, 1),
-           "timing": "append + split + combine captured in one HIP graph; mean of replays",
-           "eager_event_us": {"append": round(r["append"] * 1e3, 2), "decode": round(r["decode"] * 1e3, 2),
-                              "split": round(r["split"] * 1e3, 2)},
+           "timing": f"append + split + combine, {per_graph} steps captured in one HIP graph; replay time / "
+                     f"{per_graph}, median of 5 x {reps} back-to-back replays",
+           "single_step_graph_us": round(one * 1e3, 2),
+           "single_step_graph_note": "one step per graph, events around each replay (median): host launch-bound",
+           "eager_event_us": {"append": round(r["append_median"] * 1e3, 2),
+                              "decode": round(r["decode_median"] * 1e3, 2), "split": round(r["split_median"] * 1e3, 2)},
            "kv_bytes": int(w.kv_bytes), "kv_gbs": round(w.kv_bytes / (step_ms * 1e-3) / 1e9, 1),
            "note": "latency-bound: 2 MB of KV; eager event times include host enqueue gaps"}
-    del graph
+    del graph, graph16
     w.release()
     if cpu:
         import oracle as orc
@@ -293,6 +398,10 @@ def bench_config1(steps, warmup, cpu):
         done, el, gbs = cpu_decode_sample(orc.F32, 12, 2, 128, 16, 1024, budget_s=3.0, seqs_per_call=1)
         out["cpu"] = {"decode_us": round(el / done * 1e6, 1), "kv_gbs": round(gbs, 3), "cores": _cpu_threads(),
                       "sample": f"{done} oracle decode steps of the config-1 shape in {el:.1f} s"}
+        nt = _cpu_all_threads()
+        done, el, gbs = cpu_decode_sample(orc.F32, 12, 2, 128, 16, 1024, budget_s=3.0, seqs_per_call=1, threads=nt)
+        out["cpu_all_cores"] = {"kv_gbs": round(gbs, 3), "cores": nt, "cpu_model": _cpu_model(),
+                                "sample": f"{done} config-1 sequences decoded on {nt} threads in {el:.1f} s"}
     return out
 
 
@@ -313,20 +422,23 @@ def bench_config2(steps, warmup, cpu):
     w = DecodeWorkload(it.BF16, 28, 4, 128, 16, ctx4k, 16384, p4k, seed=2)
     cold = w.time(steps, warmup, rotate=True)
     warm = w.time(steps, warmup, rotate=False)
+    graph = w.time_graph(max(steps, 20), rotate=True)
     head = {"kv_bytes": int(w.kv_bytes), "append_bytes": int(w.append_bytes), "B": w.B, "cold": cold, "warm": warm,
-            "partition": p4k}
+            "graph": graph, "partition": p4k}
     w.release()
     rng = np.random.default_rng(22)
     ctx2 = rng.integers(256, 4097, 32) + 1
     p2 = decode_partition(it.BF16, 128, 16, 28, 4, ctx2)
     w2 = DecodeWorkload(it.BF16, 28, 4, 128, 16, ctx2, 16384, p2, seed=3)
     r2 = w2.time(steps, warmup, rotate=True)
+    dm = r2["decode_median"]
     ragged = {"workload": f"config 2 as specified: ctx U[256, 4096] + 1 appended, batch 32, {p2}-token partitions "
                           "(host planner)",
-              "kv_gbs": round(w2.kv_bytes / (r2["decode"] * 1e-3) / 1e9, 1), "decode_us": round(r2["decode"] * 1e3, 2),
-              "split_us": round(r2["split"] * 1e3, 2), "kv_bytes": int(w2.kv_bytes),
-              "append_us": round(r2["append"] * 1e3, 2),
-              "pct_hbm_peak": round(100 * w2.kv_bytes / (r2["decode"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 2)}
+              "kv_gbs": round(w2.kv_bytes / (dm * 1e-3) / 1e9, 1), "decode_us": round(dm * 1e3, 2),
+              "decode_us_mean": round(r2["decode"] * 1e3, 2), "split_us": round(r2["split_b2b"] * 1e3, 2),
+              "kv_bytes": int(w2.kv_bytes), "append_us": round(r2["append_median"] * 1e3, 2),
+              "steps_per_s": round(1e3 / (r2["append_median"] + dm), 1),
+              "pct_hbm_peak": round(100 * w2.kv_bytes / (dm * 1e-3) / 1e9 / HBM_PEAK_GBS, 2)}
     w2.release()
     torch.cuda.empty_cache()
     cpu_b = None
@@ -338,6 +450,13 @@ def bench_config2(steps, warmup, cpu):
                  "sample": f"oracle paged decode (flash_attn_f32 per head, bf16 widened to f32) of {done} sequences "
                            f"x 4096 tokens, Hq 28 / Hkv 4 / D 128, in {el:.1f} s on 1 host thread; the full step is "
                            f"32 sequences"}
+        nt = _cpu_all_threads()
+        done, el, gbs = cpu_decode_sample(orc.BF16, 28, 4, 128, 16, 4096, budget_s=8.0, seqs_per_call=8, threads=nt)
+        cpu_b["all_cores"] = {"value": round(gbs, 4), "unit": "GB/s", "cores": nt, "kind": "port",
+                              "cpu_model": _cpu_model(),
+                              "sample": f"the same oracle decode, OpenMP over (sequence, KV head) on {nt} host "
+                                        f"threads: {done} sequences x 4096 tokens in {el:.1f} s"}
+        cpu_b["cpu_model"] = _cpu_model()
     return head, ragged, cpu_b
 
 
@@ -436,8 +555,8 @@ def bench_config3(steps, warmup, cpu):
         step(evs[i])
     torch.cuda.synchronize()
     c.check()
-    app = float(np.mean([e[0].elapsed_time(e[1]) for e in evs]))
-    pre = float(np.mean([e[1].elapsed_time(e[2]) for e in evs]))
+    app = float(np.median([e[0].elapsed_time(e[1]) for e in evs]))
+    pre = float(np.median([e[1].elapsed_time(e[2]) for e in evs]))
     # Causal-exact flops: 4 D Hq sum over rows of the keys each row attends.
     flops = 4.0 * D * hq * B * sum(cached + i + 1 for i in range(chunk))
     n_tok = B * chunk
@@ -446,7 +565,8 @@ def bench_config3(steps, warmup, cpu):
            "prefill_us": round(pre * 1e3, 2), "flops": flops, "tflops": round(flops / (pre * 1e-3) / 1e12, 1),
            "pct_mfma_peak": round(100 * flops / (pre * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFS, 2),
            "append_us": round(app * 1e3, 2), "append_mtok_s": round(n_tok / (app * 1e-3) / 1e6, 1),
-           "append_gbs": round(n_tok * hkv * 2 * D * 2 * 2 / (app * 1e-3) / 1e9, 1)}
+           "append_gbs": round(n_tok * hkv * 2 * D * 2 * 2 / (app * 1e-3) / 1e9, 1),
+           "steps_per_s": round(1e3 / (app + pre), 1), "timing": "medians of event-bracketed kernels"}
     if cpu:
         import oracle as orc
 
@@ -466,6 +586,15 @@ def bench_config3(steps, warmup, cpu):
         res["cpu"] = {"gflops": round(row_flops / el / 1e9, 3), "cores": _cpu_threads(),
                       "sample": f"oracle prefill of the last {rows} query rows (all 32 heads) of one sequence in "
                                 f"{el:.1f} s; the full step is 8 x 512 rows"}
+        nt = _cpu_all_threads()
+        n_rows = min(chunk, 32 * nt)
+        t0 = time.perf_counter()
+        oc.prefill(qq, hq, cuq, tt, cl, scale, causal=True, rows=(0, chunk - n_rows, chunk), threads=nt)
+        el = time.perf_counter() - t0
+        row_flops = 4.0 * D * hq * sum(cached + chunk - r for r in range(n_rows))
+        res["cpu_all_cores"] = {"gflops": round(row_flops / el / 1e9, 3), "cores": nt, "cpu_model": _cpu_model(),
+                                "sample": f"oracle prefill of the last {n_rows} query rows of one sequence on {nt} "
+                                          f"threads (OpenMP over rows) in {el:.1f} s"}
     del c
     torch.cuda.empty_cache()
     return res
@@ -551,8 +680,8 @@ def bench_config4(steps, warmup, cpu):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     c.check()
-    upd = float(np.mean([e[0].elapsed_time(e[1]) for e in evs]))
-    dec = float(np.mean([e[1].elapsed_time(e[2]) for e in evs]))
+    upd = float(np.median([e[0].elapsed_time(e[1]) for e in evs]))
+    dec = float(np.median([e[1].elapsed_time(e[2]) for e in evs]))
     kv_bytes = n_seqs * W * hkv * 2 * D * 2
     res = {"workload": f"config 4: {steps} sliding-window steps from position {start + warmup}, 64 sequences, "
                        "Hq 16 / Hkv 2 / D 128, W 4096, block 16, 16512-block pool in seeded order; step = host "
@@ -560,7 +689,9 @@ def bench_config4(steps, warmup, cpu):
            "decode_us": round(dec * 1e3, 2), "kv_gbs": round(kv_bytes / (dec * 1e-3) / 1e9, 1),
            "pct_hbm_peak": round(100 * kv_bytes / (dec * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
            "evict_append_sync_us": round(upd * 1e3, 2), "host_manager_us": round(1e6 * float(np.mean(hosts)), 1),
-           "step_wall_us": round(wall * 1e6 / steps, 1), "blocks_evicted": n_ev, "kv_bytes": kv_bytes}
+           "step_wall_us": round(wall * 1e6 / steps, 1), "blocks_evicted": n_ev, "kv_bytes": kv_bytes,
+           "steps_per_s": round(1e6 / (wall * 1e6 / steps), 1), "gpu_steps_per_s": round(1e3 / (upd + dec), 1),
+           "timing": "medians of event-bracketed kernels; steps_per_s from the wall clock (host manager included)"}
     if cpu:
         import oracle as orc
 
@@ -568,6 +699,10 @@ def bench_config4(steps, warmup, cpu):
         res["cpu"] = {"kv_gbs": round(gbs, 4), "cores": _cpu_threads(),
                       "sample": f"oracle decode of {done} windows of 4096 tokens (Hq 16 / Hkv 2) in {el:.1f} s; "
                                 f"a step is 64 windows"}
+        nt = _cpu_all_threads()
+        done, el, gbs = cpu_decode_sample(orc.BF16, hq, hkv, D, bs, W, budget_s=4.0, seqs_per_call=8, threads=nt)
+        res["cpu_all_cores"] = {"kv_gbs": round(gbs, 4), "cores": nt, "cpu_model": _cpu_model(),
+                                "sample": f"{done} windows of 4096 tokens on {nt} threads in {el:.1f} s"}
     del c
     torch.cuda.empty_cache()
     return res
@@ -592,13 +727,16 @@ def bench_config5(steps, warmup, cpu):
     P = decode_partition(it.Q8_0, 256, 32, 24, 4, ctx)
     w = DecodeWorkload(it.Q8_0, 24, 4, 256, 32, ctx, pool_blocks, P, seed=5, replicas=1)
     r = w.time(steps, warmup, rotate=False)
+    dm, am = r["decode_median"], r["append_median"]
     res = {"workload": "config 5: Q8_0 KV, Hq 24 / Hkv 4 / D 256, block 32, batch 16, ctx U[32768, 131072], "
                        f"quantise-append 1 token per sequence + split-K decode ({P}-token partitions from the host "
                        "planner) dequantising in registers",
-           "kv_bytes": int(w.kv_bytes), "decode_us": round(r["decode"] * 1e3, 2), "split_us": round(r["split"] * 1e3, 2),
-           "kv_gbs": round(w.kv_bytes / (r["decode"] * 1e-3) / 1e9, 1),
-           "pct_hbm_peak": round(100 * w.kv_bytes / (r["decode"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
-           "append_us": round(r["append"] * 1e3, 2), "append_mtok_s": round(w.B / (r["append"] * 1e-3) / 1e6, 3),
+           "kv_bytes": int(w.kv_bytes), "decode_us": round(dm * 1e3, 2), "decode_us_mean": round(r["decode"] * 1e3, 2),
+           "split_us": round(r["split_b2b"] * 1e3, 2),
+           "kv_gbs": round(w.kv_bytes / (dm * 1e-3) / 1e9, 1),
+           "pct_hbm_peak": round(100 * w.kv_bytes / (dm * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
+           "append_us": round(am * 1e3, 2), "append_mtok_s": round(w.B / (am * 1e-3) / 1e6, 3),
+           "steps_per_s": round(1e3 / (am + dm), 1),
            "note": "working set 2.8 GB, far beyond the 256 MB last-level cache: one replica"}
     w.release()
     if cpu:
@@ -607,6 +745,11 @@ def bench_config5(steps, warmup, cpu):
         done, el, gbs = cpu_decode_sample(orc.Q8_0, 24, 4, 256, 32, 32768, budget_s=5.0, seqs_per_call=1)
         res["cpu"] = {"kv_gbs": round(gbs, 4), "cores": _cpu_threads(),
                       "sample": f"oracle Q8_0 decode of {done} sequences x 32768 tokens in {el:.1f} s"}
+        nt = _cpu_all_threads()
+        done, el, gbs = cpu_decode_sample(orc.Q8_0, 24, 4, 256, 32, 32768, budget_s=5.0, seqs_per_call=1,
+                                          threads=nt)
+        res["cpu_all_cores"] = {"kv_gbs": round(gbs, 4), "cores": nt, "cpu_model": _cpu_model(),
+                                "sample": f"{done} Q8_0 sequences x 32768 tokens on {nt} threads in {el:.1f} s"}
     return res
 
 
@@ -625,12 +768,13 @@ def bench_q4(dtype, steps, warmup):
     w = DecodeWorkload(dtype, 24, 4, 256, 32, ctx, pool_blocks, P, seed=5, replicas=1)
     r = w.time(steps, warmup, rotate=False)
     name = {it.Q4_0: "Q4_0", it.Q4_1: "Q4_1"}[dtype]
+    dm = r["decode_median"]
     res = {"workload": f"{name} KV on the config-5 shape (Hq 24 / Hkv 4 / D 256, block 32, batch 16, "
                        f"ctx U[32768, 131072], {P}-token partitions from the host planner), dequantising in registers",
-           "kv_bytes": int(w.kv_bytes), "decode_us": round(r["decode"] * 1e3, 2), "split_us": round(r["split"] * 1e3, 2),
-           "kv_gbs": round(w.kv_bytes / (r["decode"] * 1e-3) / 1e9, 1),
-           "pct_hbm_peak": round(100 * w.kv_bytes / (r["decode"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
-           "append_us": round(r["append"] * 1e3, 2)}
+           "kv_bytes": int(w.kv_bytes), "decode_us": round(dm * 1e3, 2), "split_us": round(r["split_b2b"] * 1e3, 2),
+           "kv_gbs": round(w.kv_bytes / (dm * 1e-3) / 1e9, 1),
+           "pct_hbm_peak": round(100 * w.kv_bytes / (dm * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
+           "append_us": round(r["append_median"] * 1e3, 2)}
     w.release()
     return res
 
@@ -924,9 +1068,10 @@ def main():
         w = DecodeWorkload(it.BF16, 28, 4, 128, 16, ctx4k, 16384, decode_partition(it.BF16, 128, 16, 28, 4, ctx4k),
                            seed=2)
         r = w.time(args.steps, args.warmup, rotate=True)
-        print(json.dumps({"only_headline": True, "split_us": round(r["split"] * 1e3, 2),
-                          "decode_us": round(r["decode"] * 1e3, 2),
-                          "split_gbs": round(w.kv_bytes / (r["split"] * 1e-3) / 1e9, 1)}), flush=True)
+        print(json.dumps({"only_headline": True, "split_us": round(r["split_b2b"] * 1e3, 2),
+                          "decode_us": round(r["decode_median"] * 1e3, 2),
+                          "split_gbs": round(w.kv_bytes / (r["split_b2b"] * 1e-3) / 1e9, 1),
+                          "decode_gbs": round(w.kv_bytes / (r["decode_median"] * 1e-3) / 1e9, 1)}), flush=True)
         return
 
     head, ragged, cpu_b = bench_config2(args.steps, args.warmup, cpu)
@@ -954,10 +1099,12 @@ def main():
         configs["q4_1_config5_shape"] = bench_q4(it.Q4_1, small, 10)
         _progress("q4_0 / q4_1 done")
 
-    cold, warm = head["cold"], head["warm"]
+    cold, warm, graph = head["cold"], head["warm"], head["graph"]
     kv_bytes = head["kv_bytes"]
-    gbs = kv_bytes / (cold["decode"] * 1e-3) / 1e9
-    split_gbs = kv_bytes / (cold["split"] * 1e-3) / 1e9
+    # value: KV bytes / the median decode (split + combine, one event
+    # bracket per step) of the timed steps.
+    gbs = kv_bytes / (cold["decode_median"] * 1e-3) / 1e9
+    split_gbs = kv_bytes / (cold["split_b2b"] * 1e-3) / 1e9
     traffic = None
     if os.path.exists(TRAFFIC_FILE):
         traffic = json.load(open(TRAFFIC_FILE)).get("hbm_bytes_per_launch")
@@ -980,17 +1127,25 @@ def main():
                                "replicas rotated)",
                    "global_batch": 32, "seq_len": 4096, "parallelism": "none (1 GPU)"},
         "pct_hbm_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2),
-        "decode_us": round(cold["decode"] * 1e3, 2),
-        "decode_us_median": round(cold["decode_median"] * 1e3, 2),
-        "split_us": round(cold["split"] * 1e3, 2),
+        "decode_us": round(cold["decode_median"] * 1e3, 2),
+        "decode_us_mean": round(cold["decode"] * 1e3, 2),
+        "decode_graph_us": round(graph["decode_graph"] * 1e3, 2),
+        "decode_graph_kv_gbs": round(kv_bytes / (graph["decode_graph"] * 1e-3) / 1e9, 1),
+        "decode_graph_note": "split + combine captured in a HIP graph (one per pool replica), replayed back to "
+                             "back between two events (median of 5 runs); output checked equal to the eager decode",
+        "split_us": round(cold["split_b2b"] * 1e3, 2),
+        "split_us_single_bracket": round(cold["split_median"] * 1e3, 2),
         "kv_bytes_per_step": int(kv_bytes),
-        "warm_kv_gbs": round(kv_bytes / (warm["decode"] * 1e-3) / 1e9, 1),
-        "append_mtok_s": round(head["B"] / (cold["append"] * 1e-3) / 1e6, 3),
-        "append_gbs": round(head["append_bytes"] / (cold["append"] * 1e-3) / 1e9, 2),
-        "append_us": round(cold["append"] * 1e3, 2),
+        "warm_kv_gbs": round(kv_bytes / (warm["decode_median"] * 1e-3) / 1e9, 1),
+        "append_mtok_s": round(head["B"] / (cold["append_median"] * 1e-3) / 1e6, 3),
+        "append_gbs": round(head["append_bytes"] / (cold["append_median"] * 1e-3) / 1e9, 2),
+        "append_us": round(cold["append_median"] * 1e3, 2),
+        "steps_per_s": round(1e3 / (cold["append_median"] + cold["decode_median"]), 1),
+        "timing": "HIP events on the library's stream; per-step values are medians over the timed steps",
         "roofline": {"bound": "hbm", "achieved": round(split_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(split_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "paged_decode_split<bf16,128,7> (mean of its HIP-event durations, cold)",
+                     "kernel": f"paged_decode_split<bf16,128,7> (mean duration of {args.steps} back-to-back launches "
+                               "between two HIP events, cold)",
                      "algorithmic_bytes_per_launch": int(kv_bytes)},
         "configs": configs,
     }

@@ -68,14 +68,21 @@ __device__ __forceinline__ void store_combined(void* out, int out_dtype, int64_t
   else static_cast<uint16_t*>(out)[idx] = uint16_t(f32_to_f16_bits(v));
 }
 
+// Lane `l`'s value of x (v_readlane_b32 on the bits; l uniform).
+__device__ __forceinline__ float lane_f32(float x, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), l));
+}
+
 // Merge the partitions of one (sequence, head) over a 64-dim slice (grid z):
 // M = max m_p, L = sum l_p 2^(m_p - M), O = sum O_p 2^(m_p - M) / L (the
 // split-K form of flash_attn_f32's rescaling, flash_attn.rs:42-71).  Lane d
-// owns one output dim.  The partials are read in chunks of kChunk partitions
-// whose loads are all in flight together; every lane reads the chunk's
-// (m, l) pairs itself, so no cross-lane step sits between them and the O
-// loads.  With more than one chunk, M comes from a first pass over the
-// (m, l) pairs.
+// owns one output dim; lane c also holds the (m, l) pairs of partitions c and
+// 64 + c, so M and L are wave reductions and partition p's weight comes from
+// its lane (readlane).  The pairs and the first kBatch partitions' outputs
+// are all loaded before the context length arrives (their addresses do not
+// depend on it; slots past this sequence's count hold stale bytes and get
+// weight 0 once the count is known): one memory round trip up to kBatch
+// partitions.  Partitions beyond 128 read their pairs directly.
 template <int D>
 __global__ __launch_bounds__(64) void paged_decode_combine(const float* __restrict__ ws_o,
                                                            const float* __restrict__ ws_ml,
@@ -85,73 +92,62 @@ __global__ __launch_bounds__(64) void paged_decode_combine(const float* __restri
                                                            int max_parts, void* out, int out_dtype) {
   // Partitions beyond max_parts were never computed (the split pass latched
   // the error); only the computed ones are merged.
-  constexpr int kChunk = 16;
-  const int h = blockIdx.x, b = blockIdx.y, d = 64 * blockIdx.z + threadIdx.x, lane = threadIdx.x;
+  constexpr int kBatch = 64;
+  const int h = blockIdx.x, b = blockIdx.y, lane = int(threadIdx.x), d = 64 * int(blockIdx.z) + lane;
   const int64_t row = int64_t(b) * n_heads + h;
   const float2* ml = reinterpret_cast<const float2*>(ws_ml) + row * max_parts;
   const float* op = ws_o + row * max_parts * D + d;
-  // With at most kChunk partitions the loads of all max_parts slots go out
-  // before the context length arrives (the addresses do not depend on it);
-  // slots past this sequence's count hold stale bytes and are replaced by
-  // (-inf, 0) and 0 once the count is known.
-  float2 pre_ml[kChunk];
-  float pre_o[kChunk];
-  if (max_parts <= kChunk) {
+  const float2 none = make_float2(-INFINITY, 0.0f);
+  float2 m0 = lane < max_parts ? ml[lane] : none;
+  float2 m1 = 64 + lane < max_parts ? ml[64 + lane] : none;
+  float ob[kBatch];
 #pragma unroll
-    for (int c = 0; c < kChunk; ++c) {
-      if (c < max_parts) {
-        pre_ml[c] = ml[c];
-        pre_o[c] = op[int64_t(c) * D];
-      }
-    }
-  }
+  for (int c = 0; c < kBatch; ++c)
+    if (c < max_parts) ob[c] = op[int64_t(c) * D];
   const int ctx = ctx_lens ? ctx_lens[b] : ctx_const;
   const int st = start_pos ? start_pos[b] : 0;
   const int n = ctx - st;
   // A negative start position was skipped by the split pass (and latched):
   // no partitions, zeros.
   const int np = (n > 0 && st >= 0) ? min((n + partition - 1) / partition, max_parts) : 0;
-  float mx = -INFINITY;
-  if (max_parts <= kChunk) {
-    float l = 0.0f, o = 0.0f;
-#pragma unroll
-    for (int c = 0; c < kChunk; ++c) {
-      if (c < np) mx = fmaxf(mx, pre_ml[c].x);
-    }
-#pragma unroll
-    for (int c = 0; c < kChunk; ++c) {
-      if (c < np) {
-        const float w = (pre_ml[c].x == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(pre_ml[c].x - mx);
-        l = fmaf(pre_ml[c].y, w, l);
-        o = fmaf(pre_o[c], w, o);
-      }
-    }
-    store_combined(out, out_dtype, row * D + d, l > 0.0f ? o * (1.0f / l) : 0.0f);
+  if (lane >= np) m0 = none;
+  if (64 + lane >= np) m1 = none;
+  float mx = fmaxf(m0.x, m1.x);
+  for (int p = 128 + lane; p < np; p += 64) mx = fmaxf(mx, ml[p].x);
+  mx = group_max<64>(mx);
+  if (mx == -INFINITY) {  // no partition, or every key skipped: zeros (flash_attn.rs:66-71)
+    store_combined(out, out_dtype, row * D + d, 0.0f);
     return;
   }
-  if (np > kChunk) {
-    for (int p = lane; p < np; p += 64) mx = fmaxf(mx, ml[p].x);
-    mx = group_max<64>(mx);
+  const float w0 = m0.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m0.x - mx);
+  const float w1 = m1.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m1.x - mx);
+  float l = fmaf(m0.y, w0, m1.y * w1);
+  for (int p = 128 + lane; p < np; p += 64) {
+    const float2 v = ml[p];
+    if (v.x != -INFINITY) l = fmaf(v.y, __builtin_amdgcn_exp2f(v.x - mx), l);
   }
-  float l = 0.0f, o = 0.0f;
-  for (int p0 = 0; p0 < np; p0 += kChunk) {
-    float2 mlc[kChunk];
-    float oc[kChunk];
+  l = group_sum<64>(l);
+  float o = 0.0f;
 #pragma unroll
-    for (int c = 0; c < kChunk; ++c) {
-      const bool in = p0 + c < np;
-      mlc[c] = in ? ml[p0 + c] : make_float2(-INFINITY, 0.0f);
-      oc[c] = in ? op[int64_t(p0 + c) * D] : 0.0f;
-    }
-    if (np <= kChunk) {
+  for (int c = 0; c < kBatch; ++c)
+    if (c < np) o = fmaf(ob[c], lane_f32(w0, c), o);
+  for (int p0 = kBatch; p0 < np; p0 += kBatch) {
 #pragma unroll
-      for (int c = 0; c < kChunk; ++c) mx = fmaxf(mx, mlc[c].x);
-    }
+    for (int c = 0; c < kBatch; ++c)
+      if (p0 + c < np) ob[c] = op[int64_t(p0 + c) * D];
 #pragma unroll
-    for (int c = 0; c < kChunk; ++c) {
-      const float w = (mlc[c].x == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mlc[c].x - mx);
-      l = fmaf(mlc[c].y, w, l);
-      o = fmaf(oc[c], w, o);
+    for (int c = 0; c < kBatch; ++c) {
+      const int p = p0 + c;
+      if (p < np) {
+        float w;
+        if (p < 128) {
+          w = lane_f32(w1, c);
+        } else {
+          const float2 v = ml[p];
+          w = v.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(v.x - mx);
+        }
+        o = fmaf(ob[c], w, o);
+      }
     }
   }
   store_combined(out, out_dtype, row * D + d, l > 0.0f ? o * (1.0f / l) : 0.0f);

@@ -72,6 +72,8 @@ def _load() -> C.CDLL:
         "orc_kv_gather": (i32, [P, P, P, P, i32, P, P, P, i32, P, P]),
         "orc_kv_evict": (i32, [P, P, P, P, i32]),
         "orc_paged_decode": (i32, [P, P, P, P, i32, P, i32, P, P, i32, f32, P]),
+        "orc_paged_decode_mt": (i32, [P, P, P, P, i32, P, i32, P, P, i32, f32, P, i32]),
+        "orc_paged_prefill_rows_mt": (i32, [P, P, P, P, i32, P, P, i32, P, i32, i32, i32, f32, i32, P, i32]),
         "orc_paged_prefill": (i32, [P, P, P, P, i32, P, P, i32, P, i32, f32, i32, P]),
         "orc_paged_prefill_rows": (i32, [P, P, P, P, i32, P, P, i32, P, i32, i32, i32, f32, i32, P]),
         "orc_mgr_new": (P, [P, i32, i32, i32, i32]),
@@ -336,20 +338,28 @@ class Cache:
         if lib.orc_kv_evict(self._d(), self.k.ctypes.data, self.v.ctypes.data, b.ctypes.data, b.size):
             raise ValueError("orc_kv_evict: invalid input")
 
-    def decode(self, q, n_heads, tables, ctx_lens, start_pos, scale) -> np.ndarray:
+    def decode(self, q, n_heads, tables, ctx_lens, start_pos, scale, threads: int = 1) -> np.ndarray:
+        """threads > 1: the same results on that many host threads (the
+        all-cores CPU baseline)."""
         q = _c(q, np.float32)
         t, cl = _c(tables, np.int32), _c(ctx_lens, np.int32)
         sp = None if start_pos is None else _c(start_pos, np.int32)
         out = np.zeros_like(q)
-        rc = lib.orc_paged_decode(self._d(), self.k.ctypes.data, self.v.ctypes.data, q.ctypes.data, n_heads,
-                                  t.ctypes.data, t.shape[1], cl.ctypes.data, _p(sp), cl.size, C.c_float(scale),
-                                  out.ctypes.data)
+        if threads > 1:
+            rc = lib.orc_paged_decode_mt(self._d(), self.k.ctypes.data, self.v.ctypes.data, q.ctypes.data, n_heads,
+                                         t.ctypes.data, t.shape[1], cl.ctypes.data, _p(sp), cl.size,
+                                         C.c_float(scale), out.ctypes.data, threads)
+        else:
+            rc = lib.orc_paged_decode(self._d(), self.k.ctypes.data, self.v.ctypes.data, q.ctypes.data, n_heads,
+                                      t.ctypes.data, t.shape[1], cl.ctypes.data, _p(sp), cl.size, C.c_float(scale),
+                                      out.ctypes.data)
         if rc:
             raise ValueError("orc_paged_decode: invalid input")
         return out
 
-    def prefill(self, q, n_heads, cu_q, tables, ctx_lens, scale, causal=True, rows=None) -> np.ndarray:
-        """rows=(seq, begin, end) restricts the work to one sequence's rows."""
+    def prefill(self, q, n_heads, cu_q, tables, ctx_lens, scale, causal=True, rows=None, threads: int = 1) -> np.ndarray:
+        """rows=(seq, begin, end) restricts the work to one sequence's rows
+        (threads > 1: on that many host threads, same results)."""
         q = _c(q, np.float32)
         cq, t, cl = _c(cu_q, np.int32), _c(tables, np.int32), _c(ctx_lens, np.int32)
         out = np.zeros_like(q)
@@ -359,9 +369,15 @@ class Cache:
                                        C.c_float(scale), int(causal), out.ctypes.data)
         else:
             s, b, e = rows
-            rc = lib.orc_paged_prefill_rows(self._d(), self.k.ctypes.data, self.v.ctypes.data, q.ctypes.data,
-                                            n_heads, cq.ctypes.data, t.ctypes.data, t.shape[1], cl.ctypes.data, s,
-                                            b, e, C.c_float(scale), int(causal), out.ctypes.data)
+            if threads > 1:
+                rc = lib.orc_paged_prefill_rows_mt(self._d(), self.k.ctypes.data, self.v.ctypes.data, q.ctypes.data,
+                                                   n_heads, cq.ctypes.data, t.ctypes.data, t.shape[1],
+                                                   cl.ctypes.data, s, b, e, C.c_float(scale), int(causal),
+                                                   out.ctypes.data, threads)
+            else:
+                rc = lib.orc_paged_prefill_rows(self._d(), self.k.ctypes.data, self.v.ctypes.data, q.ctypes.data,
+                                                n_heads, cq.ctypes.data, t.ctypes.data, t.shape[1], cl.ctypes.data,
+                                                s, b, e, C.c_float(scale), int(causal), out.ctypes.data)
         if rc:
             raise ValueError("orc_paged_prefill: invalid input")
         return out

@@ -687,6 +687,40 @@ int orc_paged_decode(const orc_cache_desc* c, const uint8_t* k_pool, const uint8
   return ORC_OK;
 }
 
+int orc_paged_decode_mt(const orc_cache_desc* c, const uint8_t* k_pool, const uint8_t* v_pool,
+                        const float* q, int32_t n_heads, const int32_t* block_tables,
+                        int32_t max_blocks, const int32_t* ctx_lens, const int32_t* start_pos,
+                        int32_t n_seqs, float scale, float* out, int32_t n_threads) {
+  if (!desc_ok(c) || n_heads <= 0 || n_heads % c->n_kv_heads || n_threads <= 0) return ORC_INVALID_INPUT;
+  const int32_t D = c->head_dim, Hkv = c->n_kv_heads;
+  for (int32_t b = 0; b < n_seqs; ++b) {
+    int32_t st = start_pos ? start_pos[b] : 0;
+    if (st < 0 || ctx_lens[b] - st < 0) return ORC_INVALID_INPUT;
+  }
+  int bad = 0;
+  const int64_t units = (int64_t)n_seqs * Hkv;
+#pragma omp parallel for schedule(dynamic, 1) num_threads(n_threads) reduction(| : bad)
+  for (int64_t u = 0; u < units; ++u) {
+    const int32_t b = (int32_t)(u / Hkv), kvh = (int32_t)(u % Hkv);
+    const int32_t st = start_pos ? start_pos[b] : 0;
+    const int32_t n = ctx_lens[b] - st;
+    float* kf = (float*)malloc(sizeof(float) * (size_t)(n ? n : 1) * D);
+    float* vf = (float*)malloc(sizeof(float) * (size_t)(n ? n : 1) * D);
+    if (widen_seq(c, k_pool, v_pool, block_tables + (size_t)b * max_blocks, max_blocks, kvh, st, n, kf, vf)) {
+      bad = 1;
+    } else {
+      for (int32_t h = 0; h < n_heads; ++h) {
+        if (h * Hkv / n_heads != kvh) continue; /* forward.rs:234 GQA map */
+        size_t qo = ((size_t)b * n_heads + h) * D;
+        orc_flash_attn_f32(q + qo, kf, vf, NULL, out + qo, D, n, scale);
+      }
+    }
+    free(kf);
+    free(vf);
+  }
+  return bad ? ORC_INVALID_INPUT : ORC_OK;
+}
+
 int orc_paged_prefill_rows(const orc_cache_desc* c, const uint8_t* k_pool, const uint8_t* v_pool,
                            const float* q, int32_t n_heads, const int32_t* cu_q,
                            const int32_t* block_tables, int32_t max_blocks,
@@ -703,6 +737,38 @@ int orc_paged_prefill_rows(const orc_cache_desc* c, const uint8_t* k_pool, const
     int rc = widen_seq(c, k_pool, v_pool, block_tables + (size_t)b * max_blocks, max_blocks, kvh,
                        0, ctx, kf, vf);
     if (rc) { free(kf); free(vf); return rc; }
+    for (int32_t i = row_begin; i < row_end; ++i) {
+      int32_t n_kv = causal ? (ctx - ql + i + 1) : ctx; /* causal prefix of the chunk row */
+      for (int32_t h = 0; h < n_heads; ++h) {
+        if (h * Hkv / n_heads != kvh) continue;
+        size_t qo = ((size_t)(cu_q[b] + i) * n_heads + h) * D;
+        orc_flash_attn_f32(q + qo, kf, vf, NULL, out + qo, D, n_kv, scale);
+      }
+    }
+  }
+  free(kf);
+  free(vf);
+  return ORC_OK;
+}
+
+int orc_paged_prefill_rows_mt(const orc_cache_desc* c, const uint8_t* k_pool, const uint8_t* v_pool,
+                              const float* q, int32_t n_heads, const int32_t* cu_q,
+                              const int32_t* block_tables, int32_t max_blocks,
+                              const int32_t* ctx_lens, int32_t b, int32_t row_begin,
+                              int32_t row_end, float scale, int32_t causal, float* out,
+                              int32_t n_threads) {
+  if (!desc_ok(c) || n_heads <= 0 || n_heads % c->n_kv_heads || n_threads <= 0) return ORC_INVALID_INPUT;
+  const int32_t D = c->head_dim, Hkv = c->n_kv_heads;
+  int32_t ql = cu_q[b + 1] - cu_q[b];
+  int32_t ctx = ctx_lens[b];
+  if (ql < 0 || ql > ctx) return ORC_INVALID_INPUT;
+  float* kf = (float*)malloc(sizeof(float) * (size_t)(ctx ? ctx : 1) * D);
+  float* vf = (float*)malloc(sizeof(float) * (size_t)(ctx ? ctx : 1) * D);
+  for (int32_t kvh = 0; kvh < Hkv; ++kvh) {
+    int rc = widen_seq(c, k_pool, v_pool, block_tables + (size_t)b * max_blocks, max_blocks, kvh,
+                       0, ctx, kf, vf);
+    if (rc) { free(kf); free(vf); return rc; }
+#pragma omp parallel for schedule(dynamic, 4) num_threads(n_threads)
     for (int32_t i = row_begin; i < row_end; ++i) {
       int32_t n_kv = causal ? (ctx - ql + i + 1) : ctx; /* causal prefix of the chunk row */
       for (int32_t h = 0; h < n_heads; ++h) {

@@ -188,6 +188,15 @@ int orc_paged_decode(const orc_cache_desc* c, const uint8_t* k_pool, const uint8
                      int32_t max_blocks, const int32_t* ctx_lens, const int32_t* start_pos,
                      int32_t n_seqs, float scale, float* out);
 
+/* The same results as orc_paged_decode, computed on n_threads host threads
+ * (OpenMP over the (sequence, KV head) pairs; each pair's query heads run
+ * flash_attn_f32 exactly as above).  For the all-cores CPU baseline: the
+ * reference itself is single-threaded. */
+int orc_paged_decode_mt(const orc_cache_desc* c, const uint8_t* k_pool, const uint8_t* v_pool,
+                        const float* q, int32_t n_heads, const int32_t* block_tables,
+                        int32_t max_blocks, const int32_t* ctx_lens, const int32_t* start_pos,
+                        int32_t n_seqs, float scale, float* out, int32_t n_threads);
+
 /* Chunked prefill, causal: query row i of sequence b sits at position
  * ctx_b - q_len_b + i and runs flash_attn_f32 over keys 0..that position
  * (n_kv = cached + i + 1).  q/out: [total_q][n_heads][D] f32, rows of seq b
@@ -202,6 +211,14 @@ int orc_paged_prefill_rows(const orc_cache_desc* c, const uint8_t* k_pool, const
                            const int32_t* block_tables, int32_t max_blocks,
                            const int32_t* ctx_lens, int32_t seq, int32_t row_begin,
                            int32_t row_end, float scale, int32_t causal, float* out);
+/* orc_paged_prefill_rows on n_threads host threads (OpenMP over the rows of
+ * each KV head); same results. */
+int orc_paged_prefill_rows_mt(const orc_cache_desc* c, const uint8_t* k_pool, const uint8_t* v_pool,
+                              const float* q, int32_t n_heads, const int32_t* cu_q,
+                              const int32_t* block_tables, int32_t max_blocks,
+                              const int32_t* ctx_lens, int32_t seq, int32_t row_begin,
+                              int32_t row_end, float scale, int32_t causal, float* out,
+                              int32_t n_threads);
 
 /* ---- sequence / window manager (restated on BlockPool) ----------------- */
 /* Slot rule: slot = table[pos / bs] * bs + pos % bs; a new block is taken
