@@ -201,14 +201,23 @@ def test_negative_start_is_skipped_and_latched(n_seqs):
 def test_config5_full_size_q8_0():
     """Config 5 at full size: Q8_0, Hq 24 / Hkv 4 / D 256, block 32, 16
     sequences of U[32768, 131072] tokens over a seeded permutation of the
-    pool, the planner's partition (1792 tokens: up to 74 partials merged per
-    row).  The oracle decodes the two shortest sequences over the same pages
-    (their bytes copied from the device pools into an oracle cache); a
-    second decode at 1024-token partitions agrees with the first."""
+    pool, fp32 N(0,1) sources with 1% of elements x8 (the config's
+    outliers), the planner's partition (1792 tokens: up to 74 partials
+    merged per row).
+      - Quantised bytes: 4096 sampled (token, head) rows of each append
+        chunk, their device records equal the oracle's quantize_row_q8_0 of
+        the same fp32 source rows, bit for bit.
+      - Attention: the oracle decodes the longest sequence (all 24 heads
+        over its 74 partitions) and the shortest, over the same pages (their
+        bytes copied from the device pools into an oracle cache).
+      - A second decode at 1024-token partitions agrees with the first."""
+    import os as _os
+
     import torch
     from infer_train_amd.kv import PagedKvCache
 
     hq, hkv, D, bs = 24, 4, 256, 32
+    G = D // 32
     ctx = np.random.default_rng(5).integers(32768, 131073, 16).astype(np.int32)
     nblk = (ctx + bs - 1) // bs
     nb, mb = int(nblk.sum()), int(nblk.max())
@@ -219,13 +228,35 @@ def test_config5_full_size_q8_0():
     slots = tables[seqs, pos // bs].astype(np.int64) * bs + pos % bs
     g = torch.Generator(device="cuda:0")
     g.manual_seed(55)
+    rng = np.random.default_rng(57)
     step = 1 << 16
+    page_bytes = dev.page_bytes
+    kpool = dev.k_pool.view(torch.uint8).view(nb, hkv, page_bytes)
+    checked = 0
     for s0 in range(0, slots.size, step):
         n = min(step, slots.size - s0)
         k = torch.randn((n, hkv, D), generator=g, device="cuda:0")
         v = torch.randn((n, hkv, D), generator=g, device="cuda:0")
+        k[torch.rand((n, hkv, D), generator=g, device="cuda:0") < 0.01] *= 8
+        v[torch.rand((n, hkv, D), generator=g, device="cuda:0") < 0.01] *= 8
         dev.append(k, v, to_dev(slots[s0:s0 + n]))
+        # Sampled rows of this chunk: device records = the oracle's quantiser.
+        rows = rng.integers(0, n, 4096)
+        heads = rng.integers(0, hkv, 4096)
+        src = k[torch.from_numpy(rows).cuda(), torch.from_numpy(heads).cuda()].cpu().numpy()
+        sl = slots[s0 + rows]
+        blk, tok = sl // bs, sl % bs
+        pages = kpool[torch.from_numpy(blk).cuda(), torch.from_numpy(heads).cuda()].cpu().numpy()
+        qs = pages[np.arange(4096)[:, None], tok[:, None] * D + np.arange(D)[None, :]]
+        dbytes = pages[np.arange(4096)[:, None], bs * D + tok[:, None] * (2 * G) + np.arange(2 * G)[None, :]]
+        rec = np.concatenate([dbytes.reshape(4096, G, 2), qs.reshape(4096, G, 32)], axis=2)
+        want_rec = np.stack([orc.quantize_row_q8_0(src[i]) for i in range(4096)])
+        np.testing.assert_array_equal(rec.reshape(want_rec.shape), want_rec,
+                                      err_msg=f"Q8_0 records of chunk at {s0}")
+        checked += 4096
+        del k, v
     dev.check()
+    assert checked >= 16 * 4096
     q = kv_values(56, 16 * hq * D, orc.F32).reshape(16, hq, D)
     scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
     p_plan = dev.decode_partition(hq, ctx)
@@ -238,21 +269,23 @@ def test_config5_full_size_q8_0():
         outs[partition] = from_dev(out)
     assert_close(outs[1024], outs[p_plan], *TOL[orc.Q8_0], what="config5 1024 vs planner partition")
 
-    # Oracle over the two shortest sequences' pages, renumbered 0..n-1.
-    pick = np.argsort(ctx)[:2]
+    # Oracle over the longest and the shortest sequence's pages, renumbered.
+    pick = np.array([int(np.argmax(ctx)), int(np.argmin(ctx))])
+    assert -(-int(ctx[pick[0]]) // p_plan) >= 60  # the long one merges many partials
     blocks = np.concatenate([tables[b, :nblk[b]] for b in pick])
     t2 = np.full((2, int(nblk[pick].max())), -1, np.int32)
     t2[0, :nblk[pick[0]]] = np.arange(nblk[pick[0]])
     t2[1, :nblk[pick[1]]] = nblk[pick[0]] + np.arange(nblk[pick[1]])
     ref = orc.Cache(blocks.size, bs, hkv, D, orc.Q8_0)
-    row = hkv * dev.page_bytes
+    row = hkv * page_bytes
     idx = torch.from_numpy(blocks.astype(np.int64)).to("cuda:0")
     ref.k[:] = from_dev(dev.k_pool.view(nb, row).index_select(0, idx)).reshape(-1)
     ref.v[:] = from_dev(dev.v_pool.view(nb, row).index_select(0, idx)).reshape(-1)
-    want = ref.decode(q[pick], hq, t2, ctx[pick], None, scale)
-    exact = lazy(lambda: exact_decode(ref, q[pick], hq, t2, ctx[pick], None, scale))
+    threads = max(1, min(16, len(_os.sched_getaffinity(0))))
+    want = ref.decode(q[pick], hq, t2, ctx[pick], None, scale, threads=threads)
+    exact = lazy(lambda: exact_decode(ref, q[pick], hq, t2, ctx[pick], None, scale, with_mag=True))
     got = outs[p_plan][pick].reshape(want.shape)
-    assert_close_or_closer(got, want, exact, *TOL[orc.Q8_0], what="config5 full, two shortest sequences")
+    assert_close_or_closer(got, want, exact, *TOL[orc.Q8_0], what="config5 full, longest and shortest sequences")
 
 
 @pytest.mark.parametrize("dt", [orc.F16, orc.F32])
@@ -279,7 +312,7 @@ def test_q8_0_decode_d256():
     hq, hkv, D, bs = 24, 4, 256, 32
     dev, ref, tables, ctx, q, qdt = _build(orc.Q8_0, hq, hkv, D, bs, [3000, 1025, 33], seed=7)
     scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
-    exact = lazy(lambda: exact_decode(ref, q, hq, tables, ctx, None, scale))
+    exact = lazy(lambda: exact_decode(ref, q, hq, tables, ctx, None, scale, with_mag=True))
     for partition in (512, 1024, 2048):
         got, want = _run(dev, ref, tables, ctx, q, qdt, hq, partition=partition)
         assert_close_or_closer(got, want, exact, *TOL[orc.Q8_0], what=f"q8_0 P={partition}")
@@ -300,7 +333,8 @@ def test_quant_group_sizes_and_windows(dt, D):
         for partition in (64, 256):
             got, want = _run(dev, ref, tables, ctx_a, q, qdt, hq, start=start, partition=partition)
             scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
-            assert_close_or_closer(got, want, lambda: exact_decode(ref, q, hq, tables, ctx_a, start, scale), *TOL[dt],
+            assert_close_or_closer(got, want, lambda: exact_decode(ref, q, hq, tables, ctx_a, start, scale, with_mag=True),
+                                   *TOL[dt],
                                    what=f"dt={dt} D={D} hq={hq} hkv={hkv} P={partition}")
         assert np.all(got[-1] == 0)
 
@@ -314,7 +348,7 @@ def test_quant_block_size_8(dt):
     start = np.array([0, 3, 500], np.int32)
     dev, ref, tables, ctx_a, q, qdt = _build(dt, hq, hkv, D, bs, ctx, seed=71)
     scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
-    exact = lazy(lambda: exact_decode(ref, q, hq, tables, ctx_a, start, scale))
+    exact = lazy(lambda: exact_decode(ref, q, hq, tables, ctx_a, start, scale, with_mag=True))
     for partition in (64, 512):
         got, want = _run(dev, ref, tables, ctx_a, q, qdt, hq, start=start, partition=partition)
         assert_close_or_closer(got, want, exact, *TOL[dt], what=f"dt={dt} bs=8 P={partition}")
@@ -326,7 +360,7 @@ def test_q4_decode_config5_heads(dt):
     hq, hkv, D, bs = 24, 4, 256, 32
     dev, ref, tables, ctx, q, qdt = _build(dt, hq, hkv, D, bs, [3000, 1025, 33], seed=9)
     scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
-    exact = lazy(lambda: exact_decode(ref, q, hq, tables, ctx, None, scale))
+    exact = lazy(lambda: exact_decode(ref, q, hq, tables, ctx, None, scale, with_mag=True))
     for partition in (512, 1024):
         got, want = _run(dev, ref, tables, ctx, q, qdt, hq, partition=partition)
         assert_close_or_closer(got, want, exact, *TOL[dt], what=f"dt={dt} P={partition}")

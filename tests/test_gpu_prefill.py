@@ -138,19 +138,41 @@ def test_prefill_wide_table_scalar_page_ids():
 def test_prefill_config3_rows():
     """Config 3: Hq 32, Hkv 8, D 128, bs 16; 8 sequences with 2048 cached
     tokens append a 512-token chunk; table = a permutation of a 4096-block
-    pool.  Rows checked against the oracle: the first and last 16 of
-    sequences 0 and 7 (every row would take the scalar oracle minutes)."""
-    hq, hkv = 32, 8
+    pool.  Against the oracle (on the host's threads): 64 rows of every
+    sequence -- the first and last 16 of the chunk and two blocks of 16 at
+    seeded positions inside it.  Every row of every sequence: finite, and
+    each output element inside the range of the V rows it attends (keys 0
+    .. its position of its KV head), as a convex combination must be."""
+    import os
+
+    hq, hkv, D = 32, 8, 128
     ctx = [2560] * 8
     q_lens = [512] * 8
     dev, ref, tables, ctx, cu, q, td = _setup(orc.BF16, hq, hkv, ctx, q_lens, seed=3, nb=4096)
     out, scale = _run(dev, tables, ctx, cu, q, td, hq)
     got = from_dev(out)
-    qf = widen(q, orc.BF16)
-    for s in (0, 7):
-        for b, e in ((0, 16), (496, 512)):
-            want = ref.prefill(qf, hq, cu, tables, ctx, scale, causal=True, rows=(s, b, e))
-            rows = slice(int(cu[s]) + b, int(cu[s]) + e)
-            assert_close(got[rows], want[rows], RTOL, ATOL, what=f"config3 seq {s} rows {b}:{e}")
-    # Every row is a convex combination of V rows: finite and within V's range.
     assert np.isfinite(got).all()
+    qf = widen(q, orc.BF16)
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    rng = np.random.default_rng(33)
+    for s in range(8):
+        mids = np.sort(rng.choice(np.arange(1, 30), 2, replace=False)) * 16
+        for b in (0, int(mids[0]), int(mids[1]), 496):
+            want = ref.prefill(qf, hq, cu, tables, ctx, scale, causal=True, rows=(s, b, b + 16), threads=threads)
+            rows = slice(int(cu[s]) + b, int(cu[s]) + b + 16)
+            assert_close(got[rows], want[rows], RTOL, ATOL, what=f"config3 seq {s} rows {b}:{b + 16}")
+    # Convex hull: running min / max of V over positions, per KV head and dim.
+    n = ctx.astype(np.int64)
+    cu_tok = np.concatenate([[0], np.cumsum(n)[:-1]]).astype(np.int64)
+    _, gv = ref.gather(tables, ctx, None, cu_tok, int(n.sum()))
+    vrows = widen(gv.view(np.uint16), orc.BF16).reshape(-1, D)
+    G = hq // hkv
+    for s in range(8):
+        V = vrows[int(cu_tok[s]) * hkv:(int(cu_tok[s]) + int(n[s])) * hkv].reshape(hkv, int(n[s]), D)
+        hi = np.maximum.accumulate(V, axis=1)
+        lo = np.minimum.accumulate(V, axis=1)
+        pos = int(ctx[s]) - 512 + np.arange(512)
+        o = got[int(cu[s]):int(cu[s + 1])].reshape(512, hkv, G, D)
+        up = hi[:, pos, :].transpose(1, 0, 2)[:, :, None, :]
+        dn = lo[:, pos, :].transpose(1, 0, 2)[:, :, None, :]
+        assert np.all(o <= up + 1e-4) and np.all(o >= dn - 1e-4), f"config3 seq {s}: outside the V hull"

@@ -5,6 +5,8 @@ pages (evict) before appending, syncs its block tables from the slot
 mapping, and runs split-K decode over the last W positions.  Pools must equal
 the oracle's byte for byte; outputs must be within bf16 tolerance of the
 oracle's flash_attn_f32 over the same window."""
+import os
+
 import numpy as np
 import pytest
 
@@ -14,6 +16,7 @@ from kvutil import assert_close, from_dev, kv_values, to_dev, widen
 pytestmark = pytest.mark.gpu
 
 RTOL, ATOL = 2e-3, 1e-2
+THREADS = max(1, min(16, len(os.sched_getaffinity(0))))  # host threads for the oracle's decode
 
 
 def _window_run(n_seqs, hq, hkv, W, start, steps, cap, seed, check_every, D=128, bs=16):
@@ -73,7 +76,7 @@ def _window_run(n_seqs, hq, hkv, W, start, steps, cap, seed, check_every, D=128,
             out = dev.decode(to_dev(q.view(np.int16), torch.bfloat16), tables_d, to_dev(ctx), to_dev(st), W,
                              scale=scale, out_dtype=torch.float32)
             dev.check()
-            want = ref.decode(widen(q, orc.BF16), hq, t, ctx, st, scale)
+            want = ref.decode(widen(q, orc.BF16), hq, t, ctx, st, scale, threads=THREADS)
             assert_close(from_dev(out), want, RTOL, ATOL, what=f"window decode step {step}")
             np.testing.assert_array_equal(from_dev(dev.k_pool), ref.k)
             np.testing.assert_array_equal(from_dev(dev.v_pool), ref.v)
@@ -89,6 +92,9 @@ def test_window_small_unaligned():
 
 def test_window_config4_full_size():
     """Config 4 at full size: 64 sequences, Hq 16 / Hkv 2, W 4096, from
-    position 30000, pool of 16512 blocks in seeded order; 20 steps cross the
-    first allocation (p = 30000) and the first releases."""
-    _window_run(n_seqs=64, hq=16, hkv=2, W=4096, start=30000, steps=20, cap=16512, seed=4, check_every=10)
+    position 30000, pool of 16512 blocks in seeded order; 80 steps cross five
+    allocate / free cycles (allocations at p = 30000, 30016, ..., 30064,
+    releases at p = 30015, ..., 30079, LIFO hand-offs between sequences), with
+    the pools compared byte for byte and a decode checked once per cycle."""
+    n_ev = _window_run(n_seqs=64, hq=16, hkv=2, W=4096, start=30000, steps=80, cap=16512, seed=4, check_every=16)
+    assert n_ev == 64 * 5  # one block per sequence per cycle

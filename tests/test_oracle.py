@@ -344,14 +344,28 @@ def test_exact_decode_helper_and_closer_check(orc):
     q = orc.normal(7, 2 * hq * D).reshape(2, hq, D)
     scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
     want = c.decode(q, hq, tables, ctx, start, scale)
-    exact = exact_decode(c, q, hq, tables, ctx, start, scale)
+    exact, mag = exact_decode(c, q, hq, tables, ctx, start, scale, with_mag=True)
     assert np.max(np.abs(want - exact)) < 1e-5
-    fn = lambda: exact  # noqa: E731
+    # The oracle itself is within the per-element bound the helper applies.
+    assert np.all(np.abs(want - exact) <= 1e-6 + 1e-5 * mag)
+    # mag bounds |exact| (a convex combination of the v_i) and is positive.
+    assert np.all(np.abs(exact) <= mag + 1e-12) and np.all(mag > 0)
+    fn = lambda: (exact, mag)  # noqa: E731
     assert_close_or_closer(want, want, fn, 1e-5, 1e-6)
     bad = want.copy()
     bad[1, 3, 17] += 1e-4
     with pytest.raises(AssertionError):
         assert_close_or_closer(bad, want, fn, 1e-5, 1e-6)
+    # A perturbation within the oracle's tolerance but outside the
+    # per-element bound of one cancelling element is still rejected: the
+    # bound is per element, not the output's worst error.
+    i = np.unravel_index(np.argmin(mag), mag.shape)
+    bad = want.copy()
+    bad[i] = exact[i] + 3e-5 * mag[i] + 1e-6
+    off = np.abs(bad - want) > 1e-6 + 1e-5 * np.abs(want)
+    if off[i]:
+        with pytest.raises(AssertionError):
+            assert_close_or_closer(bad, want, fn, 1e-5, 1e-6)
 
 
 # ---------------- committed fixtures (tests/golden, written by make_golden.py) --
