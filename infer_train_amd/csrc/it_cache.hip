@@ -28,30 +28,54 @@ constexpr int kThreads = 256;
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // ---------------------------------------------------------------------------
-// Append, bit copy (F32 / F16 / BF16).  One lane = one 16-byte vector of one
-// (token, head) row, for K and for V.
+// Append, bit copy (F32 / F16 / BF16).  A wave moves kVecsPerLane x 64
+// consecutive 16-byte vectors of the flattened [token][head][row] source
+// (vector j of lane l is wave_base + 64 j + l, so every instruction covers a
+// contiguous KiB), K and V; all loads are issued before the first store.
+// Rows hold a power-of-two number of vectors (head_dim * elem / 16 = 16, 32
+// or 64), so the index math is shifts plus one 32-bit division by the head
+// count.  The sources are read once: non-temporal loads.
 // ---------------------------------------------------------------------------
+constexpr int kVecsPerLane = 4;
+
 __global__ __launch_bounds__(kThreads) void kv_append_copy(
     const uint4* __restrict__ k, const uint4* __restrict__ v, char* __restrict__ kpool,
-    char* __restrict__ vpool, const int64_t* __restrict__ slots, int64_t total, int hkv,
-    int row_vecs, int log2_bs, int64_t page_bytes, int64_t n_slots, uint32_t* err) {
-  const int64_t gid = int64_t(blockIdx.x) * kThreads + threadIdx.x;
-  if (gid >= total) return;
-  const int c = int(gid % row_vecs);
-  const int64_t th = gid / row_vecs;
-  const int h = int(th % hkv);
-  const int64_t t = th / hkv;
-  const int64_t slot = slots[t];
-  if (slot < 0) return;  // padding token
-  if (slot >= n_slots) {
-    if (c == 0 && h == 0) atomicOr(err, kErrSlot);
-    return;
+    char* __restrict__ vpool, const int64_t* __restrict__ slots, int32_t total, int hkv,
+    int log2_row_vecs, int log2_bs, int64_t page_bytes, int64_t n_slots, uint32_t* err) {
+  const int32_t wave_base = (int32_t(blockIdx.x) * kThreads + int32_t(threadIdx.x & ~63u)) * kVecsPerLane;
+  const int lane = int(threadIdx.x & 63u);
+  typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+  u4 kv[kVecsPerLane], vv[kVecsPerLane];
+  int64_t slot[kVecsPerLane];
+  // Loads are unconditional (past the end a lane re-reads the last vector),
+  // so they all go out before any wait; only the stores are predicated.
+#pragma unroll
+  for (int j = 0; j < kVecsPerLane; ++j) {
+    const int32_t i = min(wave_base + 64 * j + lane, total - 1);
+    kv[j] = __builtin_nontemporal_load(reinterpret_cast<const u4*>(k) + i);
+    vv[j] = __builtin_nontemporal_load(reinterpret_cast<const u4*>(v) + i);
+    slot[j] = slots[(i >> log2_row_vecs) / hkv];
   }
-  const int64_t blk = slot >> log2_bs;
-  const int64_t off = slot & ((int64_t(1) << log2_bs) - 1);
-  const int64_t dst = (blk * hkv + h) * page_bytes + (off * row_vecs + c) * 16;
-  st16(kpool + dst, k[gid]);
-  st16(vpool + dst, v[gid]);
+#pragma unroll
+  for (int j = 0; j < kVecsPerLane; ++j) {
+    const int32_t i = wave_base + 64 * j + lane;
+    if (i >= total) continue;
+    const int32_t th = i >> log2_row_vecs;  // (token, head) row
+    const int32_t t = th / hkv;
+    const int h = th - t * hkv;
+    const int c = i & ((1 << log2_row_vecs) - 1);
+    const int64_t sl = slot[j];
+    if (sl < 0) continue;  // padding token
+    if (sl >= n_slots) {
+      if (c == 0 && h == 0) atomicOr(err, kErrSlot);
+      continue;
+    }
+    const int64_t blk = sl >> log2_bs;
+    const int64_t off = sl & ((int64_t(1) << log2_bs) - 1);
+    const int64_t dst = (blk * hkv + h) * page_bytes + ((off << log2_row_vecs) + c) * 16;
+    *reinterpret_cast<u4*>(kpool + dst) = kv[j];
+    *reinterpret_cast<u4*>(vpool + dst) = vv[j];
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -512,10 +536,14 @@ extern "C" int32_t it_kv_append(it_kv_cache* c, const void* k, const void* v, in
                        c->n_kv_heads, c->head_dim, c->log2_bs, c->page_bytes, n_slots, c->err_flag);
   } else {
     const int row_vecs = int(c->head_dim * dtype_bytes(c->dtype) / 16);
+    if (!is_pow2(row_vecs)) return fail(IT_NOT_IMPLEMENTED, "it_kv_append: %d vectors per row", row_vecs);
     const int64_t total = int64_t(n_tokens) * c->n_kv_heads * row_vecs;
-    hipLaunchKernelGGL(kv_append_copy, dim3(unsigned(cdiv(total, kThreads))), dim3(kThreads), 0, s,
-                       (const uint4*)k, (const uint4*)v, (char*)c->k_pool, (char*)c->v_pool, slots, total,
-                       c->n_kv_heads, row_vecs, c->log2_bs, c->page_bytes, n_slots, c->err_flag);
+    if (total >= (int64_t(1) << 31) - int64_t(kThreads) * kVecsPerLane)
+      return fail(IT_INVALID_INPUT, "it_kv_append: %lld vectors in one call (at most 2^31)", (long long)total);
+    hipLaunchKernelGGL(kv_append_copy, dim3(unsigned(cdiv(total, int64_t(kThreads) * kVecsPerLane))), dim3(kThreads),
+                       0, s, (const uint4*)k, (const uint4*)v, (char*)c->k_pool, (char*)c->v_pool, slots,
+                       int32_t(total), c->n_kv_heads, ilog2(row_vecs), c->log2_bs, c->page_bytes, n_slots,
+                       c->err_flag);
   }
   IT_HIP(hipGetLastError(), "it_kv_append: launch");
   return IT_OK;
