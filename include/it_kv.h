@@ -81,7 +81,11 @@ int32_t it_block_pool_new_ordered(const int64_t* order, int64_t capacity, int32_
 void it_block_pool_destroy(it_block_pool* pool);
 /* BlockPool::allocate (paged.rs:36-42): LIFO pop, refcount 1; -1 = None. */
 int64_t it_block_pool_allocate(it_block_pool* pool);
-/* BlockPool::share (paged.rs:44-46). */
+/* BlockPool::share (paged.rs:44-46), with one departure: the reference
+ * increments the refcount of any block, a free one included, which leaves
+ * that block on the free list and referenced at once (the next allocate
+ * would hand out a live block).  Here sharing a free block (refcount 0) is
+ * IT_INVALID_INPUT and changes nothing. */
 int32_t it_block_pool_share(it_block_pool* pool, int64_t id);
 /* BlockPool::free (paged.rs:48-53); a free at refcount 0 (a u32 underflow
  * in the reference) is IT_INVALID_INPUT. */

@@ -146,6 +146,17 @@ class ContinuousBatcher:
     arrival order (continuous.rs:62-73).  Each running request is bound to a
     manager sequence slot; `plan_prefill` / `plan_decode` produce the step's
     slot mapping through the manager, and `finish` releases the blocks.
+
+    Preemption (the reference declares RequestState::Preempted,
+    continuous.rs:13, but never enters it): `preempt` moves a running
+    request to Preempted, either releasing its blocks and sequence slot (the
+    request is prefilled again, prompt and generated tokens, when it resumes)
+    or keeping them (it resumes where it stopped).  `preempt_for(n)` frees
+    pool blocks by preempting, releasing, the most recently admitted running
+    requests first until n blocks are free.  `schedule()` resumes preempted
+    requests, in the order they were preempted, before it admits waiting
+    ones.  Every choice depends only on the call sequence, so block ids stay
+    deterministic.
     """
 
     def __init__(self, max_batch_size: int, manager: Optional[KvManager] = None):
@@ -156,6 +167,8 @@ class ContinuousBatcher:
         self.manager = manager
         self.seq_of: Dict[int, int] = {}
         self._free_seqs: List[int] = list(range(manager.max_seqs - 1, -1, -1)) if manager else []
+        self.preempted: deque = deque()  # preemption order
+        self.needs_prefill: set = set()  # released by preemption: prefill again on resume
 
     def add_request(self, request_id: int, prompt: Sequence[int], max_tokens: int) -> None:  # :45-60
         self.requests[request_id] = RequestContext(request_id, RequestState.Waiting, list(prompt), [], max_tokens)
@@ -163,18 +176,64 @@ class ContinuousBatcher:
 
     def schedule(self) -> List[int]:  # :62-73
         while len(self.running) < self.max_batch_size:
-            if not self.waiting:
+            if self.preempted:  # resumed first, in preemption order
+                rid = self.preempted.popleft()
+            elif self.waiting:
+                rid = self.waiting.popleft()
+            else:
                 break
-            rid = self.waiting.popleft()
             ctx = self.requests.get(rid)
             if ctx is not None:
                 ctx.state = RequestState.Running
                 self.running.append(rid)
-                if self.manager is not None:
+                if self.manager is not None and rid not in self.seq_of:
                     if not self._free_seqs:
                         raise RuntimeError("no free sequence slot in the KV manager")
                     self.seq_of[rid] = self._free_seqs.pop()
         return list(self.running)
+
+    def preempt(self, request_id: int, keep_blocks: bool = False) -> np.ndarray:
+        """Running -> Preempted.  keep_blocks False: the request's blocks are
+        released (BlockPool::free, lowest logical block first) with its
+        sequence slot, and it is prefilled again on resume; True: blocks and
+        slot stay held.  Returns the freed block ids (empty when kept)."""
+        ctx = self.requests[request_id]
+        if ctx.state != RequestState.Running:
+            raise ValueError(f"request {request_id} is {ctx.state.value}, not Running")
+        ctx.state = RequestState.Preempted
+        self.running.remove(request_id)
+        self.preempted.append(request_id)
+        freed = np.zeros(0, np.int32)
+        if not keep_blocks and self.manager is not None and request_id in self.seq_of:
+            seq = self.seq_of.pop(request_id)
+            freed = self.manager.release(seq)
+            self._free_seqs.append(seq)
+            self.needs_prefill.add(request_id)
+        return freed
+
+    def preempt_for(self, n_blocks: int) -> List[int]:
+        """Preempt (releasing) the most recently admitted running requests
+        until the pool holds n_blocks free blocks; returns them in the order
+        they were preempted.  Raises if even preempting every running request
+        does not free enough."""
+        pool = self.manager.pool
+        out: List[int] = []
+        while pool.num_free() < n_blocks:
+            if not self.running:
+                raise RuntimeError(f"cannot free {n_blocks} blocks: {pool.num_free()} free with nothing running")
+            rid = self.running[-1]
+            self.preempt(rid, keep_blocks=False)
+            out.append(rid)
+        return out
+
+    def plan_resume(self, request_ids: Sequence[int]) -> StepPlan:
+        """Prefill again the requests a releasing preemption emptied: their
+        prompt plus the tokens generated before the preemption."""
+        seqs = [self.seq_of[r] for r in request_ids]
+        lens = [len(self.requests[r].prompt_tokens) + len(self.requests[r].generated_tokens) for r in request_ids]
+        for r in request_ids:
+            self.needs_prefill.discard(r)
+        return self.manager.append(seqs, lens)
 
     def plan_prefill(self, request_ids: Sequence[int]) -> StepPlan:
         seqs = [self.seq_of[r] for r in request_ids]
@@ -188,6 +247,7 @@ class ContinuousBatcher:
         ctx = self.requests[request_id]
         ctx.state = RequestState.Finished
         self.running.remove(request_id)
+        self.needs_prefill.discard(request_id)
         freed = np.zeros(0, np.int32)
         if self.manager is not None and request_id in self.seq_of:
             seq = self.seq_of.pop(request_id)

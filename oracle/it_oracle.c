@@ -177,7 +177,8 @@ int64_t orc_pool_allocate(orc_block_pool* p) {
 }
 
 int orc_pool_share(orc_block_pool* p, int64_t id) {
-  /* paged.rs:44-46 */
+  /* paged.rs:44-46.  The reference also increments a free block's count,
+   * leaving it on the free list while referenced; that is rejected here. */
   if (id < 0 || id >= p->capacity || p->ref_counts[id] == 0) return ORC_INVALID_INPUT;
   p->ref_counts[id] += 1;
   return ORC_OK;

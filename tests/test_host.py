@@ -177,6 +177,94 @@ def test_batcher_fifo_admission_and_plans():
     assert b.schedule() == [11, 12]
 
 
+def _oracle_release(mo, pool, s):
+    """The oracle's release of sequence slot s: BlockPool::free of every held
+    block, lowest logical block first, then an empty table row."""
+    t, _, _ = mo.tables()
+    freed = [int(b) for b in t[s] if b >= 0]
+    for blk in freed:
+        assert pool.free(blk) == 0
+    mo.seed_seq(s, 0, 0, [])
+    return freed
+
+
+def test_batcher_preemption_releases_or_keeps_blocks_like_the_oracle():
+    """Preempted requests: releasing ones give their blocks back (the LIFO
+    pool hands them out again, last freed first) and are prefilled again,
+    prompt plus generated tokens, on resume; kept ones resume at their
+    position with their blocks.  Every slot, freed block and table equals
+    the oracle manager driven through the same steps."""
+    cap, bs = 12, 16
+    order = orc.permutation(3, cap)
+    pa, pb = BlockPool(cap, order=order), orc.Pool(cap, order=order)
+    m, mo = KvManager(pa, bs, 4, 8), orc.Manager(pb, bs, 4, 8)
+    b = ContinuousBatcher(3, m)
+    for rid, n in ((1, 20), (2, 33), (3, 10), (4, 5)):
+        b.add_request(rid, list(range(n)), 8)
+    assert b.schedule() == [1, 2, 3]
+    seq = dict(b.seq_of)
+    assert seq == {1: 0, 2: 1, 3: 2}
+    plan = b.plan_prefill([1, 2, 3])
+    so, _ = mo.append([0, 1, 2], [20, 33, 10])
+    np.testing.assert_array_equal(plan.slots, so)
+    for step in range(2):
+        plan = b.plan_decode()
+        so, _ = mo.append([0, 1, 2], 1)
+        np.testing.assert_array_equal(plan.slots, so)
+        for r in (1, 2, 3):
+            b.requests[r].generated_tokens.append(100 + step)
+    assert pa.num_free() == pb.num_free() == 6
+
+    # 8 free blocks wanted: request 3 (1 block) then 2 (3 blocks) preempted.
+    assert b.preempt_for(8) == [3, 2]
+    assert pa.num_free() == 10
+    f3, f2 = _oracle_release(mo, pb, 2), _oracle_release(mo, pb, 1)
+    assert [b.requests[r].state.value for r in (1, 2, 3)] == ["Running", "Preempted", "Preempted"]
+    assert b.needs_prefill == {2, 3} and 2 not in b.seq_of and 3 not in b.seq_of
+
+    # Keeping: blocks and slot stay, nothing freed.
+    assert b.preempt(1, keep_blocks=True).size == 0 and b.seq_of[1] == 0
+    assert pa.num_free() == 10 and 1 not in b.needs_prefill
+    with pytest.raises(ValueError):
+        b.preempt(1)  # already preempted
+
+    # Resumed in preemption order before the waiting request 4.
+    assert b.schedule() == [3, 2, 1]
+    assert b.requests[4].state.value == "Waiting"
+    # Slots are handed out again LIFO: request 3 takes slot 1 (freed last).
+    assert b.seq_of == {1: 0, 3: 1, 2: 2}
+    plan = b.plan_resume([3, 2])
+    assert b.needs_prefill == set()
+    so, _ = mo.append([1, 2], [12, 35])
+    np.testing.assert_array_equal(plan.slots, so)
+    # Request 3 (listed first) starts in the last block freed, request 2's
+    # last logical block: the LIFO pool.
+    assert plan.slots[0] // bs == f2[-1]
+    plan = b.plan_decode()
+    so, _ = mo.append([1, 2, 0], 1)
+    np.testing.assert_array_equal(plan.slots, so)
+    t, cl, _ = m.tables()
+    to, clo, _ = mo.tables()
+    np.testing.assert_array_equal(t, to)
+    np.testing.assert_array_equal(cl, clo)
+    assert list(cl[:3]) == [23, 13, 36]
+    for r in (1, 2, 3):
+        b.finish(r)
+    assert pa.num_free() == cap and b.schedule() == [4]
+
+
+def test_preempt_for_raises_when_nothing_is_left():
+    pool = BlockPool(4)
+    b = ContinuousBatcher(2, KvManager(pool, 16, 2, 8))
+    b.add_request(0, list(range(40)), 1)
+    b.schedule()
+    b.plan_prefill([0])
+    assert pool.num_free() == 1
+    with pytest.raises(RuntimeError, match="cannot free"):
+        b.preempt_for(5)
+    assert pool.num_free() == 4 and b.requests[0].state.value == "Preempted"
+
+
 def test_host_code_under_sanitizers(tmp_path):
     """The host allocator and slot manager (csrc/it_host.cpp, plain C++)
     built with AddressSanitizer and UndefinedBehaviorSanitizer and driven by
