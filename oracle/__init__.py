@@ -17,13 +17,17 @@ import numpy as np
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "liboracle.so")
 
-F32, F16, Q4_0, Q4_1, Q8_0, BF16 = 0, 1, 2, 3, 8, 30
+F32, F16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, BF16 = 0, 1, 2, 3, 6, 7, 8, 30
 QK8_0 = 32
 BLOCK_Q8_0_BYTES = 34
 QK4_0 = 32
 BLOCK_Q4_0_BYTES = 18
 QK4_1 = 32
 BLOCK_Q4_1_BYTES = 20
+QK5_0 = QK5_1 = 32
+BLOCK_Q5_0_BYTES = 22
+BLOCK_Q5_1_BYTES = 24
+QUANT_TYPES = (Q8_0, Q4_0, Q4_1, Q5_0, Q5_1)
 
 
 class CacheDesc(C.Structure):
@@ -64,6 +68,10 @@ def _load() -> C.CDLL:
         "orc_dequantize_row_q4_0": (None, [P, sz, P]),
         "orc_quantize_row_q4_1": (i32, [P, sz, P]),
         "orc_dequantize_row_q4_1": (None, [P, sz, P]),
+        "orc_quantize_row_q5_0": (i32, [P, sz, P]),
+        "orc_dequantize_row_q5_0": (None, [P, sz, P]),
+        "orc_quantize_row_q5_1": (i32, [P, sz, P]),
+        "orc_dequantize_row_q5_1": (None, [P, sz, P]),
         "orc_rope_f32": (i32, [P, P, sz, i64, i32, i32, f32]),
         "orc_flash_attn_f32": (None, [P, P, P, P, P, i32, i32, f32]),
         "orc_backend_flash_attention": (i32, [P, P, P, P, P, i32, i32, i32]),
@@ -264,6 +272,52 @@ def dequantize_row_q4_1(y) -> np.ndarray:
     return out
 
 
+# ---- Q5_0 / Q5_1 (type ids types.rs:116-117; blocks, quantisers and ------------
+# ---- dequantisers = ggml's, which the reference does not carry) ----------------
+def quantize_row_q5_0(x) -> np.ndarray:
+    """x: f32[n], n % 32 == 0 -> uint8[n/32, 22] packed block_q5_0 records."""
+    x = _c(x, np.float32).ravel()
+    out = np.empty((x.size // QK5_0, BLOCK_Q5_0_BYTES), np.uint8)
+    if lib.orc_quantize_row_q5_0(x.ctypes.data, x.size, out.ctypes.data):
+        raise ValueError("length not a multiple of 32")
+    return out
+
+
+def dequantize_row_q5_0(y) -> np.ndarray:
+    y = _c(y, np.uint8)
+    n = y.size // BLOCK_Q5_0_BYTES * QK5_0
+    out = np.empty(n, np.float32)
+    lib.orc_dequantize_row_q5_0(y.ctypes.data, n, out.ctypes.data)
+    return out
+
+
+def quantize_row_q5_1(x) -> np.ndarray:
+    """x: f32[n], n % 32 == 0 -> uint8[n/32, 24] packed block_q5_1 records."""
+    x = _c(x, np.float32).ravel()
+    out = np.empty((x.size // QK5_1, BLOCK_Q5_1_BYTES), np.uint8)
+    if lib.orc_quantize_row_q5_1(x.ctypes.data, x.size, out.ctypes.data):
+        raise ValueError("length not a multiple of 32")
+    return out
+
+
+def dequantize_row_q5_1(y) -> np.ndarray:
+    y = _c(y, np.uint8)
+    n = y.size // BLOCK_Q5_1_BYTES * QK5_1
+    out = np.empty(n, np.float32)
+    lib.orc_dequantize_row_q5_1(y.ctypes.data, n, out.ctypes.data)
+    return out
+
+
+RECORD_BYTES = {Q8_0: BLOCK_Q8_0_BYTES, Q4_0: BLOCK_Q4_0_BYTES, Q4_1: BLOCK_Q4_1_BYTES, Q5_0: BLOCK_Q5_0_BYTES,
+                Q5_1: BLOCK_Q5_1_BYTES}
+
+
+def dequantize_records(y, dtype: int) -> np.ndarray:
+    """Packed records of any quantised dtype -> f32 values."""
+    return {Q8_0: dequantize_row_q8_0, Q4_0: dequantize_row_q4_0, Q4_1: dequantize_row_q4_1,
+            Q5_0: dequantize_row_q5_0, Q5_1: dequantize_row_q5_1}[dtype](y)
+
+
 # ---- attention (flash_attn.rs:6-72, arm.rs:304-370) ----------------------------
 def flash_attn_f32(q, k, v, scale: float, mask=None) -> np.ndarray:
     q, k, v = _c(q, np.float32), _c(k, np.float32), _c(v, np.float32)
@@ -304,7 +358,7 @@ class Cache:
         return C.byref(self.desc)
 
     def append(self, k, v, slots) -> None:
-        src_dt = np.float32 if self.desc.dtype in (F32, Q8_0, Q4_0, Q4_1) else np.uint16
+        src_dt = np.float32 if self.desc.dtype in (F32,) + QUANT_TYPES else np.uint16
         k, v, s = _c(k, src_dt), _c(v, src_dt), _c(slots, np.int64)
         rc = lib.orc_kv_append(self._d(), self.k.ctypes.data, self.v.ctypes.data, k.ctypes.data, v.ctypes.data,
                                s.ctypes.data, s.size)
@@ -317,8 +371,8 @@ class Cache:
             return D // QK8_0 * BLOCK_Q8_0_BYTES
         if self.desc.dtype == Q4_0:
             return D // QK4_0 * BLOCK_Q4_0_BYTES
-        if self.desc.dtype == Q4_1:
-            return D // QK4_1 * BLOCK_Q4_1_BYTES
+        if self.desc.dtype in RECORD_BYTES:
+            return D // 32 * RECORD_BYTES[self.desc.dtype]
         return D * (4 if self.desc.dtype == F32 else 2)
 
     def gather(self, tables, ctx_lens, start_pos, cu_out, n_out_tokens) -> Tuple[np.ndarray, np.ndarray]:

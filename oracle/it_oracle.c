@@ -354,6 +354,102 @@ void orc_dequantize_row_q4_1(const uint8_t* y, size_t n, float* x) {
 }
 
 /* ------------------------------------------------------------------------ */
+/* Q5_0 / Q5_1 -- ggml's quantize_row_q5_{0,1}_ref and dequantize_row_q5_*  */
+/* (the reference has the type ids, types.rs:116-117, and nothing else)     */
+/* ------------------------------------------------------------------------ */
+/* (uint8_t)(float) on x86: the same cvttss2si, low byte kept unsigned. */
+static int32_t q5_trunc_u8(float f) {
+  if (f != f || fabsf(f) >= 2147483648.0f) return 0;
+  return (int32_t)(uint8_t)(int32_t)f;
+}
+
+/* qh: bit e = bit 4 of element e's 5-bit value; qs as Q4's. */
+static void q5_pack(const int32_t* q, uint8_t* qh4, uint8_t* qs16) {
+  uint32_t qh = 0;
+  for (int j = 0; j < 16; ++j) {
+    qs16[j] = (uint8_t)((q[j] & 0x0F) | ((q[j + 16] & 0x0F) << 4));
+    qh |= (((uint32_t)q[j] & 0x10u) >> 4) << j;
+    qh |= (((uint32_t)q[j + 16] & 0x10u) >> 4) << (j + 16);
+  }
+  for (int b = 0; b < 4; ++b) qh4[b] = (uint8_t)(qh >> (8 * b));
+}
+
+static int32_t q5_value(const uint8_t* qh4, const uint8_t* qs16, int e) {
+  uint32_t qh = (uint32_t)qh4[0] | ((uint32_t)qh4[1] << 8) | ((uint32_t)qh4[2] << 16) | ((uint32_t)qh4[3] << 24);
+  int32_t nib = e < 16 ? (qs16[e] & 0xF) : (qs16[e - 16] >> 4);
+  return nib | (int32_t)(((qh >> e) & 1u) << 4);
+}
+
+int orc_quantize_row_q5_0(const float* x, size_t n, uint8_t* y) {
+  if (n % ORC_QK5_0) return ORC_INVALID_INPUT;
+  for (size_t i = 0; i < n / ORC_QK5_0; ++i) {
+    const float* xb = x + i * ORC_QK5_0;
+    uint8_t* rec = y + i * ORC_BLOCK_Q5_0_BYTES;
+    float amax = 0.0f, max = 0.0f;
+    for (int j = 0; j < ORC_QK5_0; ++j) { /* strict <: the first of equal magnitudes; NaN never wins */
+      float a = fabsf(xb[j]);
+      if (amax < a) {
+        amax = a;
+        max = xb[j];
+      }
+    }
+    const float d = max / -16.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    uint16_t dh = orc_f32_to_f16(d);
+    rec[0] = (uint8_t)(dh & 0xFF);
+    rec[1] = (uint8_t)(dh >> 8);
+    int32_t q[ORC_QK5_0];
+    for (int j = 0; j < ORC_QK5_0; ++j) {
+      int32_t v = q4_trunc_i8(xb[j] * id + 16.5f);
+      q[j] = v > 31 ? 31 : v;
+    }
+    q5_pack(q, rec + 2, rec + 6);
+  }
+  return ORC_OK;
+}
+
+void orc_dequantize_row_q5_0(const uint8_t* y, size_t n, float* x) {
+  for (size_t i = 0; i < n / ORC_QK5_0; ++i) {
+    const uint8_t* rec = y + i * ORC_BLOCK_Q5_0_BYTES;
+    float d = orc_f16_to_f32((uint16_t)(rec[0] | (rec[1] << 8)));
+    for (int e = 0; e < ORC_QK5_0; ++e) x[i * ORC_QK5_0 + e] = d * (float)(q5_value(rec + 2, rec + 6, e) - 16);
+  }
+}
+
+int orc_quantize_row_q5_1(const float* x, size_t n, uint8_t* y) {
+  if (n % ORC_QK5_1) return ORC_INVALID_INPUT;
+  for (size_t i = 0; i < n / ORC_QK5_1; ++i) {
+    const float* xb = x + i * ORC_QK5_1;
+    uint8_t* rec = y + i * ORC_BLOCK_Q5_1_BYTES;
+    float mn = FLT_MAX, mx = -FLT_MAX;
+    for (int j = 0; j < ORC_QK5_1; ++j) {
+      if (xb[j] < mn) mn = xb[j];
+      if (xb[j] > mx) mx = xb[j];
+    }
+    const float d = (mx - mn) / 31.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    uint16_t dh = orc_f32_to_f16(d), mh = orc_f32_to_f16(mn);
+    rec[0] = (uint8_t)(dh & 0xFF);
+    rec[1] = (uint8_t)(dh >> 8);
+    rec[2] = (uint8_t)(mh & 0xFF);
+    rec[3] = (uint8_t)(mh >> 8);
+    int32_t q[ORC_QK5_1];
+    for (int j = 0; j < ORC_QK5_1; ++j) q[j] = q5_trunc_u8((xb[j] - mn) * id + 0.5f);
+    q5_pack(q, rec + 4, rec + 8);
+  }
+  return ORC_OK;
+}
+
+void orc_dequantize_row_q5_1(const uint8_t* y, size_t n, float* x) {
+  for (size_t i = 0; i < n / ORC_QK5_1; ++i) {
+    const uint8_t* rec = y + i * ORC_BLOCK_Q5_1_BYTES;
+    float d = orc_f16_to_f32((uint16_t)(rec[0] | (rec[1] << 8)));
+    float m = orc_f16_to_f32((uint16_t)(rec[2] | (rec[3] << 8)));
+    for (int e = 0; e < ORC_QK5_1; ++e) x[i * ORC_QK5_1 + e] = d * (float)q5_value(rec + 4, rec + 8, e) + m;
+  }
+}
+
+/* ------------------------------------------------------------------------ */
 /* rope_f32 -- src/backend/arm/rope.rs:6-44                                   */
 /* ------------------------------------------------------------------------ */
 int orc_rope_f32(const float* x, float* out, size_t n, int64_t pos, int32_t n_dims, int32_t head_dim,
@@ -444,6 +540,7 @@ static int desc_ok(const orc_cache_desc* c) {
   if (c->dtype == ORC_Q8_0) return c->head_dim % ORC_QK8_0 == 0;
   if (c->dtype == ORC_Q4_0) return c->head_dim % ORC_QK4_0 == 0;
   if (c->dtype == ORC_Q4_1) return c->head_dim % ORC_QK4_1 == 0;
+  if (c->dtype == ORC_Q5_0 || c->dtype == ORC_Q5_1) return c->head_dim % 32 == 0;
   return elem_bytes(c->dtype) != 0;
 }
 
@@ -452,7 +549,42 @@ size_t orc_page_bytes(const orc_cache_desc* c) {
   if (c->dtype == ORC_Q8_0) return bs * d + bs * (d / ORC_QK8_0) * 2;
   if (c->dtype == ORC_Q4_0) return bs * (d / 2) + bs * (d / ORC_QK4_0) * 2;
   if (c->dtype == ORC_Q4_1) return bs * (d / 2) + bs * (d / ORC_QK4_1) * 4;
+  if (c->dtype == ORC_Q5_0) return bs * (d / 2) + bs * (d / ORC_QK5_0) * 6;
+  if (c->dtype == ORC_Q5_1) return bs * (d / 2) + bs * (d / ORC_QK5_1) * 8;
   return bs * d * elem_bytes(c->dtype);
+}
+
+/* Q5 pages: the nibble plane [block_size][d / 2], then per token a side row
+ * of d/32 qh words and d/32 metadata words (fp16 d, or the (d, m) pair).
+ * A ggml record is {meta, qh, qs}. */
+static int is_q5(int32_t dt) { return dt == ORC_Q5_0 || dt == ORC_Q5_1; }
+static size_t q5_meta_bytes(int32_t dt) { return dt == ORC_Q5_1 ? 4 : 2; }
+static size_t q5_record_bytes(int32_t dt) { return dt == ORC_Q5_1 ? ORC_BLOCK_Q5_1_BYTES : ORC_BLOCK_Q5_0_BYTES; }
+
+static void q5_put_row(const orc_cache_desc* c, uint8_t* page, int32_t slot, const float* x) {
+  size_t d = (size_t)c->head_dim, ng = d / 32, mb = q5_meta_bytes(c->dtype);
+  uint8_t rec[ORC_BLOCK_Q5_1_BYTES];
+  uint8_t* qs = page + (size_t)slot * (d / 2);
+  uint8_t* side = page + (size_t)c->block_size * (d / 2) + (size_t)slot * ng * (4 + mb);
+  for (size_t g = 0; g < ng; ++g) {
+    if (c->dtype == ORC_Q5_1) orc_quantize_row_q5_1(x + g * 32, 32, rec);
+    else orc_quantize_row_q5_0(x + g * 32, 32, rec);
+    memcpy(side + ng * 4 + g * mb, rec, mb);
+    memcpy(side + g * 4, rec + mb, 4);
+    memcpy(qs + g * 16, rec + mb + 4, 16);
+  }
+}
+
+static void q5_get_row(const orc_cache_desc* c, const uint8_t* page, int32_t slot, uint8_t* dst) {
+  size_t d = (size_t)c->head_dim, ng = d / 32, mb = q5_meta_bytes(c->dtype), rb = q5_record_bytes(c->dtype);
+  const uint8_t* qs = page + (size_t)slot * (d / 2);
+  const uint8_t* side = page + (size_t)c->block_size * (d / 2) + (size_t)slot * ng * (4 + mb);
+  for (size_t g = 0; g < ng; ++g) {
+    uint8_t* rec = dst + g * rb;
+    memcpy(rec, side + ng * 4 + g * mb, mb);
+    memcpy(rec + mb, side + g * 4, 4);
+    memcpy(rec + mb + 4, qs + g * 16, 16);
+  }
 }
 
 static uint8_t* page_ptr(const orc_cache_desc* c, const uint8_t* pool, int64_t block, int32_t h) {
@@ -462,7 +594,9 @@ static uint8_t* page_ptr(const orc_cache_desc* c, const uint8_t* pool, int64_t b
 /* Write one token row (head_dim values) of one head into its page slot. */
 static void put_row(const orc_cache_desc* c, uint8_t* page, int32_t slot, const void* src_row) {
   size_t d = (size_t)c->head_dim;
-  if (c->dtype == ORC_Q8_0) {
+  if (is_q5(c->dtype)) {
+    q5_put_row(c, page, slot, (const float*)src_row);
+  } else if (c->dtype == ORC_Q8_0) {
     size_t ng = d / ORC_QK8_0;
     uint8_t rec[ORC_BLOCK_Q8_0_BYTES];
     uint8_t* qs = page + (size_t)slot * d;
@@ -506,7 +640,9 @@ static void put_row(const orc_cache_desc* c, uint8_t* page, int32_t slot, const 
 int orc_kv_append(const orc_cache_desc* c, uint8_t* k_pool, uint8_t* v_pool,
                   const void* k, const void* v, const int64_t* slots, int32_t n_tokens) {
   if (!desc_ok(c) || n_tokens < 0) return ORC_INVALID_INPUT;
-  size_t src_eb = (c->dtype == ORC_Q8_0 || c->dtype == ORC_Q4_0 || c->dtype == ORC_Q4_1) ? 4 : elem_bytes(c->dtype);
+  size_t src_eb = (c->dtype == ORC_Q8_0 || c->dtype == ORC_Q4_0 || c->dtype == ORC_Q4_1 || is_q5(c->dtype))
+                      ? 4
+                      : elem_bytes(c->dtype);
   size_t row = (size_t)c->head_dim * src_eb;
   int64_t n_slots = c->num_blocks * c->block_size;
   for (int32_t t = 0; t < n_tokens; ++t) {
@@ -528,7 +664,9 @@ int orc_kv_append(const orc_cache_desc* c, uint8_t* k_pool, uint8_t* v_pool,
  * record sequence for Q8_0. */
 static void get_row_raw(const orc_cache_desc* c, const uint8_t* page, int32_t slot, uint8_t* dst) {
   size_t d = (size_t)c->head_dim;
-  if (c->dtype == ORC_Q8_0) {
+  if (is_q5(c->dtype)) {
+    q5_get_row(c, page, slot, dst);
+  } else if (c->dtype == ORC_Q8_0) {
     size_t ng = d / ORC_QK8_0;
     const uint8_t* qs = page + (size_t)slot * d;
     const uint8_t* sc = page + (size_t)c->block_size * d + (size_t)slot * ng * 2;
@@ -567,6 +705,7 @@ static size_t row_out_bytes(const orc_cache_desc* c) {
   if (c->dtype == ORC_Q8_0) return (size_t)(c->head_dim / ORC_QK8_0) * ORC_BLOCK_Q8_0_BYTES;
   if (c->dtype == ORC_Q4_0) return (size_t)(c->head_dim / ORC_QK4_0) * ORC_BLOCK_Q4_0_BYTES;
   if (c->dtype == ORC_Q4_1) return (size_t)(c->head_dim / ORC_QK4_1) * ORC_BLOCK_Q4_1_BYTES;
+  if (is_q5(c->dtype)) return (size_t)(c->head_dim / 32) * q5_record_bytes(c->dtype);
   return (size_t)c->head_dim * elem_bytes(c->dtype);
 }
 
@@ -593,6 +732,17 @@ static void get_row_f32(const orc_cache_desc* c, const uint8_t* page, int32_t sl
       uint8_t* buf = ng * ORC_BLOCK_Q4_1_BYTES <= sizeof(rec) ? rec : (uint8_t*)malloc(ng * ORC_BLOCK_Q4_1_BYTES);
       get_row_raw(c, page, slot, buf);
       orc_dequantize_row_q4_1(buf, d, dst);
+      if (buf != rec) free(buf);
+      break;
+    }
+    case ORC_Q5_0:
+    case ORC_Q5_1: {
+      uint8_t rec[8 * ORC_BLOCK_Q5_1_BYTES * 4];
+      size_t nb = (d / 32) * q5_record_bytes(c->dtype);
+      uint8_t* buf = nb <= sizeof(rec) ? rec : (uint8_t*)malloc(nb);
+      get_row_raw(c, page, slot, buf);
+      if (c->dtype == ORC_Q5_1) orc_dequantize_row_q5_1(buf, d, dst);
+      else orc_dequantize_row_q5_0(buf, d, dst);
       if (buf != rec) free(buf);
       break;
     }

@@ -36,6 +36,8 @@ extern "C" {
 #define ORC_F16 1
 #define ORC_Q4_0 2
 #define ORC_Q4_1 3
+#define ORC_Q5_0 6
+#define ORC_Q5_1 7
 #define ORC_Q8_0 8
 #define ORC_BF16 30
 
@@ -45,6 +47,10 @@ extern "C" {
 #define ORC_BLOCK_Q4_0_BYTES 18 /* types.rs:15-22: repr(C) {u16 d; u8 qs[16]} */
 #define ORC_QK4_1 32          /* types.rs:8 */
 #define ORC_BLOCK_Q4_1_BYTES 20 /* types.rs:24-32, size asserted at :249: {u16 d; u16 m; u8 qs[16]} */
+#define ORC_QK5_0 32          /* types.rs:9 */
+#define ORC_BLOCK_Q5_0_BYTES 22 /* ggml block_q5_0: {u16 d; u8 qh[4]; u8 qs[16]} (no struct in the reference) */
+#define ORC_QK5_1 32          /* types.rs:10 */
+#define ORC_BLOCK_Q5_1_BYTES 24 /* ggml block_q5_1: {u16 d; u16 m; u8 qh[4]; u8 qs[16]} */
 
 /* ---- seeded synthetic inputs (not a reference function: test plumbing) -- */
 uint64_t orc_splitmix64(uint64_t* state);
@@ -120,6 +126,24 @@ void orc_dequantize_row_q4_0(const uint8_t* y, size_t n, float* x);
 int orc_quantize_row_q4_1(const float* x, size_t n, uint8_t* y);
 void orc_dequantize_row_q4_1(const uint8_t* y, size_t n, float* x);
 
+/* ---- Q5_0 / Q5_1 ----------------------------------------------------------- */
+/* The reference names the types (QuantType::Q5_0 = 6, Q5_1 = 7, types.rs:
+ * 116-117; KV cache formats in tools/bench.rs:66-68, 188-203) and their
+ * group size (types.rs:9-10) but has no block struct and no code for them.
+ * Restated from ggml (ggml-quants.c, not vendored).  A 5-bit value of
+ * element e of a group is its nibble (low nibble of qs[e] for e < 16, high
+ * nibble of qs[e - 16] otherwise) plus 16 x bit e of the little-endian u32
+ * qh.  quantize_row_q5_0_ref: max = the first element of largest magnitude,
+ * d = max / -16, id = d ? 1/d : 0, q = min(31, (int8_t)(x * id + 16.5f)),
+ * value f32(d) * (q - 16).  quantize_row_q5_1_ref: min / max (strict
+ * compares), d = (max - min) / 31, id = d ? 1/d : 0, q = (uint8_t)((x -
+ * min) * id + 0.5f) (no clamp), value f32(d) * q + f32(m), product and sum
+ * rounded separately.  d and m = min stored as fp16 (RNE). */
+int orc_quantize_row_q5_0(const float* x, size_t n, uint8_t* y);
+void orc_dequantize_row_q5_0(const uint8_t* y, size_t n, float* x);
+int orc_quantize_row_q5_1(const float* x, size_t n, uint8_t* y);
+void orc_dequantize_row_q5_1(const uint8_t* y, size_t n, float* x);
+
 /* ---- RoPE (src/backend/arm/rope.rs:6-44) -------------------------------- */
 /* out = x rotated pairwise: for each head row of head_dim floats and each
  * even i < n_dims, theta = (float)pos * powf(freq_base, -(float)i / n_dims),
@@ -147,7 +171,9 @@ int orc_backend_flash_attention(const float* q, const float* k, const float* v,
  * block_size*head_dim/32 fp16 scales (slot-major).  Q4_0 likewise:
  * block_size*head_dim/2 bytes of nibbles (each 32-group's 16 bytes in
  * BlockQ4_0 order), then block_size*head_dim/32 fp16 scales.  Q4_1: the
- * nibbles, then per token and group the fp16 pair (d, m). */
+ * nibbles, then per token and group the fp16 pair (d, m).  Q5_0 / Q5_1:
+ * the nibbles, then per token a side row of head_dim/32 u32 qh words
+ * followed by head_dim/32 fp16 d (Q5_0) or (d, m) pairs (Q5_1). */
 typedef struct {
   int64_t num_blocks;
   int32_t block_size;

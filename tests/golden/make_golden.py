@@ -8,6 +8,8 @@ Fixtures:
   q4_cases.json           explicit Q4_0 / Q4_1 inputs/records (ggml's quantisers,
                           which the reference does not carry): hand-worked
                           groups, equal magnitudes, -0, NaN, inf
+  q5_cases.json           the same for Q5_0 / Q5_1, plus groups that use every
+                          5-bit value and the clamp of Q5_0's +16 end
   manifest.json           seeds, shapes and SHA-256 digests of larger results
 """
 import hashlib
@@ -93,6 +95,39 @@ def q4_cases():
     return out
 
 
+def q5_cases():
+    cases = []
+    x = np.zeros(32, np.float32)
+    vals = {0: 3.0, 1: -3.0, 2: 2.5, 3: -2.5, 4: 0.49, 5: 16.0, 6: 0.51, 7: 15.9, 8: -15.9, 20: -16.0, 21: 1.0}
+    for i, v in vals.items():
+        x[i] = v
+    cases.append(("hand_d_minus_1", x))
+    e = np.zeros(32, np.float32)
+    e[[2, 7]] = [-4.0, 4.0]
+    cases.append(("equal_magnitudes", e))
+    cases.append(("zeros", np.zeros(32, np.float32)))
+    cases.append(("neg_zeros", -np.zeros(32, np.float32)))
+    r = np.arange(32, dtype=np.float32)
+    cases.append(("ramp_0_31", r))
+    m = r.copy()
+    m[16:24] = [7.4, 7.5, 7.6, 0.49, 0.5, 30.5, 30.51, 3.0]
+    cases.append(("ramp_ties", m))
+    y = np.linspace(-1, 2, 32).astype(np.float32)
+    y[5] = np.nan
+    cases.append(("nan_ignored", y))
+    z = y.copy()
+    z[9] = -np.inf
+    cases.append(("inf", z))
+    cases.append(("normal", orc.normal(48, 32)))
+    cases.append(("tiny", orc.normal(49, 32) * np.float32(1e-30)))
+    out = []
+    for name, a in cases:
+        out.append({"name": name, "x_bits": [int(u) for u in a.view(np.uint32)],
+                    "q5_0": [int(b) for b in orc.quantize_row_q5_0(a)[0]],
+                    "q5_1": [int(b) for b in orc.quantize_row_q5_1(a)[0]]})
+    return out
+
+
 def c4_log(n_steps=2768):
     cap, bs, W, start = 16512, 16, 4096, 30000
     pool = orc.Pool(cap, order=orc.permutation(4, cap))
@@ -115,6 +150,8 @@ def main():
         json.dump(q8_cases(), f, indent=0)
     with open(os.path.join(HERE, "q4_cases.json"), "w") as f:
         json.dump(q4_cases(), f, indent=0)
+    with open(os.path.join(HERE, "q5_cases.json"), "w") as f:
+        json.dump(q5_cases(), f, indent=0)
     slots, evs, tables = c4_log()
     x = orc.normal(20, 32 * 4096)
     u = orc.uniform_i32(20 ^ 0x5A5A, 0, 99, x.size)
@@ -128,6 +165,8 @@ def main():
         "q8_0_outliers": {"seed": 20, "n": int(x.size), "records_sha256": sha(orc.quantize_row_q8_0(x))},
         "q4_0_outliers": {"seed": 20, "n": int(x.size), "records_sha256": sha(orc.quantize_row_q4_0(x))},
         "q4_1_outliers": {"seed": 20, "n": int(x.size), "records_sha256": sha(orc.quantize_row_q4_1(x))},
+        "q5_0_outliers": {"seed": 20, "n": int(x.size), "records_sha256": sha(orc.quantize_row_q5_0(x))},
+        "q5_1_outliers": {"seed": 20, "n": int(x.size), "records_sha256": sha(orc.quantize_row_q5_1(x))},
     }
     with open(os.path.join(HERE, "manifest.json"), "w") as f:
         json.dump(manifest, f, indent=1)

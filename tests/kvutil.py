@@ -94,12 +94,8 @@ def exact_decode(ref, q, hq: int, tables, ctx, start, scale: float, with_mag: bo
 
     def rows(g, b):
         raw = g[int(cu[b]) * hkv * rb:(int(cu[b]) + int(n[b])) * hkv * rb].reshape(hkv, int(n[b]), rb)
-        if dt == orc.Q8_0:
-            return orc.dequantize_row_q8_0(raw).reshape(hkv, int(n[b]), D)
-        if dt == orc.Q4_0:
-            return orc.dequantize_row_q4_0(raw).reshape(hkv, int(n[b]), D)
-        if dt == orc.Q4_1:
-            return orc.dequantize_row_q4_1(raw).reshape(hkv, int(n[b]), D)
+        if dt in orc.QUANT_TYPES:
+            return orc.dequantize_records(raw, dt).reshape(hkv, int(n[b]), D)
         if dt == orc.F32:
             return raw.view(np.float32).reshape(hkv, int(n[b]), D)
         return widen(raw.view(np.uint16), dt).reshape(hkv, int(n[b]), D)

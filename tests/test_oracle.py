@@ -324,6 +324,172 @@ def test_oracle_q4_1_gather_records_equal_quantize_row(orc):
             assert bytes(rv[h, t]) == bytes(orc.quantize_row_q4_1(-x[t, h]))
 
 
+# ---------------- Q5_0 / Q5_1 ----------------------------------------------
+# The reference names the types (types.rs:116-117) and their group size
+# (types.rs:9-10) and has no code for them; blocks, quantisers and
+# dequantisers follow ggml and are pinned by hand-worked cases, special
+# values and round-trip bounds.
+def _u16(rec, i):
+    return int(rec[0, i]) | (int(rec[0, i + 1]) << 8)
+
+
+def _q5_values(rec, off):
+    """5-bit values of one record from its bytes: qh at off, qs at off + 4;
+    element e < 16 in the low nibble of qs[e], e >= 16 in the high nibble of
+    qs[e - 16], bit 4 from bit e of the little-endian qh."""
+    qh = int.from_bytes(bytes(rec[0, off:off + 4]), "little")
+    qs = rec[0, off + 4:off + 20]
+    nib = np.concatenate([qs & 0xF, qs >> 4]).astype(np.int64)
+    return nib | (((qh >> np.arange(32)) & 1) << 4)
+
+
+def test_q5_0_dequant_layout(orc):
+    rec = np.zeros((1, 22), np.uint8)
+    rec[0, :2] = np.frombuffer(np.float16(0.1).tobytes(), np.uint8)
+    rec[0, 2:6] = [0xFF, 0xFF, 0xFF, 0xFF]  # every bit 4 set, nibbles 0: value 16 - 16 = 0
+    assert np.all(orc.dequantize_row_q5_0(rec) == 0)
+    rec[0, 2:6] = [0x55, 0x55, 0x0F, 0xF0]  # qh = 0xF00F5555: bits 0, 2, .., 14, 16-19, 28-31
+    rec[0, 6:] = [j | ((15 - j) << 4) for j in range(16)]
+    d = np.float32(np.float16(0.1))
+    want = np.empty(32, np.float32)
+    for j in range(16):
+        want[j] = d * np.float32(j + (16 if j % 2 == 0 else 0) - 16)
+        hb = 16 if (j < 4 or j >= 12) else 0  # bit 16 + j of 0xF00F5555
+        want[16 + j] = d * np.float32((15 - j) + hb - 16)
+    np.testing.assert_array_equal(orc.dequantize_row_q5_0(rec), want)
+
+
+def test_q5_0_hand_worked_group(orc):
+    # max = 16.0 (index 5; the -16.0 at index 20 has the same magnitude and
+    # comes later): d = -1, id = -1, q = min(31, trunc(16.5 - x)).
+    x = np.zeros(32, np.float32)
+    vals = {0: 3.0, 1: -3.0, 2: 2.5, 3: -2.5, 4: 0.49, 5: 16.0, 6: 0.51, 7: 15.9, 8: -15.9, 20: -16.0, 21: 1.0}
+    for i, v in vals.items():
+        x[i] = v
+    rec = orc.quantize_row_q5_0(x)
+    assert rec.shape == (1, 22) and _u16(rec, 0) == _f16_bits(-1.0)
+    want = np.full(32, 16)
+    for i, q in {0: 13, 1: 19, 2: 14, 3: 19, 4: 16, 5: 0, 6: 15, 7: 0, 8: 31, 20: 31, 21: 15}.items():
+        want[i] = q  # 16.5 + 15.9 = 32.4 and 16.5 + 16 = 32.5 clamp to 31
+    np.testing.assert_array_equal(_q5_values(rec, 2), want)
+    # qh bit e is set exactly where q >= 16; with these q: everything except 0, 2, 5, 6, 7, 21
+    qh = int.from_bytes(bytes(rec[0, 2:6]), "little")
+    assert qh == 0xFFFFFFFF & ~((1 << 0) | (1 << 2) | (1 << 5) | (1 << 6) | (1 << 7) | (1 << 21))
+    np.testing.assert_array_equal(orc.dequantize_row_q5_0(rec), (want - 16).astype(np.float32) * np.float32(-1.0))
+
+
+def test_q5_0_first_of_equal_magnitudes_zero_nan_inf(orc):
+    x = np.zeros(32, np.float32)
+    x[2], x[7] = -4.0, 4.0  # max = -4: d = 0.25, id = 4: -4 -> 0, 4 -> 32 -> 31
+    rec = orc.quantize_row_q5_0(x)
+    assert _u16(rec, 0) == _f16_bits(0.25)
+    q = _q5_values(rec, 2)
+    assert q[2] == 0 and q[7] == 31 and np.all(np.delete(q, [2, 7]) == 16)
+    for z in (np.zeros(32, np.float32), -np.zeros(32, np.float32)):  # d = 0, id = 0: q = 16
+        rec = orc.quantize_row_q5_0(z)
+        assert _u16(rec, 0) & 0x7FFF == 0 and np.all(_q5_values(rec, 2) == 16)
+    y = np.linspace(-1, 1, 32).astype(np.float32)
+    y[3] = np.nan  # never the max; trunc(NaN) -> 0
+    rec = orc.quantize_row_q5_0(y)
+    assert _u16(rec, 0) == _f16_bits(0.0625) and _q5_values(rec, 2)[3] == 0
+    y[3] = -np.inf  # d = inf, id = 0: finite x -> 16; the inf element -> NaN -> 0
+    rec = orc.quantize_row_q5_0(y)
+    q = _q5_values(rec, 2)
+    assert _u16(rec, 0) == 0x7C00 and q[3] == 0 and np.all(np.delete(q, 3) == 16)
+
+
+def test_q5_0_round_trip_bound(orc):
+    x = orc.normal(24, 32 * 2048)
+    rng = np.random.default_rng(3)
+    x[rng.random(x.size) < 0.01] *= 8
+    x[:32] *= 1e-3
+    x[32:64] *= 3e3
+    rec = orc.quantize_row_q5_0(x)
+    deq = orc.dequantize_row_q5_0(rec).reshape(-1, 32)
+    xg = x.reshape(-1, 32)
+    d = np.abs(_q4_d(rec).astype(np.float32))[:, None]
+    err = np.abs(deq - xg)
+    # round half up onto d * (-16..15): at most d / 2, except the +16 end
+    # (clamped to 15) at most d; slack for the fp16 rounding of d (2^-11
+    # relative, times 16 steps)
+    assert np.all(err <= d * (1 + 16 * 2 ** -10) + 1e-30)
+    inner = np.abs(xg) < 15.5 * d
+    assert np.all(err[inner] <= (d * 0.5 * (1 + 32 * 2 ** -10))[np.nonzero(inner)[0]].ravel() + 1e-30)
+    imax = np.argmax(np.abs(xg), axis=1)  # comes back as -16 d
+    np.testing.assert_array_equal(deq[np.arange(len(xg)), imax], -16 * _q4_d(rec).astype(np.float32))
+    # every value is d times an integer in [-16, 15]
+    dd = _q4_d(rec).astype(np.float32)[:, None]
+    k = deq / np.where(dd == 0, 1, dd)
+    assert np.all(k == np.round(k)) and k.min() >= -16 and k.max() <= 15
+
+
+def test_q5_1_hand_worked_groups(orc):
+    r = np.arange(32, dtype=np.float32)  # min 0, max 31: d = 1, id = 1, q = trunc(x + 0.5) = x
+    rec = orc.quantize_row_q5_1(r)
+    assert rec.shape == (1, 24) and _u16(rec, 0) == _f16_bits(1.0) and _u16(rec, 2) == _f16_bits(0.0)
+    assert bytes(rec[0, 4:8]) == b"\x00\x00\xff\xff"  # elements 16..31 have bit 4
+    assert np.all(rec[0, 8:] == [j | (j << 4) for j in range(16)])
+    np.testing.assert_array_equal(orc.dequantize_row_q5_1(rec), r)
+    m = r.copy()
+    m[16:24] = [7.4, 7.5, 7.6, 0.49, 0.5, 30.5, 30.51, 3.0]
+    rec = orc.quantize_row_q5_1(m)
+    want = np.arange(32)
+    want[16:24] = [7, 8, 8, 0, 1, 31, 31, 3]  # round half up
+    np.testing.assert_array_equal(_q5_values(rec, 4), want)
+    np.testing.assert_array_equal(orc.dequantize_row_q5_1(rec), want.astype(np.float32))
+
+
+def test_q5_1_offset_nan_zero(orc):
+    x = np.linspace(-1, 2, 32).astype(np.float32)  # d = 3/31, m = -1
+    x[5] = np.nan  # never the min or the max; trunc(NaN) -> 0
+    rec = orc.quantize_row_q5_1(x)
+    d32 = np.float32(3.0) / np.float32(31.0)
+    assert _u16(rec, 0) == _f16_bits(d32) and _u16(rec, 2) == _f16_bits(-1.0)
+    q = _q5_values(rec, 4)
+    assert q[5] == 0 and q[0] == 0 and q[31] == 31
+    d = np.float32(np.float16(d32))
+    np.testing.assert_array_equal(orc.dequantize_row_q5_1(rec), d * q.astype(np.float32) + np.float32(-1.0))
+    rec = orc.quantize_row_q5_1(np.full(32, 2.5, np.float32))  # constant: d = 0, every q 0, value m
+    assert _u16(rec, 0) == 0 and np.all(_q5_values(rec, 4) == 0)
+    assert np.all(orc.dequantize_row_q5_1(rec) == 2.5)
+
+
+def test_q5_1_round_trip_bound(orc):
+    x = orc.normal(25, 32 * 2048)
+    rng = np.random.default_rng(4)
+    x[rng.random(x.size) < 0.01] *= 8
+    x[:32] += 5.0  # all-positive group: m far from 0
+    rec = orc.quantize_row_q5_1(x)
+    deq = orc.dequantize_row_q5_1(rec).reshape(-1, 32)
+    xg = x.reshape(-1, 32)
+    d = (rec[:, 0].astype(np.uint16) | (rec[:, 1].astype(np.uint16) << 8)).view(np.float16).astype(np.float32)
+    m = (rec[:, 2].astype(np.uint16) | (rec[:, 3].astype(np.uint16) << 8)).view(np.float16).astype(np.float32)
+    # round half up onto min + d * (0..31), then the fp16 rounding of d (31
+    # steps) and of m move the grid by at most 31 |d| 2^-11 + |m| 2^-11
+    bound = d * 0.5 + (31 * d + np.abs(m)) * 2.0 ** -11 * 1.01 + 1e-30
+    assert np.all(np.abs(deq - xg) <= bound[:, None])
+
+
+@pytest.mark.parametrize("dt", ["Q5_0", "Q5_1"])
+def test_oracle_q5_gather_records_equal_quantize_row(orc, dt):
+    dtype = getattr(orc, dt)
+    quant = orc.quantize_row_q5_0 if dt == "Q5_0" else orc.quantize_row_q5_1
+    nb, bs, hkv, D = 4, 16, 2, 128
+    c = orc.Cache(nb, bs, hkv, D, dtype)
+    assert c.page_bytes == bs * (D // 2 + D // 32 * (6 if dt == "Q5_0" else 8))
+    n = nb * bs
+    x = (orc.normal(16, n * hkv * D) * np.float32(3)).reshape(n, hkv, D)
+    c.append(x, -x, np.arange(n, dtype=np.int64))
+    tables = np.arange(nb, dtype=np.int32)[None, :]
+    gk, gv = c.gather(tables, np.array([n], np.int32), None, np.array([0], np.int64), n)
+    rb = orc.RECORD_BYTES[dtype]
+    rk, rv = gk.reshape(hkv, n, D // 32 * rb), gv.reshape(hkv, n, D // 32 * rb)
+    for h in range(hkv):
+        for t in (0, 1, 37, n - 1):
+            assert bytes(rk[h, t]) == bytes(quant(x[t, h]))
+            assert bytes(rv[h, t]) == bytes(quant(-x[t, h]))
+
+
 def test_exact_decode_helper_and_closer_check(orc):
     """The float64 tie-break the GPU decode tests use for fp32 tolerance:
     exact_decode agrees with the oracle's decode, and a result perturbed by
@@ -384,6 +550,9 @@ def test_golden_quant_cases(orc):
     for case in json.load(open(os.path.join(GOLDEN, "q4_cases.json"))):
         assert list(orc.quantize_row_q4_0(_golden_x(case))[0]) == case["q4_0"], case["name"]
         assert list(orc.quantize_row_q4_1(_golden_x(case))[0]) == case["q4_1"], case["name"]
+    for case in json.load(open(os.path.join(GOLDEN, "q5_cases.json"))):
+        assert list(orc.quantize_row_q5_0(_golden_x(case))[0]) == case["q5_0"], case["name"]
+        assert list(orc.quantize_row_q5_1(_golden_x(case))[0]) == case["q5_1"], case["name"]
 
 
 def test_golden_digests(orc):
@@ -401,6 +570,8 @@ def test_golden_digests(orc):
     assert sha(orc.quantize_row_q8_0(x)) == man["q8_0_outliers"]["records_sha256"]
     assert sha(orc.quantize_row_q4_0(x)) == man["q4_0_outliers"]["records_sha256"]
     assert sha(orc.quantize_row_q4_1(x)) == man["q4_1_outliers"]["records_sha256"]
+    assert sha(orc.quantize_row_q5_0(x)) == man["q5_0_outliers"]["records_sha256"]
+    assert sha(orc.quantize_row_q5_1(x)) == man["q5_1_outliers"]["records_sha256"]
     c1 = man["config1"]
     k = orc.normal(c1["seeds"]["k"], 1024 * 2 * 128).reshape(1024, 2, 128)
     v = orc.normal(c1["seeds"]["v"], 1024 * 2 * 128).reshape(1024, 2, 128)
@@ -640,6 +811,28 @@ def test_oracle_paged_decode_gqa_window_vs_float64(orc):
             K = np.stack([kf[tables[b, p // bs], kvh, p % bs] for p in rows])
             V = np.stack([vf[tables[b, p // bs], kvh, p % bs] for p in rows])
             np.testing.assert_allclose(got[b, h], _softmax_av(q[b, h], K, V, scale), rtol=2e-5, atol=2e-6)
+
+
+@pytest.mark.parametrize("dt", ["Q5_0", "Q5_1", "Q4_1"])
+def test_oracle_quant_decode_reads_the_dequantised_rows(orc, dt):
+    """The oracle's decode over a quantised cache attends over exactly the
+    dequantised records its gather returns (float64 softmax of those rows)."""
+    dtype = getattr(orc, dt)
+    nb, bs, hkv, hq, D = 8, 16, 2, 4, 64
+    c = orc.Cache(nb, bs, hkv, D, dtype)
+    n = nb * bs
+    c.append(orc.normal(40, n * hkv * D).reshape(n, hkv, D), orc.normal(41, n * hkv * D).reshape(n, hkv, D),
+             np.arange(n, dtype=np.int64))
+    tables = orc.permutation(42, nb).astype(np.int32)[None, :]
+    ctx = np.array([101], np.int32)
+    q = orc.normal(43, hq * D).reshape(1, hq, D)
+    got = c.decode(q, hq, tables, ctx, None, 0.125)
+    gk, gv = c.gather(tables, ctx, None, np.array([0], np.int64), 101)
+    K = orc.dequantize_records(gk, dtype).reshape(hkv, 101, D)
+    V = orc.dequantize_records(gv, dtype).reshape(hkv, 101, D)
+    for h in range(hq):
+        np.testing.assert_allclose(got[0, h], _softmax_av(q[0, h], K[h * hkv // hq], V[h * hkv // hq], 0.125),
+                                   rtol=2e-5, atol=2e-6)
 
 
 @pytest.mark.parametrize("causal", [True, False])
