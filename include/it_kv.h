@@ -39,6 +39,8 @@ extern "C" {
 #define IT_F16 1
 #define IT_Q4_0 2
 #define IT_Q4_1 3
+#define IT_Q5_0 6
+#define IT_Q5_1 7
 #define IT_Q8_0 8
 #define IT_BF16 30
 
@@ -49,6 +51,11 @@ extern "C" {
 #define IT_BLOCK_Q4_0_BYTES 18  /* sizeof(BlockQ4_0), src/types.rs:15-22 */
 #define IT_QK4_1 32             /* src/types.rs:8 */
 #define IT_BLOCK_Q4_1_BYTES 20  /* sizeof(BlockQ4_1), src/types.rs:24-32,249 */
+#define IT_QK5_0 32             /* src/types.rs:9 */
+#define IT_BLOCK_Q5_0_BYTES 22  /* ggml block_q5_0 {u16 d; u8 qh[4]; u8 qs[16]}: the reference has the
+                                   type id (types.rs:116) and no struct */
+#define IT_QK5_1 32             /* src/types.rs:10 */
+#define IT_BLOCK_Q5_1_BYTES 24  /* ggml block_q5_1 {u16 d; u16 m; u8 qh[4]; u8 qs[16]} (types.rs:117) */
 
 /* ---- operator ids for it_supports (Backend::supports_op/_quant,
  *      src/backend.rs:184-186) ------------------------------------------- */
@@ -157,6 +164,10 @@ int32_t it_kv_manager_tables(const it_kv_manager* mgr, int32_t* tables, int32_t 
 /*   d[block_size][head_dim/32] (src/types.rs:15-22).                        */
 /*   Q4_1 page: the Q4_0 nibble plane, then fp16 (d, m) pairs                */
 /*   [block_size][head_dim/32] (BlockQ4_1, src/types.rs:24-32).              */
+/*   Q5_0 / Q5_1 page: the Q4_0 nibble plane (the low four bits of each      */
+/*   5-bit value), then per token a side row: head_dim/32 u32 qh words (bit  */
+/*   e = bit 4 of element e, as ggml's block_q5_*), then head_dim/32 fp16 d  */
+/*   (Q5_0) or (d, m) pairs (Q5_1).                                          */
 /* ======================================================================== */
 typedef struct it_kv_cache it_kv_cache;
 
@@ -199,7 +210,9 @@ int32_t it_kv_cache_check(it_kv_cache* cache, void* stream);
  * F32 and quantises as ggml's quantize_row_q4_0_ref (the reference has the
  * block and its dequantisation, vec_dot.rs:425-440, but no quantiser).  A
  * Q4_1 cache takes F32 and quantises as ggml's quantize_row_q4_1_ref (the
- * reference has only the block). */
+ * reference has only the block).  Q5_0 / Q5_1 caches take F32 and quantise
+ * as ggml's quantize_row_q5_0_ref / quantize_row_q5_1_ref (the reference has
+ * only the type ids, types.rs:116-117). */
 int32_t it_kv_append(it_kv_cache* cache, const void* k, const void* v, int32_t src_dtype,
                      const int64_t* slot_mapping, int32_t n_tokens, void* stream);
 
@@ -217,8 +230,8 @@ int32_t it_kv_append(it_kv_cache* cache, const void* k, const void* v, int32_t s
  *   q_out: [n_tokens][n_heads][head_dim] of q_out_dtype: F32, or the cache
  *          dtype for BF16/F16 caches (round to nearest even)
  * F32 caches store the rotated fp32 values; BF16/F16 caches round them to
- * nearest even; Q8_0 / Q4_0 / Q4_1 caches quantise them as it_kv_append
- * does. */
+ * nearest even; Q8_0 / Q4_0 / Q4_1 / Q5_0 / Q5_1 caches quantise them as
+ * it_kv_append does. */
 typedef struct it_rope_table it_rope_table;
 /* n_dims: a multiple of 4 up to 4096; positions [0, max_pos); device memory
  * max_pos * n_dims * 4 bytes. */
@@ -239,7 +252,8 @@ int32_t it_kv_append_rope(it_kv_cache* cache, const it_rope_table* rope, const f
  * Output for sequence b: [n_kv_heads][ctx_b - start_b][head_dim] at token
  * offset cu_out[b] (element offset cu_out[b]*n_kv_heads*head_dim).  A Q8_0
  * cache writes packed 34-byte BlockQ8_0 records, head_dim/32 per row; a Q4_0
- * cache 18-byte BlockQ4_0 records, a Q4_1 cache 20-byte BlockQ4_1 ones. */
+ * cache 18-byte BlockQ4_0 records, a Q4_1 cache 20-byte BlockQ4_1 ones, Q5_0
+ * and Q5_1 caches 22- and 24-byte ggml block_q5_0 / block_q5_1 records. */
 int32_t it_kv_gather(const it_kv_cache* cache, const int32_t* block_tables, int32_t max_blocks,
                      const int32_t* ctx_lens, const int32_t* start_pos, const int64_t* cu_out,
                      int32_t n_seqs, int32_t max_tokens, void* k_out, void* v_out, void* stream);
@@ -291,7 +305,7 @@ int32_t it_paged_decode_partition(int32_t dtype, int32_t head_dim, int32_t block
  * and query head h the result equals flash_attn_f32 (flash_attn.rs:6-72)
  * over keys start_b..ctx_b-1 of KV head h*Hkv/Hq (forward.rs:231-254),
  * within fp32 tolerance.
- *   q: [n_seqs][n_heads][head_dim]; q_dtype F32 (F32, Q8_0, Q4_0, Q4_1 caches),
+ *   q: [n_seqs][n_heads][head_dim]; q_dtype F32 (F32 and quantised caches),
  *      BF16 (BF16 cache) or F16 (F16 cache)
  *   block_tables/ctx_lens/start_pos: as it_kv_gather
  *   max_tokens: upper bound of ctx_b - start_b

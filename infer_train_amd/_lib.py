@@ -15,7 +15,7 @@ LIB_PATH = os.path.join(_HERE, "libit_kv.so")
 # Status codes and dtype ids (include/it_kv.h; OpError src/types.rs:227-231,
 # QuantType src/types.rs:106-144).
 OK, NOT_IMPLEMENTED, INVALID_INPUT, DEVICE_ERROR = 0, 1, 2, 3
-F32, F16, Q4_0, Q4_1, Q8_0, BF16 = 0, 1, 2, 3, 8, 30
+F32, F16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, BF16 = 0, 1, 2, 3, 6, 7, 8, 30
 BLOCK_SIZE = 16
 QK8_0 = 32
 BLOCK_Q8_0_BYTES = 34
@@ -23,6 +23,10 @@ QK4_0 = 32
 BLOCK_Q4_0_BYTES = 18
 QK4_1 = 32
 BLOCK_Q4_1_BYTES = 20
+QK5_0 = QK5_1 = 32
+BLOCK_Q5_0_BYTES = 22  # ggml block_q5_0 (types.rs:116 has only the id)
+BLOCK_Q5_1_BYTES = 24  # ggml block_q5_1 (types.rs:117)
+QUANT_TYPES = (Q8_0, Q4_0, Q4_1, Q5_0, Q5_1)
 OP_KV_APPEND, OP_KV_GATHER, OP_KV_EVICT, OP_PAGED_DECODE, OP_PAGED_PREFILL, OP_FLASH_ATTENTION, OP_KV_COPY_BLOCKS = range(1, 8)
 
 

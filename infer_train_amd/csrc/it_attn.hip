@@ -43,6 +43,8 @@ hipError_t launch_split(int32_t dt, int d, int gc, const DecodeArgs& a, dim3 gri
     case IT_Q8_0: return launch_decode_q8_0(d, gc, a, grid, s);
     case IT_Q4_0: return launch_decode_q4_0(d, gc, a, grid, s);
     case IT_Q4_1: return launch_decode_q4_1(d, gc, a, grid, s);
+    case IT_Q5_0: return launch_decode_q5_0(d, gc, a, grid, s);
+    case IT_Q5_1: return launch_decode_q5_1(d, gc, a, grid, s);
     default: return hipErrorInvalidValue;
   }
 }

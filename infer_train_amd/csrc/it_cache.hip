@@ -1,5 +1,5 @@
 // it_cache.hip -- the paged KV cache on gfx950: pool allocation, slot-mapped
-// append (bit copy, Q8_0 or Q4_0 quantise), block-table gather, evict (page clear)
+// append (bit copy, or quantise to Q8_0 / Q4_0 / Q4_1 / Q5_0 / Q5_1), block-table gather, evict (page clear)
 // and copy-on-write page copy.
 //
 // All of these are HBM-bound data movement.  Each lane moves one 16-byte
@@ -79,7 +79,7 @@ __global__ __launch_bounds__(kThreads) void kv_append_copy(
 }
 
 // ---------------------------------------------------------------------------
-// Append with quantisation (Q8_0, Q4_0, Q4_1: the quantisers of
+// Append with quantisation (Q8_0, Q4_0, Q4_1, Q5_0, Q5_1: the quantisers of
 // it_quant.hpp).  Eight lanes own one 32-element group, four floats each (one
 // 16-byte load); blockIdx.y selects K (0) or V (1).
 // ---------------------------------------------------------------------------
@@ -203,13 +203,19 @@ __global__ __launch_bounds__(kThreads) void kv_gather_q8_0(
   }
 }
 
-// Q4_0 gather: lane = one 32-element group, written as a packed 18-byte
-// BlockQ4_0 record {u16 d; u8 qs[16]} (types.rs:15-22).
-__global__ __launch_bounds__(kThreads) void kv_gather_q4_0(
+// Q4_0 / Q4_1 / Q5_0 / Q5_1 gather: lane = one 32-element group, written as
+// a packed ggml record {meta; [qh;] qs[16]}: BlockQ4_0 {u16 d} (18 bytes,
+// types.rs:15-22), BlockQ4_1 {u16 d; u16 m} (20, types.rs:24-32),
+// block_q5_0 {u16 d; u8 qh[4]} (22) and block_q5_1 {u16 d; u16 m; u8
+// qh[4]} (24).  Records of 18 and 22 bytes are 2-byte aligned, so the
+// stores are 16-bit.
+template <int DT>
+__global__ __launch_bounds__(kThreads) void kv_gather_nib(
     const char* __restrict__ kpool, const char* __restrict__ vpool, const int32_t* __restrict__ bt,
     int max_blocks, const int32_t* __restrict__ ctx_lens, const int32_t* __restrict__ start_pos,
     const int64_t* __restrict__ cu_out, int hkv, int d, int log2_bs, int64_t page_bytes,
     int64_t num_blocks, char* __restrict__ kout, char* __restrict__ vout, uint32_t* err) {
+  using N = NibFmt<DT>;
   const int b = blockIdx.y;
   const int st = start_pos ? start_pos[b] : 0;
   const int n = ctx_lens[b] - st;
@@ -238,68 +244,34 @@ __global__ __launch_bounds__(kThreads) void kv_gather_q4_0(
   }
   const int64_t bs = int64_t(1) << log2_bs;
   const int64_t off = pos & (bs - 1);
-  const int64_t rec = ((cu_out[b] * hkv + int64_t(h) * n + i) * ng + g) * 18;
+  const int64_t rec = ((cu_out[b] * hkv + int64_t(h) * n + i) * ng + g) * N::kRecord;
   for (int which = 0; which < 2; ++which) {
     const char* page = (which ? vpool : kpool) + (int64_t(blk) * hkv + h) * page_bytes;
     const uint4 q = ld16(page + off * (d >> 1) + g * 16);
-    const uint16_t dd = *reinterpret_cast<const uint16_t*>(page + bs * (d >> 1) + (off * ng + g) * 2);
-    uint16_t* o = reinterpret_cast<uint16_t*>((which ? vout : kout) + rec);  // 2-byte aligned
-    o[0] = dd;
-    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+    const char* side = page + bs * (d >> 1) + off * (ng * N::kSide);
+    uint16_t w[N::kRecord / 2];
+    int k = 0;
+    if constexpr (N::kMin) {
+      const uint32_t dm = *reinterpret_cast<const uint32_t*>(side + N::meta_off(ng) + 4 * g);
+      w[k++] = uint16_t(dm & 0xFFFFu);
+      w[k++] = uint16_t(dm >> 16);
+    } else {
+      w[k++] = *reinterpret_cast<const uint16_t*>(side + N::meta_off(ng) + 2 * g);
+    }
+    if constexpr (N::kQ5) {
+      const uint32_t qh = *reinterpret_cast<const uint32_t*>(side + 4 * g);
+      w[k++] = uint16_t(qh & 0xFFFFu);
+      w[k++] = uint16_t(qh >> 16);
+    }
+    const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      o[1 + 2 * j] = uint16_t(w[j] & 0xFFFFu);
-      o[2 + 2 * j] = uint16_t(w[j] >> 16);
+      w[k++] = uint16_t(qw[j] & 0xFFFFu);
+      w[k++] = uint16_t(qw[j] >> 16);
     }
-  }
-}
-
-// Q4_1 gather: lane = one 32-element group, written as a packed 20-byte
-// BlockQ4_1 record {u16 d; u16 m; u8 qs[16]} (types.rs:24-32).
-__global__ __launch_bounds__(kThreads) void kv_gather_q4_1(
-    const char* __restrict__ kpool, const char* __restrict__ vpool, const int32_t* __restrict__ bt,
-    int max_blocks, const int32_t* __restrict__ ctx_lens, const int32_t* __restrict__ start_pos,
-    const int64_t* __restrict__ cu_out, int hkv, int d, int log2_bs, int64_t page_bytes,
-    int64_t num_blocks, char* __restrict__ kout, char* __restrict__ vout, uint32_t* err) {
-  const int b = blockIdx.y;
-  const int st = start_pos ? start_pos[b] : 0;
-  const int n = ctx_lens[b] - st;
-  if (st < 0) {  // skipped and latched
-    if (blockIdx.x == 0 && threadIdx.x == 0) atomicOr(err, kErrStart);
-    return;
-  }
-  if (n <= 0) return;
-  const int ng = d >> 5;
-  const int64_t gid = int64_t(blockIdx.x) * kThreads + threadIdx.x;
-  if (gid >= int64_t(hkv) * n * ng) return;
-  const int g = int(gid % ng);
-  const int64_t r = gid / ng;
-  const int i = int(r % n);
-  const int h = int(r / n);
-  const int pos = st + i;
-  const int lb = pos >> log2_bs;
-  if (lb >= max_blocks) {
-    atomicOr(err, kErrTable);
-    return;
-  }
-  const int blk = bt[int64_t(b) * max_blocks + lb];
-  if (blk < 0 || blk >= num_blocks) {
-    atomicOr(err, kErrBlock);
-    return;
-  }
-  const int64_t bs = int64_t(1) << log2_bs;
-  const int64_t off = pos & (bs - 1);
-  const int64_t rec = ((cu_out[b] * hkv + int64_t(h) * n + i) * ng + g) * 20;
-  for (int which = 0; which < 2; ++which) {
-    const char* page = (which ? vpool : kpool) + (int64_t(blk) * hkv + h) * page_bytes;
-    const uint4 q = ld16(page + off * (d >> 1) + g * 16);
-    const uint32_t dm = *reinterpret_cast<const uint32_t*>(page + bs * (d >> 1) + (off * ng + g) * 4);
-    uint32_t* o = reinterpret_cast<uint32_t*>((which ? vout : kout) + rec);  // 4-byte aligned
-    o[0] = dm;
-    o[1] = q.x;
-    o[2] = q.y;
-    o[3] = q.z;
-    o[4] = q.w;
+    uint16_t* o = reinterpret_cast<uint16_t*>((which ? vout : kout) + rec);
+#pragma unroll
+    for (int j = 0; j < N::kRecord / 2; ++j) o[j] = w[j];
   }
 }
 
@@ -371,12 +343,13 @@ int32_t check_shape(int64_t num_blocks, int32_t block_size, int32_t n_kv_heads, 
                 (long long)num_blocks, n_kv_heads, head_dim);
   if (!is_pow2(block_size) || block_size > 1024)
     return fail(IT_NOT_IMPLEMENTED, "kv cache: block_size %d must be a power of two <= 1024", block_size);
-  if (dtype == IT_Q8_0 || dtype == IT_Q4_0 || dtype == IT_Q4_1) {
-    if (head_dim % 32) return fail(IT_INVALID_INPUT, "kv cache: Q8_0/Q4_0/Q4_1 need head_dim %% 32 == 0");
-    if (block_size < 8) return fail(IT_NOT_IMPLEMENTED, "kv cache: Q8_0/Q4_0/Q4_1 need block_size >= 8");
+  if (is_quant(dtype)) {
+    if (head_dim % 32) return fail(IT_INVALID_INPUT, "kv cache: quantised dtypes need head_dim %% 32 == 0");
+    if (block_size < 8) return fail(IT_NOT_IMPLEMENTED, "kv cache: quantised dtypes need block_size >= 8");
   } else if (dtype_bytes(dtype) == 0) {
     return fail(IT_NOT_IMPLEMENTED,
-                "kv cache: dtype %d not supported (F32=0, F16=1, Q4_0=2, Q4_1=3, Q8_0=8, BF16=30)", dtype);
+                "kv cache: dtype %d not supported (F32=0, F16=1, Q4_0=2, Q4_1=3, Q5_0=6, Q5_1=7, Q8_0=8, BF16=30)",
+                dtype);
   } else if ((head_dim * dtype_bytes(dtype)) % 16) {
     return fail(IT_NOT_IMPLEMENTED, "kv cache: head_dim*elem_bytes must be a multiple of 16");
   }
@@ -429,6 +402,8 @@ extern "C" int64_t it_kv_page_bytes(int32_t block_size, int32_t head_dim, int32_
   if (dtype == IT_Q8_0) return int64_t(block_size) * head_dim + int64_t(block_size) * (head_dim / IT_QK8_0) * 2;
   if (dtype == IT_Q4_0) return int64_t(block_size) * (head_dim / 2) + int64_t(block_size) * (head_dim / IT_QK4_0) * 2;
   if (dtype == IT_Q4_1) return int64_t(block_size) * (head_dim / 2) + int64_t(block_size) * (head_dim / IT_QK4_1) * 4;
+  if (dtype == IT_Q5_0) return int64_t(block_size) * (head_dim / 2) + int64_t(block_size) * (head_dim / IT_QK5_0) * 6;
+  if (dtype == IT_Q5_1) return int64_t(block_size) * (head_dim / 2) + int64_t(block_size) * (head_dim / IT_QK5_1) * 8;
   int64_t e = dtype_bytes(dtype);
   return e ? int64_t(block_size) * head_dim * e : -1;
 }
@@ -518,7 +493,7 @@ extern "C" int32_t it_kv_append(it_kv_cache* c, const void* k, const void* v, in
   if (n_tokens < 0) return fail(IT_INVALID_INPUT, "it_kv_append: n_tokens %d < 0", n_tokens);
   if (n_tokens == 0) return IT_OK;
   if (!k || !v || !slots) return fail(IT_INVALID_INPUT, "it_kv_append: NULL tensor");
-  const bool quant = c->dtype == IT_Q8_0 || c->dtype == IT_Q4_0 || c->dtype == IT_Q4_1;
+  const bool quant = is_quant(c->dtype);
   const int32_t want = quant ? IT_F32 : c->dtype;
   if (src_dtype != want)
     return fail(IT_NOT_IMPLEMENTED, "it_kv_append: cache dtype %d takes source dtype %d, got %d", c->dtype, want, src_dtype);
@@ -529,8 +504,11 @@ extern "C" int32_t it_kv_append(it_kv_cache* c, const void* k, const void* v, in
   if (quant) {
     const int64_t total = int64_t(n_tokens) * c->n_kv_heads * (c->head_dim / 4);
     dim3 grid(unsigned(cdiv(total, kThreads)), 2);
-    auto* kern = c->dtype == IT_Q8_0 ? kv_append_quant<IT_Q8_0>
-                 : (c->dtype == IT_Q4_0 ? kv_append_quant<IT_Q4_0> : kv_append_quant<IT_Q4_1>);
+    auto* kern = c->dtype == IT_Q8_0   ? kv_append_quant<IT_Q8_0>
+                 : c->dtype == IT_Q4_0 ? kv_append_quant<IT_Q4_0>
+                 : c->dtype == IT_Q4_1 ? kv_append_quant<IT_Q4_1>
+                 : c->dtype == IT_Q5_0 ? kv_append_quant<IT_Q5_0>
+                                       : kv_append_quant<IT_Q5_1>;
     hipLaunchKernelGGL(kern, grid, dim3(kThreads), 0, s,
                        (const float4*)k, (const float4*)v, (char*)c->k_pool, (char*)c->v_pool, slots, total,
                        c->n_kv_heads, c->head_dim, c->log2_bs, c->page_bytes, n_slots, c->err_flag);
@@ -561,10 +539,14 @@ extern "C" int32_t it_kv_gather(const it_kv_cache* c, const int32_t* bt, int32_t
   if (n_seqs > 65535) return fail(IT_NOT_IMPLEMENTED, "it_kv_gather: n_seqs %d > 65535", n_seqs);
   DeviceGuard g(c->device);
   hipStream_t s = (hipStream_t)stream;
-  if (c->dtype == IT_Q8_0 || c->dtype == IT_Q4_0 || c->dtype == IT_Q4_1) {
+  if (is_quant(c->dtype)) {
     const int64_t per_seq = int64_t(c->n_kv_heads) * max_tokens * (c->head_dim / 32);
     dim3 grid(unsigned(cdiv(per_seq, kThreads)), unsigned(n_seqs));
-    auto* kern = c->dtype == IT_Q8_0 ? kv_gather_q8_0 : (c->dtype == IT_Q4_0 ? kv_gather_q4_0 : kv_gather_q4_1);
+    auto* kern = c->dtype == IT_Q8_0   ? kv_gather_q8_0
+                 : c->dtype == IT_Q4_0 ? kv_gather_nib<IT_Q4_0>
+                 : c->dtype == IT_Q4_1 ? kv_gather_nib<IT_Q4_1>
+                 : c->dtype == IT_Q5_0 ? kv_gather_nib<IT_Q5_0>
+                                       : kv_gather_nib<IT_Q5_1>;
     hipLaunchKernelGGL(kern, grid, dim3(kThreads), 0, s,
                        (const char*)c->k_pool, (const char*)c->v_pool,
                        bt, max_blocks, ctx_lens, start_pos, cu_out, c->n_kv_heads, c->head_dim, c->log2_bs,
@@ -627,8 +609,7 @@ extern "C" int32_t it_kv_copy_blocks(it_kv_cache* c, const int32_t* src, const i
 }
 
 extern "C" int32_t it_supports(int32_t op, int32_t dtype) {
-  const bool kv = dtype == IT_F32 || dtype == IT_F16 || dtype == IT_BF16 || dtype == IT_Q8_0 || dtype == IT_Q4_0 ||
-                  dtype == IT_Q4_1;
+  const bool kv = dtype == IT_F32 || dtype == IT_F16 || dtype == IT_BF16 || is_quant(dtype);
   switch (op) {
     case IT_OP_KV_APPEND:
     case IT_OP_KV_GATHER:

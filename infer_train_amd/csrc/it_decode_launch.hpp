@@ -68,4 +68,6 @@ hipError_t launch_decode_f32(int d, int gc, const DecodeArgs& a, dim3 grid, hipS
 hipError_t launch_decode_q8_0(int d, int gc, const DecodeArgs& a, dim3 grid, hipStream_t s);
 hipError_t launch_decode_q4_0(int d, int gc, const DecodeArgs& a, dim3 grid, hipStream_t s);
 hipError_t launch_decode_q4_1(int d, int gc, const DecodeArgs& a, dim3 grid, hipStream_t s);
+hipError_t launch_decode_q5_0(int d, int gc, const DecodeArgs& a, dim3 grid, hipStream_t s);
+hipError_t launch_decode_q5_1(int d, int gc, const DecodeArgs& a, dim3 grid, hipStream_t s);
 }  // namespace itkv

@@ -58,6 +58,11 @@
 // (BlockQ4_1, src/types.rs:24-32): the same nibbles, then fp16 (d, m) pairs;
 // a value is f32(d) * nibble + f32(m) (ggml), taken here as f32(d) (nibble -
 // 8) + m' with m' = m + 8 d, the offset term a further small MFMA product.
+// Q5_0 / Q5_1 (ggml block_q5_*, type ids types.rs:116-117): the nibble plane
+// holds the low four bits of each 5-bit value q, and a token's side row its
+// groups' u32 qh words (bit e = bit 4 of element e) and then their d (Q5_0)
+// or (d, m) pairs (Q5_1); a value is f32(d) (q - 16), or f32(d) q + f32(m)
+// taken as f32(d) (q - 16) + m' with m' = m + 16 d.
 #pragma once
 #include <hip/hip_runtime.h>
 
@@ -74,15 +79,21 @@ template <int DT, int D>
 struct SplitFmt {
   static constexpr bool k16 = DT == IT_BF16 || DT == IT_F16;
   static constexpr bool kQ8 = DT == IT_Q8_0;
-  static constexpr bool kQ41 = DT == IT_Q4_1;                      // Q4_1: (d, m) per group
-  static constexpr bool kQ4 = DT == IT_Q4_0 || kQ41;               // nibble planes
-  static constexpr bool kQuant = kQ8 || kQ4;                       // MFMA products, fp16 group scales
+  static constexpr bool kQ5 = DT == IT_Q5_0 || DT == IT_Q5_1;      // + a qh word per group
+  static constexpr bool kOff = DT == IT_Q4_1 || DT == IT_Q5_1;     // (d, m) per group: an offset term
+  static constexpr bool kNib = DT == IT_Q4_0 || DT == IT_Q4_1 || kQ5;  // nibble planes
+  static constexpr bool kQuant = kQ8 || kNib;                       // MFMA products, fp16 group scales
   static constexpr int kElem = DT == IT_F32 ? 4 : (kQuant ? 1 : 2);  // bytes per main-plane element
-  static constexpr int kRow = kQ4 ? D / 2 : D * kElem;            // main-plane bytes per token
+  static constexpr int kRow = kNib ? D / 2 : D * kElem;            // main-plane bytes per token
   static constexpr int kGroup = kGroupTok * kRow;                 // main-plane bytes per group
   static constexpr int kDma = kGroup / 1024;                      // 16-byte-per-lane loads per group
-  static constexpr int kScaleRow = kQuant ? (kQ41 ? D / 8 : D / 16) : 0;  // group scales per token (bytes)
-  static constexpr int kScaleGroup = kGroupTok * kScaleRow;       // 128..512 B
+  static constexpr int kMetaStride = kOff ? 4 : 2;                // bytes of a group's d or (d, m)
+  static constexpr int kMetaOff = kQ5 ? D / 8 : 0;                // where the d words start in a side row
+  static constexpr int kScaleRow = kQuant ? kMetaOff + D / 32 * kMetaStride : 0;  // side-row bytes per token
+  static constexpr int kScaleGroup = kGroupTok * kScaleRow;       // 128..1024 B
+  // B-operand factor: int8 8 (q - 16) for Q5, 16 (nibble - 8) for Q4.
+  static constexpr float kBScale = kQ5 ? 0.125f : (kNib ? 0.0625f : 1.0f);
+  static constexpr float kMid = kQ5 ? 16.0f : 8.0f;                // m' = m + kMid d
   static constexpr int kScaleLoads = (kScaleGroup + 255) / 256;   // dword loads (64 lanes x 4 B) per group
   static constexpr int kSlot = kGroup + kScaleGroup;
   static constexpr int kLoads = kDma + kScaleLoads;               // vmcnt units per group
@@ -93,7 +104,7 @@ struct SplitFmt {
   static constexpr int kDpv = D / 64;                             // PV dims per lane
   static constexpr int kScratch = k16 ? 256 : 512;                // probability scratch per wave (B)
   static_assert(D == 128 || D == 256, "head_dim 128 or 256");
-  static_assert(kGroup % 1024 == 0 && kScaleGroup <= 512, "group geometry");
+  static_assert(kGroup % 1024 == 0 && kScaleGroup <= 1024, "group geometry");
 };
 
 template <int DT>
@@ -107,6 +118,8 @@ inline int split_slot_bytes(int32_t dt, int d) {
     case IT_F32: return split_slot_bytes<IT_F32>(d);
     case IT_Q4_0: return split_slot_bytes<IT_Q4_0>(d);
     case IT_Q4_1: return split_slot_bytes<IT_Q4_1>(d);
+    case IT_Q5_0: return split_slot_bytes<IT_Q5_0>(d);
+    case IT_Q5_1: return split_slot_bytes<IT_Q5_1>(d);
     default: return split_slot_bytes<IT_Q8_0>(d);
   }
 }
@@ -298,11 +311,26 @@ __device__ __forceinline__ uint4 nib8_bf16(uint32_t w) {
   return make_uint4(pair(i8_f32<0>(lo), i8_f32<1>(lo)), pair(i8_f32<2>(lo), i8_f32<3>(lo)),
                     pair(i8_f32<0>(hi), i8_f32<1>(hi)), pair(i8_f32<2>(hi), i8_f32<3>(hi)));
 }
-// Q4_1 value d n + m taken as d (n - 8) + m', m' = m + 8 d: the nibble part
-// is Q4_0's, and m' sits near the group's mean, so neither part is much
-// larger than the value (with m the group minimum the two would cancel).
-__device__ __forceinline__ float q41_offset(uint32_t dm) {
-  return fmaf(8.0f, f16_bits_to_f32(dm & 0xFFFFu), f16_bits_to_f32(dm >> 16));
+// Four nibble bytes of a Q5 group and the fifth bits of their values (bit i
+// of lo4: the low nibble of byte i; of hi4: its high nibble) as eight bf16
+// values 8 (q - 16), low nibbles first, exactly: q << 3 fills a byte, its top
+// bit flipped the byte read as int8 is 8 (q - 16).  The factor 8 goes into d.
+__device__ __forceinline__ uint4 nib5_bf16(uint32_t w, uint32_t lo4, uint32_t hi4) {
+  auto spread = [](uint32_t t) { return (__umul24(t, 0x204081u) & 0x01010101u) << 7; };  // bit i -> bit 8 i + 7
+  const uint32_t lo = (((w << 3) & 0x78787878u) | spread(lo4)) ^ 0x80808080u;
+  const uint32_t hi = (((w >> 1) & 0x78787878u) | spread(hi4)) ^ 0x80808080u;
+  auto pair = [](uint32_t f0, uint32_t f1) { return __builtin_amdgcn_perm(f1, f0, 0x07060302u); };
+  return make_uint4(pair(i8_f32<0>(lo), i8_f32<1>(lo)), pair(i8_f32<2>(lo), i8_f32<3>(lo)),
+                    pair(i8_f32<0>(hi), i8_f32<1>(hi)), pair(i8_f32<2>(hi), i8_f32<3>(hi)));
+}
+// Q4_1 value d n + m taken as d (n - 8) + m', m' = m + 8 d (Q5_1: d q + m as
+// d (q - 16) + m', m' = m + 16 d): the integer part is Q4_0's (Q5_0's), and
+// m' sits near the group's mean, so neither part is much larger than the
+// value (with m the group minimum the two would cancel).
+template <int DT>
+__device__ __forceinline__ float off_mprime(uint32_t dm) {
+  constexpr float kMid = (DT == IT_Q5_1) ? 16.0f : 8.0f;
+  return fmaf(kMid, f16_bits_to_f32(dm & 0xFFFFu), f16_bits_to_f32(dm >> 16));
 }
 // x = hi + mid + lo exactly, each part a bf16 (round to nearest even): the
 // three parts carry the 24 significant bits of an fp32.  Two values per
@@ -391,7 +419,7 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
   using F = SplitFmt<DT, D>;
   constexpr int RB = F::kRow, GB = F::kGroup, SLOT = F::kSlot, NI = F::kDma, NL = F::kLoads;
   constexpr int PQ = F::kPieces, NQ = F::kQRegs, DPV = F::kDpv;
-  constexpr bool k16 = F::k16, kQ = F::kQuant, kQ4 = F::kQ4, kQ41 = F::kQ41;
+  constexpr bool k16 = F::k16, kQ = F::kQuant, kNib = F::kNib, kOff = F::kOff;
   constexpr int NT = 64 * NW;  // threads
   static_assert(GC >= 1 && GC <= 8, "1..8 heads per workgroup");
   static_assert(NW == 2 || NW == 4, "2 or 4 waves");
@@ -535,20 +563,20 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
   } else {
     const int hq = lane & 15;
     const float* qp = static_cast<const float*>(a.q) + (int64_t(b) * a.n_heads + head0 + (hq < GC ? hq : 0)) * D +
-                      (kQ4 ? 4 : 8) * qr_row;
+                      (kNib ? 4 : 8) * qr_row;
     float qsum[NK];
 #pragma unroll
     for (int ks = 0; ks < NK; ++ks) {
       float4 x0 = *reinterpret_cast<const float4*>(qp + 32 * ks);
-      float4 x1 = *reinterpret_cast<const float4*>(qp + 32 * ks + (kQ4 ? 16 : 4));
+      float4 x1 = *reinterpret_cast<const float4*>(qp + 32 * ks + (kNib ? 16 : 4));
       if (hq >= GC) x0 = x1 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-      if constexpr (kQ41) qsum[ks] = ((x0.x + x0.y) + (x0.z + x0.w)) + ((x1.x + x1.y) + (x1.z + x1.w));
+      if constexpr (kOff) qsum[ks] = ((x0.x + x0.y) + (x0.z + x0.w)) + ((x1.x + x1.y) + (x1.z + x1.w));
       split3_bf16(x0.x, x0.y, qa[0][ks].x, qa[1][ks].x, qa[2][ks].x);
       split3_bf16(x0.z, x0.w, qa[0][ks].y, qa[1][ks].y, qa[2][ks].y);
       split3_bf16(x1.x, x1.y, qa[0][ks].z, qa[1][ks].z, qa[2][ks].z);
       split3_bf16(x1.z, x1.w, qa[0][ks].w, qa[1][ks].w, qa[2][ks].w);
     }
-    if constexpr (kQ41) {
+    if constexpr (kOff) {
       float qg[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int ks = 0; ks < NK; ++ks) {
@@ -692,16 +720,24 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
       // token t (Q4_0: bytes 4 kh .. + 4 of the group's 16, as 16 (n - 8))
       // and ends holding S[4 kh + i][t], i = 0..3.
       const char* krow = slot + qk_tok * RB;
+      const char* const kside = slot + GB + qk_tok * F::kScaleRow;
       uint16_t dsc[NK];
 #pragma unroll
       for (int ks = 0; ks < NK; ++ks)
-        dsc[ks] = *reinterpret_cast<const uint16_t*>(slot + GB + qk_tok * F::kScaleRow + (kQ41 ? 4 : 2) * ks);
+        dsc[ks] = *reinterpret_cast<const uint16_t*>(kside + F::kMetaOff + F::kMetaStride * ks);
+      // Q5: the fifth bits of the lane's eight values of group ks, bits
+      // 4 kh .. + 4 (low nibbles) and 16 + 4 kh .. + 4 (high) of qh.
+      uint32_t qh5[F::kQ5 ? NK : 1];
+      if constexpr (F::kQ5) {
+#pragma unroll
+        for (int ks = 0; ks < NK; ++ks) qh5[ks] = *reinterpret_cast<const uint32_t*>(kside + 4 * ks) >> (4 * qr_row);
+      }
       // All K reads first; then the three passes of each group are software
       // pipelined across groups, so that no MFMA waits for the one before it.
       uint2 kr[NK];
 #pragma unroll
       for (int ks = 0; ks < NK; ++ks) {
-        if constexpr (kQ4) {
+        if constexpr (kNib) {
           const int pc = ks ^ (qk_tok & F::kSwz);  // a Q4_0 group is one 16-byte piece
           kr[ks] = make_uint2(*reinterpret_cast<const uint32_t*>(krow + (pc << 4) + 4 * qr_row), 0u);
         } else {
@@ -714,7 +750,8 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
       Unroll<0, NK + 2>::run([&](auto kc) {
         constexpr int k = decltype(kc)::value;
         if constexpr (k < NK) {
-          kb[k] = kQ4 ? nib8_bf16(kr[k].x) : i8x8_bf16(kr[k]);
+          if constexpr (F::kQ5) kb[k] = nib5_bf16(kr[k].x, qh5[k] & 0xFu, (qh5[k] >> 16) & 0xFu);
+          else kb[k] = kNib ? nib8_bf16(kr[k].x) : i8x8_bf16(kr[k]);
           acc[k] = mfma16(qa[0][k], kb[k], v4f{0.0f, 0.0f, 0.0f, 0.0f});
         }
         if constexpr (k >= 1 && k - 1 < NK) acc[k - 1] = mfma16(qa[1][k - 1], kb[k - 1], acc[k - 1]);
@@ -723,11 +760,11 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
       v4f sv = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int ks = 0; ks < NK; ++ks) {
-        const float d = f16_bits_to_f32(dsc[ks]) * (kQ4 ? 0.0625f : 1.0f);  // exact
+        const float d = f16_bits_to_f32(dsc[ks]) * F::kBScale;  // exact
 #pragma unroll
         for (int i = 0; i < 4; ++i) sv[i] = fmaf(d, acc[ks][i], sv[i]);
       }
-      if constexpr (kQ41) {
+      if constexpr (kOff) {
         // + sum over groups G of m'_G(t) qsum[h][G]: lane (kh, t) holds
         // B[G = 4 kh + j][t] = m'_G(t), zero past the groups; both operands
         // in three exact bf16 parts.
@@ -735,8 +772,7 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int G = 4 * qr_row + j;
-          mv[j] = G < NK ? q41_offset(*reinterpret_cast<const uint32_t*>(slot + GB + qk_tok * F::kScaleRow +
-                                                                          4 * (G < NK ? G : 0)))
+          mv[j] = G < NK ? off_mprime<DT>(*reinterpret_cast<const uint32_t*>(kside + F::kMetaOff + 4 * (G < NK ? G : 0)))
                          : 0.0f;
         }
         uint2 mb[3];
@@ -909,15 +945,15 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
       for (int j = 0; j < 4; ++j)
         pj[j] = (tb + 4 * kq + j < nt && !none_h) ? __builtin_amdgcn_exp2f(sj[j] - m_h) : 0.0f;
       lsum += (pj[0] + pj[1]) + (pj[2] + pj[3]);
-      if constexpr (kQ41) {
+      if constexpr (kOff) {
         // The offset term: M[h][G] += sum over the item's tokens of p[h][t]
         // m'_G(t); B[t][G = hm] for the lane's four tokens, zero past the
         // groups; both operands in three exact bf16 parts.
         float mv[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          mv[j] = hm < NK ? q41_offset(*reinterpret_cast<const uint32_t*>(slot + GB + (4 * kq + j) * F::kScaleRow +
-                                                                           4 * (hm < NK ? hm : 0)))
+          mv[j] = hm < NK ? off_mprime<DT>(*reinterpret_cast<const uint32_t*>(slot + GB + (4 * kq + j) * F::kScaleRow +
+                                                                               F::kMetaOff + 4 * (hm < NK ? hm : 0)))
                           : 0.0f;
         uint2 mb[3], pa[3];
         split3_bf16(mv[0], mv[1], mb[0].x, mb[1].x, mb[2].x);
@@ -929,18 +965,21 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
 #pragma unroll
           for (int r = 0; r < 3; ++r) mo = mfma16k16(pa[p], mb[r], mo);
       }
-      if constexpr (kQ4) {
+      if constexpr (kNib) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) pj[j] *= 0.0625f;  // exact; undoes B's factor 16
+        for (int j = 0; j < 4; ++j) pj[j] *= F::kBScale;  // exact; undoes B's factor 16 (Q5: 8)
       }
-      const char* const vrow = slot + (4 * kq) * RB + (kQ4 ? 1 : 2) * hm;
-      // The scale rows of the lane's four tokens, NK fp16 each.
+      const char* const vrow = slot + (4 * kq) * RB + (kNib ? 1 : 2) * hm;
+      // The scale rows of the lane's four tokens, NK fp16 each (Q5: read
+      // per group below, with the group's qh words).
       const char* const srow = slot + GB + (4 * kq) * F::kScaleRow;
-      constexpr int SW = (F::kScaleRow > 0 ? F::kScaleRow : 4) / 4;  // dwords per token row
+      constexpr int SW = F::kQ5 ? 1 : (F::kScaleRow > 0 ? F::kScaleRow : 4) / 4;  // dwords per token row
       uint32_t dw[4][SW];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        if constexpr (SW % 4 == 0) {
+        if constexpr (F::kQ5) {
+          dw[j][0] = 0u;
+        } else if constexpr (SW % 4 == 0) {
 #pragma unroll
           for (int c = 0; c < SW / 4; ++c) {
             const uint4 t = *reinterpret_cast<const uint4*>(srow + j * F::kScaleRow + 16 * c);
@@ -954,7 +993,9 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
       // fp16 d of group G for token 4 kq + j (Q4_1 rows hold (d, m) pairs).
       auto dbits = [&](int j, auto gc) -> uint32_t {
         constexpr int G = decltype(gc)::value;
-        if constexpr (kQ41) return dw[j][G] & 0xFFFFu;
+        if constexpr (F::kQ5)
+          return *reinterpret_cast<const uint16_t*>(srow + j * F::kScaleRow + F::kMetaOff + F::kMetaStride * G);
+        else if constexpr (kOff) return dw[j][G] & 0xFFFFu;
         else return G & 1 ? dw[j][G / 2] >> 16 : dw[j][G / 2] & 0xFFFFu;
       };
       Unroll<0, NK>::run([&](auto gc) {
@@ -968,11 +1009,25 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
         split3_bf16(x[2], x[3], ah.y, am.y, al.y);
         auto pair = [](uint32_t f0, uint32_t f1) { return __builtin_amdgcn_perm(f1, f0, 0x07060302u); };
         uint2 b0, b1;
-        if constexpr (kQ4) {
+        if constexpr (kNib) {
           uint32_t w = 0;
 #pragma unroll
           for (int j = 0; j < 4; ++j) w |= uint32_t(*reinterpret_cast<const uint8_t*>(vrow + j * RB + 16 * G)) << (8 * j);
-          const uint4 t = nib8_bf16(w);  // tokens 4 kq + j: low nibbles (tile 0), then high (tile 1)
+          uint4 t;  // tokens 4 kq + j: low nibbles (tile 0), then high (tile 1)
+          if constexpr (F::kQ5) {
+            // Fifth bits of element hm (low nibble) and 16 + hm (high) of
+            // each token, from the group's qh words.
+            uint32_t lo4 = 0u, hi4 = 0u;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const uint32_t qh = *reinterpret_cast<const uint32_t*>(srow + j * F::kScaleRow + 4 * G) >> hm;
+              lo4 |= (qh & 1u) << j;
+              hi4 |= ((qh >> 16) & 1u) << j;
+            }
+            t = nib5_bf16(w, lo4, hi4);
+          } else {
+            t = nib8_bf16(w);
+          }
           b0 = make_uint2(t.x, t.y);
           b1 = make_uint2(t.z, t.w);
         } else {
@@ -1074,7 +1129,7 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
   float* const red = reinterpret_cast<float*>(smem);  // [NW][GC][D]
   if constexpr (kQ) {
     const int hm = lane & 15;
-    if constexpr (kQ41) {
+    if constexpr (kOff) {
       // M[h][G] of this wave into its probability scratch (unused on this
       // path): [8 heads][8 groups] fp32.
       float* const s_mo = reinterpret_cast<float*>(s_pp + wave * (F::kScratch / 4));
@@ -1089,7 +1144,7 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
 #pragma unroll
         for (int g = 0; g < NK; ++g) {
           float* const row = &red[(wave * GC + h) * D + 32 * g];
-          if constexpr (kQ4) {
+          if constexpr (kNib) {
             row[hm] = o8[g][0][i];
             row[16 + hm] = o8[g][1][i];
           } else {
@@ -1124,7 +1179,7 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
     if constexpr (NW == 2) o = red[i] + red[GC * D + i];
     else o = (red[i] + red[GC * D + i]) + (red[2 * GC * D + i] + red[3 * GC * D + i]);
     const int g = i / D, d = i - g * D;
-    if constexpr (kQ41) {  // + the offset term of dim d's group, from every wave
+    if constexpr (kOff) {  // + the offset term of dim d's group, from every wave
       const float* const s_mo = reinterpret_cast<const float*>(s_pp);
 #pragma unroll
       for (int w = 0; w < NW; ++w) o += s_mo[w * (F::kScratch / 4) + g * 8 + d / 32];

@@ -19,6 +19,11 @@ enum : uint32_t {
   kErrStart = 32u,      // negative start position (the sequence is skipped)
 };
 
+// Quantised KV formats (32-element groups, F32 source rows).
+inline bool is_quant(int32_t dt) {
+  return dt == IT_Q8_0 || dt == IT_Q4_0 || dt == IT_Q4_1 || dt == IT_Q5_0 || dt == IT_Q5_1;
+}
+
 inline bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
 inline int ilog2(int64_t x) {
   int r = 0;

@@ -16,9 +16,16 @@
 //        types.rs:24-32): min / max (strict compares: NaN never wins, the
 //        first of equal values stays), d = (max - min) / 15, nibble =
 //        min(15, (int8_t)((x - min) id + 0.5f)), d and m = min as fp16.
-// Q4 products and sums are rounded separately (no FMA: this library builds
-// with -ffp-contract=fast), and (int8_t) of NaN or an out-of-range value is
-// 0, as x86's cvttss2si gives; byte j = nibble j | nibble (j + 16) << 4.
+//  Q5_0  ggml's quantize_row_q5_0_ref (the reference has only the type id,
+//        types.rs:116): Q4_0's max, d = max / -16, q = min(31, (int8_t)(x id
+//        + 16.5f)).
+//  Q5_1  ggml's quantize_row_q5_1_ref (types.rs:117): Q4_1's min / max, d =
+//        (max - min) / 31, q = (uint8_t)((x - min) id + 0.5f), no clamp.
+// Q4/Q5 products and sums are rounded separately (no FMA: this library
+// builds with -ffp-contract=fast), and (int8_t) / (uint8_t) of NaN or an
+// out-of-range value is 0, as x86's cvttss2si gives; byte j = nibble j |
+// nibble (j + 16) << 4 (the low four bits of a Q5 value), and Q5's u32 qh
+// holds bit 4 of element e's value at bit e.
 #pragma once
 #include <hip/hip_runtime.h>
 
@@ -46,11 +53,25 @@ __device__ __forceinline__ float mul_rn(float a, float b) {
 }
 
 // What a lane stores: `qs` at its place in the group's main-plane bytes
-// (Q8_0: four int8 at byte 4 l8; Q4_0 / Q4_1: four bytes at byte 4 l8, lanes
-// 0-3 only) and, from lane 0, the group's scale word `meta` (Q8_0 / Q4_0:
-// fp16 d; Q4_1: fp16 d | fp16 m << 16).
+// (Q8_0: four int8 at byte 4 l8; Q4 / Q5: four bytes at byte 4 l8, lanes
+// 0-3 only) and, from lane 0, the group's scale word `meta` (Q8_0 / Q4_0 /
+// Q5_0: fp16 d; Q4_1 / Q5_1: fp16 d | fp16 m << 16) and Q5's `qh`.
 struct QuantGroup {
-  uint32_t qs, meta;
+  uint32_t qs, meta, qh;
+};
+
+// Where the 4- and 5-bit formats keep a group's words in a page of bs rows:
+// the nibble plane u8 [bs][d / 2], then per token a side row of
+// (Q5 only) d/32 u32 qh words, then d/32 metadata words (fp16 d, or the
+// (d, m) pair as one u32).
+template <int DT>
+struct NibFmt {
+  static constexpr bool kQ5 = DT == IT_Q5_0 || DT == IT_Q5_1;
+  static constexpr bool kMin = DT == IT_Q4_1 || DT == IT_Q5_1;     // (d, m) pairs
+  static constexpr int kMeta = kMin ? 4 : 2;                        // metadata bytes per group
+  static constexpr int kSide = kMeta + (kQ5 ? 4 : 0);               // side-row bytes per group
+  static constexpr int kRecord = 16 + kSide;                        // ggml block bytes
+  __host__ __device__ static constexpr int meta_off(int ng) { return kQ5 ? 4 * ng : 0; }
 };
 
 __device__ __forceinline__ int32_t q8_round(float x, float scale) {
@@ -62,16 +83,76 @@ __device__ __forceinline__ int32_t q8_round(float x, float scale) {
   return int32_t(r);
 }
 
-// (int8_t)(r) as ggml's x86 build computes it, then min(15, .), low byte.
-__device__ __forceinline__ uint32_t q4_nibble(float r) {
-  if (!(fabsf(r) < 2147483648.0f)) return 0u;
-  return uint32_t(min(int32_t(int8_t(int32_t(r))), 15)) & 0xFFu;
+// (int8_t)(r) and (uint8_t)(r) as ggml's x86 build computes them: truncate
+// to int32 (NaN and out-of-range give 0x80000000), keep the low byte.
+__device__ __forceinline__ int32_t trunc_i8(float r) {
+  if (!(fabsf(r) < 2147483648.0f)) return 0;
+  return int32_t(int8_t(int32_t(r)));
+}
+__device__ __forceinline__ int32_t trunc_u8(float r) {
+  if (!(fabsf(r) < 2147483648.0f)) return 0;
+  return int32_t(uint8_t(int32_t(r)));
+}
+// Q4's min(15, (int8_t)r), low byte.
+__device__ __forceinline__ uint32_t q4_nibble(float r) { return uint32_t(min(trunc_i8(r), 15)) & 0xFFu; }
+
+// The value of largest magnitude in an 8-lane group of four floats per lane
+// (equal magnitudes: the lower element index; NaN never wins; none: 0).
+__device__ __forceinline__ float group_absmax_first(const float (&xs)[4], int l8) {
+  float am = 0.0f, mx = 0.0f;
+  int im = 32;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float a = fabsf(xs[e]);
+    if (am < a) am = a, mx = xs[e], im = 4 * l8 + e;
+  }
+  auto step = [&](auto ctrl) {
+    constexpr int C = decltype(ctrl)::value;
+    const float a2 = dpp_f<C>(am), m2 = dpp_f<C>(mx);
+    const int i2 = __builtin_amdgcn_mov_dpp(im, C, 0xF, 0xF, true);
+    if (a2 > am || (a2 == am && i2 < im)) am = a2, mx = m2, im = i2;
+  };
+  step(std::integral_constant<int, kDppQuadXor1>{});
+  step(std::integral_constant<int, kDppQuadXor2>{});
+  step(std::integral_constant<int, kDppHalfMirror>{});
+  return mx;
+}
+
+// Min and max of an 8-lane group (strict compares: NaN never wins, the
+// first of equal values stays; FLT_MAX / -FLT_MAX when every element is NaN).
+__device__ __forceinline__ void group_minmax(const float (&xs)[4], int l8, float& mn, float& mx) {
+  mn = FLT_MAX, mx = -FLT_MAX;
+  int imn = 32, imx = 32;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    if (xs[e] < mn) mn = xs[e], imn = 4 * l8 + e;
+    if (xs[e] > mx) mx = xs[e], imx = 4 * l8 + e;
+  }
+  auto step = [&](auto ctrl) {
+    constexpr int C = decltype(ctrl)::value;
+    const float mn2 = dpp_f<C>(mn), mx2 = dpp_f<C>(mx);
+    const int imn2 = __builtin_amdgcn_mov_dpp(imn, C, 0xF, 0xF, true);
+    const int imx2 = __builtin_amdgcn_mov_dpp(imx, C, 0xF, 0xF, true);
+    if (mn2 < mn || (mn2 == mn && imn2 < imn)) mn = mn2, imn = imn2;
+    if (mx2 > mx || (mx2 == mx && imx2 < imx)) mx = mx2, imx = imx2;
+  };
+  step(std::integral_constant<int, kDppQuadXor1>{});
+  step(std::integral_constant<int, kDppQuadXor2>{});
+  step(std::integral_constant<int, kDppHalfMirror>{});
+}
+
+// OR of a word over an 8-lane group.
+__device__ __forceinline__ uint32_t group_or8(uint32_t v) {
+  v |= uint32_t(__builtin_amdgcn_mov_dpp(int(v), kDppQuadXor1, 0xF, 0xF, true));
+  v |= uint32_t(__builtin_amdgcn_mov_dpp(int(v), kDppQuadXor2, 0xF, 0xF, true));
+  v |= uint32_t(__builtin_amdgcn_mov_dpp(int(v), kDppHalfMirror, 0xF, 0xF, true));
+  return v;
 }
 
 template <int DT>
 __device__ __forceinline__ QuantGroup quant_group(float4 x, int l8) {
   const float xs[4] = {x.x, x.y, x.z, x.w};
-  QuantGroup out{0u, 0u};
+  QuantGroup out{0u, 0u, 0u};
   if constexpr (DT == IT_Q8_0) {
     auto absn = [](float f) { return f == f ? fabsf(f) : 0.0f; };
     float amax = fmaxf(fmaxf(absn(x.x), absn(x.y)), fmaxf(absn(x.z), absn(x.w)));
@@ -83,54 +164,44 @@ __device__ __forceinline__ QuantGroup quant_group(float4 x, int l8) {
       out.meta = f16_bits_rne(scale);
     }
   } else if constexpr (DT == IT_Q4_0) {
-    // (|max|, element index, max): larger magnitude wins, equal magnitudes go
-    // to the lower index; "none" is (0, 32).
-    float am = 0.0f, mx = 0.0f;
-    int im = 32;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float a = fabsf(xs[e]);
-      if (am < a) am = a, mx = xs[e], im = 4 * l8 + e;
-    }
-    auto step = [&](auto ctrl) {
-      constexpr int C = decltype(ctrl)::value;
-      const float a2 = dpp_f<C>(am), m2 = dpp_f<C>(mx);
-      const int i2 = __builtin_amdgcn_mov_dpp(im, C, 0xF, 0xF, true);
-      if (a2 > am || (a2 == am && i2 < im)) am = a2, mx = m2, im = i2;
-    };
-    step(std::integral_constant<int, kDppQuadXor1>{});
-    step(std::integral_constant<int, kDppQuadXor2>{});
-    step(std::integral_constant<int, kDppHalfMirror>{});
-    const float d = mx / -8.0f;
+    const float d = group_absmax_first(xs, l8) / -8.0f;
     const float id = d != 0.0f ? 1.0f / d : 0.0f;
 #pragma unroll
     for (int e = 0; e < 4; ++e) out.qs |= q4_nibble(mul_rn(xs[e], id) + 8.5f) << (8 * e);
     out.meta = f16_bits_rne(d);
-  } else {
-    static_assert(DT == IT_Q4_1, "Q8_0, Q4_0 or Q4_1");
-    float mn = FLT_MAX, mx = -FLT_MAX;
-    int imn = 32, imx = 32;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      if (xs[e] < mn) mn = xs[e], imn = 4 * l8 + e;
-      if (xs[e] > mx) mx = xs[e], imx = 4 * l8 + e;
-    }
-    auto step = [&](auto ctrl) {
-      constexpr int C = decltype(ctrl)::value;
-      const float mn2 = dpp_f<C>(mn), mx2 = dpp_f<C>(mx);
-      const int imn2 = __builtin_amdgcn_mov_dpp(imn, C, 0xF, 0xF, true);
-      const int imx2 = __builtin_amdgcn_mov_dpp(imx, C, 0xF, 0xF, true);
-      if (mn2 < mn || (mn2 == mn && imn2 < imn)) mn = mn2, imn = imn2;
-      if (mx2 > mx || (mx2 == mx && imx2 < imx)) mx = mx2, imx = imx2;
-    };
-    step(std::integral_constant<int, kDppQuadXor1>{});
-    step(std::integral_constant<int, kDppQuadXor2>{});
-    step(std::integral_constant<int, kDppHalfMirror>{});
+  } else if constexpr (DT == IT_Q4_1) {
+    float mn, mx;
+    group_minmax(xs, l8, mn, mx);
     const float d = (mx - mn) / 15.0f;
     const float id = d != 0.0f ? 1.0f / d : 0.0f;
 #pragma unroll
     for (int e = 0; e < 4; ++e) out.qs |= q4_nibble(mul_rn(xs[e] - mn, id) + 0.5f) << (8 * e);
     out.meta = f16_bits_rne(d) | (f16_bits_rne(mn) << 16);
+  } else {
+    static_assert(DT == IT_Q5_0 || DT == IT_Q5_1, "Q8_0, Q4_0, Q4_1, Q5_0 or Q5_1");
+    int32_t q[4];
+    if constexpr (DT == IT_Q5_0) {
+      const float d = group_absmax_first(xs, l8) / -16.0f;
+      const float id = d != 0.0f ? 1.0f / d : 0.0f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) q[e] = min(trunc_i8(mul_rn(xs[e], id) + 16.5f), 31);
+      out.meta = f16_bits_rne(d);
+    } else {
+      float mn, mx;
+      group_minmax(xs, l8, mn, mx);
+      const float d = (mx - mn) / 31.0f;
+      const float id = d != 0.0f ? 1.0f / d : 0.0f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) q[e] = trunc_u8(mul_rn(xs[e] - mn, id) + 0.5f);
+      out.meta = f16_bits_rne(d) | (f16_bits_rne(mn) << 16);
+    }
+    uint32_t hb = 0u;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      out.qs |= (uint32_t(q[e]) & 0xFu) << (8 * e);
+      hb |= ((uint32_t(q[e]) >> 4) & 1u) << e;
+    }
+    out.qh = group_or8(hb << (4 * l8));
   }
   if constexpr (DT != IT_Q8_0) {
     // Lane i < 4 of the group takes lane i + 4's bytes (DPP row_shl:4):
@@ -150,12 +221,16 @@ __device__ __forceinline__ void store_group(char* page, int64_t off, int64_t bs,
     *reinterpret_cast<uint32_t*>(page + off * d + cv * 4) = q.qs;
     if (l8 == 0) *reinterpret_cast<uint16_t*>(page + bs * d + (off * (d >> 5) + g) * 2) = uint16_t(q.meta);
   } else {
+    using N = NibFmt<DT>;
     if (l8 < 4) *reinterpret_cast<uint32_t*>(page + off * (d >> 1) + g * 16 + l8 * 4) = q.qs;
     if (l8 == 0) {
-      if constexpr (DT == IT_Q4_1)
-        *reinterpret_cast<uint32_t*>(page + bs * (d >> 1) + (off * (d >> 5) + g) * 4) = q.meta;
+      const int ng = d >> 5;
+      char* const side = page + bs * (d >> 1) + off * (ng * N::kSide);
+      if constexpr (N::kQ5) *reinterpret_cast<uint32_t*>(side + 4 * g) = q.qh;
+      if constexpr (N::kMin)
+        *reinterpret_cast<uint32_t*>(side + N::meta_off(ng) + 4 * g) = q.meta;
       else
-        *reinterpret_cast<uint16_t*>(page + bs * (d >> 1) + (off * (d >> 5) + g) * 2) = uint16_t(q.meta);
+        *reinterpret_cast<uint16_t*>(side + N::meta_off(ng) + 2 * g) = uint16_t(q.meta);
     }
   }
 }

@@ -8,7 +8,8 @@
 // on the device: the device only multiplies and adds, so its results equal
 // the CPU's bit for bit.  One lane rotates one 16-byte vector (two pairs) of
 // one (token, head) row; K and V lanes then convert (or quantise: Q8_0,
-// Q4_0, Q4_1) and store like the plain append, Q lanes write the rotated query.
+// Q4_0, Q4_1, Q5_0, Q5_1) and store like the plain append, Q lanes write the
+// rotated query.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -111,7 +112,7 @@ __global__ __launch_bounds__(kThreads) void kv_append_rope(RopeAppendArgs a) {
     else static_cast<uint2*>(a.q_out)[gid] = pack4<IT_F16>(x);
     return;
   }
-  if constexpr (DT == IT_Q8_0 || DT == IT_Q4_0 || DT == IT_Q4_1) {
+  if constexpr (DT == IT_Q8_0 || DT == IT_Q4_0 || DT == IT_Q4_1 || DT == IT_Q5_0 || DT == IT_Q5_1) {
     // Eight lanes own one 32-element group (rows of d/4 vectors, d % 32 ==
     // 0): the group's reductions run before any lane leaves.
     const QuantGroup qg = quant_group<DT>(x, cv & 7);
@@ -207,7 +208,7 @@ extern "C" int32_t it_kv_append_rope(it_kv_cache* c, const it_rope_table* rope, 
   if (rope->n_dims > c->head_dim)
     return fail(IT_INVALID_INPUT, "%s: table n_dims %d > head_dim %d", who, rope->n_dims, c->head_dim);
   if (rope->device != c->device) return fail(IT_INVALID_INPUT, "%s: table and cache on different devices", who);
-  const bool quant = c->dtype == IT_Q8_0 || c->dtype == IT_Q4_0 || c->dtype == IT_Q4_1;
+  const bool quant = is_quant(c->dtype);
   if (c->dtype != IT_F32 && c->dtype != IT_BF16 && c->dtype != IT_F16 && !quant)
     return fail(IT_NOT_IMPLEMENTED, "%s: cache dtype %d", who, c->dtype);
   const bool q_ok = q_out_dtype == IT_F32 || ((c->dtype == IT_BF16 || c->dtype == IT_F16) && q_out_dtype == c->dtype);
@@ -253,6 +254,8 @@ extern "C" int32_t it_kv_append_rope(it_kv_cache* c, const it_rope_table* rope, 
     case IT_F16: hipLaunchKernelGGL(kv_append_rope<IT_F16>, grid, dim3(kThreads), 0, s, a); break;
     case IT_Q4_0: hipLaunchKernelGGL(kv_append_rope<IT_Q4_0>, grid, dim3(kThreads), 0, s, a); break;
     case IT_Q4_1: hipLaunchKernelGGL(kv_append_rope<IT_Q4_1>, grid, dim3(kThreads), 0, s, a); break;
+    case IT_Q5_0: hipLaunchKernelGGL(kv_append_rope<IT_Q5_0>, grid, dim3(kThreads), 0, s, a); break;
+    case IT_Q5_1: hipLaunchKernelGGL(kv_append_rope<IT_Q5_1>, grid, dim3(kThreads), 0, s, a); break;
     default: hipLaunchKernelGGL(kv_append_rope<IT_Q8_0>, grid, dim3(kThreads), 0, s, a); break;
   }
   const hipError_t e = hipGetLastError();

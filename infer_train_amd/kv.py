@@ -12,7 +12,7 @@ from typing import Optional, Tuple
 
 import torch
 
-from ._lib import BF16, CacheDesc, F16, F32, Q4_0, Q4_1, Q8_0, check, lib
+from ._lib import BF16, CacheDesc, F16, F32, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, check, lib
 
 __all__ = ["PagedKvCache", "RopeTable", "flash_attention", "torch_dtype_id", "stream_handle"]
 
@@ -63,7 +63,9 @@ class RopeTable:
 class PagedKvCache:
     """Paged K/V pools in HBM, [num_blocks][n_kv_heads] pages of block_size
     token rows (Q8_0 pages: int8 rows then fp16 group scales; Q4_0 pages:
-    rows of BlockQ4_0 nibble bytes then fp16 group scales)."""
+    rows of BlockQ4_0 nibble bytes then fp16 group scales; Q4_1 the same
+    with (d, m) pairs; Q5_0 / Q5_1 the nibble rows then per token the
+    groups' u32 qh words and their d or (d, m))."""
 
     def __init__(self, num_blocks: int, block_size: int, n_kv_heads: int, head_dim: int, dtype: int = BF16,
                  device: int = 0):
@@ -99,8 +101,8 @@ class PagedKvCache:
         pool = self.k_pool if which == "k" else self.v_pool
         if self.dtype == Q8_0:
             raise TypeError("use q8_planes() for a Q8_0 cache")
-        if self.dtype in (Q4_0, Q4_1):
-            raise TypeError("use q4_planes() for a Q4_0 / Q4_1 cache")
+        if self.dtype in (Q4_0, Q4_1, Q5_0, Q5_1):
+            raise TypeError("use q4_planes() for a Q4_0 / Q4_1 cache, q5_planes() for Q5_0 / Q5_1")
         return pool.view(_ID_TORCH[self.dtype]).view(self.num_blocks, self.n_kv_heads, self.block_size, self.head_dim)
 
     def q8_planes(self, which: str = "k") -> Tuple[torch.Tensor, torch.Tensor]:
@@ -120,6 +122,23 @@ class PagedKvCache:
         shape = (self.num_blocks, self.n_kv_heads, bs, D // 32) + ((2,) if self.dtype == Q4_1 else ())
         d = pool[:, :, bs * D // 2:].contiguous().view(torch.int16).reshape(shape)
         return qs, d
+
+    def q5_planes(self, which: str = "k") -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        """(qs uint8 [nb, H, bs, D/2] (low four bits of each value), qh int32
+        [nb, H, bs, D/32], scales fp16 bits int16 [nb, H, bs, D/32] (Q5_0: d) or
+        [nb, H, bs, D/32, 2] (Q5_1: d, m)) of a Q5_0 / Q5_1 cache."""
+        if self.dtype not in (Q5_0, Q5_1):
+            raise TypeError("q5_planes() needs a Q5_0 / Q5_1 cache")
+        pool = (self.k_pool if which == "k" else self.v_pool).view(self.num_blocks, self.n_kv_heads, self.page_bytes)
+        bs, D = self.block_size, self.head_dim
+        ng, mb = D // 32, 4 if self.dtype == Q5_1 else 2
+        nb, H = self.num_blocks, self.n_kv_heads
+        qs = pool[:, :, : bs * D // 2].reshape(nb, H, bs, D // 2)
+        side = pool[:, :, bs * D // 2:].reshape(nb, H, bs, ng * (4 + mb))
+        qh = side[..., : 4 * ng].contiguous().view(torch.int32)
+        shape = (nb, H, bs, ng) + ((2,) if self.dtype == Q5_1 else ())
+        d = side[..., 4 * ng:].contiguous().view(torch.int16).reshape(shape)
+        return qs, qh, d
 
     def check(self) -> None:
         """Raise if a kernel latched a device-side range error (syncs the stream)."""

@@ -45,8 +45,15 @@ def test_status_codes_and_pure_queries():
     assert lib.it_supports(L.OP_PAGED_DECODE, L.BF16) == 1
     assert lib.it_supports(L.OP_PAGED_DECODE, L.Q4_0) == 1
     assert lib.it_supports(L.OP_PAGED_DECODE, L.Q4_1) == 1
-    assert lib.it_supports(L.OP_PAGED_DECODE, 6) == 0  # Q5_0 caches are not implemented
+    for dt in (L.Q5_0, L.Q5_1):
+        for op in (L.OP_KV_APPEND, L.OP_KV_GATHER, L.OP_KV_EVICT, L.OP_KV_COPY_BLOCKS, L.OP_PAGED_DECODE):
+            assert lib.it_supports(op, dt) == 1
+        assert lib.it_supports(L.OP_PAGED_PREFILL, dt) == 0
+    assert lib.it_supports(L.OP_PAGED_DECODE, 9) == 0  # Q8_1 caches are not implemented
     assert lib.it_kv_page_bytes(32, 256, L.Q4_1) == 32 * 128 + 32 * 8 * 4  # 5120
+    # nibble plane + per token 8 groups of (qh u32, d fp16) / (qh u32, d and m fp16)
+    assert lib.it_kv_page_bytes(16, 128, L.Q5_0) == 16 * 64 + 16 * 4 * 6  # 1408 = 16 x 4 x 22 bytes
+    assert lib.it_kv_page_bytes(32, 256, L.Q5_1) == 32 * 128 + 32 * 8 * 8  # 6144 = 32 x 8 x 24 bytes
     assert lib.it_supports(L.OP_PAGED_PREFILL, L.Q4_0) == 0
     assert lib.it_supports(L.OP_PAGED_PREFILL, L.BF16) == 1
     assert lib.it_supports(L.OP_PAGED_PREFILL, L.F16) == 1  # F16 caches run the same MFMA kernel
@@ -114,7 +121,8 @@ def test_invalid_input_before_device():
     h = C.c_void_p()
     assert lib.it_kv_cache_new(0, 16, 12, 2, 128, L.BF16, C.byref(h)) == L.NOT_IMPLEMENTED  # bs not 2^k
     assert lib.it_kv_cache_new(0, 16, 16, 2, 100, L.Q8_0, C.byref(h)) == L.INVALID_INPUT  # D % 32
-    assert lib.it_kv_cache_new(0, 16, 16, 2, 128, 6, C.byref(h)) == L.NOT_IMPLEMENTED  # Q5_0
+    assert lib.it_kv_cache_new(0, 16, 16, 2, 128, 9, C.byref(h)) == L.NOT_IMPLEMENTED  # Q8_1
+    assert lib.it_kv_cache_new(0, 16, 16, 2, 100, L.Q5_1, C.byref(h)) == L.INVALID_INPUT  # D % 32
     assert lib.it_kv_cache_new(0, 16, 16, 2, 96 + 8, L.Q4_0, C.byref(h)) == L.INVALID_INPUT  # D % 32
 
 

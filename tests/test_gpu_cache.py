@@ -1,5 +1,6 @@
 """GPU parity of the data-movement kernels: slot-mapped append (bit copy,
-Q8_0 and Q4_0 quantise), block-table gather, evict and copy-on-write page copy.  Every
+Q8_0 / Q4_0 / Q4_1 / Q5_0 / Q5_1 quantise), block-table gather, evict and
+copy-on-write page copy.  Every
 result is compared byte for byte with the oracle on the same seeded inputs;
 pools start filled with a sentinel so stray writes show up."""
 import numpy as np
@@ -28,7 +29,7 @@ def _pair(num_blocks, bs, hkv, D, dt):
 
 
 def _src(seed, n_tokens, hkv, D, dt):
-    if dt in (orc.Q8_0, orc.Q4_0, orc.Q4_1):
+    if dt in orc.QUANT_TYPES:
         k = kv_values(seed, n_tokens * hkv * D, orc.F32, outliers=True)
         v = kv_values(seed + 1, n_tokens * hkv * D, orc.F32, outliers=True)
     else:
@@ -40,7 +41,7 @@ def _src(seed, n_tokens, hkv, D, dt):
 def _dev_src(a, dt):
     import torch
 
-    if dt in (orc.F32, orc.Q8_0, orc.Q4_0, orc.Q4_1):
+    if dt in (orc.F32,) + orc.QUANT_TYPES:
         return to_dev(a)
     return to_dev(a.view(np.int16), torch.bfloat16 if dt == orc.BF16 else torch.float16)
 
@@ -58,7 +59,9 @@ def _assert_pools(dev, ref, what):
 @pytest.mark.parametrize("dt,D,bs", [(orc.BF16, 128, 16), (orc.F32, 128, 16), (orc.F16, 128, 16),
                                      (orc.BF16, 256, 32), (orc.Q8_0, 256, 32), (orc.Q8_0, 128, 16),
                                      (orc.Q4_0, 256, 32), (orc.Q4_0, 128, 16), (orc.Q4_0, 64, 8),
-                                     (orc.Q4_1, 256, 32), (orc.Q4_1, 128, 16), (orc.Q4_1, 64, 8)])
+                                     (orc.Q4_1, 256, 32), (orc.Q4_1, 128, 16), (orc.Q4_1, 64, 8),
+                                     (orc.Q5_0, 256, 32), (orc.Q5_0, 128, 16), (orc.Q5_0, 64, 8), (orc.Q5_0, 32, 16),
+                                     (orc.Q5_1, 256, 32), (orc.Q5_1, 128, 16), (orc.Q5_1, 64, 8), (orc.Q5_1, 32, 8)])
 def test_append_bit_exact(dt, D, bs):
     hkv, nb, n = 4, 64, 300
     dev, ref = _pair(nb, bs, hkv, D, dt)
@@ -99,11 +102,11 @@ def test_append_q8_special_groups():
     _assert_pools(dev, ref, "append q8 special")
 
 
-@pytest.mark.parametrize("dt", [orc.Q4_0, orc.Q4_1])
-def test_append_q4_special_groups(dt):
-    """Q4_0 / Q4_1 (ggml's quantisers; the reference has none): equal
-    magnitudes of both signs, all-zero, -0, constant, subnormal, NaN, inf and
-    a group whose 1/d overflows."""
+@pytest.mark.parametrize("dt", [orc.Q4_0, orc.Q4_1, orc.Q5_0, orc.Q5_1])
+def test_append_nibble_special_groups(dt):
+    """Q4_0 / Q4_1 / Q5_0 / Q5_1 (ggml's quantisers; the reference has
+    none): equal magnitudes of both signs, all-zero, -0, constant,
+    subnormal, NaN, inf and a group whose 1/d overflows."""
     hkv, D, bs, nb = 1, 256, 32, 4
     dev, ref = _pair(nb, bs, hkv, D, dt)
     g = np.zeros((8, 32), np.float32)
@@ -118,7 +121,7 @@ def test_append_q4_special_groups(dt):
     g[6] = orc.normal(6, 32)
     g[6, 2] = -np.inf
     g[7] = orc.normal(7, 32) * np.float32(6e4)
-    if dt == orc.Q4_1:  # min over +0 and -0: the first stays
+    if dt in (orc.Q4_1, orc.Q5_1):  # min over +0 and -0: the first stays
         g[1, :16] = 1.0
         g[1, [3, 9]] = [0.0, -0.0]
     rows = [np.roll(g.reshape(-1), 32 * s) for s in range(8)]
@@ -127,29 +130,30 @@ def test_append_q4_special_groups(dt):
     slots = np.array([0, 5, 31, 32, 63, 64, 100, 127], np.int64)
     ref.append(k, v, slots)
     dev.append(to_dev(k), to_dev(v), to_dev(slots))
-    _assert_pools(dev, ref, f"append q4 special dt={dt}")
+    _assert_pools(dev, ref, f"append nibble special dt={dt}")
 
 
-@pytest.mark.parametrize("dt", [orc.Q8_0, orc.Q4_0, orc.Q4_1])
+@pytest.mark.parametrize("dt", [orc.Q8_0, orc.Q4_0, orc.Q4_1, orc.Q5_0, orc.Q5_1])
 def test_append_golden_cases(dt):
     """The committed quantiser fixtures (tests/golden/q8_cases.json,
-    q4_cases.json): each case is one 32-element token row of a D = 32 cache;
-    append, then gather the records and compare them with the fixture bytes."""
+    q4_cases.json, q5_cases.json): each case is one 32-element token row of a
+    D = 32 cache; append, then gather the records and compare them with the
+    fixture bytes."""
     import json
     import os
 
     import torch
 
     golden = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
-    name = "q8_cases.json" if dt == orc.Q8_0 else "q4_cases.json"
-    key = {orc.Q8_0: "record", orc.Q4_0: "q4_0", orc.Q4_1: "q4_1"}[dt]
+    name = {orc.Q8_0: "q8_cases.json", orc.Q5_0: "q5_cases.json", orc.Q5_1: "q5_cases.json"}.get(dt, "q4_cases.json")
+    key = {orc.Q8_0: "record", orc.Q4_0: "q4_0", orc.Q4_1: "q4_1", orc.Q5_0: "q5_0", orc.Q5_1: "q5_1"}[dt]
     cases = json.load(open(os.path.join(golden, name)))
     x = np.stack([np.array(c["x_bits"], np.uint32).view(np.float32) for c in cases]).reshape(-1, 1, 32)
     n = len(cases)
     dev, _ = _pair(4, 8, 1, 32, dt)
     slots = np.arange(n, dtype=np.int64)
     dev.append(to_dev(x), to_dev(-x), to_dev(slots))
-    rb = {orc.Q8_0: 34, orc.Q4_0: 18, orc.Q4_1: 20}[dt]
+    rb = orc.RECORD_BYTES[dt]
     ko = torch.zeros(n * rb, dtype=torch.uint8, device="cuda:0")
     vo = torch.zeros(n * rb, dtype=torch.uint8, device="cuda:0")
     tables = np.arange(4, dtype=np.int32)[None, :]
@@ -189,7 +193,8 @@ def test_append_bad_slot_is_latched_not_written():
 
 
 @pytest.mark.parametrize("dt,D,bs", [(orc.BF16, 128, 16), (orc.F32, 128, 16), (orc.Q8_0, 256, 32),
-                                     (orc.Q4_0, 128, 16), (orc.Q4_1, 256, 32)])
+                                     (orc.Q4_0, 128, 16), (orc.Q4_1, 256, 32), (orc.Q5_0, 128, 16),
+                                     (orc.Q5_0, 256, 32), (orc.Q5_1, 128, 16), (orc.Q5_1, 256, 32)])
 def test_gather_bit_exact(dt, D, bs):
     import torch
 
@@ -227,15 +232,17 @@ def test_gather_bit_exact(dt, D, bs):
         want = np.concatenate(rows).ravel()
         off = int(cu[b]) * hkv * (D // 32) * 34
         np.testing.assert_array_equal(from_dev(ko)[off:off + want.size], want)
-    if dt == orc.Q4_0:  # AoS records equal quantize_row_q4_0 of the source rows
+    quant_row = {orc.Q4_0: orc.quantize_row_q4_0, orc.Q5_0: orc.quantize_row_q5_0,
+                 orc.Q5_1: orc.quantize_row_q5_1}.get(dt)
+    if quant_row is not None:  # AoS records equal the ggml quantiser of the source rows
         b = 3
         rows = []
         for h in range(hkv):
             for i in range(n[b]):
                 t = int(sum(ctx[:b])) + int(start[b]) + i
-                rows.append(orc.quantize_row_q4_0(v[t, h]))
+                rows.append(quant_row(v[t, h]))
         want = np.concatenate(rows).ravel()
-        off = int(cu[b]) * hkv * (D // 32) * 18
+        off = int(cu[b]) * hkv * (D // 32) * orc.RECORD_BYTES[dt]
         np.testing.assert_array_equal(from_dev(vo)[off:off + want.size], want)
 
 
@@ -301,7 +308,8 @@ def _to_cache_src(x, dt):
 
 
 @pytest.mark.parametrize("dt,D,bs", [(orc.BF16, 128, 16), (orc.F32, 128, 16), (orc.F16, 128, 16),
-                                     (orc.Q8_0, 256, 32), (orc.Q4_0, 128, 16), (orc.Q4_1, 256, 32)])
+                                     (orc.Q8_0, 256, 32), (orc.Q4_0, 128, 16), (orc.Q4_1, 256, 32),
+                                     (orc.Q5_0, 128, 16), (orc.Q5_1, 256, 32)])
 def test_append_rope_bit_exact(dt, D, bs):
     """RoPE then append (forward.rs:195-229): the cache pools and the rotated
     q equal the oracle's rope_f32 (rope.rs:6-44) followed by its append,

@@ -15,8 +15,8 @@ from kvutil import (assert_close, assert_close_or_closer, exact_decode, from_dev
 pytestmark = pytest.mark.gpu
 
 TOL = {orc.F32: (1e-5, 1e-6), orc.Q8_0: (1e-5, 1e-6), orc.Q4_0: (1e-5, 1e-6), orc.Q4_1: (1e-5, 1e-6),
-       orc.BF16: (2e-3, 1e-2), orc.F16: (2e-3, 1e-2)}
-QUANT = (orc.Q8_0, orc.Q4_0, orc.Q4_1)
+       orc.Q5_0: (1e-5, 1e-6), orc.Q5_1: (1e-5, 1e-6), orc.BF16: (2e-3, 1e-2), orc.F16: (2e-3, 1e-2)}
+QUANT = orc.QUANT_TYPES
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 
 
@@ -321,7 +321,7 @@ def test_q8_0_decode_d256():
 @pytest.mark.parametrize("dt", QUANT)
 @pytest.mark.parametrize("D", [128, 256])
 def test_quant_group_sizes_and_windows(dt, D):
-    """Q8_0, Q4_0 and Q4_1 (products on MFMA) at every heads-per-workgroup count
+    """Q8_0, Q4_0, Q4_1, Q5_0 and Q5_1 (products on MFMA) at every heads-per-workgroup count
     1..8 (the tiles' padding rows and the second row of four heads), contexts
     that end inside a 16-token group and inside a page, window start
     positions, and two partition sizes; fp32 tolerance against the oracle."""
@@ -354,9 +354,10 @@ def test_quant_block_size_8(dt):
         assert_close_or_closer(got, want, exact, *TOL[dt], what=f"dt={dt} bs=8 P={partition}")
 
 
-@pytest.mark.parametrize("dt", [orc.Q4_0, orc.Q4_1])
-def test_q4_decode_config5_heads(dt):
-    """Config-5 heads (Hq 24, Hkv 4, D 256, bs 32) on a Q4_0 / Q4_1 cache."""
+@pytest.mark.parametrize("dt", [orc.Q4_0, orc.Q4_1, orc.Q5_0, orc.Q5_1])
+def test_nibble_decode_config5_heads(dt):
+    """Config-5 heads (Hq 24, Hkv 4, D 256, bs 32) on a Q4_0 / Q4_1 / Q5_0 /
+    Q5_1 cache."""
     hq, hkv, D, bs = 24, 4, 256, 32
     dev, ref, tables, ctx, q, qdt = _build(dt, hq, hkv, D, bs, [3000, 1025, 33], seed=9)
     scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
