@@ -779,6 +779,252 @@ def bench_q4(dtype, steps, warmup):
     return res
 
 
+def _probe_copies(rs):
+    """Counter values of the --copy-probe copies: the first four 256 MiB
+    copyBuffer dispatches of the run (later pool fills use the same kernel
+    and grid and are not the probe)."""
+    cp = sorted(((int(r["Dispatch_Id"]), float(r["Counter_Value"])) for r in rs
+                 if "copyBuffer" in r["Kernel_Name"] and r["Grid_Size"] == "131072"))
+    return [v for _, v in cp[:4]]
+
+
+# ---- data-movement kernels under rocprofv3 ------------------------------------
+MOVER_WARM, MOVER_REPS = 3, 20
+MOVER_SQ = ["SQ_WAVES", "SQ_INSTS_VMEM_RD", "SQ_INSTS_VMEM_WR", "SQ_INSTS_VALU", "SQ_INSTS_SALU", "SQ_INSTS_SMEM",
+            "SQ_INSTS_LDS", "SQ_BUSY_CYCLES"]
+
+
+def movers_plan():
+    """The workloads of `--only-movers`, in launch order: (name, kernel-name
+    substring, what it is, algorithmic bytes read, written).  Each runs
+    MOVER_WARM + MOVER_REPS launches; the summary takes the last MOVER_REPS
+    of each (workloads of one kernel are told apart by that order)."""
+    bf, d128, d256 = 2, 128, 256
+    c3_tok = 8 * 512  # config 3's chunk: 8 sequences x 512 tokens, Hkv 8
+    c2_tok = 32       # config 2's step: one token per sequence, Hkv 4
+    q8_tok = 4096     # a config-5-shaped chunk (Hkv 4, D 256), fp32 source
+    g_tok = 32 * 4096  # config 2 at 4k gathered (Hkv 4)
+    gq_tok = 4 * 8192  # four config-5 sequences of 8192 tokens (Q8_0, Hkv 4)
+    ev_big, ev_c4 = 4096, 64  # blocks cleared per call (config-4 pages: Hkv 2, 4 KiB)
+    c4_kv = 64 * 4096 * 2 * d128 * bf * 2  # config 4: 64 windows of 4096 tokens, K and V
+    return [
+        ("append_copy_c2_step", "kv_append_copy", "config 2 step: 32 tokens, bf16, Hkv 4, D 128",
+         c2_tok * 4 * d128 * bf * 2, c2_tok * 4 * d128 * bf * 2),
+        ("append_copy_c3_chunk", "kv_append_copy", "config 3 chunk: 8 x 512 tokens, bf16, Hkv 8, D 128",
+         c3_tok * 8 * d128 * bf * 2, c3_tok * 8 * d128 * bf * 2),
+        ("append_quant_q8_0_chunk", "kv_append_quant<8>", "Q8_0 quantise-append of 4096 tokens, Hkv 4, D 256",
+         q8_tok * 4 * d256 * 4 * 2, q8_tok * 4 * d256 * 34 // 32 * 2),
+        ("gather_bf16_c2_4k", "kv_gather_vec", "gather of config 2 at 4k: 32 x 4096 tokens, bf16, Hkv 4",
+         g_tok * 4 * d128 * bf * 2, g_tok * 4 * d128 * bf * 2),
+        ("gather_q8_0_c5", "kv_gather_q8_0", "gather of 4 x 8192 Q8_0 tokens as BlockQ8_0 records, Hkv 4, D 256",
+         gq_tok * 4 * d256 * 34 // 32 * 2, gq_tok * 4 * d256 * 34 // 32 * 2),
+        ("clear_blocks_4096", "kv_clear_blocks", "evict 4096 config-4 blocks (2 heads x 4 KiB, K and V)",
+         ev_big * 4, ev_big * 2 * 4096 * 2),
+        ("clear_blocks_c4_step", "kv_clear_blocks", "evict 64 config-4 blocks (one window step's frees)",
+         ev_c4 * 4, ev_c4 * 2 * 4096 * 2),
+        ("decode_window_c4", "paged_decode_split", "config 4 decode: 64 windows of 4096 tokens, bf16, Hq 16 / Hkv 2",
+         c4_kv, 0),
+    ]
+
+
+def run_movers():
+    """Launch every movers_plan() workload MOVER_WARM + MOVER_REPS times (for
+    rocprofv3 runs; prints one JSON line of mean event times)."""
+    import torch
+
+    import infer_train_amd as it
+    from infer_train_amd.kv import PagedKvCache, decode_partition
+
+    dev = _dev()
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    rng = np.random.default_rng(7)
+    times = {}
+
+    def timed(name, fn):
+        for _ in range(MOVER_WARM):
+            fn()
+        torch.cuda.synchronize()
+        ev = _events(2)
+        ev[0].record()
+        for _ in range(MOVER_REPS):
+            fn()
+        ev[1].record()
+        torch.cuda.synchronize()
+        times[name] = round(ev[0].elapsed_time(ev[1]) * 1e3 / MOVER_REPS, 2)
+        _progress(f"movers: {name} {times[name]} us")
+
+    def bf16(*shape):
+        return torch.randn(shape, generator=g, device=dev).to(torch.bfloat16)
+
+    # appends (bf16 copies)
+    c2 = PagedKvCache(16384, 16, 4, 128, it.BF16)
+    sl2 = torch.from_numpy(rng.permutation(16384 * 16)[:32].astype(np.int64)).to(dev)
+    k2, v2 = bf16(32, 4, 128), bf16(32, 4, 128)
+    timed("append_copy_c2_step", lambda: c2.append(k2, v2, sl2))
+    c3 = PagedKvCache(4096, 16, 8, 128, it.BF16)
+    sl3 = torch.from_numpy(rng.permutation(4096 * 16)[:4096].astype(np.int64)).to(dev)
+    k3, v3 = bf16(4096, 8, 128), bf16(4096, 8, 128)
+    timed("append_copy_c3_chunk", lambda: c3.append(k3, v3, sl3))
+    del c3, k3, v3
+    # Q8_0 quantise-append
+    c5 = PagedKvCache(8192, 32, 4, 256, it.Q8_0)
+    sl5 = torch.from_numpy(rng.permutation(8192 * 32)[:4096].astype(np.int64)).to(dev)
+    k5 = torch.randn((4096, 4, 256), generator=g, device=dev)
+    v5 = torch.randn((4096, 4, 256), generator=g, device=dev)
+    timed("append_quant_q8_0_chunk", lambda: c5.append(k5, v5, sl5))
+    del k5, v5
+    # gathers
+    c2.view("k").copy_(bf16(*c2.view("k").shape))
+    c2.view("v").copy_(bf16(*c2.view("v").shape))
+    perm = rng.permutation(16384).astype(np.int32)
+    t2 = torch.from_numpy(perm[:32 * 256].reshape(32, 256).copy()).to(dev)
+    ctx2 = torch.full((32,), 4096, dtype=torch.int32, device=dev)
+    cu2 = torch.arange(32, dtype=torch.int64, device=dev) * 4096
+    ko = torch.empty(32 * 4096 * 4 * 128 * 2, dtype=torch.uint8, device=dev)
+    vo = torch.empty_like(ko)
+    timed("gather_bf16_c2_4k", lambda: c2.gather(t2, ctx2, None, cu2, 4096, ko, vo))
+    del ko, vo
+    perm5 = rng.permutation(8192).astype(np.int32)
+    t5 = torch.from_numpy(perm5[:4 * 256].reshape(4, 256).copy()).to(dev)
+    ctx5 = torch.full((4,), 8192, dtype=torch.int32, device=dev)
+    cu5 = torch.arange(4, dtype=torch.int64, device=dev) * 8192
+    rec = 4 * 8192 * 4 * (256 // 32) * 34
+    kq, vq = torch.empty(rec, dtype=torch.uint8, device=dev), torch.empty(rec, dtype=torch.uint8, device=dev)
+    timed("gather_q8_0_c5", lambda: c5.gather(t5, ctx5, None, cu5, 8192, kq, vq))
+    del c5, kq, vq
+    # evict (config-4 pages)
+    c4 = PagedKvCache(16512, 16, 2, 128, it.BF16)
+    big = torch.from_numpy(rng.permutation(16512)[:4096].astype(np.int32)).to(dev)
+    small = torch.from_numpy(rng.permutation(16512)[:64].astype(np.int32)).to(dev)
+    timed("clear_blocks_4096", lambda: c4.evict(big))
+    timed("clear_blocks_c4_step", lambda: c4.evict(small))
+    # config-4 windowed decode: 64 sequences at position 32000, window 4096
+    c4.view("k").copy_(bf16(*c4.view("k").shape))
+    c4.view("v").copy_(bf16(*c4.view("v").shape))
+    mb = 32768 // 16 + 1
+    ctx4 = np.full(64, 32000, np.int32)
+    st4 = ctx4 - 4096
+    t4 = np.full((64, mb), -1, np.int32)
+    p4 = rng.permutation(16512).astype(np.int32)
+    k = 0
+    for s in range(64):
+        lo, hi = st4[s] // 16, (ctx4[s] - 1) // 16
+        t4[s, lo:hi + 1] = p4[k:k + hi - lo + 1]
+        k += hi - lo + 1
+    P = decode_partition(it.BF16, 128, 16, 16, 2, np.full(64, 4096))
+    q4 = bf16(64, 16, 128)
+    out4 = torch.empty_like(q4)
+    ws = c4.decode_workspace(64, 16, 4096, P)
+    t4d, c4d, s4d = (torch.from_numpy(x).to(dev) for x in (t4, ctx4, st4))
+    timed("decode_window_c4", lambda: c4.decode(q4, t4d, c4d, s4d, 4096, partition=P, out=out4, ws=ws))
+    print(json.dumps({"only_movers": True, "event_us": times}), flush=True)
+
+
+def summarize_movers_profile(d, args):
+    """Summarise rocprofv3 CSVs of `bench.py --only-movers --copy-probe`
+    runs (DIR/trace, DIR/fetch, DIR/write, DIR/sq) into
+    profiles/data_movement.md: per workload the kernel-trace duration, HBM
+    bytes fetched / written (counters calibrated by the 256 MiB copy)
+    against the algorithmic bytes, and bytes per VMEM instruction."""
+    import csv
+
+    def rows(sub, name):
+        path = os.path.join(d, sub, "run_" + name + ".csv")
+        return list(csv.DictReader(open(path))) if os.path.exists(path) else []
+
+    plan = movers_plan()
+
+    def assign(rs, key_name, key_id):
+        """Map each plan entry to the dispatch ids of its last MOVER_REPS launches."""
+        by_kernel = {}
+        for r in rs:
+            by_kernel.setdefault(r[key_name], set()).add(int(r[key_id]))
+        out, used = {}, {}
+        for name, ksub, _, _, _ in plan:
+            ids = sorted(i for kn, s in by_kernel.items() if ksub in kn for i in s)
+            start = used.get(ksub, 0)
+            mine = ids[start:start + MOVER_WARM + MOVER_REPS]
+            used[ksub] = start + MOVER_WARM + MOVER_REPS
+            out[name] = set(mine[MOVER_WARM:])
+        return out
+
+    trace = rows("trace", "kernel_trace")
+    ids_t = assign(trace, "Kernel_Name", "Dispatch_Id")
+    dur = {}
+    for name in ids_t:
+        ds = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in trace
+              if int(r["Dispatch_Id"]) in ids_t[name]]
+        dur[name] = float(np.mean(ds)) if ds else float("nan")
+
+    def counter(sub):
+        rs = rows(sub, "counter_collection")
+        copy = _probe_copies(rs)
+        ids = assign(rs, "Kernel_Name", "Dispatch_Id")
+        per = {}
+        for name, idset in ids.items():
+            acc = {}
+            for r in rs:
+                if int(r["Dispatch_Id"]) in idset:
+                    acc.setdefault(r["Counter_Name"], {}).setdefault(r["Dispatch_Id"], 0.0)
+                    acc[r["Counter_Name"]][r["Dispatch_Id"]] += float(r["Counter_Value"])
+            per[name] = {k: float(np.median(list(v.values()))) for k, v in acc.items()}
+        return (float(np.mean(copy)) if copy else float("nan")), per
+
+    f_copy, fetch = counter("fetch")
+    w_copy, write = counter("write")
+    _, sq = counter("sq")
+    f_scale = (256 << 20) / (f_copy * 1024.0)
+    w_scale = (256 << 20) / (w_copy * 1024.0)
+    cmd = "python3 bench.py --only-movers --copy-probe"
+    lines = ["# Data-movement kernels and the config-4 windowed decode: time, HBM traffic, access width", "",
+             "Commands (from the repository root on the GPU box; `cd /tmp && export TMPDIR=/tmp` first):", "",
+             "```",
+             f"rocprofv3 --kernel-trace --stats --output-format csv -d OUT/trace -o run -- {cmd}",
+             f"rocprofv3 --pmc FETCH_SIZE --output-format csv -d OUT/fetch -o run -- {cmd}",
+             f"rocprofv3 --pmc WRITE_SIZE --output-format csv -d OUT/write -o run -- {cmd}",
+             f"rocprofv3 --pmc {' '.join(MOVER_SQ)} --output-format csv -d OUT/sq -o run -- {cmd}",
+             "python3 bench.py --summarize-movers-profile OUT",
+             "```", "",
+             f"Counter calibration: a 256 MiB device copy (`__amd_rocclr_copyBuffer`, grid 131072) reads {f_copy:.0f} "
+             f"KiB by FETCH_SIZE and writes {w_copy:.0f} KiB by WRITE_SIZE, so one counted byte is {f_scale:.3f} B "
+             f"fetched and {w_scale:.3f} B written.  Each workload: {MOVER_WARM} warm-up launches, then "
+             f"{MOVER_REPS} measured (kernel-trace mean; counters median over the measured dispatches).", "",
+             "| Workload | Kernel | us | Alg. read MB | Alg. write MB | HBM fetch MB | HBM write MB | traffic / alg. "
+             "| GB/s (alg.) | % of 8 TB/s | VMEM_RD | VMEM_WR | B per VMEM op |",
+             "|---|---|---|---|---|---|---|---|---|---|---|---|---|"]
+    for name, ksub, what, rd, wr in plan:
+        t = dur.get(name, float("nan"))
+        fb = fetch.get(name, {}).get("FETCH_SIZE", float("nan")) * 1024.0 * f_scale
+        wb = write.get(name, {}).get("WRITE_SIZE", float("nan")) * 1024.0 * w_scale
+        s = sq.get(name, {})
+        vr, vw = s.get("SQ_INSTS_VMEM_RD", float("nan")), s.get("SQ_INSTS_VMEM_WR", float("nan"))
+        alg = rd + wr
+        gbs = alg / (t * 1e-6) / 1e9 if t == t and t > 0 else float("nan")
+        per_op = alg / (vr + vw) if (vr + vw) > 0 else float("nan")
+        lines.append(f"| {name}: {what} | `{ksub}` | {t:.2f} | {rd / 1e6:.2f} | {wr / 1e6:.2f} | {fb / 1e6:.2f} | "
+                     f"{wb / 1e6:.2f} | {(fb + wb) / alg:.3f} | {gbs:.0f} | {100 * gbs / HBM_PEAK_GBS:.1f} | "
+                     f"{vr:.0f} | {vw:.0f} | {per_op:.0f} |")
+    lines += ["", "## SQ counters (median per dispatch)", "", "| Workload | " + " | ".join(MOVER_SQ) + " |",
+              "|---|" + "---|" * len(MOVER_SQ)]
+    for name, *_ in plan:
+        s = sq.get(name, {})
+        lines.append(f"| {name} | " + " | ".join(f"{s.get(k, float('nan')):.0f}" for k in MOVER_SQ) + " |")
+    lines += ["", "Reading the table: a wave-level VMEM instruction of 64 lanes x 16 B moves 1024 B, so "
+                  "'B per VMEM op' near 1024 means every load and store is a 16-byte-per-lane access "
+                  "(global_load_dwordx4 / global_store_dwordx4, or global_load_lds_dwordx4 in the decode); "
+                  "'traffic / alg.' near 1.0 means no byte is fetched or written twice.  The VMEM counts also "
+                  "hold the small index loads: the appends read one int64 slot per wave and four 16-byte "
+                  "vectors (kv_append_copy: 16384 data loads + 8192 slot loads = 24576 for config 3, every data "
+                  "load and store 1024 B); the gathers read block-table entries; the decode's VMEM_WR are its "
+                  "(m, l, O) partials.  The Q8_0 quantise-append stores 4 int8 per lane (8 lanes per 32-group) "
+                  "and one fp16 scale per group, so its stores are 256 B and 16 B per wave instruction; its "
+                  "loads are 16 B per lane."]
+    os.makedirs(os.path.join(ROOT, "profiles"), exist_ok=True)
+    open(os.path.join(ROOT, "profiles", "data_movement.md"), "w").write("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
 def summarize_profile(d, args):
     """Summarise rocprofv3 CSVs of `bench.py --only-headline --copy-probe`
     runs: DIR/trace (--kernel-trace --stats), DIR/fetch (--pmc FETCH_SIZE),
@@ -799,7 +1045,7 @@ def summarize_profile(d, args):
 
     def counter(sub, cname):
         rs = rows(sub, "counter_collection")
-        copy = [float(r["Counter_Value"]) for r in rs if "copyBuffer" in r["Kernel_Name"] and r["Grid_Size"] == "131072"]
+        copy = _probe_copies(rs)
         dec = [float(r["Counter_Value"]) for r in rs if kname in r["Kernel_Name"]]
         return float(np.mean(copy)), float(np.mean(dec)), len(dec)
 
@@ -1016,6 +1262,10 @@ def main():
                     help="run only config 3 (chunk append + causal prefill) (for rocprofv3 runs)")
     ap.add_argument("--summarize-prefill-profile", metavar="DIR",
                     help="CPU only: summarise rocprofv3 output of --only-prefill runs into profiles/")
+    ap.add_argument("--only-movers", action="store_true",
+                    help="run only the data-movement kernels and the config-4 decode (for rocprofv3 runs)")
+    ap.add_argument("--summarize-movers-profile", metavar="DIR",
+                    help="CPU only: summarise rocprofv3 output of --only-movers runs into profiles/data_movement.md")
     ap.add_argument("--summarize-profile", metavar="DIR",
                     help="CPU only: summarise rocprofv3 output DIR/{trace,fetch,write} of an --only-headline "
                          "--copy-probe run into profiles/")
@@ -1028,6 +1278,9 @@ def main():
         return
     if args.summarize_config5_profile:
         summarize_config5_profile(args.summarize_config5_profile, args)
+        return
+    if args.summarize_movers_profile:
+        summarize_movers_profile(args.summarize_movers_profile, args)
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus > 1 is not supported. Decode would shard by "
@@ -1047,6 +1300,10 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+
+    if args.only_movers:
+        run_movers()
+        return
 
     if args.only_config5:
         r = bench_config5(args.steps, args.warmup, False)
