@@ -1118,6 +1118,39 @@ PREFILL_SQ = [["SQ_WAVES", "SQ_INSTS_VALU", "SQ_INSTS_MFMA", "SQ_INSTS_LDS", "SQ
                "SQ_ACTIVE_INST_LDS", "SQ_INSTS_VALU_MFMA_MOPS_BF16", "SQ_WAIT_ANY", "SQ_INSTS_VMEM_RD"]]
 
 
+def _traffic_lines(d, kname, alg_bytes, what):
+    """Lines for a summary: HBM bytes per launch of kernel `kname` from
+    DIR/fetch and DIR/write (--pmc FETCH_SIZE / WRITE_SIZE of a --copy-probe
+    run), calibrated by the probe's 256 MiB copies, against `alg_bytes`."""
+    import csv
+
+    out = []
+    vals = {}
+    for sub, cname in (("fetch", "FETCH_SIZE"), ("write", "WRITE_SIZE")):
+        path = os.path.join(d, sub, "run_counter_collection.csv")
+        if not os.path.exists(path):
+            return out
+        rs = list(csv.DictReader(open(path)))
+        copy = _probe_copies(rs)
+        per = {}
+        for r in rs:
+            if kname in r["Kernel_Name"] and r["Counter_Name"] == cname:
+                per[r["Dispatch_Id"]] = per.get(r["Dispatch_Id"], 0.0) + float(r["Counter_Value"])
+        if not copy or not per:
+            return out
+        scale = (256 << 20) / (float(np.mean(copy)) * 1024.0)
+        vals[sub] = (float(np.median(list(per.values()))) * 1024.0 * scale, scale, len(per))
+    fb, fs, nf = vals["fetch"]
+    wb, ws, nw = vals["write"]
+    out += ["", "## HBM traffic per launch (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, calibrated)", "",
+            f"Calibration: the probe's 256 MiB copies give {fs:.3f} B per counted FETCH byte and {ws:.3f} B per "
+            "counted WRITE byte.", "",
+            f"{nf} / {nw} dispatches (median): fetched {fb / 1e6:.2f} MB, written {wb / 1e6:.2f} MB, total "
+            f"{(fb + wb) / 1e6:.2f} MB per launch against {alg_bytes / 1e6:.2f} MB algorithmic ({what}): "
+            f"{(fb + wb) / alg_bytes:.3f}x."]
+    return out
+
+
 def summarize_prefill_profile(d, args):
     """Summarise rocprofv3 CSVs of `bench.py --only-prefill` runs: DIR/trace
     (--kernel-trace --stats) and DIR/sq0, DIR/sq1 (--pmc, PREFILL_SQ) into
@@ -1132,11 +1165,13 @@ def summarize_prefill_profile(d, args):
     trace = [r for r in rows("trace", "kernel_trace") if kname in r["Kernel_Name"]]
     durs = np.array([(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in trace])
     flops = 4.0 * 128 * 32 * 8 * sum(2048 + i + 1 for i in range(512))  # config 3, as bench_config3
-    cmd = "python3 bench.py --only-prefill --steps {s} --warmup {w}".format(s=args.steps, w=args.warmup)
+    cmd = "python3 bench.py --only-prefill --steps {s} --warmup {w} --copy-probe".format(s=args.steps, w=args.warmup)
     lines = ["# paged_prefill_kernel -- config 3 (8 x 512-token chunks over 2048 cached, causal, bf16)", "",
              "Commands (from the repository root on the GPU box; `cd /tmp && export TMPDIR=/tmp` first):", "",
              "```",
-             f"rocprofv3 --kernel-trace --stats --output-format csv -d OUT/trace -o run -- {cmd}"]
+             f"rocprofv3 --kernel-trace --stats --output-format csv -d OUT/trace -o run -- {cmd}",
+             f"rocprofv3 --pmc FETCH_SIZE --output-format csv -d OUT/fetch -o run -- {cmd}",
+             f"rocprofv3 --pmc WRITE_SIZE --output-format csv -d OUT/write -o run -- {cmd}"]
     for i, grp in enumerate(PREFILL_SQ):
         lines.append(f"rocprofv3 --pmc {' '.join(grp)} --output-format csv -d OUT/sq{i} -o run -- {cmd}")
     lines += [f"python3 bench.py --summarize-prefill-profile OUT --steps {args.steps} --warmup {args.warmup}", "```",
@@ -1149,6 +1184,9 @@ def summarize_prefill_profile(d, args):
                   f"{np.median(durs):.2f} us -> {tf:.1f} TFLOP/s of algorithmic flops ({flops} per launch: "
                   f"4 D Hq sum over query rows of keys attended) = {100 * tf / MFMA_BF16_PEAK_TFS:.1f}% of the "
                   f"{MFMA_BF16_PEAK_TFS:.0f} TFLOP/s dense bf16 peak."]
+    # q [8 x 512][32][128] bf16 read, out written (bf16), K/V of 2560 keys x 8 sequences x 8 heads read
+    alg = 2 * (8 * 512 * 32 * 128 * 2) + 8 * 2560 * 8 * 128 * 2 * 2
+    lines += _traffic_lines(d, kname, alg, "q and out 33.5 MB each, the 8 sequences' K/V pages 83.9 MB")
     med = {}
     for i in range(len(PREFILL_SQ)):
         sub = f"sq{i}"
@@ -1196,12 +1234,14 @@ def summarize_config5_profile(d, args):
     ctx = rng.integers(32768, 131073, 16)
     kv_bytes = float(ctx.astype(np.int64).sum()) * 4 * 2 * 256 * 34 / 32
     part = decode_partition(it.Q8_0, 256, 32, 24, 4, ctx, None, 256)
-    cmd = "python3 bench.py --only-config5 --steps {s} --warmup {w}".format(s=args.steps, w=args.warmup)
+    cmd = "python3 bench.py --only-config5 --steps {s} --warmup {w} --copy-probe".format(s=args.steps, w=args.warmup)
     lines = ["# paged_decode_split (Q8_0, D 256) -- config 5 (batch 16, ctx U[32768, 131072], "
              f"Hq 24 / Hkv 4, {part}-token partitions)", "",
              "Commands (from the repository root on the GPU box; `cd /tmp && export TMPDIR=/tmp` first):", "",
              "```",
-             f"rocprofv3 --kernel-trace --stats --output-format csv -d OUT/trace -o run -- {cmd}"]
+             f"rocprofv3 --kernel-trace --stats --output-format csv -d OUT/trace -o run -- {cmd}",
+             f"rocprofv3 --pmc FETCH_SIZE --output-format csv -d OUT/fetch -o run -- {cmd}",
+             f"rocprofv3 --pmc WRITE_SIZE --output-format csv -d OUT/write -o run -- {cmd}"]
     for i, grp in enumerate(PREFILL_SQ):
         lines.append(f"rocprofv3 --pmc {' '.join(grp)} --output-format csv -d OUT/sq{i} -o run -- {cmd}")
     lines += [f"python3 bench.py --summarize-config5-profile OUT --steps {args.steps} --warmup {args.warmup}", "```",
@@ -1213,6 +1253,7 @@ def summarize_config5_profile(d, args):
     lines += ["", f"Split kernel, kernel trace: {durs.size} dispatches, mean {durs.mean():.2f} us, median "
                   f"{np.median(durs):.2f} us -> {gbs:.0f} GB/s of KV bytes ({kv_bytes:.0f} per launch) = "
                   f"{100 * gbs / HBM_PEAK_GBS:.1f}% of {HBM_PEAK_GBS:.0f} GB/s."]
+    lines += _traffic_lines(d, kname, kv_bytes, "the Q8_0 K/V pages of every context, qs and scales")
     med = {}
     for i in range(len(PREFILL_SQ)):
         sub = f"sq{i}"
