@@ -5,14 +5,16 @@ Headline (`value`): config 2 at its 4k target -- batched paged decode,
 bf16, Hq 28 / Hkv 4 / D 128, block size 16, batch 32 with every sequence at
 4096 tokens after the step's append, pages a seeded permutation of a
 16384-block pool, split-K over 512-token partitions (the host planner's choice).  One step = slot-mapped
-append of 1 token per sequence + split-K decode + combine; value = KV bytes
-read per step / median(split + combine time) over the timed steps, the
-algorithmic bytes sum_b ctx_b * Hkv * 2 * D * 2.  Three pool replicas are
-rotated so the 256 MB last-level cache does not hold the previous step's
-pages (cold); warm numbers (one replica) and the decode captured in a HIP
-graph are reported beside it.  Kernel times are HIP events recorded on the
-stream the kernels run on (torch's current stream); the roofline's kernel
-time is the mean of back-to-back split launches between two events.
+append of 1 token per sequence + split-K decode + combine.  The timed region
+is K whole steps back to back between two HIP events, synchronised on both
+sides (ms_per_step); value = KV bytes read per decode / the decode's time
+(split + combine) in K decodes issued back to back, the algorithmic bytes
+sum_b ctx_b * Hkv * 2 * D * 2.  Three pool replicas are rotated so the
+256 MB last-level cache does not hold the previous step's pages (cold);
+warm numbers (one replica) and the decode captured in a HIP graph are
+reported beside it.  Kernel times are HIP events recorded on the stream the
+kernels run on (torch's current stream); the roofline's kernel time is the
+mean of back-to-back split launches between two events.
 
 The other configs run at their full shapes and are reported under
 "configs": config 1 (fp32 single-sequence step), config 2 as specified
@@ -93,6 +95,29 @@ def _cpu_model():
 # ---------------------------------------------------------------------------
 # Decode (configs 1, 2, 5)
 # ---------------------------------------------------------------------------
+_SLEEP_CYCLES_PER_MS = None
+
+
+def _gpu_hold(ms):
+    """Queue a GPU spin of about `ms` milliseconds on the current stream
+    (torch.cuda._sleep, a loop over a fixed clock count, so it always ends):
+    the kernels the host enqueues next are queued before the GPU reaches
+    them, and events around them time the GPU, not the Python harness's
+    enqueue rate (a native caller of the C ABI enqueues in microseconds)."""
+    global _SLEEP_CYCLES_PER_MS
+    import torch
+
+    if _SLEEP_CYCLES_PER_MS is None:
+        torch.cuda.synchronize()
+        e0, e1 = _events(2)
+        e0.record()
+        torch.cuda._sleep(200000)
+        e1.record()
+        torch.cuda.synchronize()
+        _SLEEP_CYCLES_PER_MS = 200000 / max(e0.elapsed_time(e1), 1e-3)
+    torch.cuda._sleep(int(_SLEEP_CYCLES_PER_MS * ms))
+
+
 class DecodeWorkload:
     """A paged decode batch with `replicas` copies of the pools."""
 
@@ -129,7 +154,7 @@ class DecodeWorkload:
         self.caches = []
         for _ in range(replicas):
             c = PagedKvCache(pool_blocks, bs, hkv, D, dtype)
-            if dtype in (it.Q8_0, it.Q4_0, it.Q4_1):
+            if dtype in it.QUANT_TYPES:
                 # Only the pages the tables name are filled, through the
                 # quantising append (N(0,1) with 1% of elements x8).
                 used = np.concatenate([t[b, : (int(cc) + bs - 1) // bs] for b, cc in enumerate(self.ctx)])
@@ -148,10 +173,10 @@ class DecodeWorkload:
                 c.view("k").copy_(torch.randn(c.view("k").shape, generator=g, device=dev).to(td))
                 c.view("v").copy_(torch.randn(c.view("v").shape, generator=g, device=dev).to(td))
             self.caches.append(c)
-        qd = {it.Q8_0: torch.float32, it.Q4_0: torch.float32, it.Q4_1: torch.float32, it.F32: torch.float32,
-              it.BF16: torch.bfloat16, it.F16: torch.float16}[dtype]
+        qd = torch.float32 if dtype in it.QUANT_TYPES + (it.F32,) else {it.BF16: torch.bfloat16,
+                                                                        it.F16: torch.float16}[dtype]
         self.q = torch.randn((B, hq, D), generator=g, device=dev).to(qd)
-        src_t = torch.float32 if dtype in (it.Q8_0, it.Q4_0, it.Q4_1, it.F32) else qd
+        src_t = torch.float32 if dtype in it.QUANT_TYPES + (it.F32,) else qd
         self.k_new = torch.randn((B, hkv, D), generator=g, device=dev).to(src_t)
         self.v_new = torch.randn((B, hkv, D), generator=g, device=dev).to(src_t)
         self.out = torch.empty((B, hq, D), dtype=qd, device=dev)
@@ -159,9 +184,9 @@ class DecodeWorkload:
         self.ws = self.caches[0].decode_workspace(B, hq, self.max_tokens, partition)
         self.scale = 1.0 / math.sqrt(D)
         elem = {it.BF16: 2.0, it.F16: 2.0, it.F32: 4.0, it.Q8_0: 34.0 / 32.0, it.Q4_0: 18.0 / 32.0,
-                it.Q4_1: 20.0 / 32.0}[dtype]
+                it.Q4_1: 20.0 / 32.0, it.Q5_0: 22.0 / 32.0, it.Q5_1: 24.0 / 32.0}[dtype]
         self.kv_bytes = float(self.ctx.astype(np.int64).sum()) * hkv * 2 * D * elem
-        src_elem = 4.0 if dtype in (it.Q8_0, it.Q4_0, it.Q4_1, it.F32) else 2.0
+        src_elem = 4.0 if dtype in it.QUANT_TYPES + (it.F32,) else 2.0
         self.append_bytes = B * hkv * 2 * D * (src_elem + elem)
 
     def _split(self, c):
@@ -196,21 +221,46 @@ class DecodeWorkload:
         self._combine(c)
 
     def time(self, steps, warmup, rotate=True):
-        """Per-kernel times (ms) over `steps` event-bracketed steps: mean and
-        median of append and of decode (split + combine), wall per step; then
-        `steps` more steps with events around the split kernel alone (its mean
-        is the roofline's kernel duration)."""
+        """Times in ms.  The timed region: `steps` whole steps (append ->
+        split -> combine, replicas rotated) back to back between two events,
+        synchronised on both sides: step_b2b per step (and wall).  Then
+        `steps` decodes (split + combine) back to back: decode_b2b; `steps`
+        split launches back to back: split_b2b (the roofline's kernel
+        duration).  Then per-step event brackets (append, decode, split
+        alone): means and medians, which carry each bracket's own event
+        overhead."""
         torch = self.torch
         n_rep = len(self.caches) if rotate else 1
         for i in range(warmup):
             self.step(i % n_rep)
         torch.cuda.synchronize()
-        evs = [_events(3) for _ in range(steps)]
+        hold = 2.0 + 0.2 * steps  # ms: more than the harness needs to enqueue the steps
         t0 = time.perf_counter()
+        _gpu_hold(hold)
+        e0, e1 = _events(2)
+        e0.record()
+        h0 = time.perf_counter()
+        for i in range(steps):
+            self.step(i % n_rep)
+        enq = (time.perf_counter() - h0) * 1e3
+        e1.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        step_b2b = e0.elapsed_time(e1) / steps
+        _gpu_hold(hold)
+        e0, e1 = _events(2)
+        e0.record()
+        for i in range(steps):
+            c = self.caches[i % n_rep]
+            self._split(c)
+            self._combine(c)
+        e1.record()
+        torch.cuda.synchronize()
+        decode_b2b = e0.elapsed_time(e1) / steps
+        evs = [_events(3) for _ in range(steps)]
         for i in range(steps):
             self.step(i % n_rep, evs[i])
         torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
         app = np.array([e[0].elapsed_time(e[1]) for e in evs])
         dec = np.array([e[1].elapsed_time(e[2]) for e in evs])
         evs2 = [_events(2) for _ in range(steps)]
@@ -221,6 +271,7 @@ class DecodeWorkload:
         # The split kernel alone, `steps` launches back to back between two
         # events (replicas rotated): its mean launch duration, without the
         # per-bracket event overhead of single launches.
+        _gpu_hold(hold)
         e0, e1 = _events(2)
         e0.record()
         for i in range(steps):
@@ -233,7 +284,8 @@ class DecodeWorkload:
         return {"append": float(app.mean()), "append_median": float(np.median(app)), "decode": float(dec.mean()),
                 "decode_median": float(np.median(dec)), "split": float(split.mean()),
                 "split_median": float(np.median(split)), "split_b2b": float(split_b2b),
-                "step_wall": wall * 1e3 / steps}
+                "decode_b2b": float(decode_b2b), "step_b2b": float(step_b2b), "step_wall": wall * 1e3 / steps,
+                "enqueue_per_step": enq / steps, "hold_ms": hold}
 
     def time_graph(self, replays, rotate=True):
         """split + combine captured in one HIP graph per pool replica, as a
@@ -267,6 +319,7 @@ class DecodeWorkload:
             graphs[i % n_rep].replay()
         t = []
         for _ in range(5):
+            _gpu_hold(2.0 + 0.05 * replays)
             e0, e1 = _events(2)
             e0.record()
             for i in range(replays):
@@ -431,13 +484,14 @@ def bench_config2(steps, warmup, cpu):
     p2 = decode_partition(it.BF16, 128, 16, 28, 4, ctx2)
     w2 = DecodeWorkload(it.BF16, 28, 4, 128, 16, ctx2, 16384, p2, seed=3)
     r2 = w2.time(steps, warmup, rotate=True)
-    dm = r2["decode_median"]
+    dm = r2["decode_b2b"]
     ragged = {"workload": f"config 2 as specified: ctx U[256, 4096] + 1 appended, batch 32, {p2}-token partitions "
                           "(host planner)",
               "kv_gbs": round(w2.kv_bytes / (dm * 1e-3) / 1e9, 1), "decode_us": round(dm * 1e3, 2),
-              "decode_us_mean": round(r2["decode"] * 1e3, 2), "split_us": round(r2["split_b2b"] * 1e3, 2),
+              "decode_us_single_bracket": round(r2["decode_median"] * 1e3, 2),
+              "split_us": round(r2["split_b2b"] * 1e3, 2),
               "kv_bytes": int(w2.kv_bytes), "append_us": round(r2["append_median"] * 1e3, 2),
-              "steps_per_s": round(1e3 / (r2["append_median"] + dm), 1),
+              "step_us": round(r2["step_b2b"] * 1e3, 2), "steps_per_s": round(1e3 / r2["step_b2b"], 1),
               "pct_hbm_peak": round(100 * w2.kv_bytes / (dm * 1e-3) / 1e9 / HBM_PEAK_GBS, 2)}
     w2.release()
     torch.cuda.empty_cache()
@@ -727,16 +781,16 @@ def bench_config5(steps, warmup, cpu):
     P = decode_partition(it.Q8_0, 256, 32, 24, 4, ctx)
     w = DecodeWorkload(it.Q8_0, 24, 4, 256, 32, ctx, pool_blocks, P, seed=5, replicas=1)
     r = w.time(steps, warmup, rotate=False)
-    dm, am = r["decode_median"], r["append_median"]
+    dm, am = r["decode_b2b"], r["append_median"]
     res = {"workload": "config 5: Q8_0 KV, Hq 24 / Hkv 4 / D 256, block 32, batch 16, ctx U[32768, 131072], "
                        f"quantise-append 1 token per sequence + split-K decode ({P}-token partitions from the host "
                        "planner) dequantising in registers",
-           "kv_bytes": int(w.kv_bytes), "decode_us": round(dm * 1e3, 2), "decode_us_mean": round(r["decode"] * 1e3, 2),
-           "split_us": round(r["split_b2b"] * 1e3, 2),
+           "kv_bytes": int(w.kv_bytes), "decode_us": round(dm * 1e3, 2),
+           "decode_us_single_bracket": round(r["decode_median"] * 1e3, 2), "split_us": round(r["split_b2b"] * 1e3, 2),
            "kv_gbs": round(w.kv_bytes / (dm * 1e-3) / 1e9, 1),
            "pct_hbm_peak": round(100 * w.kv_bytes / (dm * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
            "append_us": round(am * 1e3, 2), "append_mtok_s": round(w.B / (am * 1e-3) / 1e6, 3),
-           "steps_per_s": round(1e3 / (am + dm), 1),
+           "step_us": round(r["step_b2b"] * 1e3, 2), "steps_per_s": round(1e3 / r["step_b2b"], 1),
            "note": "working set 2.8 GB, far beyond the 256 MB last-level cache: one replica"}
     w.release()
     if cpu:
@@ -754,7 +808,7 @@ def bench_config5(steps, warmup, cpu):
 
 
 def bench_q4(dtype, steps, warmup):
-    """Q4_0 / Q4_1 KV (formats beyond the five configs) on the config-5 shape:
+    """Q4_0 / Q4_1 / Q5_0 / Q5_1 KV (formats beyond the five configs) on the config-5 shape:
     Hq 24 / Hkv 4 / D 256, block 32, batch 16, ctx U[32768, 131072],
     partitions from the host planner; quantise-append 1 token per sequence + split-K
     decode."""
@@ -767,8 +821,8 @@ def bench_q4(dtype, steps, warmup):
     P = decode_partition(dtype, 256, 32, 24, 4, ctx)
     w = DecodeWorkload(dtype, 24, 4, 256, 32, ctx, pool_blocks, P, seed=5, replicas=1)
     r = w.time(steps, warmup, rotate=False)
-    name = {it.Q4_0: "Q4_0", it.Q4_1: "Q4_1"}[dtype]
-    dm = r["decode_median"]
+    name = {it.Q4_0: "Q4_0", it.Q4_1: "Q4_1", it.Q5_0: "Q5_0", it.Q5_1: "Q5_1"}[dtype]
+    dm = r["decode_b2b"]
     res = {"workload": f"{name} KV on the config-5 shape (Hq 24 / Hkv 4 / D 256, block 32, batch 16, "
                        f"ctx U[32768, 131072], {P}-token partitions from the host planner), dequantising in registers",
            "kv_bytes": int(w.kv_bytes), "decode_us": round(dm * 1e3, 2), "split_us": round(r["split_b2b"] * 1e3, 2),
@@ -1367,9 +1421,11 @@ def main():
                            seed=2)
         r = w.time(args.steps, args.warmup, rotate=True)
         print(json.dumps({"only_headline": True, "split_us": round(r["split_b2b"] * 1e3, 2),
-                          "decode_us": round(r["decode_median"] * 1e3, 2),
+                          "decode_us": round(r["decode_b2b"] * 1e3, 2), "step_us": round(r["step_b2b"] * 1e3, 2),
+                          "enqueue_us": round(r["enqueue_per_step"] * 1e3, 2),
+                          "decode_single_bracket_us": round(r["decode_median"] * 1e3, 2),
                           "split_gbs": round(w.kv_bytes / (r["split_b2b"] * 1e-3) / 1e9, 1),
-                          "decode_gbs": round(w.kv_bytes / (r["decode_median"] * 1e-3) / 1e9, 1)}), flush=True)
+                          "decode_gbs": round(w.kv_bytes / (r["decode_b2b"] * 1e-3) / 1e9, 1)}), flush=True)
         return
 
     head, ragged, cpu_b = bench_config2(args.steps, args.warmup, cpu)
@@ -1393,15 +1449,15 @@ def main():
     if 5 in want:
         import infer_train_amd as it
 
-        configs["q4_0_config5_shape"] = bench_q4(it.Q4_0, small, 10)
-        configs["q4_1_config5_shape"] = bench_q4(it.Q4_1, small, 10)
-        _progress("q4_0 / q4_1 done")
+        for name, dt in (("q4_0", it.Q4_0), ("q4_1", it.Q4_1), ("q5_0", it.Q5_0), ("q5_1", it.Q5_1)):
+            configs[f"{name}_config5_shape"] = bench_q4(dt, small, 10)
+            _progress(f"{name} done")
 
     cold, warm, graph = head["cold"], head["warm"], head["graph"]
     kv_bytes = head["kv_bytes"]
-    # value: KV bytes / the median decode (split + combine, one event
-    # bracket per step) of the timed steps.
-    gbs = kv_bytes / (cold["decode_median"] * 1e-3) / 1e9
+    # value: KV bytes per decode (split + combine) / the decode's time in
+    # `steps` decodes issued back to back between two events.
+    gbs = kv_bytes / (cold["decode_b2b"] * 1e-3) / 1e9
     split_gbs = kv_bytes / (cold["split_b2b"] * 1e-3) / 1e9
     traffic = None
     if os.path.exists(TRAFFIC_FILE):
@@ -1413,7 +1469,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(cold["step_wall"], 4),
+        "ms_per_step": round(cold["step_b2b"], 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -1425,8 +1481,10 @@ def main():
                                "replicas rotated)",
                    "global_batch": 32, "seq_len": 4096, "parallelism": "none (1 GPU)"},
         "pct_hbm_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2),
-        "decode_us": round(cold["decode_median"] * 1e3, 2),
-        "decode_us_mean": round(cold["decode"] * 1e3, 2),
+        "decode_us": round(cold["decode_b2b"] * 1e3, 2),
+        "decode_us_single_bracket": round(cold["decode_median"] * 1e3, 2),
+        "step_us": round(cold["step_b2b"] * 1e3, 2),
+        "step_wall_us": round(cold["step_wall"] * 1e3, 2),
         "decode_graph_us": round(graph["decode_graph"] * 1e3, 2),
         "decode_graph_kv_gbs": round(kv_bytes / (graph["decode_graph"] * 1e-3) / 1e9, 1),
         "decode_graph_note": "split + combine captured in a HIP graph (one per pool replica), replayed back to "
@@ -1434,12 +1492,20 @@ def main():
         "split_us": round(cold["split_b2b"] * 1e3, 2),
         "split_us_single_bracket": round(cold["split_median"] * 1e3, 2),
         "kv_bytes_per_step": int(kv_bytes),
-        "warm_kv_gbs": round(kv_bytes / (warm["decode_median"] * 1e-3) / 1e9, 1),
+        "warm_kv_gbs": round(kv_bytes / (warm["decode_b2b"] * 1e-3) / 1e9, 1),
         "append_mtok_s": round(head["B"] / (cold["append_median"] * 1e-3) / 1e6, 3),
         "append_gbs": round(head["append_bytes"] / (cold["append_median"] * 1e-3) / 1e9, 2),
         "append_us": round(cold["append_median"] * 1e3, 2),
-        "steps_per_s": round(1e3 / (cold["append_median"] + cold["decode_median"]), 1),
-        "timing": "HIP events on the library's stream; per-step values are medians over the timed steps",
+        "steps_per_s": round(1e3 / cold["step_b2b"], 1),
+        "host_enqueue_us_per_step": round(cold["enqueue_per_step"] * 1e3, 2),
+        "timing": "HIP events on the library's stream.  Timed region: `steps` whole steps (append + split + "
+                  "combine, 3 pool replicas rotated) back to back between two events, synchronised on both sides "
+                  "(ms_per_step, step_us); then `steps` decodes (split + combine) back to back (decode_us, the "
+                  "value); then `steps` split launches back to back (split_us, the roofline).  Each of these "
+                  "regions is queued behind a bounded GPU sleep (torch.cuda._sleep) longer than the Python "
+                  "harness takes to enqueue it (host_enqueue_us_per_step), so the events time the kernels as a "
+                  "native caller would issue them.  *_single_bracket and append_us: medians of per-step event "
+                  "brackets, which include each bracket's event overhead",
         "roofline": {"bound": "hbm", "achieved": round(split_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(split_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": f"paged_decode_split<bf16,128,7> (mean duration of {args.steps} back-to-back launches "
