@@ -244,9 +244,16 @@ class ContinuousBatcher:
         return self.manager.append([self.seq_of[r] for r in self.running], 1)
 
     def finish(self, request_id: int) -> np.ndarray:
+        """Running or Preempted -> Finished; the request's blocks (if it
+        still holds them) and sequence slot are released."""
         ctx = self.requests[request_id]
+        if ctx.state == RequestState.Running:
+            self.running.remove(request_id)
+        elif ctx.state == RequestState.Preempted:
+            self.preempted.remove(request_id)
+        else:
+            raise ValueError(f"request {request_id} is {ctx.state.value}")
         ctx.state = RequestState.Finished
-        self.running.remove(request_id)
         self.needs_prefill.discard(request_id)
         freed = np.zeros(0, np.int32)
         if self.manager is not None and request_id in self.seq_of:

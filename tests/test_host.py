@@ -253,6 +253,22 @@ def test_batcher_preemption_releases_or_keeps_blocks_like_the_oracle():
     assert pa.num_free() == cap and b.schedule() == [4]
 
 
+def test_finish_a_preempted_request():
+    pool = BlockPool(8)
+    b = ContinuousBatcher(2, KvManager(pool, 16, 2, 8))
+    b.add_request(0, list(range(20)), 1)
+    b.add_request(1, list(range(5)), 1)
+    b.schedule()
+    b.plan_prefill([0, 1])
+    b.preempt(0, keep_blocks=True)
+    assert pool.num_free() == 5
+    assert list(b.finish(0)) != [] and pool.num_free() == 7  # its kept blocks go back
+    assert 0 not in b.preempted and b.requests[0].state.value == "Finished"
+    with pytest.raises(ValueError):
+        b.finish(0)
+    assert b.schedule() == [1]
+
+
 def test_preempt_for_raises_when_nothing_is_left():
     pool = BlockPool(4)
     b = ContinuousBatcher(2, KvManager(pool, 16, 2, 8))
