@@ -17,19 +17,24 @@
 //                 are in-lane plus one v_permlane32_swap with lane ^ 32;
 //   O^T += V^T P^T the probabilities go back into MFMA operands straight
 //                 from the S^T registers (bf16/f16 pairs, v_cvt_pk), and
-//                 V^T comes from the row-major V tile through
-//                 ds_read_b64_tr_b16 transposing loads, in the key order the
-//                 S^T registers hold.
-// Software pipelining: the loop body issues S^T of block kb + 1 and the
-// softmax and O update of block kb in one basic block, so the MFMA pipe
-// works on the next block's scores while the VALU turns this block's scores
-// into probabilities.  Fully visible blocks (every key precedes every query
-// of the workgroup and kend) run a loop without per-key masks; the blocks
-// the causal diagonal or kend cut run a masked copy of it.
+//                 V^T comes from a transposed copy of the V block in LDS
+//                 (made once per block by all waves, keys permuted into the
+//                 order the S^T registers hold them), one ds_read_b128 per
+//                 MFMA like the K operand.
+// Ping-pong: the two waves sharing a SIMD alternate between a matrix phase
+// (P.V of one block and S^T of the next: MFMA and LDS reads) and a softmax
+// phase (VALU), separated by workgroup barriers, so the MFMA pipe and the
+// VALU work at the same time.  Fully visible blocks (every key precedes
+// every query of the workgroup and kend) run a loop without per-key masks;
+// the blocks the causal diagonal or kend cut run a masked copy of it.
+// Workgroups are placed so that the query blocks of one (sequence, KV head)
+// share an XCD and its L2.
 // K and V blocks (16 KiB each) are staged in LDS by direct global->LDS loads
-// into rings of 4 K and 3 V slots, issued two blocks ahead; 16-byte chunks
-// are XOR-swizzled by row so MFMA operand reads are conflict-free.  Page ids
-// come from the block table through scalar loads (they do not count against
+// into rings of 3 K and 3 V slots, issued three blocks ahead; 16-byte chunks
+// are XOR-swizzled by row so MFMA operand reads are conflict-free.  Each V
+// block is transposed into one of 2 V^T slots the step before it is used.
+// Page ids come from the workgroup's LDS copy of its block-table row, or
+// through scalar loads when the row does not fit (they do not count against
 // the vector-memory counter that orders the rings).  Online softmax in fp32
 // (exp2 domain), accumulators fp32.
 #include <hip/hip_runtime.h>
@@ -45,9 +50,16 @@ constexpr int kQB = 32;               // query positions per wave tile
 constexpr int kKB = 64;               // keys per block
 constexpr int kRowB = kD * 2;         // bytes per K/V row
 constexpr int kPlaneB = kKB * kRowB;  // 16 KiB
-constexpr int kRingK = 4;             // K slots
-constexpr int kRingV = 3;             // V slots
-constexpr int kLds = (kRingK + kRingV) * kPlaneB;  // 112 KiB
+constexpr int kRingK = 3;             // K slots
+constexpr int kRingV = 3;             // V slots (row-major, as loaded)
+// V^T slots: row d holds dim d of the block's 64 keys, key k at position
+// vt_pos(k); rows padded to 144 bytes so both the 16-byte operand reads (8
+// consecutive rows per pass) and the 4-byte transpose stores are
+// conflict-free.
+constexpr int kVtRow = 144;
+constexpr int kVtB = kD * kVtRow;     // 18 KiB
+constexpr int kRingVt = 2;
+constexpr int kLds = (kRingK + kRingV) * kPlaneB + kRingVt * kVtB;  // 132 KiB
 constexpr int kMaxLds = 160 * 1024;                // per workgroup (one per CU)
 constexpr int kMaxGroup = 8;          // query heads per KV head
 
@@ -67,6 +79,7 @@ struct PrefillArgs {
   uint32_t num_blocks32;  // pool blocks (clamped to 2^31 - 1)
   float scale_log2;
   int n_heads, n_kv_heads, group, q_tiles, max_blocks, log2_bs, causal, out_f32;
+  int n_qb;               // query blocks per (sequence, KV head)
 };
 
 // Query tiles per workgroup for a GQA group: up to 8 waves of work.
@@ -85,6 +98,11 @@ __device__ __forceinline__ void dma_b128(const void* g, uint32_t m0) {
 __device__ __forceinline__ int sw(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
 // Byte offset of 16-byte chunk c of row r in a swizzled tile.
 __device__ __forceinline__ int swz(int r, int c) { return r * kRowB + ((c ^ sw(r)) << 4); }
+// Position of key k (0..63) in a V^T row: bits 2 and 3 of k swapped.  The
+// P.V k-step (n, t) takes, in lane half h, element e of its operand from key
+// 32 n + 16 t + 8 (e / 4) + 4 h + e % 4, which sits at position
+// 32 n + 16 t + 8 h + e: one 16-byte read per lane.
+__device__ __forceinline__ int vt_pos(int k) { return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1); }
 
 template <bool kBf16>
 __device__ __forceinline__ v16f mfma(const uint4& a, const uint4& b, const v16f& c) {
@@ -136,9 +154,19 @@ template <bool kBf16, int W, bool kTab>
 __global__ __launch_bounds__(64 * W) void paged_prefill_kernel(PrefillArgs a) {
   extern __shared__ __attribute__((aligned(16))) char smem[];  // K ring, V ring, [table]
   constexpr int kDmaPerWave = (16 + W - 1) / W;  // 1 KiB loads per wave per plane (16 per plane)
-  // Query blocks in decreasing order: in causal attention later blocks see
-  // more keys, so the longest workgroups are dispatched first.
-  const int qb = gridDim.x - 1 - blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  // Workgroup id -> (sequence, KV head, query block).  The dispatcher deals
+  // ids to the 8 XCDs round-robin; the ids are remapped so that all query
+  // blocks of one (sequence, KV head), which stream the same K/V pages, run
+  // on one XCD and share its L2 (in id order each XCD would fetch every
+  // sequence's pages).  Within a (sequence, KV head) query blocks go in
+  // decreasing order: in causal attention later blocks see more keys, so
+  // the longest workgroups start first.
+  const int n_full = int(gridDim.x) & ~7;
+  const int id = blockIdx.x;
+  const int unit = id < n_full ? (id & 7) * (n_full >> 3) + (id >> 3) : id;
+  const int pair = unit / a.n_qb;
+  const int qb = a.n_qb - 1 - (unit - pair * a.n_qb);
+  const int kvh = pair % a.n_kv_heads, b = pair / a.n_kv_heads;
   const int q_begin = a.cu_q[b];
   const int q_len = a.cu_q[b + 1] - q_begin;
   const int ctx = a.ctx_lens[b];
@@ -203,6 +231,7 @@ __global__ __launch_bounds__(64 * W) void paged_prefill_kernel(PrefillArgs a) {
       (const __attribute__((address_space(4))) int32_t*)(a.bt + int64_t(b) * a.max_blocks);
   char* const k_ring = smem;
   char* const v_ring = smem + kRingK * kPlaneB;
+  char* const vt_ring = smem + (kRingK + kRingV) * kPlaneB;
   const uint32_t k_m0 = lds_off(k_ring), v_m0 = lds_off(v_ring);
   const int64_t page_stride = int64_t(a.n_kv_heads) * a.page_bytes;  // bytes per pool block
   const char* const k_head = a.k_pool + int64_t(kvh) * a.page_bytes;
@@ -250,16 +279,49 @@ __global__ __launch_bounds__(64 * W) void paged_prefill_kernel(PrefillArgs a) {
   };
   auto k_slot = [&](int kb) { return k_ring + (kb % kRingK) * kPlaneB; };
   auto v_slot = [&](int kb) { return v_ring + (kb % kRingV) * kPlaneB; };
-  // Iteration kb issues K(kb + 3) and V(kb + 2), needed two iterations
-  // later, with page ids fetched one iteration ahead: kblk holds block
-  // kb + 3's and vblk block kb + 2's (the previous iteration's kblk).
-  int vblk[kDmaPerWave], kblk[kDmaPerWave];
+  auto vt_slot = [&](int kb) { return vt_ring + (kb & 1) * kVtB; };
+  // Iteration kb issues K(kb + 3) and V(kb + 3), needed two iterations
+  // later (V is transposed the iteration before it is used), with page ids
+  // fetched one iteration ahead: kblk holds block kb + 3's.
+  int kblk[kDmaPerWave];
   auto issue_step = [&](int kb) __attribute__((always_inline)) {
     dma_plane(k_head, kb + 3, k_m0 + uint32_t((kb + 3) % kRingK) * kPlaneB, kblk);
-    dma_plane(v_head, kb + 2, v_m0 + uint32_t((kb + 2) % kRingV) * kPlaneB, vblk);
-#pragma unroll
-    for (int j = 0; j < kDmaPerWave; ++j) vblk[j] = kblk[j];
+    dma_plane(v_head, kb + 3, v_m0 + uint32_t((kb + 3) % kRingV) * kPlaneB, kblk);
     page_ids(kb + 4, kblk);
+  };
+  // V block kb (row-major slot) -> V^T slot kb & 1, in 8 units of 16 dims
+  // spread over the waves (wave w takes units w, w + W, ...).  Lane l of a
+  // unit u packs keys 2 kp and 2 kp + 1 (kp = l % 32) of dims
+  // 8 dg .. 8 dg + 7 (dg = 2 u + l / 32) into 8 dwords, one per V^T row;
+  // the two keys sit side by side there (vt_pos keeps bit 0).  Split into
+  // the reads, issued before the softmax, and the stores after it.
+  constexpr int kTu = (8 + W - 1) / W;  // units per wave
+  const int tr_kp = lane & 31, tr_half = lane >> 5;
+  auto transpose_read = [&](int kb, uint4 (&r)[kTu][2]) __attribute__((always_inline)) {
+    const char* src = v_slot(kb);
+#pragma unroll
+    for (int j = 0; j < kTu; ++j) {
+      const int dg = 2 * min(wave + W * j, 7) + tr_half;  // a unit past 7 repeats unit 7 (not stored)
+      r[j][0] = *reinterpret_cast<const uint4*>(src + swz(2 * tr_kp, dg));
+      r[j][1] = *reinterpret_cast<const uint4*>(src + swz(2 * tr_kp + 1, dg));
+    }
+  };
+  auto transpose_store = [&](int kb, const uint4 (&r)[kTu][2]) __attribute__((always_inline)) {
+    char* const dst = vt_slot(kb) + 2 * vt_pos(2 * tr_kp);
+#pragma unroll
+    for (int j = 0; j < kTu; ++j) {
+      if (wave + W * j < 8) {  // uniform
+        char* const d = dst + (16 * (wave + W * j) + 8 * tr_half) * kVtRow;
+        const uint32_t a0[4] = {r[j][0].x, r[j][0].y, r[j][0].z, r[j][0].w};
+        const uint32_t a1[4] = {r[j][1].x, r[j][1].y, r[j][1].z, r[j][1].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          // dim 8 dg + 2 i: low halves of the two keys; dim 8 dg + 2 i + 1: high halves
+          *reinterpret_cast<uint32_t*>(d + (2 * i) * kVtRow) = __builtin_amdgcn_perm(a1[i], a0[i], 0x05040100u);
+          *reinterpret_cast<uint32_t*>(d + (2 * i + 1) * kVtRow) = __builtin_amdgcn_perm(a1[i], a0[i], 0x07060302u);
+        }
+      }
+    }
   };
 
   // S^T of key block kb: two 32-key tiles; s[n][r] is key 64 kb + 32 n +
@@ -287,8 +349,6 @@ __global__ __launch_bounds__(64 * W) void paged_prefill_kernel(PrefillArgs a) {
   constexpr float kLazy = 8.0f;
   float m_run = -INFINITY, l_run = 0.0f;
   const float exp_in = fabsf(a.scale_log2);  // q carries the scale's sign
-  const int tr_key = 4 * (lane >> 5) + ((lane & 15) >> 2);
-  const int tr_dim = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
   // Last visible key of this lane's query relative to block kb's first key
   // and to this lane's half (register c of a block holds key offset
   // 4 half + c, c = 32 n + 8 (r / 4) + r % 4).
@@ -364,46 +424,23 @@ __global__ __launch_bounds__(64 * W) void paged_prefill_kernel(PrefillArgs a) {
   // block kb, then S^T of block kb + 1 into s.
   auto matrix_phase = [&](int kb) __attribute__((always_inline)) {
     __builtin_amdgcn_sched_barrier(0);
-    // k-step (n, t), element e of lane half h <-> key 32 n + 16 t + 8 (e / 4)
-    // + 4 h + e % 4: the keys s[n][8 t + e] holds.  Transposing load c
-    // (e = 4 c + j) of lane L reads key 32 n + 16 t + 8 c + 4 (L / 32)
-    // + (L % 16) / 4, dims 32 dt + 16 ((L / 16) % 2) + 4 (L % 4) + [0, 4).
-    const char* vt = v_slot(kb);
+    // k-step (n, t): lane L reads V^T row 32 dt + L % 32 at positions
+    // 32 n + 16 t + 8 (L / 32) + [0, 8), the keys s[n][8 t + e] holds.
+    const char* vt = vt_slot(kb) + col * kVtRow + 16 * half;
 #pragma unroll
     for (int n = 0; n < 2; ++n)
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int dt = 0; dt < kD / 32; ++dt) {
-          uint32_t w[4];
-#pragma unroll
-          for (int c = 0; c < 2; ++c) {
-            const int key = 32 * n + 16 * t + 8 * c + tr_key;
-            const int dim = 32 * dt + tr_dim;
-            const char* ptr = vt + swz(key, dim >> 3) + ((dim & 4) << 1);
-            const v4s r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)(ptr));
-            w[2 * c] = uint32_t(uint16_t(r[0])) | (uint32_t(uint16_t(r[1])) << 16);
-            w[2 * c + 1] = uint32_t(uint16_t(r[2])) | (uint32_t(uint16_t(r[3])) << 16);
-          }
-          o[dt] = mfma<kBf16>(make_uint4(w[0], w[1], w[2], w[3]), pk[n][t], o[dt]);
+          const uint4 w = *reinterpret_cast<const uint4*>(vt + 32 * dt * kVtRow + 64 * n + 32 * t);
+          o[dt] = mfma<kBf16>(w, pk[n][t], o[dt]);
         }
     qk(kb + 1, s);
-    // Operand loads two MFMAs ahead: 6 transposing V reads, then per PV
-    // MFMA two more, then the K reads one per QK MFMA.
-    __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
-#pragma unroll
-    for (int i = 0; i < 13; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-    }
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    // Operand reads three MFMAs ahead, one per MFMA.
     __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
 #pragma unroll
-    for (int i = 0; i < 13; ++i) {
+    for (int i = 0; i < 29; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
@@ -411,22 +448,29 @@ __global__ __launch_bounds__(64 * W) void paged_prefill_kernel(PrefillArgs a) {
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  // Prologue: K(0), (K(1), V(0)), (K(2), V(1)); S^T of block 0.  A
-  // workgroup with no keys (nkb uniform) skips straight to the zero output.
+  // Prologue: (K(0), V(0)), (K(1), V(1)), (K(2), V(2)); V(0) transposed;
+  // S^T of block 0.  A workgroup with no keys (nkb uniform) skips straight
+  // to the zero output.
   if (nkb > 0) {
   {
     int b0[kDmaPerWave], b1[kDmaPerWave];
     page_ids(0, b0);
     page_ids(1, b1);
-    page_ids(2, vblk);
-    page_ids(3, kblk);
+    page_ids(2, kblk);
     dma_plane(k_head, 0, k_m0, b0);
-    dma_plane(k_head, 1, k_m0 + uint32_t(kPlaneB), b1);
     dma_plane(v_head, 0, v_m0, b0);
-    dma_plane(k_head, 2, k_m0 + uint32_t(2 * kPlaneB), vblk);
+    dma_plane(k_head, 1, k_m0 + uint32_t(kPlaneB), b1);
     dma_plane(v_head, 1, v_m0 + uint32_t(kPlaneB), b1);
+    dma_plane(k_head, 2, k_m0 + uint32_t(2 * kPlaneB), kblk);
+    dma_plane(v_head, 2, v_m0 + uint32_t(2 * kPlaneB), kblk);
+    page_ids(3, kblk);
   }
   asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(4 * kDmaPerWave) : "memory");
+  {
+    uint4 r[kTu][2];
+    transpose_read(0, r);
+    transpose_store(0, r);
+  }
   qk(0, s);
   // Ping-pong: waves 0-3 (one per SIMD) run step kb as the matrix phase of
   // block kb, a workgroup barrier, then the softmax phase of block kb + 1;
@@ -436,9 +480,9 @@ __global__ __launch_bounds__(64 * W) void paged_prefill_kernel(PrefillArgs a) {
   // probabilities first, one half step ahead.  A step's softmax phases are
   // unmasked while blocks kb and kb + 1 are whole; the last step's block
   // nkb has no visible key.
-  // At a step's start K(kb + 1) and V(kb) have landed (only step kb - 1's
-  // loads may be outstanding) and every wave is done with the slots step kb
-  // refills.
+  // At a step's start K(kb + 1), V(kb + 1) and V^T(kb) are in LDS (only
+  // step kb - 1's loads may be outstanding) and every wave is done with the
+  // slots step kb refills.
   // The phases use registers only, so the compiler may move them across a
   // barrier; each barrier therefore either consumes the probabilities the
   // phase before it made (so that phase stays before it) or produces the
@@ -470,7 +514,13 @@ __global__ __launch_bounds__(64 * W) void paged_prefill_kernel(PrefillArgs a) {
       asm volatile("s_barrier\n\tv_mov_b32 %0, 0xff800000" : "=v"(ninf) : : "memory");
     return ninf;
   };
+  // Every wave also transposes its share of V(kb + 1) during its softmax
+  // phase of step kb: V(kb + 1) has landed at the step's start, and V^T slot
+  // (kb + 1) & 1 was last read by the matrix phases of step kb - 1.  (The
+  // last step transposes the refilled copy of the last block; no step reads
+  // it.)
   const int u_end = max(n_vis - 1, 0);
+  uint4 tr[kTu][2];
   if (wave < 4) {
     softmax_phase(0, true, -INFINITY);
 #pragma nounroll
@@ -478,21 +528,29 @@ __global__ __launch_bounds__(64 * W) void paged_prefill_kernel(PrefillArgs a) {
       barrier_after_softmax(true);
       issue_step(kb);
       matrix_phase(kb);
-      softmax_phase(kb + 1, false, barrier_before_softmax(false));
+      const float ninf = barrier_before_softmax(false);
+      transpose_read(kb + 1, tr);
+      softmax_phase(kb + 1, false, ninf);
+      transpose_store(kb + 1, tr);
     }
 #pragma nounroll
     for (int kb = u_end; kb < nkb; ++kb) {
       barrier_after_softmax(true);
       issue_step(kb);
       matrix_phase(kb);
-      softmax_phase(kb + 1, true, barrier_before_softmax(false));
+      const float ninf = barrier_before_softmax(false);
+      transpose_read(kb + 1, tr);
+      softmax_phase(kb + 1, true, ninf);
+      transpose_store(kb + 1, tr);
     }
   } else {
 #pragma nounroll
     for (int kb = 0; kb < u_end; ++kb) {
       const float ninf = barrier_before_softmax(true);
       issue_step(kb);
+      transpose_read(kb + 1, tr);
       softmax_phase(kb, false, ninf);
+      transpose_store(kb + 1, tr);
       barrier_after_softmax(false);
       matrix_phase(kb);
     }
@@ -500,7 +558,9 @@ __global__ __launch_bounds__(64 * W) void paged_prefill_kernel(PrefillArgs a) {
     for (int kb = u_end; kb < nkb; ++kb) {
       const float ninf = barrier_before_softmax(true);
       issue_step(kb);
+      transpose_read(kb + 1, tr);
       softmax_phase(kb, true, ninf);
+      transpose_store(kb + 1, tr);
       barrier_after_softmax(false);
       matrix_phase(kb);
     }
@@ -548,7 +608,7 @@ hipError_t launch_prefill_t(const PrefillArgs& a, dim3 grid, size_t smem, hipStr
 
 template <bool kBf16, int W>
 hipError_t launch_prefill_w(const PrefillArgs& a, dim3 grid, hipStream_t s) {
-  // The table row fits beside the rings up to (160 - 112) KiB / 4 B entries.
+  // The table row fits beside the rings up to (160 - 132) KiB / 4 B entries.
   const size_t tab = (size_t(a.max_blocks) * 4 + 15) & ~size_t(15);
   if (kLds + tab <= size_t(kMaxLds)) return launch_prefill_t<kBf16, W, true>(a, grid, kLds + tab, s);
   return launch_prefill_t<kBf16, W, false>(a, grid, kLds, s);
@@ -610,11 +670,14 @@ extern "C" int32_t it_paged_prefill(const it_kv_cache* c, const void* q, int32_t
   a.log2_bs = c->log2_bs;
   a.causal = causal ? 1 : 0;
   a.out_f32 = out_dtype == IT_F32;
+  const int wg_q = kQB * a.q_tiles;
+  a.n_qb = (max_q_len + wg_q - 1) / wg_q;
+  const int64_t n_wg = int64_t(a.n_qb) * c->n_kv_heads * n_seqs;
+  if (n_wg > INT32_MAX) return fail(IT_INVALID_INPUT, "%s: %lld workgroups (max 2^31 - 1)", who, (long long)n_wg);
+  const dim3 grid(static_cast<unsigned>(n_wg), 1u, 1u);
   int dev = -1;
   (void)hipGetDevice(&dev);
   if (dev != c->device) (void)hipSetDevice(c->device);
-  const int wg_q = kQB * a.q_tiles;
-  const dim3 grid(unsigned((max_q_len + wg_q - 1) / wg_q), unsigned(c->n_kv_heads), unsigned(n_seqs));
   const hipError_t e = c->dtype == IT_BF16 ? launch_prefill<true>(a, grid, (hipStream_t)stream)
                                            : launch_prefill<false>(a, grid, (hipStream_t)stream);
   if (dev >= 0 && dev != c->device) (void)hipSetDevice(dev);
