@@ -50,6 +50,7 @@ class KvManager:
         h = C.c_void_p()
         check(lib.it_kv_manager_new(pool.handle, block_size, max_seqs, max_blocks_per_seq, window, C.byref(h)))
         self._h = h
+        self._destroy = lib.it_kv_manager_destroy  # bound now: module globals may be gone at exit
 
     def seed_seq(self, seq: int, pos: int, first_block: int, blocks: Sequence[int]) -> None:
         arr = np.ascontiguousarray(np.asarray(blocks, dtype=np.int32))
@@ -119,8 +120,8 @@ class KvManager:
     def __del__(self):
         h = getattr(self, "_h", None)
         if h is not None and h.value:
-            lib.it_kv_manager_destroy(h)
-            self._h = C.c_void_p()
+            self._destroy(h)
+            self._h = None
 
 
 class RequestState(Enum):  # continuous.rs:8-15

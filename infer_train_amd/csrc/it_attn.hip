@@ -95,14 +95,18 @@ int32_t run_decode(const char* who, int32_t cache_dt, int32_t q_dtype, int32_t o
   a.chunks = a.group / gc;
   if (int64_t(a.n_kv_heads) * a.chunks > 65535) return fail(IT_NOT_IMPLEMENTED, "%s: too many head chunks", who);
   a.max_pages = (a.partition >> a.log2_bs) + 2;
-  const int64_t n_wg = int64_t(a.max_parts) * a.n_kv_heads * a.chunks * n_seqs;
-  // Per-sequence contexts: map workgroups to the non-empty units in order
-  // (every wave scans the n_seqs context lengths once, so only up to 512).
-  a.compact = (a.ctx_lens != nullptr && n_seqs <= kCompactSeqs && n_wg < (int64_t(1) << 31)) ? 1 : 0;
+  a.n_seqs = n_seqs;
+  const int64_t n_units = int64_t(a.max_parts) * a.n_kv_heads * a.chunks * n_seqs;
+  // Per-sequence contexts: a one-dimensional grid over the non-empty units
+  // (every wave scans the n_seqs context lengths, so only up to 512), a
+  // multiple of 8 workgroups so that every XCD's range of units is covered.
+  a.compact = (a.ctx_lens != nullptr && n_seqs <= kCompactSeqs && n_units < (int64_t(1) << 30)) ? 1 : 0;
+  const int64_t n_wg = a.compact ? (n_units + 7) / 8 * 8 : n_units;
   const size_t smem = decode_smem_bytes(cache_dt, gc, d, a.partition, a.max_pages, n_wg);
   if (smem > kMaxDecodeLds) return fail(IT_INVALID_INPUT, "%s: partition %d needs %zu bytes of LDS", who, a.partition, smem);
   if (max_tokens > 0 && (phases & 1)) {
-    dim3 grid(unsigned(a.max_parts), unsigned(a.n_kv_heads * a.chunks), unsigned(n_seqs));
+    const dim3 grid = a.compact ? dim3(unsigned(n_wg), 1u, 1u)
+                                : dim3(unsigned(a.max_parts), unsigned(a.n_kv_heads * a.chunks), unsigned(n_seqs));
     hipError_t e = launch_split(cache_dt, d, gc, a, grid, s);
     if (e != hipSuccess) return fail(IT_DEVICE_ERROR, "%s: split launch: %s", who, hipGetErrorString(e));
   }

@@ -35,7 +35,8 @@ struct DecodeArgs {
   int partition;            // tokens per split, multiple of 64
   int max_parts;
   int max_pages;            // page-list entries per partition: (partition >> log2_bs) + 2
-  int compact;              // 1: workgroup L runs the L-th non-empty unit (needs ctx_lens)
+  int compact;              // 1: one-dimensional grid over the non-empty units (needs ctx_lens)
+  int n_seqs;
 };
 
 constexpr float kLog2e = 1.4426950408889634f;

@@ -239,7 +239,7 @@ class PagedKvCache:
         destroy = getattr(self, "_destroy", None)
         if h is not None and h.value and destroy is not None:
             destroy(h)
-            self._h = C.c_void_p()
+            self._h = None
 
 
 def decode_partition(dtype: int, head_dim: int, block_size: int, n_heads: int, n_kv_heads: int, ctx_lens,

@@ -33,6 +33,7 @@ class BlockPool:
                 raise ValueError("order must have `capacity` entries")
             check(lib.it_block_pool_new_ordered(arr.ctypes.data, int(capacity), int(quant_type), C.byref(h)))
         self._h = h
+        self._destroy = lib.it_block_pool_destroy  # bound now: module globals may be gone at exit
 
     @property
     def handle(self) -> C.c_void_p:
@@ -63,5 +64,5 @@ class BlockPool:
     def __del__(self):
         h = getattr(self, "_h", None)
         if h is not None and h.value:
-            lib.it_block_pool_destroy(h)
-            self._h = C.c_void_p()
+            self._destroy(h)
+            self._h = None
