@@ -73,8 +73,8 @@ __global__ __launch_bounds__(kThreads) void kv_append_copy(
     const int64_t blk = sl >> log2_bs;
     const int64_t off = sl & ((int64_t(1) << log2_bs) - 1);
     const int64_t dst = (blk * hkv + h) * page_bytes + ((off << log2_row_vecs) + c) * 16;
-    *reinterpret_cast<u4*>(kpool + dst) = kv[j];
-    *reinterpret_cast<u4*>(vpool + dst) = vv[j];
+    __builtin_nontemporal_store(kv[j], reinterpret_cast<u4*>(kpool + dst));
+    __builtin_nontemporal_store(vv[j], reinterpret_cast<u4*>(vpool + dst));
   }
 }
 
@@ -147,8 +147,8 @@ __global__ __launch_bounds__(kThreads) void kv_gather_vec(
   const int64_t src = (int64_t(blk) * hkv + h) * page_bytes +
                       (int64_t(pos & ((1 << log2_bs) - 1)) * row_vecs + c) * 16;
   const int64_t dst = (cu_out[b] * hkv + int64_t(h) * n + i) * row_vecs + c;
-  kout[dst] = ld16(kpool + src);
-  vout[dst] = ld16(vpool + src);
+  st16(kout + dst, ld16_nt(kpool + src));
+  st16(vout + dst, ld16_nt(vpool + src));
 }
 
 // Q8_0 gather: lane = one 32-element group, written as a packed 34-byte
@@ -307,8 +307,8 @@ __global__ __launch_bounds__(kThreads) void kv_copy_blocks(char* __restrict__ kp
     return;
   }
   for (int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x; i < block_vecs; i += int64_t(gridDim.x) * kThreads) {
-    st16(kpool + (d * block_vecs + i) * 16, ld16(kpool + (s * block_vecs + i) * 16));
-    st16(vpool + (d * block_vecs + i) * 16, ld16(vpool + (s * block_vecs + i) * 16));
+    st16(kpool + (d * block_vecs + i) * 16, ld16_nt(kpool + (s * block_vecs + i) * 16));
+    st16(vpool + (d * block_vecs + i) * 16, ld16_nt(vpool + (s * block_vecs + i) * 16));
   }
 }
 

@@ -78,5 +78,19 @@ __device__ __forceinline__ float group_max(float x) {
 // Load helpers: 16-byte vector loads/stores on raw byte addresses.
 __device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
 __device__ __forceinline__ void st16(void* p, uint4 v) { *reinterpret_cast<uint4*>(p) = v; }
+// Streaming 16-byte accesses (nt: not kept in L2).  Measured on the data
+// movers: nt loads make the bf16 page gather 26% faster (and the quantised
+// gather, which reads 32-byte group pieces, 30% slower); nt stores help only
+// the append's scattered row stores (2%) and slow contiguous or zeroing
+// stores.
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ld16_nt(const void* p) {
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void st16_nt(void* p, uint4 v) {
+  const u32x4 w = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(p));
+}
 
 }  // namespace itkv
