@@ -306,13 +306,14 @@ int32_t it_paged_decode_partition(int32_t dtype, int32_t head_dim, int32_t block
  * over keys start_b..ctx_b-1 of KV head h*Hkv/Hq (forward.rs:231-254),
  * within fp32 tolerance.
  *   q: [n_seqs][n_heads][head_dim]; q_dtype F32 (F32 and quantised caches),
- *      BF16 (BF16 cache) or F16 (F16 cache)
+ *      BF16 (BF16 cache) or F16 (F16 cache); 16-byte aligned
  *   block_tables/ctx_lens/start_pos: as it_kv_gather
  *   max_tokens: upper bound of ctx_b - start_b
  *   partition: tokens per split, a multiple of 64 in [64, 2048]
  *              (it_paged_decode_partition picks one for a batch)
- *   ws: it_paged_decode_workspace(...) bytes, device
- *   out: [n_seqs][n_heads][head_dim] of out_dtype (F32 or q_dtype)
+ *   ws: it_paged_decode_workspace(...) bytes, device, 256-byte aligned
+ *   out: [n_seqs][n_heads][head_dim] of out_dtype (F32 or q_dtype); 8-byte
+ *        aligned for F32, 4-byte for 16-bit types
  * Two kernels: the split pass writes (m, l, O) per partition, the combine
  * pass merges them.  n_heads must be a multiple of n_kv_heads. */
 int32_t it_paged_decode(const it_kv_cache* cache, const void* q, int32_t q_dtype, int32_t n_heads,

@@ -50,13 +50,23 @@ hipError_t launch_split(int32_t dt, int d, int gc, const DecodeArgs& a, dim3 gri
 }
 
 hipError_t launch_combine(int d, const DecodeArgs& a, int n_seqs, void* out, int32_t out_dtype, hipStream_t s) {
-  dim3 grid(unsigned(a.n_heads), unsigned(n_seqs), unsigned(d / 64));
+  // One workgroup per (row, 128-dim slice), rows placed on the XCD whose
+  // split workgroups wrote them (CombineMap): grid.x = 8 * the largest XCD
+  // range.
+  CombineMap map;
+  map.gc = a.group / a.chunks;
+  map.max_parts = a.max_parts;
+  map.n_rows = int64_t(n_seqs) * a.n_heads;
+  map.q8 = (int64_t(n_seqs) * a.n_kv_heads * a.chunks * a.max_parts + 7) / 8;
+  int64_t widest = 0;
+  for (int x = 0; x < 8; ++x) widest = std::max(widest, map.first_row(x + 1) - map.first_row(x));
+  const dim3 grid(unsigned(8 * widest), 1u, unsigned(d / 128));
   if (d == 128)
-    hipLaunchKernelGGL(paged_decode_combine<128>, grid, dim3(64), 0, s, a.ws_o, a.ws_ml, a.ctx_lens,
-                       a.start_pos, a.ctx_const, a.n_heads, a.partition, a.max_parts, out, out_dtype);
+    hipLaunchKernelGGL(paged_decode_combine<128>, grid, dim3(64), 0, s, a.ws_o, a.ws_ml, a.ctx_lens, a.start_pos,
+                       a.ctx_const, a.n_heads, a.partition, map, out, out_dtype);
   else if (d == 256)
-    hipLaunchKernelGGL(paged_decode_combine<256>, grid, dim3(64), 0, s, a.ws_o, a.ws_ml, a.ctx_lens,
-                       a.start_pos, a.ctx_const, a.n_heads, a.partition, a.max_parts, out, out_dtype);
+    hipLaunchKernelGGL(paged_decode_combine<256>, grid, dim3(64), 0, s, a.ws_o, a.ws_ml, a.ctx_lens, a.start_pos,
+                       a.ctx_const, a.n_heads, a.partition, map, out, out_dtype);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
@@ -82,6 +92,8 @@ int32_t run_decode(const char* who, int32_t cache_dt, int32_t q_dtype, int32_t o
     return fail(IT_INVALID_INPUT, "%s: n_heads %d must be a positive multiple of n_kv_heads %d", who, a.n_heads,
                 a.n_kv_heads);
   if (!a.q || !out || !ws) return fail(IT_INVALID_INPUT, "%s: NULL tensor", who);
+  if (reinterpret_cast<uintptr_t>(out) & (out_dtype == IT_F32 ? 7u : 3u))
+    return fail(IT_INVALID_INPUT, "%s: out must be %d-byte aligned", who, out_dtype == IT_F32 ? 8 : 4);
   if ((reinterpret_cast<uintptr_t>(a.q) & 15u) || (reinterpret_cast<uintptr_t>(ws) & 255u))
     return fail(IT_INVALID_INPUT, "%s: q must be 16-byte and ws 256-byte aligned", who);
   a.max_parts = max_tokens > 0 ? (max_tokens + a.partition - 1) / a.partition : 1;

@@ -61,50 +61,69 @@ __device__ __forceinline__ void dma_b32(const void* g, uint32_t m0) {
 }
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// One merged output element in the caller's dtype.  The value is o / l when
-// l > 0, else zero (flash_attn.rs:66-71: multiply by 1/s when s > 0).
-__device__ __forceinline__ void store_combined(void* out, int out_dtype, int64_t idx, float v) {
-  if (out_dtype == IT_F32) static_cast<float*>(out)[idx] = v;
-  else if (out_dtype == IT_BF16) static_cast<uint16_t*>(out)[idx] = uint16_t(f32_to_bf16_bits(v));
-  else static_cast<uint16_t*>(out)[idx] = uint16_t(f32_to_f16_bits(v));
-}
-
 // Lane `l`'s value of x (v_readlane_b32 on the bits; l uniform).
 __device__ __forceinline__ float lane_f32(float x, int l) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), l));
 }
 
-// Merge the partitions of one (sequence, head) over a 64-dim slice (grid z):
-// M = max m_p, L = sum l_p 2^(m_p - M), O = sum O_p 2^(m_p - M) / L (the
-// split-K form of flash_attn_f32's rescaling, flash_attn.rs:42-71).  Lane d
-// owns one output dim; lane c also holds the (m, l) pairs of partitions c and
-// 64 + c, so M and L are wave reductions and partition p's weight comes from
-// its lane (readlane).  The pairs and the first kBatch partitions' outputs
-// are all loaded before the context length arrives (their addresses do not
-// depend on it; slots past this sequence's count hold stale bytes and get
-// weight 0 once the count is known): one memory round trip up to kBatch
-// partitions.  Partitions beyond 128 read their pairs directly.
+// Where a combine workgroup's row sits.  The split pass deals its units to
+// the XCDs in contiguous ranges of q8 = ceil(T / 8) units (T = n_seqs * hc *
+// max_parts when every sequence fills max_parts partitions); head row r =
+// b * n_heads + h belongs to unit row u = r / gc, whose first unit is
+// u * max_parts.  So XCD x wrote the rows [first_row(x), first_row(x + 1)),
+// and combine workgroup L (on XCD L % 8, dealt round-robin) takes row
+// first_row(L % 8) + L / 8 of that range: it reads the partials from the L2
+// they were written to (measured on config 2 at 4k: 0.24 us per decode).
+// For unequal contexts the split's ranges move and some rows are read from
+// another XCD; the mapping is a bijection onto the rows either way.
+struct CombineMap {
+  int64_t q8;      // units per XCD range under equal contexts
+  int64_t n_rows;  // n_seqs * n_heads
+  int gc;          // heads per unit row
+  int max_parts;
+  __host__ __device__ int64_t first_row(int64_t x) const {
+    const int64_t u = (x * q8 + max_parts - 1) / max_parts;
+    return u * gc < n_rows ? u * gc : n_rows;
+  }
+};
+
+// Merge the partitions of one (sequence, head) row over a 128-dim slice
+// (grid z): M = max m_p, L = sum l_p 2^(m_p - M), O = sum O_p 2^(m_p - M) / L
+// (the split-K form of flash_attn_f32's rescaling, flash_attn.rs:42-71).
+// One wave per row slice, two adjacent dims per lane (8-byte partial loads
+// and one packed store: half the workgroups and load instructions of one dim
+// per lane, 0.9 us less per config-2 decode).  Lane c also holds the (m, l)
+// pairs of partitions c and 64 + c, so M and L are wave reductions and
+// partition p's weight comes from its lane (readlane).  The pairs and the
+// first kBatch partitions' outputs are all loaded before the context length
+// arrives (their addresses do not depend on it; slots past this sequence's
+// count hold stale bytes and get weight 0 once the count is known): one
+// memory round trip up to kBatch partitions.  Partitions beyond 128 read
+// their pairs directly.
 template <int D>
 __global__ __launch_bounds__(64) void paged_decode_combine(const float* __restrict__ ws_o,
                                                            const float* __restrict__ ws_ml,
                                                            const int32_t* __restrict__ ctx_lens,
                                                            const int32_t* __restrict__ start_pos,
                                                            int ctx_const, int n_heads, int partition,
-                                                           int max_parts, void* out, int out_dtype) {
+                                                           CombineMap map, void* out, int out_dtype) {
   // Partitions beyond max_parts were never computed (the split pass latched
   // the error); only the computed ones are merged.
-  constexpr int kBatch = 64;
-  const int h = blockIdx.x, b = blockIdx.y, lane = int(threadIdx.x), d = 64 * int(blockIdx.z) + lane;
-  const int64_t row = int64_t(b) * n_heads + h;
+  constexpr int kBatch = 32;
+  const int max_parts = map.max_parts;
+  const int x = int(blockIdx.x & 7);
+  const int64_t row = map.first_row(x) + (blockIdx.x >> 3);
+  if (row >= map.first_row(x + 1)) return;  // uniform for the workgroup
+  const int b = int(row / n_heads), lane = int(threadIdx.x), d = 2 * (64 * int(blockIdx.z) + lane);
   const float2* ml = reinterpret_cast<const float2*>(ws_ml) + row * max_parts;
   const float* op = ws_o + row * max_parts * D + d;
   const float2 none = make_float2(-INFINITY, 0.0f);
   float2 m0 = lane < max_parts ? ml[lane] : none;
   float2 m1 = 64 + lane < max_parts ? ml[64 + lane] : none;
-  float ob[kBatch];
+  float2 ob[kBatch];
 #pragma unroll
   for (int c = 0; c < kBatch; ++c)
-    if (c < max_parts) ob[c] = op[int64_t(c) * D];
+    if (c < max_parts) ob[c] = *reinterpret_cast<const float2*>(op + int64_t(c) * D);
   const int ctx = ctx_lens ? ctx_lens[b] : ctx_const;
   const int st = start_pos ? start_pos[b] : 0;
   const int n = ctx - st;
@@ -116,42 +135,56 @@ __global__ __launch_bounds__(64) void paged_decode_combine(const float* __restri
   float mx = fmaxf(m0.x, m1.x);
   for (int p = 128 + lane; p < np; p += 64) mx = fmaxf(mx, ml[p].x);
   mx = group_max<64>(mx);
-  if (mx == -INFINITY) {  // no partition, or every key skipped: zeros (flash_attn.rs:66-71)
-    store_combined(out, out_dtype, row * D + d, 0.0f);
-    return;
-  }
-  const float w0 = m0.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m0.x - mx);
-  const float w1 = m1.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m1.x - mx);
-  float l = fmaf(m0.y, w0, m1.y * w1);
-  for (int p = 128 + lane; p < np; p += 64) {
-    const float2 v = ml[p];
-    if (v.x != -INFINITY) l = fmaf(v.y, __builtin_amdgcn_exp2f(v.x - mx), l);
-  }
-  l = group_sum<64>(l);
-  float o = 0.0f;
-#pragma unroll
-  for (int c = 0; c < kBatch; ++c)
-    if (c < np) o = fmaf(ob[c], lane_f32(w0, c), o);
-  for (int p0 = kBatch; p0 < np; p0 += kBatch) {
+  float o0 = 0.0f, o1 = 0.0f, l = 0.0f;
+  if (mx != -INFINITY) {  // else no partition, or every key skipped: zeros (flash_attn.rs:66-71)
+    const float w0 = m0.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m0.x - mx);
+    const float w1 = m1.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m1.x - mx);
+    l = fmaf(m0.y, w0, m1.y * w1);
+    for (int p = 128 + lane; p < np; p += 64) {
+      const float2 v = ml[p];
+      if (v.x != -INFINITY) l = fmaf(v.y, __builtin_amdgcn_exp2f(v.x - mx), l);
+    }
+    l = group_sum<64>(l);
 #pragma unroll
     for (int c = 0; c < kBatch; ++c)
-      if (p0 + c < np) ob[c] = op[int64_t(p0 + c) * D];
+      if (c < np) {
+        const float w = lane_f32(w0, c);
+        o0 = fmaf(ob[c].x, w, o0);
+        o1 = fmaf(ob[c].y, w, o1);
+      }
+    for (int p0 = kBatch; p0 < np; p0 += kBatch) {
 #pragma unroll
-    for (int c = 0; c < kBatch; ++c) {
-      const int p = p0 + c;
-      if (p < np) {
-        float w;
-        if (p < 128) {
-          w = lane_f32(w1, c);
-        } else {
-          const float2 v = ml[p];
-          w = v.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(v.x - mx);
+      for (int c = 0; c < kBatch; ++c)
+        if (p0 + c < np) ob[c] = *reinterpret_cast<const float2*>(op + int64_t(p0 + c) * D);
+#pragma unroll
+      for (int c = 0; c < kBatch; ++c) {
+        const int p = p0 + c;
+        if (p < np) {
+          float w;
+          if (p < 64) {
+            w = lane_f32(w0, p);
+          } else if (p < 128) {
+            w = lane_f32(w1, p - 64);
+          } else {
+            const float2 v = ml[p];
+            w = v.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(v.x - mx);
+          }
+          o0 = fmaf(ob[c].x, w, o0);
+          o1 = fmaf(ob[c].y, w, o1);
         }
-        o = fmaf(ob[c], w, o);
       }
     }
   }
-  store_combined(out, out_dtype, row * D + d, l > 0.0f ? o * (1.0f / l) : 0.0f);
+  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+  const float r0 = l > 0.0f ? o0 * inv : 0.0f, r1 = l > 0.0f ? o1 * inv : 0.0f;
+  const int64_t oi = row * D + d;
+  if (out_dtype == IT_F32) {
+    *reinterpret_cast<float2*>(static_cast<float*>(out) + oi) = make_float2(r0, r1);
+  } else {
+    const uint32_t lo = out_dtype == IT_BF16 ? f32_to_bf16_bits(r0) : f32_to_f16_bits(r0);
+    const uint32_t hi = out_dtype == IT_BF16 ? f32_to_bf16_bits(r1) : f32_to_f16_bits(r1);
+    *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(out) + oi) = lo | (hi << 16);
+  }
 }
 
 }  // namespace itkv

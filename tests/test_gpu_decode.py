@@ -198,6 +198,23 @@ def test_negative_start_is_skipped_and_latched(n_seqs):
     dev.check()  # the flag was cleared
 
 
+def test_misaligned_out_is_rejected():
+    """The combine stores two adjacent output elements at once, so out must
+    be 8-byte aligned for F32 and 4-byte aligned for 16-bit types:
+    InvalidInput before any launch, nothing written."""
+    import torch
+    from infer_train_amd import InvalidInput
+
+    hq, hkv, D, bs = 8, 2, 128, 16
+    dev, ref, tables, ctx, q, qdt = _build(orc.BF16, hq, hkv, D, bs, [100, 50], seed=3)
+    qd = to_dev(q.view(np.int16), torch.bfloat16)
+    for dt in (torch.float32, torch.bfloat16):
+        buf = torch.zeros(2 * hq * D + 1, dtype=dt, device="cuda:0")
+        with pytest.raises(InvalidInput, match="aligned"):
+            dev.decode(qd, to_dev(tables), to_dev(ctx), None, int(ctx.max()), out=buf[1:].view(2, hq, D))
+        assert not bool(buf.any())
+
+
 def test_config5_full_size_q8_0():
     """Config 5 at full size: Q8_0, Hq 24 / Hkv 4 / D 256, block 32, 16
     sequences of U[32768, 131072] tokens over a seeded permutation of the
