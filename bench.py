@@ -624,8 +624,28 @@ def bench_config3(steps, warmup, cpu):
         step(evs[i])
     torch.cuda.synchronize()
     c.check()
-    app = float(np.median([e[0].elapsed_time(e[1]) for e in evs]))
-    pre = float(np.median([e[1].elapsed_time(e[2]) for e in evs]))
+    app_1 = float(np.median([e[0].elapsed_time(e[1]) for e in evs]))
+    pre_1 = float(np.median([e[1].elapsed_time(e[2]) for e in evs]))
+
+    def b2b(fn, n):
+        """ms per call of `n` calls back to back, queued behind a GPU hold,
+        REGIONS times: the median region."""
+        runs = []
+        for _ in range(REGIONS):
+            _gpu_hold(2.0 + 0.1 * n)
+            e0, e1 = _events(2)
+            e0.record()
+            for _ in range(n):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            runs.append(e0.elapsed_time(e1) / n)
+        return float(np.median(runs))
+
+    step_b2b = b2b(step, steps)
+    pre = b2b(lambda: c.prefill(q, cu, chunk, tables, ctx, scale=scale, causal=True, out=out), steps)
+    app = b2b(lambda: c.append(kn, vn, slots_d), steps)
+    c.check()
     # Causal-exact flops: 4 D Hq sum over rows of the keys each row attends.
     flops = 4.0 * D * hq * B * sum(cached + i + 1 for i in range(chunk))
     n_tok = B * chunk
@@ -635,7 +655,11 @@ def bench_config3(steps, warmup, cpu):
            "pct_mfma_peak": round(100 * flops / (pre * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFS, 2),
            "append_us": round(app * 1e3, 2), "append_mtok_s": round(n_tok / (app * 1e-3) / 1e6, 1),
            "append_gbs": round(n_tok * hkv * 2 * D * 2 * 2 / (app * 1e-3) / 1e9, 1),
-           "steps_per_s": round(1e3 / (app + pre), 1), "timing": "medians of event-bracketed kernels"}
+           "step_us": round(step_b2b * 1e3, 2), "steps_per_s": round(1e3 / step_b2b, 1),
+           "prefill_us_single_bracket": round(pre_1 * 1e3, 2), "append_us_single_bracket": round(app_1 * 1e3, 2),
+           "timing": "prefill_us / append_us / step_us: `steps` calls back to back between two events, queued behind "
+                     "a bounded GPU sleep, median of 5 such regions; *_single_bracket: medians of per-step event "
+                     "brackets"}
     if cpu:
         import oracle as orc
 
