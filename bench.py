@@ -922,8 +922,10 @@ def movers_plan():
     return [
         ("append_copy_c2_step", "kv_append_copy", "config 2 step: 32 tokens, bf16, Hkv 4, D 128",
          c2_tok * 4 * d128 * bf * 2, c2_tok * 4 * d128 * bf * 2),
-        ("append_copy_c3_chunk", "kv_append_copy", "config 3 chunk: 8 x 512 tokens, bf16, Hkv 8, D 128",
-         c3_tok * 8 * d128 * bf * 2, c3_tok * 8 * d128 * bf * 2),
+        ("append_copy_c3_chunk", "kv_append_copy", "config 3 chunk: 8 x 512 consecutive positions (2048..2559) "
+         "through a permuted block table, bf16, Hkv 8, D 128", c3_tok * 8 * d128 * bf * 2, c3_tok * 8 * d128 * bf * 2),
+        ("append_copy_random_4096", "kv_append_copy", "4096 tokens to random slots (no two in one page row run), "
+         "bf16, Hkv 8, D 128", c3_tok * 8 * d128 * bf * 2, c3_tok * 8 * d128 * bf * 2),
         ("append_quant_q8_0_chunk", "kv_append_quant<8>", "Q8_0 quantise-append of 4096 tokens, Hkv 4, D 256",
          q8_tok * 4 * d256 * 4 * 2, q8_tok * 4 * d256 * 34 // 32 * 2),
         ("gather_bf16_c2_4k", "kv_gather_vec", "gather of config 2 at 4k: 32 x 4096 tokens, bf16, Hkv 4",
@@ -975,9 +977,15 @@ def run_movers():
     k2, v2 = bf16(32, 4, 128), bf16(32, 4, 128)
     timed("append_copy_c2_step", lambda: c2.append(k2, v2, sl2))
     c3 = PagedKvCache(4096, 16, 8, 128, it.BF16)
-    sl3 = torch.from_numpy(rng.permutation(4096 * 16)[:4096].astype(np.int64)).to(dev)
+    # Config 3's slot mapping: positions 2048..2559 of 8 sequences whose
+    # 160-block tables are a permutation of the pool.
+    t3 = rng.permutation(4096)[: 8 * 160].reshape(8, 160).astype(np.int64)
+    pos3 = np.arange(2048, 2560)
+    sl3 = torch.from_numpy(np.concatenate([t3[b, pos3 // 16] * 16 + pos3 % 16 for b in range(8)])).to(dev)
     k3, v3 = bf16(4096, 8, 128), bf16(4096, 8, 128)
     timed("append_copy_c3_chunk", lambda: c3.append(k3, v3, sl3))
+    slr = torch.from_numpy(rng.permutation(4096 * 16)[:4096].astype(np.int64)).to(dev)
+    timed("append_copy_random_4096", lambda: c3.append(k3, v3, slr))
     del c3, k3, v3
     # Q8_0 quantise-append
     c5 = PagedKvCache(8192, 32, 4, 256, it.Q8_0)
