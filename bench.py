@@ -293,13 +293,25 @@ class DecodeWorkload:
             torch.cuda.synchronize()
             split_runs.append(e0.elapsed_time(e1) / steps)
         split_b2b = float(np.median(split_runs))
+        # The append alone, `steps` launches back to back, REGIONS times.
+        append_runs = []
+        for _ in range(REGIONS):
+            _gpu_hold(hold)
+            e0, e1 = _events(2)
+            e0.record()
+            for i in range(steps):
+                self.caches[i % n_rep].append(self.k_new, self.v_new, self.slots)
+            e1.record()
+            torch.cuda.synchronize()
+            append_runs.append(e0.elapsed_time(e1) / steps)
+        append_b2b = float(np.median(append_runs))
         for c in self.caches:
             c.check()
         return {"append": float(app.mean()), "append_median": float(np.median(app)), "decode": float(dec.mean()),
                 "decode_median": float(np.median(dec)), "split": float(split.mean()),
                 "split_median": float(np.median(split)), "split_b2b": float(split_b2b),
                 "decode_b2b": float(decode_b2b), "decode_b2b_runs": [float(x) for x in decode_runs],
-                "split_b2b_runs": [float(x) for x in split_runs], "step_b2b": float(step_b2b), "step_wall": wall * 1e3 / steps,
+                "split_b2b_runs": [float(x) for x in split_runs], "append_b2b": append_b2b, "step_b2b": float(step_b2b), "step_wall": wall * 1e3 / steps,
                 "enqueue_per_step": enq / steps, "hold_ms": hold}
 
     def time_graph(self, replays, rotate=True):
@@ -505,7 +517,7 @@ def bench_config2(steps, warmup, cpu):
               "kv_gbs": round(w2.kv_bytes / (dm * 1e-3) / 1e9, 1), "decode_us": round(dm * 1e3, 2),
               "decode_us_single_bracket": round(r2["decode_median"] * 1e3, 2),
               "split_us": round(r2["split_b2b"] * 1e3, 2),
-              "kv_bytes": int(w2.kv_bytes), "append_us": round(r2["append_median"] * 1e3, 2),
+              "kv_bytes": int(w2.kv_bytes), "append_us": round(r2["append_b2b"] * 1e3, 2),
               "step_us": round(r2["step_b2b"] * 1e3, 2), "steps_per_s": round(1e3 / r2["step_b2b"], 1),
               "pct_hbm_peak": round(100 * w2.kv_bytes / (dm * 1e-3) / 1e9 / HBM_PEAK_GBS, 2)}
     w2.release()
@@ -782,26 +794,36 @@ def bench_config4(steps, warmup, cpu):
     ctx_d = torch.from_numpy(ctx).to(dev)
     st_d = torch.from_numpy(np.maximum(ctx - W, 0).astype(np.int32)).to(dev)
     torch.cuda.synchronize()
-    _gpu_hold(2.0 + 0.2 * steps)
-    e0, e1 = _events(2)
-    e0.record()
-    for _ in range(steps):
-        c.decode(q, tables, ctx_d, st_d, W, scale=scale, partition=P, out=out, ws=ws)
-    e1.record()
-    torch.cuda.synchronize()
-    dec = e0.elapsed_time(e1) / steps
+
+    def b2b(phase):
+        runs = []
+        for _ in range(REGIONS):
+            _gpu_hold(2.0 + 0.2 * steps)
+            e0, e1 = _events(2)
+            e0.record()
+            for _ in range(steps):
+                c.decode(q, tables, ctx_d, st_d, W, scale=scale, partition=P, out=out, ws=ws, phase=phase)
+            e1.record()
+            torch.cuda.synchronize()
+            runs.append(e0.elapsed_time(e1) / steps)
+        return float(np.median(runs))
+
+    dec = b2b("both")
+    split = b2b("split")
     kv_bytes = n_seqs * W * hkv * 2 * D * 2
     res = {"workload": f"config 4: {steps} sliding-window steps from position {start + warmup}, 64 sequences, "
                        "Hq 16 / Hkv 2 / D 128, W 4096, block 16, 16512-block pool in seeded order; step = host "
                        "window manager + evict + append + table sync + windowed split-K decode",
            "decode_us": round(dec * 1e3, 2), "kv_gbs": round(kv_bytes / (dec * 1e-3) / 1e9, 1),
            "pct_hbm_peak": round(100 * kv_bytes / (dec * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
-           "decode_us_single_bracket": round(dec1 * 1e3, 2),
+           "decode_us_single_bracket": round(dec1 * 1e3, 2), "split_us": round(split * 1e3, 2),
+           "split_pct_hbm_peak": round(100 * kv_bytes / (split * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
            "evict_append_sync_us": round(upd * 1e3, 2), "host_manager_us": round(1e6 * float(np.mean(hosts)), 1),
            "step_wall_us": round(wall * 1e6 / steps, 1), "blocks_evicted": n_ev, "kv_bytes": kv_bytes,
            "steps_per_s": round(1e6 / (wall * 1e6 / steps), 1), "gpu_steps_per_s": round(1e3 / (upd + dec), 1),
-           "timing": "decode_us: the last step's windowed decode issued `steps` times back to back between two "
-                     "events, queued behind a bounded GPU sleep; *_single_bracket and evict_append_sync_us: "
+           "timing": "decode_us (split_us): the last step's windowed decode (split pass) issued `steps` times back "
+                     "to back between two events, queued behind a bounded GPU sleep, median of 5 such regions; "
+                     "*_single_bracket and evict_append_sync_us: "
                      "medians of the steps' event brackets (they include host launch gaps); steps_per_s from "
                      "the wall clock (host window manager included)"}
     if cpu:
@@ -839,7 +861,7 @@ def bench_config5(steps, warmup, cpu):
     P = decode_partition(it.Q8_0, 256, 32, 24, 4, ctx)
     w = DecodeWorkload(it.Q8_0, 24, 4, 256, 32, ctx, pool_blocks, P, seed=5, replicas=1)
     r = w.time(steps, warmup, rotate=False)
-    dm, am = r["decode_b2b"], r["append_median"]
+    dm, am = r["decode_b2b"], r["append_b2b"]
     res = {"workload": "config 5: Q8_0 KV, Hq 24 / Hkv 4 / D 256, block 32, batch 16, ctx U[32768, 131072], "
                        f"quantise-append 1 token per sequence + split-K decode ({P}-token partitions from the host "
                        "planner) dequantising in registers",
@@ -886,7 +908,7 @@ def bench_q4(dtype, steps, warmup):
            "kv_bytes": int(w.kv_bytes), "decode_us": round(dm * 1e3, 2), "split_us": round(r["split_b2b"] * 1e3, 2),
            "kv_gbs": round(w.kv_bytes / (dm * 1e-3) / 1e9, 1),
            "pct_hbm_peak": round(100 * w.kv_bytes / (dm * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
-           "append_us": round(r["append_median"] * 1e3, 2)}
+           "append_us": round(r["append_b2b"] * 1e3, 2)}
     w.release()
     return res
 
@@ -1560,20 +1582,22 @@ def main():
         "split_us_single_bracket": round(cold["split_median"] * 1e3, 2),
         "kv_bytes_per_step": int(kv_bytes),
         "warm_kv_gbs": round(kv_bytes / (warm["decode_b2b"] * 1e-3) / 1e9, 1),
-        "append_mtok_s": round(head["B"] / (cold["append_median"] * 1e-3) / 1e6, 3),
-        "append_gbs": round(head["append_bytes"] / (cold["append_median"] * 1e-3) / 1e9, 2),
-        "append_us": round(cold["append_median"] * 1e3, 2),
+        "append_mtok_s": round(head["B"] / (cold["append_b2b"] * 1e-3) / 1e6, 3),
+        "append_gbs": round(head["append_bytes"] / (cold["append_b2b"] * 1e-3) / 1e9, 2),
+        "append_us": round(cold["append_b2b"] * 1e3, 2),
+        "append_us_single_bracket": round(cold["append_median"] * 1e3, 2),
         "steps_per_s": round(1e3 / cold["step_b2b"], 1),
         "host_enqueue_us_per_step": round(cold["enqueue_per_step"] * 1e3, 2),
         "timing": "HIP events on the library's stream.  Timed region: `steps` whole steps (append + split + "
                   "combine, 3 pool replicas rotated) back to back between two events, synchronised on both sides "
                   "(ms_per_step, step_us); then `steps` decodes (split + combine) back to back, 5 times, the median "
                   "region (decode_us, the value; every region in decode_us_runs); then `steps` split launches back "
-                  "to back, 5 times, the median (split_us, the roofline).  Each of these "
+                  "to back, 5 times, the median (split_us, the roofline); then `steps` appends back to back, 5 "
+                  "times, the median (append_us, append_mtok_s, append_gbs).  Each of these "
                   "regions is queued behind a bounded GPU sleep (torch.cuda._sleep) longer than the Python "
                   "harness takes to enqueue it (host_enqueue_us_per_step), so the events time the kernels as a "
-                  "native caller would issue them.  *_single_bracket and append_us: medians of per-step event "
-                  "brackets, which include each bracket's event overhead",
+                  "native caller would issue them.  *_single_bracket: medians of per-step event brackets, which "
+                  "include each bracket's event overhead",
         "roofline": {"bound": "hbm", "achieved": round(split_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(split_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": f"paged_decode_split<bf16,128,7> (mean duration of {args.steps} back-to-back launches "
