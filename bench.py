@@ -1426,6 +1426,113 @@ def summarize_config5_profile(d, args):
     print("\n".join(lines))
 
 
+# (source file, kernel symbol substring, what it is)
+ISA_KERNELS = [
+    ("it_decode_bf16.hip", "paged_decode_splitILi30ELi128ELi7ELi2ELi2E", "split-K decode, bf16, D 128, 7 heads, 2 waves, 2-slot rings (config 2 headline)"),
+    ("it_decode_q8_0.hip", "paged_decode_splitILi8ELi256ELi6ELi4ELi2E", "split-K decode, Q8_0, D 256, 6 heads, 4 waves (config 5)"),
+    ("it_attn.hip", "paged_decode_combineILi128E", "combine pass, D 128"),
+    ("it_prefill.hip", "paged_prefill_kernelILb1ELi8ELb1E", "chunked prefill, bf16, 8 waves (config 3)"),
+    ("it_cache.hip", "kv_append_copy", "append, bit copy"),
+    ("it_cache.hip", "kv_append_quantILi8E", "quantise-append, Q8_0"),
+    ("it_cache.hip", "kv_gather_vec", "block-table gather, 16/32-bit caches"),
+    ("it_cache.hip", "kv_clear_blocks", "evict (page clear)"),
+]
+ISA_CLASSES = [
+    ("global_load_lds_dwordx4", lambda i, l: i == "global_load_lds_dwordx4"),
+    ("global_load_dwordx4", lambda i, l: i == "global_load_dwordx4"),
+    ("global_store_dwordx4", lambda i, l: i == "global_store_dwordx4"),
+    ("other global/buffer", lambda i, l: (i.startswith("global_") or i.startswith("buffer_"))
+     and i not in ("global_load_lds_dwordx4", "global_load_dwordx4", "global_store_dwordx4")),
+    ("ds_read_b128", lambda i, l: i == "ds_read_b128"),
+    ("other ds_*", lambda i, l: i.startswith("ds_") and i != "ds_read_b128"),
+    ("v_mfma_*", lambda i, l: i.startswith("v_mfma")),
+    ("DPP (row_newbcast)", lambda i, l: "row_newbcast" in l),
+    ("DPP (other)", lambda i, l: ("quad_perm" in l or "row_shr" in l or "row_ror" in l or "row_bcast" in l
+                                  or "row_mirror" in l or "row_half_mirror" in l) and "row_newbcast" not in l),
+    ("v_permlane*_swap", lambda i, l: i.startswith("v_permlane")),
+    ("ds_swizzle / ds_bpermute", lambda i, l: i in ("ds_swizzle_b32", "ds_bpermute_b32")),
+    ("v_dot2*", lambda i, l: i.startswith("v_dot2")),
+    ("s_setprio", lambda i, l: i == "s_setprio"),
+    ("s_barrier", lambda i, l: i == "s_barrier"),
+    ("all instructions", lambda i, l: True),
+]
+
+
+def isa_census(args):
+    """CPU only: compile the path's device code to gfx950 assembly (hipcc -S,
+    the Makefile's flags) and count, per kernel, the instruction classes the
+    design relies on, with the register and LDS figures of each kernel's
+    metadata.  Writes profiles/isa_census.md."""
+    import re
+    import subprocess
+    import tempfile
+
+    csrc = os.path.join(ROOT, "infer_train_amd", "csrc")
+    flags = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-I" + os.path.join(ROOT, "include"), "-Xclang",
+             "-target-feature", "-Xclang", "-packed-fp32-ops", "-fno-gpu-flush-denormals-to-zero",
+             "-ffp-contract=fast", "--cuda-device-only", "-S"]
+    quant = {"it_decode_q8_0.hip"}  # built with -mllvm -amdgpu-mfma-vgpr-form, as in the Makefile
+    asm = {}
+    with tempfile.TemporaryDirectory() as td:
+        for src in sorted({k[0] for k in ISA_KERNELS}):
+            out = os.path.join(td, src + ".s")
+            extra = ["-mllvm", "-amdgpu-mfma-vgpr-form"] if src in quant else []
+            subprocess.run(["/opt/rocm/bin/hipcc"] + flags + extra + [os.path.join(csrc, src), "-o", out], check=True,
+                           stderr=subprocess.DEVNULL)
+            asm[src] = open(out).read()
+    rows = []
+    for src, sym, what in ISA_KERNELS:
+        text = asm[src]
+        m = re.search(r"^(_Z\S*" + sym + r"\S*):", text, re.M)
+        if not m:
+            rows.append((src, sym, what, None, None))
+            continue
+        name = m.group(1)
+        body = text[m.end():text.index(".Lfunc_end", m.end())]
+        counts = {c: 0 for c, _ in ISA_CLASSES}
+        for line in body.splitlines():
+            t = line.strip()
+            if not t or t.startswith((";", ".", "//")) or t.endswith(":"):
+                continue
+            ins = t.split()[0]
+            for c, f in ISA_CLASSES:
+                if f(ins, t):
+                    counts[c] += 1
+        meta = {}
+        mm = re.search(r"\.name:\s+" + re.escape(name) + r"\b", text)
+        if mm:
+            seg = text[max(0, mm.start() - 3000):mm.start() + 1500]
+            for key in ("vgpr_count", "agpr_count", "sgpr_count", "vgpr_spill_count", "group_segment_fixed_size"):
+                km = list(re.finditer(r"\." + key + r":\s+(\d+)", seg))
+                if km:  # the entry nearest the kernel's .name
+                    meta[key] = int(min(km, key=lambda x: abs(x.start() - (mm.start() - max(0, mm.start() - 3000)))).group(1))
+        rows.append((src, sym, what, counts, meta))
+    lines = ["# ISA census of the path's kernels (gfx950, this build)", "",
+             "Static instruction counts in each kernel's code (not dynamic counts: a loop body counts once), from",
+             "", "```", "python3 bench.py --isa-census", "```", "",
+             "which compiles each source with the Makefile's device flags (`hipcc --offload-arch=gfx950 -O3 "
+             "-Xclang -target-feature -Xclang -packed-fp32-ops -fno-gpu-flush-denormals-to-zero "
+             "--cuda-device-only -S`) and reads the kernels' metadata for registers and static LDS.", ""]
+    hdr = ["Kernel", "what"] + [c for c, _ in ISA_CLASSES] + ["VGPR", "AGPR", "SGPR", "VGPR spills"]
+    lines.append("| " + " | ".join(hdr) + " |")
+    lines.append("|" + "---|" * len(hdr))
+    for src, sym, what, counts, meta in rows:
+        if counts is None:
+            lines.append(f"| `{sym}` | {what} | not found |")
+            continue
+        vals = [str(counts[c]) for c, _ in ISA_CLASSES]
+        mv = [str(meta.get(k, "")) for k in ("vgpr_count", "agpr_count", "sgpr_count", "vgpr_spill_count")]
+        lines.append(f"| `{sym}` ({src}) | {what} | " + " | ".join(vals + mv) + " |")
+    lines += ["", "Reading it: the decode's K/V pages arrive by `global_load_lds_dwordx4` (64 lanes x 16 B straight "
+              "into LDS), its 16-bit dot products are `v_dot2*` with DPP `row_newbcast` operands and its "
+              "reductions `v_permlane*_swap` / DPP; only the quantised decode and the prefill issue `v_mfma`. "
+              "The data movers (append, gather, evict) load and store 16 B per lane (`global_load_dwordx4` / "
+              "`global_store_dwordx4`)."]
+    os.makedirs(os.path.join(ROOT, "profiles"), exist_ok=True)
+    open(os.path.join(ROOT, "profiles", "isa_census.md"), "w").write("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -1449,10 +1556,16 @@ def main():
                     help="run only the data-movement kernels and the config-4 decode (for rocprofv3 runs)")
     ap.add_argument("--summarize-movers-profile", metavar="DIR",
                     help="CPU only: summarise rocprofv3 output of --only-movers runs into profiles/data_movement.md")
+    ap.add_argument("--isa-census", action="store_true",
+                    help="CPU only: count the instruction classes of the path's kernels in this build's gfx950 "
+                         "assembly into profiles/isa_census.md")
     ap.add_argument("--summarize-profile", metavar="DIR",
                     help="CPU only: summarise rocprofv3 output DIR/{trace,fetch,write} of an --only-headline "
                          "--copy-probe run into profiles/")
     args = ap.parse_args()
+    if args.isa_census:
+        isa_census(args)
+        return
     if args.summarize_profile:
         summarize_profile(args.summarize_profile, args)
         return

@@ -153,6 +153,21 @@ def test_many_sequences_unit_mapping():
     assert_close(got, want, *TOL[orc.BF16], what="600 seqs")
 
 
+@pytest.mark.parametrize("D", [128, 256])
+def test_many_partitions_per_row(D):
+    """Rows with 1, 33, 100 and 141 partitions of 64 tokens: the combine
+    prefetches 32 partials per lane, weighs partitions 0-63 and 64-127 from
+    the lanes holding their (m, l) pairs, and reads the pairs of partitions
+    128 and up directly; every range is crossed.  fp32 and bf16 output, a
+    128- and a 256-dim head (one and two combine slices per row)."""
+    hq, hkv, bs = 8, 2, 16
+    ctx = [3, 2100, 6400, 9000]  # 1, 33, 100, 141 partitions
+    dev, ref, tables, c, q, qdt = _build(orc.BF16, hq, hkv, D, bs, ctx, seed=31)
+    for out_f32 in (True, False):
+        got, want = _run(dev, ref, tables, c, q, qdt, hq, partition=64, out_f32=out_f32)
+        assert_close(got, want, *TOL[orc.BF16], what=f"many partitions D={D} f32out={out_f32}")
+
+
 def test_uniform_lengths():
     """Equal lengths without start positions (the headline's shape at a
     smaller batch): full and partial last partitions, 64- and 512-token
