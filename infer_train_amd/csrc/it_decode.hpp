@@ -110,6 +110,7 @@ __global__ __launch_bounds__(64) void paged_decode_combine(const float* __restri
   // Partitions beyond max_parts were never computed (the split pass latched
   // the error); only the computed ones are merged.
   constexpr int kBatch = 32;
+  static_assert(kBatch <= 64, "the first batch takes its weights from lanes 0-63 of w0");
   const int max_parts = map.max_parts;
   const int x = int(blockIdx.x & 7);
   const int64_t row = map.first_row(x) + (blockIdx.x >> 3);
