@@ -315,46 +315,52 @@ class DecodeWorkload:
                 "enqueue_per_step": enq / steps, "hold_ms": hold}
 
     def time_graph(self, replays, rotate=True):
-        """split + combine captured in one HIP graph per pool replica, as a
-        serving loop that captures its decode would run them; `replays`
-        back-to-back replays (replicas rotated) between two events, 5 times:
-        the median per-replay time.  The first replay's output must equal the
-        eager decode's."""
+        """split + combine captured in a HIP graph, as a serving loop that
+        captures its decode steps would run them: one graph holds one decode
+        per pool replica (3 with rotation), so its launch is shared by
+        those decodes.  `replays` back-to-back replays between two events, 5
+        times: the median per-decode time.  The first replay's outputs must
+        equal the eager decodes'."""
         torch = self.torch
         n_rep = len(self.caches) if rotate else 1
-        self._split(self.caches[0])
-        self._combine(self.caches[0])
-        torch.cuda.synchronize()
-        eager = self.out.clone()
-        graphs = []
+        outs = [torch.empty_like(self.out) for _ in range(n_rep)]
+        eager = []
+        for i in range(n_rep):
+            self._split(self.caches[i])
+            self._combine(self.caches[i])
+            torch.cuda.synchronize()
+            eager.append(self.out.clone())
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
             self._split(self.caches[0])
             self._combine(self.caches[0])
         torch.cuda.current_stream().wait_stream(side)
-        for i in range(n_rep):
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g):
+        saved = self.out
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(n_rep):
+                self.out = outs[i]
                 self._split(self.caches[i])
                 self._combine(self.caches[i])
-            graphs.append(g)
-        graphs[0].replay()
+        self.out = saved
+        g.replay()
         torch.cuda.synchronize()
-        assert torch.equal(self.out, eager), "graph replay differs from the eager decode"
-        for i in range(3):
-            graphs[i % n_rep].replay()
+        for i in range(n_rep):
+            assert torch.equal(outs[i], eager[i]), "graph replay differs from the eager decode"
+        for _ in range(3):
+            g.replay()
         t = []
         for _ in range(5):
             _gpu_hold(2.0 + 0.05 * replays)
             e0, e1 = _events(2)
             e0.record()
-            for i in range(replays):
-                graphs[i % n_rep].replay()
+            for _ in range(replays):
+                g.replay()
             e1.record()
             torch.cuda.synchronize()
-            t.append(e0.elapsed_time(e1) / replays)
-        del graphs
+            t.append(e0.elapsed_time(e1) / (replays * n_rep))
+        del g
         return {"decode_graph": float(np.median(t))}
 
     def release(self):
@@ -1689,8 +1695,9 @@ def main():
         "step_wall_us": round(cold["step_wall"] * 1e3, 2),
         "decode_graph_us": round(graph["decode_graph"] * 1e3, 2),
         "decode_graph_kv_gbs": round(kv_bytes / (graph["decode_graph"] * 1e-3) / 1e9, 1),
-        "decode_graph_note": "split + combine captured in a HIP graph (one per pool replica), replayed back to "
-                             "back between two events (median of 5 runs); output checked equal to the eager decode",
+        "decode_graph_note": "one HIP graph holding a split + combine per pool replica (3), replayed back to back "
+                             "between two events (median of 5 runs), per decode; outputs checked equal to the eager "
+                             "decodes",
         "split_us": round(cold["split_b2b"] * 1e3, 2),
         "split_us_single_bracket": round(cold["split_median"] * 1e3, 2),
         "kv_bytes_per_step": int(kv_bytes),
