@@ -62,11 +62,11 @@ hipError_t launch_combine(int d, const DecodeArgs& a, int n_seqs, void* out, int
   for (int x = 0; x < 8; ++x) widest = std::max(widest, map.first_row(x + 1) - map.first_row(x));
   const dim3 grid(unsigned(8 * widest), 1u, unsigned(d / 128));
   if (d == 128)
-    hipLaunchKernelGGL(paged_decode_combine<128>, grid, dim3(64), 0, s, a.ws_o, a.ws_ml, a.ctx_lens, a.start_pos,
-                       a.ctx_const, a.n_heads, a.partition, map, out, out_dtype);
+    hipLaunchKernelGGL(paged_decode_combine<128>, grid, dim3(64), 0, s, a.ws_o, a.ws_ml, map.q8, map.n_rows, map.gc,
+                       map.max_parts, a.n_heads, a.ctx_lens, a.start_pos, a.ctx_const, a.partition, out, out_dtype);
   else if (d == 256)
-    hipLaunchKernelGGL(paged_decode_combine<256>, grid, dim3(64), 0, s, a.ws_o, a.ws_ml, a.ctx_lens, a.start_pos,
-                       a.ctx_const, a.n_heads, a.partition, map, out, out_dtype);
+    hipLaunchKernelGGL(paged_decode_combine<256>, grid, dim3(64), 0, s, a.ws_o, a.ws_ml, map.q8, map.n_rows, map.gc,
+                       map.max_parts, a.n_heads, a.ctx_lens, a.start_pos, a.ctx_const, a.partition, out, out_dtype);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();

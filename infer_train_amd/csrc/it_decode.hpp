@@ -100,18 +100,26 @@ struct CombineMap {
 // count hold stale bytes and get weight 0 once the count is known): one
 // memory round trip up to kBatch partitions.  Partitions beyond 128 read
 // their pairs directly.
+// The leading scalar arguments (the map's fields, the workspace and the
+// length pointers: 16 dwords) are preloaded into SGPRs at wave launch
+// (kernarg preloading, gfx950), so the first loads do not wait for a
+// kernel-argument fetch.
 template <int D>
 __global__ __launch_bounds__(64) void paged_decode_combine(const float* __restrict__ ws_o,
-                                                           const float* __restrict__ ws_ml,
+                                                           const float* __restrict__ ws_ml, int64_t q8,
+                                                           int64_t n_rows, int gc, int max_parts, int n_heads,
                                                            const int32_t* __restrict__ ctx_lens,
-                                                           const int32_t* __restrict__ start_pos,
-                                                           int ctx_const, int n_heads, int partition,
-                                                           CombineMap map, void* out, int out_dtype) {
+                                                           const int32_t* __restrict__ start_pos, int ctx_const,
+                                                           int partition, void* out, int out_dtype) {
   // Partitions beyond max_parts were never computed (the split pass latched
   // the error); only the computed ones are merged.
   constexpr int kBatch = 32;
   static_assert(kBatch <= 64, "the first batch takes its weights from lanes 0-63 of w0");
-  const int max_parts = map.max_parts;
+  CombineMap map;
+  map.q8 = q8;
+  map.n_rows = n_rows;
+  map.gc = gc;
+  map.max_parts = max_parts;
   const int x = int(blockIdx.x & 7);
   const int64_t row = map.first_row(x) + (blockIdx.x >> 3);
   if (row >= map.first_row(x + 1)) return;  // uniform for the workgroup
