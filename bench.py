@@ -1426,8 +1426,9 @@ def summarize_config5_profile(d, args):
             # the MFMA busy count sums all 1024 SIMDs.
             frac = med["SQ_VALU_MFMA_BUSY_CYCLES"] / (med["SQ_BUSY_CYCLES"] * 32)
             lines += ["", f"MFMA pipe busy {100 * frac:.1f}% of SIMD cycles (SQ_VALU_MFMA_BUSY_CYCLES over "
-                          "SQ_BUSY_CYCLES x 32 SIMDs per shader engine). The kernel is bound by VALU and MFMA "
-                          "issue, not HBM: fp32-exact Q8_0 products run on MFMA as three exact bf16 passes."]
+                          "SQ_BUSY_CYCLES x 32 SIMDs per shader engine). The kernel is not HBM-bound (traffic "
+                          "near 1.0x, below 70% of peak): its time goes to VALU and MFMA issue for the fp32-exact "
+                          "Q8_0 products, which run on MFMA as three exact bf16 passes."]
     open(os.path.join(ROOT, "profiles", "decode_split_config5.md"), "w").write("\n".join(lines) + "\n")
     print("\n".join(lines))
 
