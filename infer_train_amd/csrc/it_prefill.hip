@@ -158,12 +158,22 @@ __global__ __launch_bounds__(64 * W) void paged_prefill_kernel(PrefillArgs a) {
   // ids to the 8 XCDs round-robin; the ids are remapped so that all query
   // blocks of one (sequence, KV head), which stream the same K/V pages, run
   // on one XCD and share its L2 (in id order each XCD would fetch every
-  // sequence's pages).  Within a (sequence, KV head) query blocks go in
-  // decreasing order: in causal attention later blocks see more keys, so
-  // the longest workgroups start first.
+  // sequence's pages).  In causal attention later query blocks see more
+  // keys, so each XCD takes its units longest first: the k-th workgroup of
+  // an XCD holding ppx whole (sequence, KV head) pairs takes query rank
+  // k / ppx of pair k % ppx.  Workgroups start in id order on whichever CU
+  // frees first, so a CU whose first workgroup was short takes the longest
+  // one left (config 3, two workgroups per CU: 166 against 174 us with
+  // query blocks in pair order).
   const int n_full = int(gridDim.x) & ~7;
   const int id = blockIdx.x;
-  const int unit = id < n_full ? (id & 7) * (n_full >> 3) + (id >> 3) : id;
+  const int per_xcd = n_full >> 3;
+  int k = id >> 3;
+  if (per_xcd % a.n_qb == 0) {
+    const int ppx = per_xcd / a.n_qb;
+    k = (k % ppx) * a.n_qb + k / ppx;
+  }
+  const int unit = id < n_full ? (id & 7) * per_xcd + k : id;
   const int pair = unit / a.n_qb;
   const int qb = a.n_qb - 1 - (unit - pair * a.n_qb);
   const int kvh = pair % a.n_kv_heads, b = pair / a.n_kv_heads;
