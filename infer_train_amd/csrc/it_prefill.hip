@@ -169,7 +169,7 @@ __global__ __launch_bounds__(64 * W) void paged_prefill_kernel(PrefillArgs a) {
   const int id = blockIdx.x;
   const int per_xcd = n_full >> 3;
   int k = id >> 3;
-  if (per_xcd % a.n_qb == 0) {
+  if (per_xcd > 0 && per_xcd % a.n_qb == 0) {
     const int ppx = per_xcd / a.n_qb;
     k = (k % ppx) * a.n_qb + k / ppx;
   }
