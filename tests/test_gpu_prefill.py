@@ -77,6 +77,21 @@ def test_prefill_small_causal(dt, hq, hkv):
     assert_close(from_dev(out), want, RTOL, ATOL, what=f"prefill dt={dt} hq={hq} hkv={hkv}")
 
 
+def test_prefill_longest_first_order_with_tail_workgroups():
+    """Workgroup ids are dealt to XCDs as 8 ranges; an XCD holding whole
+    (sequence, KV head) pairs takes its query blocks longest first.  Here 9
+    sequences x 2 KV heads x 2 query blocks of 64 rows = 36 workgroups:
+    ranges of 4 (2 pairs each, so the remap is not the identity), and 4 tail
+    workgroups past the last full set of 8 keep their ids.  Every row of
+    every sequence against the oracle."""
+    ctx = [128 + 16 * i for i in range(9)]
+    q_lens = [128] * 9
+    dev, ref, tables, ctx, cu, q, td = _setup(orc.BF16, 8, 2, ctx, q_lens, seed=71)
+    out, scale = _run(dev, tables, ctx, cu, q, td, 8)
+    want = ref.prefill(widen(q, orc.BF16), 8, cu, tables, ctx, scale, causal=True)
+    assert_close(from_dev(out), want, RTOL, ATOL, what="prefill, 36 workgroups")
+
+
 def test_prefill_non_causal_and_bf16_out():
     hq, hkv = 8, 2
     dev, ref, tables, ctx, cu, q, td = _setup(orc.BF16, hq, hkv, [130, 77], [33, 77], seed=5)
