@@ -125,15 +125,55 @@ void it_kv_manager_destroy(it_kv_manager* mgr);
  * logical blocks first_block.., with the next token at position `pos`. */
 int32_t it_kv_manager_seed_seq(it_kv_manager* mgr, int32_t seq, int64_t pos, int64_t first_block,
                                const int32_t* blocks, int32_t n_blocks);
-/* Append n_tokens[i] tokens to seqs[i], in list order.  Writes
- * sum(n_tokens) slots into slots_out and the freed block ids, in free
- * order, into evicted_out (capacity evicted_cap).  On error the manager
- * state is unspecified. */
+/* One step's plan, filled by it_kv_manager_step.  The caller owns every
+ * array; a NULL pointer marks an output it does not want.
+ * Blocks "released" by a sequence drop that sequence's reference
+ * (BlockPool::free, paged.rs:48-53); only those whose refcount reaches 0
+ * return to the pool.  `evicted` lists exactly those, in free order: the
+ * pages to clear with it_kv_evict.  A block that another (forked) sequence
+ * still holds is released but not listed, and its pages stay intact.
+ * Returned blocks go back on the pool's free list when the step ends, in
+ * free order, so within one step no block is both freed and handed out
+ * again.  A token whose block the window returns later in the same step
+ * (a step that appends more tokens than the window holds) gets slot -1:
+ * it is never written.
+ * Device order of a step: it_kv_copy_blocks(cow_src, cow_dst), then
+ * it_kv_evict(evicted), then the append, then it_kv_sync_tables; a copy
+ * source the same step returns to the pool is read before it is cleared. */
+typedef struct {
+  int64_t* slots;      /* [tokens_cap] slot of every new token, in list order */
+  int32_t* token_seq;  /* [tokens_cap] its sequence, or NULL (it_kv_sync_tables' seq) */
+  int32_t* token_pos;  /* [tokens_cap] its position, or NULL (it_kv_sync_tables' pos) */
+  int32_t tokens_cap;
+  int32_t n_tokens;    /* out: sum(n_tokens) */
+  int32_t* evicted;    /* [evicted_cap] blocks returned to the pool by the window */
+  int32_t evicted_cap;
+  int32_t n_evicted;   /* out */
+  int32_t* cow_src;    /* [cow_cap] copy-on-write pairs (page copies to make  */
+  int32_t* cow_dst;    /*   before the append); cow_src NULL = no copy-on-write */
+  int32_t cow_cap;
+  int32_t n_cow;       /* out */
+  int32_t* ctx_lens;   /* [max_seqs] after the step (next position), or NULL */
+  int32_t* start_pos;  /* [max_seqs] after the step (window start, else 0), or NULL */
+} it_kv_step_plan;
+
+/* Append n_tokens[i] tokens to seqs[i], in list order (a sequence may be
+ * listed more than once), and fill `plan`.  Sequence ids, counts and
+ * tokens_cap are checked before any state changes; a later error (pool
+ * exhausted, a capacity exceeded) leaves the manager state unspecified.
+ * No counterpart in the reference: its batcher (continuous.rs:28-74)
+ * admits requests but builds no slot mapping; this is that step. */
+int32_t it_kv_manager_step(it_kv_manager* mgr, const int32_t* seqs, const int32_t* n_tokens,
+                           int32_t n, it_kv_step_plan* plan);
+/* it_kv_manager_step with slots (sized sum(n_tokens)) and the evicted list
+ * only. */
 int32_t it_kv_manager_append(it_kv_manager* mgr, const int32_t* seqs, const int32_t* n_tokens,
                              int32_t n, int64_t* slots_out, int32_t* evicted_out,
                              int32_t evicted_cap, int32_t* n_evicted);
 /* Release every block of `seq` (BlockPool::free, lowest logical block
- * first) and reset it to position 0; the freed ids go to evicted_out. */
+ * first) and reset it to position 0.  The blocks that return to the pool
+ * (refcount 0) go to evicted_out; evicted_cap must cover every block the
+ * sequence holds, else IT_INVALID_INPUT and nothing changes. */
 int32_t it_kv_manager_release_seq(it_kv_manager* mgr, int32_t seq, int32_t* evicted_out,
                                   int32_t evicted_cap, int32_t* n_evicted);
 /* Prefix sharing: dst takes src's blocks and position; each block gets
@@ -141,6 +181,7 @@ int32_t it_kv_manager_release_seq(it_kv_manager* mgr, int32_t seq, int32_t* evic
  * to a shared partial block copies it (copy-on-write): the manager
  * allocates a fresh block and reports the (src, dst) pair in cow_out. */
 int32_t it_kv_manager_fork(it_kv_manager* mgr, int32_t src_seq, int32_t dst_seq);
+/* it_kv_manager_step with copy-on-write, slots, evicted and cow lists. */
 int32_t it_kv_manager_append_cow(it_kv_manager* mgr, const int32_t* seqs, const int32_t* n_tokens,
                                  int32_t n, int64_t* slots_out, int32_t* evicted_out,
                                  int32_t evicted_cap, int32_t* n_evicted, int32_t* cow_src,
@@ -182,6 +223,7 @@ typedef struct {
   int32_t dtype;
   int32_t device;
   int32_t owns_memory;
+  int32_t n_layers;    /* layers in each pool (1 for a layer view) */
 } it_kv_cache_desc;
 
 int64_t it_kv_page_bytes(int32_t block_size, int32_t head_dim, int32_t dtype);
@@ -193,6 +235,27 @@ int32_t it_kv_cache_new(int32_t device, int64_t num_blocks, int32_t block_size,
 int32_t it_kv_cache_wrap(int32_t device, void* k_pool, void* v_pool, int64_t num_blocks,
                          int32_t block_size, int32_t n_kv_heads, int32_t head_dim, int32_t dtype,
                          it_kv_cache** out);
+/* Every layer of a model in one cache: the reference's per-layer
+ * kv_cache_k/kv_cache_v (forward.rs:17-18, 36-37, indexed by layer_idx at
+ * :224-228).  Each pool holds n_layers (1..4096) layers one after another,
+ * [n_layers][num_blocks][n_kv_heads] pages, so one block id (one manager,
+ * one block table) names the same pages in every layer.  it_kv_evict and
+ * it_kv_copy_blocks on a multi-layer cache act on every layer in one
+ * launch; it_kv_sync_tables and it_kv_cache_check take it as it is.  The
+ * per-layer entry points (append, append_rope, gather, decode, prefill)
+ * take a layer's view from it_kv_cache_layer and return IT_INVALID_INPUT
+ * for a multi-layer handle. */
+int32_t it_kv_cache_new_layers(int32_t device, int32_t n_layers, int64_t num_blocks, int32_t block_size,
+                               int32_t n_kv_heads, int32_t head_dim, int32_t dtype, it_kv_cache** out);
+/* Wraps caller-owned pools of n_layers * num_blocks * n_kv_heads * page_bytes
+ * bytes each. */
+int32_t it_kv_cache_wrap_layers(int32_t device, int32_t n_layers, void* k_pool, void* v_pool,
+                                int64_t num_blocks, int32_t block_size, int32_t n_kv_heads,
+                                int32_t head_dim, int32_t dtype, it_kv_cache** out);
+/* A one-layer view of layer `layer` (no allocation on the device: the
+ * view's pools point into the parent's, and it shares the parent's
+ * latched-error word).  Destroy views before their parent. */
+int32_t it_kv_cache_layer(const it_kv_cache* cache, int32_t layer, it_kv_cache** out);
 int32_t it_kv_cache_destroy(it_kv_cache* cache);
 int32_t it_kv_cache_describe(const it_kv_cache* cache, it_kv_cache_desc* out);
 /* Synchronises `stream`, then reports (and clears) a latched device-side
@@ -258,8 +321,8 @@ int32_t it_kv_gather(const it_kv_cache* cache, const int32_t* block_tables, int3
                      const int32_t* ctx_lens, const int32_t* start_pos, const int64_t* cu_out,
                      int32_t n_seqs, int32_t max_tokens, void* k_out, void* v_out, void* stream);
 
-/* Evict: zero every page (all heads, K and V) of the given blocks, so a
- * recycled block starts clean.  blocks: int32[n], device. */
+/* Evict: zero every page (all heads, K and V, every layer) of the given
+ * blocks, so a recycled block starts clean.  blocks: int32[n], device. */
 int32_t it_kv_evict(it_kv_cache* cache, const int32_t* blocks, int32_t n, void* stream);
 
 /* Keep a device block table in step with the slot mapping: for each token
@@ -272,7 +335,8 @@ int32_t it_kv_sync_tables(it_kv_cache* cache, int32_t* tables, int32_t max_block
                           const int32_t* seq, const int32_t* pos, const int64_t* slots, int32_t n,
                           void* stream);
 
-/* Copy-on-write page copy: block dst[i] := block src[i] (all heads, K, V). */
+/* Copy-on-write page copy: block dst[i] := block src[i] (all heads, K, V,
+ * every layer). */
 int32_t it_kv_copy_blocks(it_kv_cache* cache, const int32_t* src, const int32_t* dst, int32_t n,
                           void* stream);
 

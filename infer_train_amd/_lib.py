@@ -67,6 +67,27 @@ class CacheDesc(C.Structure):
         ("dtype", C.c_int32),
         ("device", C.c_int32),
         ("owns_memory", C.c_int32),
+        ("n_layers", C.c_int32),
+    ]
+
+
+class StepPlanC(C.Structure):
+    """it_kv_step_plan (include/it_kv.h)."""
+    _fields_ = [
+        ("slots", C.c_void_p),
+        ("token_seq", C.c_void_p),
+        ("token_pos", C.c_void_p),
+        ("tokens_cap", C.c_int32),
+        ("n_tokens", C.c_int32),
+        ("evicted", C.c_void_p),
+        ("evicted_cap", C.c_int32),
+        ("n_evicted", C.c_int32),
+        ("cow_src", C.c_void_p),
+        ("cow_dst", C.c_void_p),
+        ("cow_cap", C.c_int32),
+        ("n_cow", C.c_int32),
+        ("ctx_lens", C.c_void_p),
+        ("start_pos", C.c_void_p),
     ]
 
 
@@ -92,6 +113,7 @@ SIGNATURES = {
     "it_kv_manager_new": (i32, [P, i32, i32, i32, i32, PP]),
     "it_kv_manager_destroy": (None, [P]),
     "it_kv_manager_seed_seq": (i32, [P, i32, i64, i64, P, i32]),
+    "it_kv_manager_step": (i32, [P, P, P, i32, C.POINTER(StepPlanC)]),
     "it_kv_manager_append": (i32, [P, P, P, i32, P, P, i32, P]),
     "it_kv_manager_release_seq": (i32, [P, i32, P, i32, P]),
     "it_kv_manager_fork": (i32, [P, i32, i32]),
@@ -100,6 +122,9 @@ SIGNATURES = {
     "it_kv_page_bytes": (i64, [i32, i32, i32]),
     "it_kv_cache_new": (i32, [i32, i64, i32, i32, i32, i32, PP]),
     "it_kv_cache_wrap": (i32, [i32, P, P, i64, i32, i32, i32, i32, PP]),
+    "it_kv_cache_new_layers": (i32, [i32, i32, i64, i32, i32, i32, i32, PP]),
+    "it_kv_cache_wrap_layers": (i32, [i32, i32, P, P, i64, i32, i32, i32, i32, PP]),
+    "it_kv_cache_layer": (i32, [P, i32, PP]),
     "it_kv_cache_destroy": (i32, [P]),
     "it_kv_cache_describe": (i32, [P, C.POINTER(CacheDesc)]),
     "it_kv_cache_check": (i32, [P, P]),

@@ -11,7 +11,7 @@ from typing import Dict, List, Optional, Sequence, Tuple
 
 import numpy as np
 
-from ._lib import check, lib
+from ._lib import StepPlanC, check, lib
 from .memory import BlockPool
 
 __all__ = ["KvManager", "ContinuousBatcher", "RequestState", "RequestContext", "StepPlan"]
@@ -19,26 +19,33 @@ __all__ = ["KvManager", "ContinuousBatcher", "RequestState", "RequestContext", "
 
 @dataclass
 class StepPlan:
-    """What one append step hands to the device: the slot of every new token,
-    the blocks freed by the window (to clear with kv_evict) and the
-    copy-on-write page pairs (to copy with kv_copy_blocks before the append)."""
+    """What one append step hands to the device: the slot of every new token
+    with its sequence and position (it_kv_sync_tables' inputs), the blocks
+    the step returned to the pool (refcount 0: the pages to clear with
+    kv_evict), the copy-on-write page pairs (to copy with kv_copy_blocks
+    before the append), and every sequence slot's context length and window
+    start after the step."""
 
     slots: np.ndarray
     evicted: np.ndarray
     cow_src: np.ndarray = field(default_factory=lambda: np.zeros(0, np.int32))
     cow_dst: np.ndarray = field(default_factory=lambda: np.zeros(0, np.int32))
-    # Sequence and position of every new token (for it_kv_sync_tables).
     token_seq: np.ndarray = field(default_factory=lambda: np.zeros(0, np.int32))
     token_pos: np.ndarray = field(default_factory=lambda: np.zeros(0, np.int32))
+    ctx_lens: Optional[np.ndarray] = None
+    start_pos: Optional[np.ndarray] = None
 
 
 class KvManager:
-    """Slot mapping and block tables over a BlockPool.
+    """Slot mapping and block tables over a BlockPool (native:
+    it_kv_manager_step).
 
     slot(pos) = table[pos // bs] * bs + pos % bs; a block is allocated when
     pos % bs == 0.  With `window` W > 0, before the token at position p every
-    held block whose last position is < p - W + 1 is released (oldest first).
-    Sequences of one step are processed in the order listed.
+    held block whose last position is < p - W + 1 drops this sequence's
+    reference (oldest first); the blocks whose refcount reaches 0 are the
+    step's `evicted` list.  Sequences of one step are processed in the order
+    listed.
     """
 
     def __init__(self, pool: BlockPool, block_size: int, max_seqs: int, max_blocks_per_seq: int, window: int = 0):
@@ -51,47 +58,54 @@ class KvManager:
         check(lib.it_kv_manager_new(pool.handle, block_size, max_seqs, max_blocks_per_seq, window, C.byref(h)))
         self._h = h
         self._destroy = lib.it_kv_manager_destroy  # bound now: module globals may be gone at exit
+        # Reused output buffers of it_kv_manager_step (grown on demand); the
+        # plan returned to the caller holds copies.
+        self._plan = StepPlanC()
+        self._tok_cap = 0
+        # Blocks returned to the pool in one step: at most the pool's capacity.
+        self._ev = np.empty(pool.capacity() + 1, np.int32)
+        self._cs = np.empty(0, np.int32)
+        self._cd = np.empty(0, np.int32)
+        self._plan.evicted = self._ev.ctypes.data
+        self._plan.evicted_cap = self._ev.size
+
+    def _grow(self, total: int) -> None:
+        cap = max(total, 2 * self._tok_cap, 64)
+        self._slots = np.empty(cap, np.int64)
+        self._tseq = np.empty(cap, np.int32)
+        self._tpos = np.empty(cap, np.int32)
+        self._cs = np.empty(cap, np.int32)
+        self._cd = np.empty(cap, np.int32)
+        pl = self._plan
+        pl.slots, pl.token_seq, pl.token_pos = self._slots.ctypes.data, self._tseq.ctypes.data, self._tpos.ctypes.data
+        pl.tokens_cap = cap
+        pl.cow_cap = cap  # at most one copy per token
+        self._tok_cap = cap
 
     def seed_seq(self, seq: int, pos: int, first_block: int, blocks: Sequence[int]) -> None:
         arr = np.ascontiguousarray(np.asarray(blocks, dtype=np.int32))
         check(lib.it_kv_manager_seed_seq(self._h, seq, int(pos), int(first_block), arr.ctypes.data, arr.size))
 
     def append(self, seqs: Sequence[int], n_tokens: Sequence[int] | int = 1, cow: bool = False) -> StepPlan:
-        seqs_a = np.ascontiguousarray(np.asarray(seqs, dtype=np.int32))
+        """One step: n_tokens[i] tokens to seqs[i] (in list order)."""
+        seqs_a = np.ascontiguousarray(seqs, dtype=np.int32)
         if np.isscalar(n_tokens):
             nt = np.full(seqs_a.size, int(n_tokens), dtype=np.int32)
         else:
-            nt = np.ascontiguousarray(np.asarray(n_tokens, dtype=np.int32))
+            nt = np.ascontiguousarray(n_tokens, dtype=np.int32)
         total = int(nt.sum())
-        before = self.positions()
-        token_seq = np.repeat(seqs_a, nt).astype(np.int32)
-        # Each token's position: its sequence's position before the call plus
-        # the tokens of that sequence listed before it (a sequence may be
-        # listed more than once, as the native manager allows).
-        token_pos = np.empty(total, dtype=np.int32)
-        run = before.astype(np.int64)
-        off = 0
-        for sq, k in zip(seqs_a.tolist(), nt.tolist()):
-            token_pos[off:off + k] = run[sq] + np.arange(k)
-            run[sq] += k
-            off += k
-        slots = np.empty(max(total, 1), dtype=np.int64)
-        # Upper bound of frees: every block of every listed sequence.
-        cap = int(seqs_a.size * self.max_blocks + 1)
-        ev = np.empty(cap, dtype=np.int32)
-        nev = C.c_int32(0)
-        if cow:
-            cs = np.empty(cap, dtype=np.int32)
-            cd = np.empty(cap, dtype=np.int32)
-            nc = C.c_int32(0)
-            check(lib.it_kv_manager_append_cow(self._h, seqs_a.ctypes.data, nt.ctypes.data, seqs_a.size,
-                                               slots.ctypes.data, ev.ctypes.data, cap, C.byref(nev),
-                                               cs.ctypes.data, cd.ctypes.data, cap, C.byref(nc)))
-            return StepPlan(slots[:total], ev[:nev.value].copy(), cs[:nc.value].copy(), cd[:nc.value].copy(),
-                            token_seq, token_pos)
-        check(lib.it_kv_manager_append(self._h, seqs_a.ctypes.data, nt.ctypes.data, seqs_a.size,
-                                       slots.ctypes.data, ev.ctypes.data, cap, C.byref(nev)))
-        return StepPlan(slots[:total], ev[:nev.value].copy(), token_seq=token_seq, token_pos=token_pos)
+        if total > self._tok_cap:
+            self._grow(total)
+        ctx = np.empty(self.max_seqs, np.int32)
+        st = np.empty(self.max_seqs, np.int32)
+        pl = self._plan
+        pl.cow_src = self._cs.ctypes.data if cow else None
+        pl.cow_dst = self._cd.ctypes.data if cow else None
+        pl.ctx_lens, pl.start_pos = ctx.ctypes.data, st.ctypes.data
+        check(lib.it_kv_manager_step(self._h, seqs_a.ctypes.data, nt.ctypes.data, seqs_a.size, C.byref(pl)))
+        n, ne, nc = pl.n_tokens, pl.n_evicted, pl.n_cow
+        return StepPlan(self._slots[:n].copy(), self._ev[:ne].copy(), self._cs[:nc].copy(), self._cd[:nc].copy(),
+                        self._tseq[:n].copy(), self._tpos[:n].copy(), ctx, st)
 
     def positions(self) -> np.ndarray:
         """Next position (= context length) of every sequence slot."""
@@ -100,6 +114,8 @@ class KvManager:
         return cl
 
     def release(self, seq: int) -> np.ndarray:
+        """Drop every block of `seq`; returns the blocks that went back to
+        the pool (refcount 0), the pages to clear."""
         cap = self.max_blocks
         ev = np.empty(cap, dtype=np.int32)
         nev = C.c_int32(0)
@@ -197,7 +213,9 @@ class ContinuousBatcher:
         """Running -> Preempted.  keep_blocks False: the request's blocks are
         released (BlockPool::free, lowest logical block first) with its
         sequence slot, and it is prefilled again on resume; True: blocks and
-        slot stay held.  Returns the freed block ids (empty when kept)."""
+        slot stay held.  Returns the blocks that went back to the pool
+        (refcount 0: the pages to clear; a block a forked request still
+        holds is not among them), empty when kept."""
         ctx = self.requests[request_id]
         if ctx.state != RequestState.Running:
             raise ValueError(f"request {request_id} is {ctx.state.value}, not Running")
@@ -246,7 +264,8 @@ class ContinuousBatcher:
 
     def finish(self, request_id: int) -> np.ndarray:
         """Running or Preempted -> Finished; the request's blocks (if it
-        still holds them) and sequence slot are released."""
+        still holds them) and sequence slot are released.  Returns the
+        blocks that went back to the pool (refcount 0)."""
         ctx = self.requests[request_id]
         if ctx.state == RequestState.Running:
             self.running.remove(request_id)

@@ -203,6 +203,7 @@ int32_t paged_decode_phases(const char* who, const it_kv_cache* c, const void* q
                             int32_t max_tokens, float scale, int32_t partition, void* ws, size_t ws_bytes,
                             void* out, int32_t out_dtype, void* stream, int phases) {
   if (!c) return fail(IT_INVALID_INPUT, "%s: cache is NULL", who);
+  if (int32_t rc = one_layer(c, who)) return rc;
   if (!block_tables || !ctx_lens) return fail(IT_INVALID_INPUT, "%s: NULL block_tables/ctx_lens", who);
   if (max_blocks <= 0) return fail(IT_INVALID_INPUT, "%s: max_blocks %d", who, max_blocks);
   if (!(scale == scale)) return fail(IT_INVALID_INPUT, "%s: scale is NaN", who);
@@ -270,7 +271,9 @@ std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices] = {};
 
 // The device address of `scratch` on `device` (current), or NULL with the
-// thread's message set.
+// thread's message set.  it_kv_cache_new / _wrap look it up for the
+// cache's device already (noalloc_prepare), so a call made under graph
+// capture finds it here without a runtime call.
 void* scratch_address(int device) {
   if (device < 0 || device >= kMaxDevices) {
     fail(IT_DEVICE_ERROR, "it_paged_decode_noalloc: device %d outside [0, %d)", device, kMaxDevices);
@@ -289,6 +292,8 @@ void* scratch_address(int device) {
   return g_scratch_ptr[device];
 }
 }  // namespace
+
+int32_t itkv::noalloc_prepare(int device) { return scratch_address(device) ? IT_OK : IT_DEVICE_ERROR; }
 
 extern "C" int32_t it_paged_decode_noalloc(const it_kv_cache* c, const void* q, int32_t q_dtype, int32_t n_heads,
                                            const int32_t* block_tables, int32_t max_blocks, const int32_t* ctx_lens,

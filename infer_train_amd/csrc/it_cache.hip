@@ -24,6 +24,7 @@ using namespace itkv;
 
 namespace {
 constexpr int kThreads = 256;
+constexpr int32_t kMaxLayers = 4096;
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
@@ -91,6 +92,32 @@ __global__ __launch_bounds__(kThreads) void kv_append_copy(
     __builtin_nontemporal_store(kv[j], reinterpret_cast<u4*>(kpool + dst));
     __builtin_nontemporal_store(vv[j], reinterpret_cast<u4*>(vpool + dst));
   }
+}
+
+// Append, bit copy, for rows that are not a power-of-two number of 16-byte
+// vectors (e.g. BF16 head_dim 96 = 12 vectors): one vector per lane in
+// (token, head, vector) order, indices by division.
+__global__ __launch_bounds__(kThreads) void kv_append_copy_rows(
+    const uint4* __restrict__ k, const uint4* __restrict__ v, char* __restrict__ kpool,
+    char* __restrict__ vpool, const int64_t* __restrict__ slots, int64_t total, int hkv, int row_vecs,
+    int log2_bs, int64_t page_bytes, int64_t n_slots, uint32_t* err) {
+  const int64_t gid = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  if (gid >= total) return;
+  const int c = int(gid % row_vecs);
+  const int64_t th = gid / row_vecs;
+  const int h = int(th % hkv);
+  const int64_t t = th / hkv;
+  const int64_t sl = slots[t];
+  if (sl < 0) return;  // padding token
+  if (sl >= n_slots) {
+    if (c == 0 && h == 0) atomicOr(err, kErrSlot);
+    return;
+  }
+  const int64_t blk = sl >> log2_bs;
+  const int64_t off = sl & ((int64_t(1) << log2_bs) - 1);
+  const int64_t dst = (blk * hkv + h) * page_bytes + (off * row_vecs + c) * 16;
+  st16(kpool + dst, ld16_nt(k + gid));
+  st16(vpool + dst, ld16_nt(v + gid));
 }
 
 // ---------------------------------------------------------------------------
@@ -293,14 +320,18 @@ __global__ __launch_bounds__(kThreads) void kv_gather_nib(
 // ---------------------------------------------------------------------------
 // Evict (zero pages) and copy-on-write page copy.  grid.y = list entry.
 // ---------------------------------------------------------------------------
+// grid.z = layer: a multi-layer cache clears (copies) the block in every
+// layer in one launch.
 __global__ __launch_bounds__(kThreads) void kv_clear_blocks(char* __restrict__ kpool,
                                                             char* __restrict__ vpool,
                                                             const int32_t* __restrict__ blocks,
                                                             int64_t block_vecs, int64_t num_blocks,
-                                                            uint32_t* err) {
+                                                            int64_t layer_bytes, uint32_t* err) {
+  kpool += int64_t(blockIdx.z) * layer_bytes;
+  vpool += int64_t(blockIdx.z) * layer_bytes;
   const int blk = blocks[blockIdx.y];
   if (blk < 0 || blk >= num_blocks) {
-    if (blockIdx.x == 0 && threadIdx.x == 0) atomicOr(err, kErrBlock);
+    if (blockIdx.x == 0 && blockIdx.z == 0 && threadIdx.x == 0) atomicOr(err, kErrBlock);
     return;
   }
   const uint4 z = make_uint4(0u, 0u, 0u, 0u);
@@ -315,10 +346,12 @@ __global__ __launch_bounds__(kThreads) void kv_copy_blocks(char* __restrict__ kp
                                                            const int32_t* __restrict__ src,
                                                            const int32_t* __restrict__ dst,
                                                            int64_t block_vecs, int64_t num_blocks,
-                                                           uint32_t* err) {
+                                                           int64_t layer_bytes, uint32_t* err) {
+  kpool += int64_t(blockIdx.z) * layer_bytes;
+  vpool += int64_t(blockIdx.z) * layer_bytes;
   const int s = src[blockIdx.y], d = dst[blockIdx.y];
   if (s < 0 || s >= num_blocks || d < 0 || d >= num_blocks) {
-    if (blockIdx.x == 0 && threadIdx.x == 0) atomicOr(err, kErrBlock);
+    if (blockIdx.x == 0 && blockIdx.z == 0 && threadIdx.x == 0) atomicOr(err, kErrBlock);
     return;
   }
   for (int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x; i < block_vecs; i += int64_t(gridDim.x) * kThreads) {
@@ -371,7 +404,7 @@ int32_t check_shape(int64_t num_blocks, int32_t block_size, int32_t n_kv_heads, 
   return IT_OK;
 }
 
-int32_t make_cache(int32_t device, void* k, void* v, int64_t num_blocks, int32_t block_size,
+int32_t make_cache(int32_t device, void* k, void* v, int32_t n_layers, int64_t num_blocks, int32_t block_size,
                    int32_t n_kv_heads, int32_t head_dim, int32_t dtype, int32_t owns, it_kv_cache** out) {
   auto* c = new (std::nothrow) it_kv_cache;
   if (!c) return fail(IT_DEVICE_ERROR, "kv cache: out of host memory");
@@ -379,6 +412,9 @@ int32_t make_cache(int32_t device, void* k, void* v, int64_t num_blocks, int32_t
   c->v_pool = v;
   c->num_blocks = num_blocks;
   c->page_bytes = it_kv_page_bytes(block_size, head_dim, dtype);
+  c->layer_bytes = num_blocks * n_kv_heads * c->page_bytes;
+  c->n_layers = n_layers;
+  c->owns_flag = 1;
   c->block_size = block_size;
   c->log2_bs = ilog2(block_size);
   c->n_kv_heads = n_kv_heads;
@@ -393,6 +429,9 @@ int32_t make_cache(int32_t device, void* k, void* v, int64_t num_blocks, int32_t
     delete c;
     return fail(IT_DEVICE_ERROR, "kv cache: error word allocation: %s", hipGetErrorString(e));
   }
+  // A failed lookup here is retried (and reported) by the first
+  // no-allocation decode.
+  (void)noalloc_prepare(device);
   *out = c;
   return IT_OK;
 }
@@ -423,14 +462,17 @@ extern "C" int64_t it_kv_page_bytes(int32_t block_size, int32_t head_dim, int32_
   return e ? int64_t(block_size) * head_dim * e : -1;
 }
 
-extern "C" int32_t it_kv_cache_new(int32_t device, int64_t num_blocks, int32_t block_size,
-                                   int32_t n_kv_heads, int32_t head_dim, int32_t dtype,
-                                   it_kv_cache** out) {
+extern "C" int32_t it_kv_cache_new_layers(int32_t device, int32_t n_layers, int64_t num_blocks,
+                                          int32_t block_size, int32_t n_kv_heads, int32_t head_dim,
+                                          int32_t dtype, it_kv_cache** out) {
   if (!out) return fail(IT_INVALID_INPUT, "it_kv_cache_new: out is NULL");
   *out = nullptr;
+  if (n_layers <= 0 || n_layers > kMaxLayers)
+    return fail(IT_INVALID_INPUT, "it_kv_cache_new: n_layers %d outside [1, %d]", n_layers, kMaxLayers);
   if (int32_t rc = check_shape(num_blocks, block_size, n_kv_heads, head_dim, dtype)) return rc;
   DeviceGuard g(device);
-  const size_t bytes = size_t(num_blocks) * size_t(n_kv_heads) * size_t(it_kv_page_bytes(block_size, head_dim, dtype));
+  const size_t bytes = size_t(n_layers) * size_t(num_blocks) * size_t(n_kv_heads) *
+                       size_t(it_kv_page_bytes(block_size, head_dim, dtype));
   void *k = nullptr, *v = nullptr;
   hipError_t e = hipMalloc(&k, bytes);
   if (e == hipSuccess) e = hipMalloc(&v, bytes);
@@ -441,7 +483,7 @@ extern "C" int32_t it_kv_cache_new(int32_t device, int64_t num_blocks, int32_t b
     if (v) (void)hipFree(v);
     return fail(IT_DEVICE_ERROR, "it_kv_cache_new: %zu bytes per pool: %s", bytes, hipGetErrorString(e));
   }
-  int32_t rc = make_cache(device, k, v, num_blocks, block_size, n_kv_heads, head_dim, dtype, 1, out);
+  int32_t rc = make_cache(device, k, v, n_layers, num_blocks, block_size, n_kv_heads, head_dim, dtype, 1, out);
   if (rc) {
     (void)hipFree(k);
     (void)hipFree(v);
@@ -449,16 +491,48 @@ extern "C" int32_t it_kv_cache_new(int32_t device, int64_t num_blocks, int32_t b
   return rc;
 }
 
-extern "C" int32_t it_kv_cache_wrap(int32_t device, void* k_pool, void* v_pool, int64_t num_blocks,
-                                    int32_t block_size, int32_t n_kv_heads, int32_t head_dim,
-                                    int32_t dtype, it_kv_cache** out) {
+extern "C" int32_t it_kv_cache_new(int32_t device, int64_t num_blocks, int32_t block_size,
+                                   int32_t n_kv_heads, int32_t head_dim, int32_t dtype,
+                                   it_kv_cache** out) {
+  return it_kv_cache_new_layers(device, 1, num_blocks, block_size, n_kv_heads, head_dim, dtype, out);
+}
+
+extern "C" int32_t it_kv_cache_wrap_layers(int32_t device, int32_t n_layers, void* k_pool, void* v_pool,
+                                           int64_t num_blocks, int32_t block_size, int32_t n_kv_heads,
+                                           int32_t head_dim, int32_t dtype, it_kv_cache** out) {
   if (!out) return fail(IT_INVALID_INPUT, "it_kv_cache_wrap: out is NULL");
   *out = nullptr;
   if (!k_pool || !v_pool) return fail(IT_INVALID_INPUT, "it_kv_cache_wrap: NULL pool");
   if (!aligned16(k_pool) || !aligned16(v_pool)) return fail(IT_INVALID_INPUT, "it_kv_cache_wrap: pools must be 16-byte aligned");
+  if (n_layers <= 0 || n_layers > kMaxLayers)
+    return fail(IT_INVALID_INPUT, "it_kv_cache_wrap: n_layers %d outside [1, %d]", n_layers, kMaxLayers);
   if (int32_t rc = check_shape(num_blocks, block_size, n_kv_heads, head_dim, dtype)) return rc;
   DeviceGuard g(device);
-  return make_cache(device, k_pool, v_pool, num_blocks, block_size, n_kv_heads, head_dim, dtype, 0, out);
+  return make_cache(device, k_pool, v_pool, n_layers, num_blocks, block_size, n_kv_heads, head_dim, dtype, 0, out);
+}
+
+extern "C" int32_t it_kv_cache_wrap(int32_t device, void* k_pool, void* v_pool, int64_t num_blocks,
+                                    int32_t block_size, int32_t n_kv_heads, int32_t head_dim,
+                                    int32_t dtype, it_kv_cache** out) {
+  return it_kv_cache_wrap_layers(device, 1, k_pool, v_pool, num_blocks, block_size, n_kv_heads, head_dim, dtype,
+                                 out);
+}
+
+extern "C" int32_t it_kv_cache_layer(const it_kv_cache* c, int32_t layer, it_kv_cache** out) {
+  if (!out) return fail(IT_INVALID_INPUT, "it_kv_cache_layer: out is NULL");
+  *out = nullptr;
+  if (!c) return fail(IT_INVALID_INPUT, "it_kv_cache_layer: cache is NULL");
+  if (layer < 0 || layer >= c->n_layers)
+    return fail(IT_INVALID_INPUT, "it_kv_cache_layer: layer %d outside [0, %d)", layer, c->n_layers);
+  auto* v = new (std::nothrow) it_kv_cache(*c);
+  if (!v) return fail(IT_DEVICE_ERROR, "it_kv_cache_layer: out of host memory");
+  v->k_pool = static_cast<char*>(c->k_pool) + int64_t(layer) * c->layer_bytes;
+  v->v_pool = static_cast<char*>(c->v_pool) + int64_t(layer) * c->layer_bytes;
+  v->n_layers = 1;
+  v->owns_memory = 0;
+  v->owns_flag = 0;
+  *out = v;
+  return IT_OK;
 }
 
 extern "C" int32_t it_kv_cache_destroy(it_kv_cache* c) {
@@ -468,7 +542,7 @@ extern "C" int32_t it_kv_cache_destroy(it_kv_cache* c) {
     (void)hipFree(c->k_pool);
     (void)hipFree(c->v_pool);
   }
-  (void)hipFree(c->err_flag);
+  if (c->owns_flag) (void)hipFree(c->err_flag);
   delete c;
   return IT_OK;
 }
@@ -485,6 +559,7 @@ extern "C" int32_t it_kv_cache_describe(const it_kv_cache* c, it_kv_cache_desc* 
   d->dtype = c->dtype;
   d->device = c->device;
   d->owns_memory = c->owns_memory;
+  d->n_layers = c->n_layers;
   return IT_OK;
 }
 
@@ -505,6 +580,7 @@ extern "C" int32_t it_kv_cache_check(it_kv_cache* c, void* stream) {
 extern "C" int32_t it_kv_append(it_kv_cache* c, const void* k, const void* v, int32_t src_dtype,
                                 const int64_t* slots, int32_t n_tokens, void* stream) {
   if (!c) return fail(IT_INVALID_INPUT, "it_kv_append: cache is NULL");
+  if (int32_t rc = one_layer(c, "it_kv_append")) return rc;
   if (n_tokens < 0) return fail(IT_INVALID_INPUT, "it_kv_append: n_tokens %d < 0", n_tokens);
   if (n_tokens == 0) return IT_OK;
   if (!k || !v || !slots) return fail(IT_INVALID_INPUT, "it_kv_append: NULL tensor");
@@ -529,7 +605,14 @@ extern "C" int32_t it_kv_append(it_kv_cache* c, const void* k, const void* v, in
                        c->n_kv_heads, c->head_dim, c->log2_bs, c->page_bytes, n_slots, c->err_flag);
   } else {
     const int row_vecs = int(c->head_dim * dtype_bytes(c->dtype) / 16);
-    if (!is_pow2(row_vecs)) return fail(IT_NOT_IMPLEMENTED, "it_kv_append: %d vectors per row", row_vecs);
+    if (!is_pow2(row_vecs)) {
+      const int64_t total = int64_t(n_tokens) * c->n_kv_heads * row_vecs;
+      hipLaunchKernelGGL(kv_append_copy_rows, dim3(unsigned(cdiv(total, kThreads))), dim3(kThreads), 0, s,
+                         (const uint4*)k, (const uint4*)v, (char*)c->k_pool, (char*)c->v_pool, slots, total,
+                         c->n_kv_heads, row_vecs, c->log2_bs, c->page_bytes, n_slots, c->err_flag);
+      IT_HIP(hipGetLastError(), "it_kv_append: launch");
+      return IT_OK;
+    }
     // Vectors in whole token groups of TPG = 64 / row_vecs tokens.
     const int64_t tpg = row_vecs < 64 ? 64 / row_vecs : 1;
     const int64_t total = cdiv(n_tokens, tpg) * tpg * c->n_kv_heads * row_vecs;
@@ -548,6 +631,7 @@ extern "C" int32_t it_kv_gather(const it_kv_cache* c, const int32_t* bt, int32_t
                                 int32_t n_seqs, int32_t max_tokens, void* k_out, void* v_out,
                                 void* stream) {
   if (!c) return fail(IT_INVALID_INPUT, "it_kv_gather: cache is NULL");
+  if (int32_t rc = one_layer(c, "it_kv_gather")) return rc;
   if (n_seqs < 0 || max_tokens < 0 || max_blocks <= 0)
     return fail(IT_INVALID_INPUT, "it_kv_gather: n_seqs=%d max_tokens=%d max_blocks=%d", n_seqs, max_tokens, max_blocks);
   if (n_seqs == 0 || max_tokens == 0) return IT_OK;
@@ -587,9 +671,10 @@ extern "C" int32_t it_kv_evict(it_kv_cache* c, const int32_t* blocks, int32_t n,
   if (!blocks) return fail(IT_INVALID_INPUT, "it_kv_evict: blocks is NULL");
   DeviceGuard g(c->device);
   const int64_t block_vecs = c->page_bytes * c->n_kv_heads / 16;
-  dim3 grid(unsigned(cdiv(block_vecs, kThreads) > 64 ? 64 : cdiv(block_vecs, kThreads)), unsigned(n));
+  dim3 grid(unsigned(cdiv(block_vecs, kThreads) > 64 ? 64 : cdiv(block_vecs, kThreads)), unsigned(n),
+            unsigned(c->n_layers));
   hipLaunchKernelGGL(kv_clear_blocks, grid, dim3(kThreads), 0, (hipStream_t)stream, (char*)c->k_pool,
-                     (char*)c->v_pool, blocks, block_vecs, c->num_blocks, c->err_flag);
+                     (char*)c->v_pool, blocks, block_vecs, c->num_blocks, c->layer_bytes, c->err_flag);
   IT_HIP(hipGetLastError(), "it_kv_evict: launch");
   return IT_OK;
 }
@@ -617,9 +702,10 @@ extern "C" int32_t it_kv_copy_blocks(it_kv_cache* c, const int32_t* src, const i
   if (!src || !dst) return fail(IT_INVALID_INPUT, "it_kv_copy_blocks: NULL list");
   DeviceGuard g(c->device);
   const int64_t block_vecs = c->page_bytes * c->n_kv_heads / 16;
-  dim3 grid(unsigned(cdiv(block_vecs, kThreads) > 64 ? 64 : cdiv(block_vecs, kThreads)), unsigned(n));
+  dim3 grid(unsigned(cdiv(block_vecs, kThreads) > 64 ? 64 : cdiv(block_vecs, kThreads)), unsigned(n),
+            unsigned(c->n_layers));
   hipLaunchKernelGGL(kv_copy_blocks, grid, dim3(kThreads), 0, (hipStream_t)stream, (char*)c->k_pool,
-                     (char*)c->v_pool, src, dst, block_vecs, c->num_blocks, c->err_flag);
+                     (char*)c->v_pool, src, dst, block_vecs, c->num_blocks, c->layer_bytes, c->err_flag);
   IT_HIP(hipGetLastError(), "it_kv_copy_blocks: launch");
   return IT_OK;
 }

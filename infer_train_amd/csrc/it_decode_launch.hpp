@@ -17,15 +17,10 @@ inline size_t decode_smem_bytes(int32_t dt, int gc, int d, int partition, int ma
 template <int DT, int D, int GC, int NW, int R>
 hipError_t launch_split_shape(const DecodeArgs& a, dim3 grid, size_t smem, hipStream_t s) {
   if (smem > 64 * 1024) {
-    // Above 64 KiB the kernel must opt in.  Idempotent, so a race between
-    // threads setting it is harmless.
-    static bool opted = false;
-    if (!opted) {
-      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&paged_decode_split<DT, D, GC, NW, R>),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, int(kMaxDecodeLds));
-      if (e != hipSuccess) return e;
-      opted = true;
-    }
+    static std::atomic<uint64_t> opted{0};
+    const hipError_t e = opt_in_lds(reinterpret_cast<const void*>(&paged_decode_split<DT, D, GC, NW, R>),
+                                    int(kMaxDecodeLds), opted);
+    if (e != hipSuccess) return e;
   }
   hipLaunchKernelGGL((paged_decode_split<DT, D, GC, NW, R>), grid, dim3(64 * NW), smem, s, a);
   return hipGetLastError();

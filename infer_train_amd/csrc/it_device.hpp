@@ -6,7 +6,23 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 namespace itkv {
+
+// A kernel that asks for more than 64 KiB of dynamic LDS must opt in, once
+// per device.  `opted` holds one bit per device (one word per kernel
+// instantiation): threads that race on a first call may both set the
+// idempotent attribute, and none reads a torn flag.  Devices past 63 set
+// it on every launch.
+inline hipError_t opt_in_lds(const void* fn, int bytes, std::atomic<uint64_t>& opted) {
+  int dev = -1;
+  const uint64_t bit = (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64) ? uint64_t(1) << dev : 0;
+  if (bit && (opted.load(std::memory_order_acquire) & bit)) return hipSuccess;
+  const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e == hipSuccess) opted.fetch_or(bit, std::memory_order_release);
+  return e;
+}
 
 // ---- 16-bit float conversions ---------------------------------------------
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }

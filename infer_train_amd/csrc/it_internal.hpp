@@ -41,11 +41,13 @@ inline int64_t dtype_bytes(int32_t dt) {
 }  // namespace itkv
 
 struct it_kv_cache {
-  void* k_pool;
-  void* v_pool;
-  uint32_t* err_flag;  // device word
+  void* k_pool;        // layer 0 of the K pool
+  void* v_pool;        // layer 0 of the V pool
+  uint32_t* err_flag;  // device word (a layer view shares its parent's)
   int64_t num_blocks;
   int64_t page_bytes;
+  int64_t layer_bytes;  // bytes of one layer of one pool: num_blocks * n_kv_heads * page_bytes
+  int32_t n_layers;     // layers in each pool (a layer view: 1)
   int32_t block_size;
   int32_t log2_bs;
   int32_t n_kv_heads;
@@ -53,4 +55,20 @@ struct it_kv_cache {
   int32_t dtype;
   int32_t device;
   int32_t owns_memory;
+  int32_t owns_flag;    // 0 for a layer view
 };
+
+namespace itkv {
+// Entry points that read or write one layer's pages take a one-layer cache
+// (a single-layer cache or a view from it_kv_cache_layer).
+inline int32_t one_layer(const it_kv_cache* c, const char* who) {
+  if (c && c->n_layers != 1)
+    return fail(IT_INVALID_INPUT, "%s: the cache holds %d layers; pass the layer's view (it_kv_cache_layer)", who,
+                c->n_layers);
+  return IT_OK;
+}
+// Looks up the device address of the no-allocation decode's array on the
+// current device (done once per device; it_kv_cache_new/_wrap call it so
+// that the first no-allocation decode does no lookup).
+int32_t noalloc_prepare(int device);
+}  // namespace itkv

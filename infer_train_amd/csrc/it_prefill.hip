@@ -605,13 +605,10 @@ __global__ __launch_bounds__(64 * W) void paged_prefill_kernel(PrefillArgs a) {
 
 template <bool kBf16, int W, bool kTab>
 hipError_t launch_prefill_t(const PrefillArgs& a, dim3 grid, size_t smem, hipStream_t s) {
-  static bool opted = false;  // idempotent: a race between threads setting it is harmless
-  if (!opted) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&paged_prefill_kernel<kBf16, W, kTab>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
-    if (e != hipSuccess) return e;
-    opted = true;
-  }
+  static std::atomic<uint64_t> opted{0};
+  const hipError_t e =
+      opt_in_lds(reinterpret_cast<const void*>(&paged_prefill_kernel<kBf16, W, kTab>), kMaxLds, opted);
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL((paged_prefill_kernel<kBf16, W, kTab>), grid, dim3(64 * W), smem, s, a);
   return hipGetLastError();
 }
@@ -642,6 +639,7 @@ extern "C" int32_t it_paged_prefill(const it_kv_cache* c, const void* q, int32_t
                                     int32_t causal, void* out, int32_t out_dtype, void* stream) {
   const char* who = "it_paged_prefill";
   if (!c) return fail(IT_INVALID_INPUT, "%s: cache is NULL", who);
+  if (int32_t rc = one_layer(c, who)) return rc;
   if (c->dtype != IT_BF16 && c->dtype != IT_F16)
     return fail(IT_NOT_IMPLEMENTED, "%s: cache dtype %d (BF16 or F16 supported)", who, c->dtype);
   if (q_dtype != c->dtype) return fail(IT_NOT_IMPLEMENTED, "%s: q dtype %d must equal the cache dtype", who, q_dtype);

@@ -201,6 +201,7 @@ extern "C" int32_t it_kv_append_rope(it_kv_cache* c, const it_rope_table* rope, 
                                      void* stream) {
   const char* who = "it_kv_append_rope";
   if (!c || !rope) return fail(IT_INVALID_INPUT, "%s: cache or table is NULL", who);
+  if (int32_t rc = one_layer(c, who)) return rc;
   if (n_tokens < 0) return fail(IT_INVALID_INPUT, "%s: n_tokens %d < 0", who, n_tokens);
   if (n_heads <= 0 || n_heads % c->n_kv_heads)
     return fail(IT_INVALID_INPUT, "%s: n_heads %d must be a positive multiple of n_kv_heads %d", who, n_heads,

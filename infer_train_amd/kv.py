@@ -65,20 +65,26 @@ class PagedKvCache:
     token rows (Q8_0 pages: int8 rows then fp16 group scales; Q4_0 pages:
     rows of BlockQ4_0 nibble bytes then fp16 group scales; Q4_1 the same
     with (d, m) pairs; Q5_0 / Q5_1 the nibble rows then per token the
-    groups' u32 qh words and their d or (d, m))."""
+    groups' u32 qh words and their d or (d, m)).
+
+    n_layers > 1 holds every layer of a model (the reference's per-layer
+    kv_cache_k/v, forward.rs:17-18): each pool is n_layers such layers one
+    after another, so one block id names the same pages in every layer.
+    evict / copy_blocks / sync_tables act on the whole cache (every layer in
+    one launch); append, gather, decode and prefill go through `layer(l)`."""
 
     def __init__(self, num_blocks: int, block_size: int, n_kv_heads: int, head_dim: int, dtype: int = BF16,
-                 device: int = 0):
+                 device: int = 0, n_layers: int = 1):
         page = lib.it_kv_page_bytes(block_size, head_dim, dtype)
         if page <= 0:
             raise ValueError("unsupported cache shape")
-        nbytes = num_blocks * n_kv_heads * page
+        nbytes = n_layers * num_blocks * n_kv_heads * page
         dev = torch.device("cuda", device)
         self.k_pool = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
         self.v_pool = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
         h = C.c_void_p()
-        check(lib.it_kv_cache_wrap(device, self.k_pool.data_ptr(), self.v_pool.data_ptr(), num_blocks, block_size,
-                                   n_kv_heads, head_dim, dtype, C.byref(h)))
+        check(lib.it_kv_cache_wrap_layers(device, n_layers, self.k_pool.data_ptr(), self.v_pool.data_ptr(),
+                                          num_blocks, block_size, n_kv_heads, head_dim, dtype, C.byref(h)))
         self._h = h
         # Bound now: at interpreter exit the module global may already be gone.
         self._destroy = lib.it_kv_cache_destroy
@@ -86,10 +92,33 @@ class PagedKvCache:
         self.dtype = dtype
         self.page_bytes = page
         self.device = dev
+        self.n_layers = n_layers
+        self._parent = None
 
     @property
     def handle(self) -> C.c_void_p:
         return self._h
+
+    def layer(self, index: int) -> "PagedKvCache":
+        """One layer of a multi-layer cache (it_kv_cache_layer): a cache
+        object whose pools are that layer's bytes of this cache's pools."""
+        h = C.c_void_p()
+        check(lib.it_kv_cache_layer(self._h, int(index), C.byref(h)))
+        view = object.__new__(PagedKvCache)
+        lb = self.num_blocks * self.n_kv_heads * self.page_bytes
+        view.k_pool = self.k_pool[index * lb:(index + 1) * lb]
+        view.v_pool = self.v_pool[index * lb:(index + 1) * lb]
+        view._h = h
+        view._destroy = lib.it_kv_cache_destroy
+        for name in ("num_blocks", "block_size", "n_kv_heads", "head_dim", "dtype", "page_bytes", "device"):
+            setattr(view, name, getattr(self, name))
+        view.n_layers = 1
+        view._parent = self  # destroyed before the parent
+        return view
+
+    def _one_layer(self) -> None:
+        if self.n_layers != 1:
+            raise TypeError("a multi-layer cache: take one layer's view with layer(l)")
 
     def describe(self) -> CacheDesc:
         d = CacheDesc()
@@ -98,6 +127,7 @@ class PagedKvCache:
 
     def view(self, which: str = "k") -> torch.Tensor:
         """Typed view [num_blocks, n_kv_heads, block_size, head_dim] (F32/F16/BF16)."""
+        self._one_layer()
         pool = self.k_pool if which == "k" else self.v_pool
         if self.dtype == Q8_0:
             raise TypeError("use q8_planes() for a Q8_0 cache")
@@ -107,6 +137,7 @@ class PagedKvCache:
 
     def q8_planes(self, which: str = "k") -> Tuple[torch.Tensor, torch.Tensor]:
         """(qs int8 [nb, H, bs, D], d fp16 bits int16 [nb, H, bs, D/32]) of a Q8_0 cache."""
+        self._one_layer()
         pool = (self.k_pool if which == "k" else self.v_pool).view(self.num_blocks, self.n_kv_heads, self.page_bytes)
         bs, D = self.block_size, self.head_dim
         qs = pool[:, :, : bs * D].view(torch.int8).reshape(self.num_blocks, self.n_kv_heads, bs, D)
@@ -116,6 +147,7 @@ class PagedKvCache:
     def q4_planes(self, which: str = "k") -> Tuple[torch.Tensor, torch.Tensor]:
         """(qs uint8 [nb, H, bs, D/2], scales fp16 bits int16 [nb, H, bs, D/32] (Q4_0: d) or
         [nb, H, bs, D/32, 2] (Q4_1: d, m)) of a Q4_0 / Q4_1 cache."""
+        self._one_layer()
         pool = (self.k_pool if which == "k" else self.v_pool).view(self.num_blocks, self.n_kv_heads, self.page_bytes)
         bs, D = self.block_size, self.head_dim
         qs = pool[:, :, : bs * D // 2].reshape(self.num_blocks, self.n_kv_heads, bs, D // 2)
@@ -127,6 +159,7 @@ class PagedKvCache:
         """(qs uint8 [nb, H, bs, D/2] (low four bits of each value), qh int32
         [nb, H, bs, D/32], scales fp16 bits int16 [nb, H, bs, D/32] (Q5_0: d) or
         [nb, H, bs, D/32, 2] (Q5_1: d, m)) of a Q5_0 / Q5_1 cache."""
+        self._one_layer()
         if self.dtype not in (Q5_0, Q5_1):
             raise TypeError("q5_planes() needs a Q5_0 / Q5_1 cache")
         pool = (self.k_pool if which == "k" else self.v_pool).view(self.num_blocks, self.n_kv_heads, self.page_bytes)

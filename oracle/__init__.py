@@ -88,6 +88,9 @@ def _load() -> C.CDLL:
         "orc_mgr_destroy": (None, [P]),
         "orc_mgr_seed_seq": (i32, [P, i32, i64, i64, P, i32]),
         "orc_mgr_append": (i32, [P, P, P, i32, P, P, i32, P]),
+        "orc_mgr_append_cow": (i32, [P, P, P, i32, i32, P, P, i32, P, P, P, i32, P]),
+        "orc_mgr_fork": (i32, [P, i32, i32]),
+        "orc_mgr_release": (i32, [P, i32, P, i32, P]),
         "orc_mgr_tables": (i32, [P, P, i32, P, P]),
     }
     for name, (res, args) in sig.items():
@@ -448,18 +451,35 @@ class Manager:
         if lib.orc_mgr_seed_seq(self.h, s, pos, first_block, b.ctypes.data, b.size):
             raise ValueError("seed_seq")
 
-    def append(self, seqs, n_tokens=1) -> Tuple[np.ndarray, np.ndarray]:
+    def append(self, seqs, n_tokens=1, cow: bool = False):
+        """Slots and the blocks returned to the pool (refcount 0) of one step;
+        cow=True also returns the copy-on-write (shared, fresh) pairs."""
         s = _c(seqs, np.int32)
         nt = np.full(s.size, n_tokens, np.int32) if np.isscalar(n_tokens) else _c(n_tokens, np.int32)
         slots = np.empty(max(int(nt.sum()), 1), np.int64)
         cap = s.size * self.max_blocks + 1
         ev = np.empty(cap, np.int32)
         ne = C.c_int32(0)
-        rc = lib.orc_mgr_append(self.h, s.ctypes.data, nt.ctypes.data, s.size, slots.ctypes.data, ev.ctypes.data,
-                                cap, C.byref(ne))
+        cs, cd, nc = np.empty(cap, np.int32), np.empty(cap, np.int32), C.c_int32(0)
+        rc = lib.orc_mgr_append_cow(self.h, s.ctypes.data, nt.ctypes.data, s.size, int(cow), slots.ctypes.data,
+                                    ev.ctypes.data, cap, C.byref(ne), cs.ctypes.data, cd.ctypes.data, cap,
+                                    C.byref(nc))
         if rc:
             raise ValueError("orc_mgr_append failed")
+        if cow:
+            return slots[: int(nt.sum())], ev[: ne.value].copy(), cs[: nc.value].copy(), cd[: nc.value].copy()
         return slots[: int(nt.sum())], ev[: ne.value].copy()
+
+    def fork(self, src: int, dst: int) -> None:
+        if lib.orc_mgr_fork(self.h, src, dst):
+            raise ValueError("orc_mgr_fork failed")
+
+    def release(self, s: int) -> np.ndarray:
+        ev = np.empty(self.max_blocks, np.int32)
+        ne = C.c_int32(0)
+        if lib.orc_mgr_release(self.h, s, ev.ctypes.data, self.max_blocks, C.byref(ne)):
+            raise ValueError("orc_mgr_release failed")
+        return ev[: ne.value].copy()
 
     def tables(self):
         t = np.empty((self.max_seqs, self.max_blocks), np.int32)

@@ -992,42 +992,134 @@ int orc_mgr_seed_seq(orc_kv_manager* m, int32_t s, int64_t pos, int64_t first_bl
   return ORC_OK;
 }
 
-int orc_mgr_append(orc_kv_manager* m, const int32_t* seqs, const int32_t* n_tokens, int32_t n,
-                   int64_t* slots_out, int32_t* evicted_out, int32_t evicted_cap,
-                   int32_t* n_evicted) {
-  int32_t ne = 0;
+/* One step's rules (restated on BlockPool, paged.rs:21-58):
+ *  - window: before position p, every held block whose last position is
+ *    < p - W + 1 drops this sequence's reference (BlockPool::free), oldest
+ *    first;
+ *  - a block whose refcount reaches 0 is returned to the pool's free list
+ *    when the step ends, in free order (so within one step no block is
+ *    freed and handed out again), and is listed in evicted_out; a block a
+ *    forked sequence still holds is not;
+ *  - tokens of the step written into a block the step returns get slot -1
+ *    (dead: the window dropped them before the step ended). */
+static int64_t mgr_drop_ref(orc_block_pool* p, int64_t id) {
+  if (id < 0 || id >= p->capacity || p->ref_counts[id] == 0) return -1;
+  p->ref_counts[id] -= 1; /* the push of a block reaching 0 waits for the step's end */
+  return p->ref_counts[id];
+}
+
+static int mgr_end_step(orc_kv_manager* m, const int32_t* freed, int32_t n_freed, int rc) {
+  for (int32_t i = 0; i < n_freed; ++i) m->pool->free_list[m->pool->n_free++] = freed[i];
+  return rc;
+}
+
+int orc_mgr_append_cow(orc_kv_manager* m, const int32_t* seqs, const int32_t* n_tokens, int32_t n,
+                       int32_t cow, int64_t* slots_out, int32_t* evicted_out, int32_t evicted_cap,
+                       int32_t* n_evicted, int32_t* cow_src, int32_t* cow_dst, int32_t cow_cap,
+                       int32_t* n_cow) {
+  int32_t ne = 0, nc = 0;
   size_t t = 0;
   for (int32_t i = 0; i < n; ++i) {
     int32_t s = seqs[i];
-    if (s < 0 || s >= m->max_seqs || n_tokens[i] < 0) return ORC_INVALID_INPUT;
+    if (s < 0 || s >= m->max_seqs || n_tokens[i] < 0) return mgr_end_step(m, evicted_out, ne, ORC_INVALID_INPUT);
     int32_t* row = m->table + (size_t)s * m->max_blocks;
     for (int32_t k = 0; k < n_tokens[i]; ++k) {
       int64_t p = m->pos[s];
-      if (m->window > 0) { /* free blocks that fall out of [p-W+1, p] */
-        while (m->first[s] * m->bs + m->bs - 1 < p - m->window + 1) {
-          int64_t j = m->first[s];
-          if (j >= m->max_blocks) return ORC_INVALID_INPUT;
-          if (row[j] >= 0) {
-            if (orc_pool_free(m->pool, row[j])) return ORC_INVALID_INPUT;
-            if (ne >= evicted_cap) return ORC_INVALID_INPUT;
-            evicted_out[ne++] = row[j];
-            row[j] = -1;
+      while (m->window > 0 && m->first[s] * m->bs + m->bs - 1 < p - m->window + 1) {
+        int64_t j = m->first[s];
+        if (j >= m->max_blocks) return mgr_end_step(m, evicted_out, ne, ORC_INVALID_INPUT);
+        if (row[j] >= 0) {
+          int32_t id = row[j];
+          int64_t left = mgr_drop_ref(m->pool, id);
+          if (left < 0) return mgr_end_step(m, evicted_out, ne, ORC_INVALID_INPUT);
+          if (left == 0) {
+            if (ne >= evicted_cap) { /* undo: the block stays free */
+              m->pool->free_list[m->pool->n_free++] = id;
+              return mgr_end_step(m, evicted_out, ne, ORC_INVALID_INPUT);
+            }
+            evicted_out[ne++] = id;
+            /* Dead tokens: every slot of this step inside the block. */
+            for (size_t u = 0; u < t; ++u)
+              if (slots_out[u] >= 0 && slots_out[u] / m->bs == id) slots_out[u] = -1;
           }
-          m->first[s] = j + 1;
+          row[j] = -1;
         }
+        m->first[s] = j + 1;
       }
       int64_t lb = p / m->bs;
-      if (lb >= m->max_blocks) return ORC_INVALID_INPUT;
+      if (lb >= m->max_blocks) return mgr_end_step(m, evicted_out, ne, ORC_INVALID_INPUT);
       if (p % m->bs == 0) {
         int64_t id = orc_pool_allocate(m->pool);
-        if (id < 0) return ORC_INVALID_INPUT; /* pool exhausted */
+        if (id < 0) return mgr_end_step(m, evicted_out, ne, ORC_INVALID_INPUT); /* pool exhausted */
+        row[lb] = (int32_t)id;
+      } else if (row[lb] < 0) {
+        return mgr_end_step(m, evicted_out, ne, ORC_INVALID_INPUT);
+      } else if (cow && orc_pool_ref_count(m->pool, row[lb]) > 1) {
+        /* Copy-on-write: the token would write into a partial block another
+         * sequence also holds.  A fresh block takes the copy; this sequence
+         * drops its reference to the shared one. */
+        if (nc >= cow_cap) return mgr_end_step(m, evicted_out, ne, ORC_INVALID_INPUT);
+        int64_t id = orc_pool_allocate(m->pool);
+        if (id < 0) return mgr_end_step(m, evicted_out, ne, ORC_INVALID_INPUT);
+        cow_src[nc] = row[lb];
+        cow_dst[nc] = (int32_t)id;
+        ++nc;
+        if (mgr_drop_ref(m->pool, row[lb]) < 1) return mgr_end_step(m, evicted_out, ne, ORC_INVALID_INPUT);
         row[lb] = (int32_t)id;
       }
-      if (row[lb] < 0) return ORC_INVALID_INPUT;
       slots_out[t++] = (int64_t)row[lb] * m->bs + p % m->bs;
       m->pos[s] = p + 1;
     }
   }
+  *n_evicted = ne;
+  if (n_cow) *n_cow = nc;
+  return mgr_end_step(m, evicted_out, ne, ORC_OK);
+}
+
+int orc_mgr_append(orc_kv_manager* m, const int32_t* seqs, const int32_t* n_tokens, int32_t n,
+                   int64_t* slots_out, int32_t* evicted_out, int32_t evicted_cap,
+                   int32_t* n_evicted) {
+  return orc_mgr_append_cow(m, seqs, n_tokens, n, 0, slots_out, evicted_out, evicted_cap, n_evicted, NULL,
+                            NULL, 0, NULL);
+}
+
+int orc_mgr_fork(orc_kv_manager* m, int32_t src, int32_t dst) {
+  /* dst takes src's blocks (BlockPool::share, paged.rs:44-46 each) and its
+   * position; dst must hold nothing. */
+  if (src < 0 || src >= m->max_seqs || dst < 0 || dst >= m->max_seqs || src == dst) return ORC_INVALID_INPUT;
+  int32_t* drow = m->table + (size_t)dst * m->max_blocks;
+  const int32_t* srow = m->table + (size_t)src * m->max_blocks;
+  for (int32_t j = 0; j < m->max_blocks; ++j)
+    if (drow[j] >= 0) return ORC_INVALID_INPUT;
+  for (int32_t j = 0; j < m->max_blocks; ++j) {
+    if (srow[j] < 0) continue;
+    if (orc_pool_share(m->pool, srow[j])) return ORC_INVALID_INPUT;
+    drow[j] = srow[j];
+  }
+  m->pos[dst] = m->pos[src];
+  m->first[dst] = m->first[src];
+  return ORC_OK;
+}
+
+int orc_mgr_release(orc_kv_manager* m, int32_t s, int32_t* evicted_out, int32_t evicted_cap,
+                    int32_t* n_evicted) {
+  /* Every held block, lowest logical block first, drops this sequence's
+   * reference; the blocks whose refcount reaches 0 are reported. */
+  if (s < 0 || s >= m->max_seqs) return ORC_INVALID_INPUT;
+  int32_t* row = m->table + (size_t)s * m->max_blocks;
+  int32_t ne = 0;
+  for (int32_t j = 0; j < m->max_blocks; ++j) {
+    if (row[j] < 0) continue;
+    int32_t id = row[j];
+    if (orc_pool_free(m->pool, id)) return ORC_INVALID_INPUT;
+    if (orc_pool_ref_count(m->pool, id) == 0) {
+      if (ne >= evicted_cap) return ORC_INVALID_INPUT;
+      evicted_out[ne++] = id;
+    }
+    row[j] = -1;
+  }
+  m->pos[s] = 0;
+  m->first[s] = 0;
   *n_evicted = ne;
   return ORC_OK;
 }

@@ -261,10 +261,29 @@ void orc_mgr_destroy(orc_kv_manager* m);
 int orc_mgr_seed_seq(orc_kv_manager* m, int32_t s, int64_t pos, int64_t first_block,
                      const int32_t* blocks, int32_t n);
 /* Append n_tokens[i] tokens to sequence seqs[i], i = 0..n-1 in order.
- * Writes sum(n_tokens) slots and the freed block ids (in free order). */
+ * Writes sum(n_tokens) slots and, in free order, the ids of the blocks the
+ * window returned to the pool (refcount 0); a released block that another
+ * sequence still holds is not listed.  Returned blocks go back on the free
+ * list when the step ends (none is freed and handed out again within one
+ * step), and the step's tokens inside them get slot -1 (dead). */
 int orc_mgr_append(orc_kv_manager* m, const int32_t* seqs, const int32_t* n_tokens, int32_t n,
                    int64_t* slots_out, int32_t* evicted_out, int32_t evicted_cap,
                    int32_t* n_evicted);
+/* As orc_mgr_append; with cow != 0 a token written into a partial block
+ * whose refcount is > 1 first moves its sequence to a fresh block and lists
+ * the (shared, fresh) pair in cow_src/cow_dst (the page copy to make). */
+int orc_mgr_append_cow(orc_kv_manager* m, const int32_t* seqs, const int32_t* n_tokens, int32_t n,
+                       int32_t cow, int64_t* slots_out, int32_t* evicted_out, int32_t evicted_cap,
+                       int32_t* n_evicted, int32_t* cow_src, int32_t* cow_dst, int32_t cow_cap,
+                       int32_t* n_cow);
+/* Prefix sharing: empty sequence dst takes src's blocks (BlockPool::share,
+ * paged.rs:44-46) and position. */
+int orc_mgr_fork(orc_kv_manager* m, int32_t src, int32_t dst);
+/* Sequence s drops every block (BlockPool::free, lowest logical block
+ * first) and restarts at position 0; the blocks returned to the pool are
+ * listed. */
+int orc_mgr_release(orc_kv_manager* m, int32_t s, int32_t* evicted_out, int32_t evicted_cap,
+                    int32_t* n_evicted);
 /* Export block tables (absolute logical index, -1 = not held), positions
  * (ctx lens) and window starts. */
 int orc_mgr_tables(const orc_kv_manager* m, int32_t* tables, int32_t max_blocks,

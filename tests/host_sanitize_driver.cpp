@@ -5,7 +5,13 @@
 //   - num_free + (distinct blocks some sequence holds) == capacity;
 //   - every table entry is held (ref_count >= 1), and a block's ref_count is
 //     the number of table entries naming it;
-//   - each returned slot lies in the block the table names for its position;
+//   - each returned slot lies in the block the table names for its position,
+//     and it_kv_manager_step's token sequence / position are that token's;
+//   - the evicted list is exactly the blocks that went back to the pool:
+//     every listed block is free afterwards, and every block some sequence
+//     held before the step and none holds after it is listed (a block that
+//     a fork still holds is never listed);
+//   - release_seq with too small a capacity changes nothing;
 //   - error paths (pool exhausted, table full, bad ids) return a status and
 //     leave no memory error behind.
 // Exit status 0 = all checks held; 1 = a check failed (message on stderr).
@@ -54,6 +60,30 @@ void check_state(const Ctx& c) {
     fail("free + held != capacity", it_block_pool_num_free(c.pool), long(refs.size()));
 }
 
+// Blocks named by any table.
+std::vector<char> held_blocks(const Ctx& c) {
+  std::vector<int32_t> t(size_t(c.seqs) * c.mb);
+  if (it_kv_manager_tables(c.mgr, t.data(), c.mb, nullptr, nullptr) != IT_OK) fail("tables");
+  std::vector<char> h(size_t(it_block_pool_capacity(c.pool)), 0);
+  for (int32_t b : t)
+    if (b >= 0) h[size_t(b)] = 1;
+  return h;
+}
+
+void check_evicted(const Ctx& c, const std::vector<char>& before, const int32_t* ev, int32_t n_ev) {
+  const std::vector<char> after = held_blocks(c);
+  std::vector<char> listed(before.size(), 0);
+  for (int32_t i = 0; i < n_ev; ++i) {
+    if (ev[i] < 0 || size_t(ev[i]) >= before.size()) fail("evicted id range", ev[i]);
+    // Listed blocks went back to the pool; a LIFO hand-off in the same step
+    // may have allocated one again (then it is held with refcount 1).
+    if (!after[size_t(ev[i])] && it_block_pool_ref_count(c.pool, ev[i]) != 0) fail("evicted but held", ev[i]);
+    listed[size_t(ev[i])] = 1;
+  }
+  for (size_t b = 0; b < before.size(); ++b)
+    if (before[b] && !after[b] && !listed[b]) fail("freed but not listed", long(b));
+}
+
 void check_slots(const Ctx& c, const std::vector<int32_t>& seqs, const std::vector<int32_t>& ntok,
                  const std::vector<int32_t>& ctx_before, const std::vector<int64_t>& slots) {
   std::vector<int32_t> t(size_t(c.seqs) * c.mb);
@@ -93,15 +123,44 @@ int run(int window, uint32_t seed) {
       // so their capacity errors are taken too.
       const int32_t ev_cap = (rng() % 6 == 0) ? int32_t(rng() % 3) : int32_t(ev.size());
       const int32_t cow_cap = (rng() % 6 == 0) ? int32_t(rng() % 2) : int32_t(cs.size());
-      const int32_t rc =
-          (op < 40) ? it_kv_manager_append(c.mgr, seqs.data(), ntok.data(), int32_t(seqs.size()), slots.data(),
-                                           ev.data(), ev_cap, &n_ev)
-                    : it_kv_manager_append_cow(c.mgr, seqs.data(), ntok.data(), int32_t(seqs.size()), slots.data(),
-                                               ev.data(), ev_cap, &n_ev, cs.data(), cd.data(), cow_cap, &n_cow);
-      if (rc == IT_OK) g_evicted += n_ev;
+      const std::vector<char> held_before = held_blocks(c);
+      std::vector<int32_t> tseq(slots.size(), -7), tpos(slots.size(), -7), ctx_after(c.seqs, -7);
+      const bool via_step = op >= 20 && op < 40;
+      int32_t rc;
+      if (op < 20) {
+        rc = it_kv_manager_append(c.mgr, seqs.data(), ntok.data(), int32_t(seqs.size()), slots.data(), ev.data(),
+                                  ev_cap, &n_ev);
+      } else if (via_step) {
+        it_kv_step_plan pl{};
+        pl.slots = slots.data();
+        pl.token_seq = tseq.data();
+        pl.token_pos = tpos.data();
+        pl.tokens_cap = int32_t(slots.size());
+        pl.evicted = ev.data();
+        pl.evicted_cap = ev_cap;
+        pl.ctx_lens = ctx_after.data();
+        rc = it_kv_manager_step(c.mgr, seqs.data(), ntok.data(), int32_t(seqs.size()), &pl);
+        n_ev = pl.n_evicted;
+      } else {
+        rc = it_kv_manager_append_cow(c.mgr, seqs.data(), ntok.data(), int32_t(seqs.size()), slots.data(), ev.data(),
+                                      ev_cap, &n_ev, cs.data(), cd.data(), cow_cap, &n_cow);
+      }
+      if (rc == IT_OK) {
+        g_evicted += n_ev;
+        check_evicted(c, held_before, ev.data(), n_ev);
+      }
+      if (rc == IT_OK && via_step) {
+        size_t k = 0;
+        for (size_t i = 0; i < seqs.size(); ++i)
+          for (int j = 0; j < ntok[i]; ++j, ++k)
+            if (tseq[k] != seqs[i] || tpos[k] != before[i] + j) fail("token seq/pos", tseq[k], tpos[k]);
+        std::vector<int32_t> ctx_now(c.seqs);
+        if (it_kv_manager_tables(c.mgr, nullptr, c.mb, ctx_now.data(), nullptr) != IT_OK) fail("ctx");
+        if (ctx_now != ctx_after) fail("step ctx_lens");
+      }
       if (rc != IT_OK) {
         ++g_errors;
-        if (std::strstr(it_last_error(), "evicted_out capacity")) ++g_ev_cap;
+        if (std::strstr(it_last_error(), "evicted capacity")) ++g_ev_cap;
         if (std::strstr(it_last_error(), "cow capacity")) ++g_cow_cap;
         // Whatever the error, no table names a freed block and no block is
         // lost: the counters hold before the recovery too.
@@ -119,8 +178,19 @@ int run(int window, uint32_t seed) {
       }
     } else if (op < 90) {  // release one sequence
       int32_t n_ev = 0;
-      if (it_kv_manager_release_seq(c.mgr, int32_t(rng() % c.seqs), ev.data(), int32_t(ev.size()), &n_ev) != IT_OK)
-        fail("release");
+      const int32_t s = int32_t(rng() % c.seqs);
+      const std::vector<char> held_before = held_blocks(c);
+      if (ctx[s] > 0) {
+        // Too small a capacity: an error, and nothing changes.
+        std::vector<int32_t> t0(size_t(c.seqs) * c.mb), t1(size_t(c.seqs) * c.mb);
+        it_kv_manager_tables(c.mgr, t0.data(), c.mb, nullptr, nullptr);
+        const int64_t free0 = it_block_pool_num_free(c.pool);
+        if (it_kv_manager_release_seq(c.mgr, s, ev.data(), 0, &n_ev) == IT_OK) fail("release cap 0 accepted", s);
+        it_kv_manager_tables(c.mgr, t1.data(), c.mb, nullptr, nullptr);
+        if (t0 != t1 || it_block_pool_num_free(c.pool) != free0) fail("release error changed state", s);
+      }
+      if (it_kv_manager_release_seq(c.mgr, s, ev.data(), int32_t(ev.size()), &n_ev) != IT_OK) fail("release");
+      check_evicted(c, held_before, ev.data(), n_ev);
     } else {  // fork into an empty sequence, if there is one
       int dst = -1;
       for (int s = 0; s < c.seqs; ++s)
@@ -187,7 +257,7 @@ int main() {
     run(0, seed);
     run(100, seed);
   }
-  std::printf("host sanitize driver: ok (%ld error recoveries, %ld of them evicted_out capacity, %ld cow capacity; "
+  std::printf("host sanitize driver: ok (%ld error recoveries, %ld of them evicted capacity, %ld cow capacity; "
               "%ld forks, %ld copy-on-write pairs, %ld evictions)\n",
               g_errors, g_ev_cap, g_cow_cap, g_forks, g_cows, g_evicted);
   // Each path must have been taken, or the run proves little.

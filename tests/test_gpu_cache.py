@@ -61,7 +61,9 @@ def _assert_pools(dev, ref, what):
                                      (orc.Q4_0, 256, 32), (orc.Q4_0, 128, 16), (orc.Q4_0, 64, 8),
                                      (orc.Q4_1, 256, 32), (orc.Q4_1, 128, 16), (orc.Q4_1, 64, 8),
                                      (orc.Q5_0, 256, 32), (orc.Q5_0, 128, 16), (orc.Q5_0, 64, 8), (orc.Q5_0, 32, 16),
-                                     (orc.Q5_1, 256, 32), (orc.Q5_1, 128, 16), (orc.Q5_1, 64, 8), (orc.Q5_1, 32, 8)])
+                                     (orc.Q5_1, 256, 32), (orc.Q5_1, 128, 16), (orc.Q5_1, 64, 8), (orc.Q5_1, 32, 8),
+                                     # rows that are not a power-of-two number of 16-byte vectors
+                                     (orc.BF16, 96, 16), (orc.F16, 80, 16), (orc.F32, 48, 16), (orc.F32, 12, 8)])
 def test_append_bit_exact(dt, D, bs):
     hkv, nb, n = 4, 64, 300
     dev, ref = _pair(nb, bs, hkv, D, dt)

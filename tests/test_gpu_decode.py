@@ -126,6 +126,28 @@ def test_config2_full_size_bf16():
     assert_close(got, want, *TOL[orc.BF16], what="config2 full")
 
 
+def test_headline_config2_4k_full_size():
+    """The headline workload itself: 32 sequences x 4096 tokens (Hq 28, Hkv
+    4, D 128, bs 16) over a 16384-block pool in seeded random order,
+    512-token partitions, bf16 q.  The 16-bit decode rounds the softmax
+    weights to bf16 before P.V; the printed margin (max over elements of
+    |got - ref| / (atol + rtol |ref|), 1.0 = at the tolerance) records what
+    that leaves of the bf16 tolerance."""
+    hq, hkv, D, bs = 28, 4, 128, 16
+    ctx = np.full(32, 4096, np.int32)
+    dev, ref, tables, ctx, q, qdt = _build(orc.BF16, hq, hkv, D, bs, ctx, seed=44, nb=16384, mb=256)
+    rtol, atol = TOL[orc.BF16]
+    margins = []
+    for out_f32 in (False, True):
+        got, want = _run(dev, ref, tables, ctx, q, qdt, hq, partition=512, out_f32=out_f32)
+        assert_close(got, want, rtol, atol, what=f"headline f32out={out_f32}")
+        err = np.abs(got.astype(np.float64) - want)
+        margins.append(float((err / (atol + rtol * np.abs(want))).max()))
+        print(f"headline 32x4096 out {'f32' if out_f32 else 'bf16'}: max |err| {err.max():.3g}, "
+              f"{margins[-1]:.3f} of the bf16 tolerance")
+    assert max(margins) < 1.0
+
+
 def test_many_sequences_unit_mapping():
     """Workgroups run the non-empty (sequence, head, partition) units in
     order, found by a prefix sum over the context lengths 64 sequences at a

@@ -178,14 +178,10 @@ def test_batcher_fifo_admission_and_plans():
 
 
 def _oracle_release(mo, pool, s):
-    """The oracle's release of sequence slot s: BlockPool::free of every held
-    block, lowest logical block first, then an empty table row."""
-    t, _, _ = mo.tables()
-    freed = [int(b) for b in t[s] if b >= 0]
-    for blk in freed:
-        assert pool.free(blk) == 0
-    mo.seed_seq(s, 0, 0, [])
-    return freed
+    """The oracle's release of sequence slot s (BlockPool::free of every held
+    block, lowest logical block first, then an empty table row); returns the
+    blocks that went back to the pool."""
+    return [int(b) for b in mo.release(s)]
 
 
 def test_batcher_preemption_releases_or_keeps_blocks_like_the_oracle():
@@ -310,3 +306,133 @@ def test_host_code_under_sanitizers(tmp_path):
         pytest.skip("another preloaded library precedes the sanitizer runtime in this environment")
     assert r.returncode == 0, (r.stdout + r.stderr)[-3000:]
     assert "host sanitize driver: ok" in r.stdout
+
+
+def test_window_does_not_evict_blocks_a_fork_holds():
+    """Pool 16, block size 4, window 8: seq 0 takes 10 tokens, seq 1 forks
+    it, seq 0 appends 4 more with copy-on-write.  The window drops seq 0's
+    reference to block 15 at p = 11, but seq 1 still holds it: it is not
+    listed for clearing, keeps refcount 1 and stays in seq 1's table.  Plans
+    equal the oracle manager's; seq 1's own window later lists it."""
+    pool, opool = BlockPool(16), orc.Pool(16)
+    m, mo = KvManager(pool, 4, 2, 8, 8), orc.Manager(opool, 4, 2, 8, 8)
+    p = m.append([0], [10])
+    np.testing.assert_array_equal(p.slots, mo.append([0], [10])[0])
+    m.fork(0, 1)
+    mo.fork(0, 1)
+    p = m.append([0], [4], cow=True)
+    so, eo, cs, cd = mo.append([0], [4], cow=True)
+    np.testing.assert_array_equal(p.slots, so)
+    np.testing.assert_array_equal(p.evicted, eo)
+    np.testing.assert_array_equal(p.cow_src, cs)
+    np.testing.assert_array_equal(p.cow_dst, cd)
+    assert p.evicted.size == 0 and pool.ref_count(15) == 1
+    t, _, _ = m.tables()
+    assert t[1, 0] == 15 and t[0, 0] == -1
+    p = m.append([1], [2], cow=True)
+    assert list(p.evicted) == [15] and pool.ref_count(15) == 0
+    assert list(p.evicted) == list(mo.append([1], [2], cow=True)[1])
+    # Release returns only what no other sequence holds.
+    freed = m.release(0)
+    assert sorted(freed.tolist()) == sorted(mo.release(0).tolist()) == [11, 12]
+    assert pool.ref_count(14) == 1
+
+
+def test_manager_fork_cow_window_release_equal_oracle():
+    """Random appends (plain and copy-on-write), forks and releases, with
+    and without a window: every plan (slots, per-token sequence and
+    position, evicted list, copy pairs, context lengths, window starts) and
+    every table equals the oracle manager's."""
+    rng = np.random.default_rng(23)
+    for W in (0, 12, 40):
+        cap, bs, S, mb = 48, 4, 5, 40
+        order = orc.permutation(W + 3, cap)
+        pa, pb = BlockPool(cap, order=order), orc.Pool(cap, order=order)
+        ma, mo = KvManager(pa, bs, S, mb, W), orc.Manager(pb, bs, S, mb, W)
+        n_dead = 0
+        for _ in range(600):
+            _, ctx0, _ = mo.tables()
+            op = rng.integers(10)
+            if op < 7:
+                seqs = rng.permutation(S)[: int(rng.integers(1, S + 1))]
+                # Now and then more tokens than the window holds in one step.
+                nt = rng.integers(0, W + 20 if op == 0 else 6, seqs.size)
+                if (ctx0[seqs] + nt).max() >= mb * bs or pb.num_free() < seqs.size * (nt.max() // bs + 3) + 2:
+                    for s in range(S):
+                        np.testing.assert_array_equal(ma.release(s), mo.release(s))
+                    continue
+                cow = bool(op % 2)
+                plan = ma.append(seqs, nt, cow=cow)
+                want = mo.append(seqs, nt, cow=cow)
+                if cow:  # (without copy-on-write, forks writing one shared page collide by design)
+                    live = plan.slots[plan.slots >= 0]
+                    assert np.unique(live).size == live.size, "two live tokens of one step share a slot"
+                n_dead += int((plan.slots < 0).sum())
+                np.testing.assert_array_equal(plan.slots, want[0])
+                np.testing.assert_array_equal(plan.evicted, want[1])
+                if cow:
+                    np.testing.assert_array_equal(plan.cow_src, want[2])
+                    np.testing.assert_array_equal(plan.cow_dst, want[3])
+                np.testing.assert_array_equal(plan.token_seq, np.repeat(seqs, nt))
+                np.testing.assert_array_equal(plan.token_pos, np.concatenate(
+                    [ctx0[s] + np.arange(n) for s, n in zip(seqs, nt)]).astype(np.int32))
+                _, ctx1, st1 = mo.tables()
+                np.testing.assert_array_equal(plan.ctx_lens, ctx1)
+                np.testing.assert_array_equal(plan.start_pos, st1)
+            elif op < 9:
+                s = int(rng.integers(S))
+                np.testing.assert_array_equal(ma.release(s), mo.release(s))
+            else:
+                empty = [s for s in range(S) if ctx0[s] == 0]
+                src = int(rng.integers(S))
+                if empty and empty[0] != src:
+                    ma.fork(src, empty[0])
+                    mo.fork(src, empty[0])
+            for x, y in zip(ma.tables(), mo.tables()):
+                np.testing.assert_array_equal(x, y)
+            assert pa.num_free() == pb.num_free()
+        assert n_dead > 0 or W == 0
+
+
+def test_release_with_too_small_capacity_changes_nothing():
+    from infer_train_amd._lib import lib
+    import ctypes as C
+
+    pool = BlockPool(16)
+    m = KvManager(pool, 4, 2, 8)
+    m.append([0], [10])
+    before = m.tables()[0].copy()
+    ev = np.empty(2, np.int32)
+    n = C.c_int32(0)
+    rc = lib.it_kv_manager_release_seq(m._h, 0, ev.ctypes.data, 2, C.byref(n))
+    assert rc == 2 and "capacity" in lib.it_last_error().decode()
+    np.testing.assert_array_equal(m.tables()[0], before)
+    assert pool.num_free() == 13
+    assert sorted(m.release(0).tolist()) == [13, 14, 15]
+
+
+def test_step_longer_than_window_marks_dead_tokens():
+    """Pool 16, block size 4, window 8: one step appends 14 tokens.  At
+    p = 11 the window returns block 15 (positions 0-3) to the pool: those
+    four tokens are dead (slot -1, never written), block 15 is listed for
+    clearing, and it goes back on the free list only when the step ends, so
+    p = 12 opens block 12, not 15, and no two tokens share a slot.  The next
+    step releases block 14 and the one after opens it again (LIFO: the last
+    block pushed back).  Equal to the oracle manager."""
+    pool, opool = BlockPool(16), orc.Pool(16)
+    m, mo = KvManager(pool, 4, 1, 8, 8), orc.Manager(opool, 4, 1, 8, 8)
+    p = m.append([0], [14])
+    so, eo = mo.append([0], [14])
+    np.testing.assert_array_equal(p.slots, so)
+    np.testing.assert_array_equal(p.evicted, eo)
+    assert list(p.slots[:4]) == [-1] * 4
+    assert list(p.slots[4:] // 4) == [14] * 4 + [13] * 4 + [12] * 2
+    assert list(p.evicted) == [15] and pool.ref_count(15) == 0
+    assert list(p.token_pos) == list(range(14)) and p.ctx_lens[0] == 14 and p.start_pos[0] == 6
+    p = m.append([0], [2])
+    np.testing.assert_array_equal(p.slots, mo.append([0], [2])[0])
+    # p = 15 releases block 14 (positions 4-7, written by the first step).
+    assert list(p.slots // 4) == [12, 12] and list(p.evicted) == [14]
+    p = m.append([0], [2])  # p = 16 opens a block: 14, the last one pushed back
+    np.testing.assert_array_equal(p.slots, mo.append([0], [2])[0])
+    assert list(p.slots // 4) == [14, 14] and p.evicted.size == 0

@@ -923,3 +923,164 @@ def test_rope_rejects_bad_shapes(orc):
         orc.rope(np.ones(100, np.float32), 1, 64, 64)  # not a multiple of head_dim
     with pytest.raises(ValueError):
         orc.rope(np.ones(64, np.float32), 1, 63, 64)  # odd n_dims
+
+
+# ---------------- manager: prefix sharing under a window --------------------
+def test_window_release_keeps_blocks_a_fork_holds(orc):
+    """Pool 16, block size 4, window 8.  Seq 0 takes 10 tokens (blocks 15,
+    14, 13), seq 1 forks it, seq 0 appends 4 more with copy-on-write.  At
+    p = 11 the window drops seq 0's reference to block 15, which seq 1 still
+    holds: BlockPool::free (paged.rs:48-53) leaves it at refcount 1, off the
+    free list, so it is not an evicted page.  When seq 1's own window passes
+    it, the refcount reaches 0 and it is listed."""
+    pool = orc.Pool(16)
+    m = orc.Manager(pool, 4, 2, 8, 8)
+    slots, ev = m.append([0], [10])
+    assert list(slots // 4) == [15] * 4 + [14] * 4 + [13] * 2 and ev.size == 0
+    m.fork(0, 1)
+    assert [pool.ref_count(b) for b in (15, 14, 13)] == [2, 2, 2]
+    slots, ev, cs, cd = m.append([0], [4], cow=True)
+    # p=10 writes into shared partial block 13: copied to 12 (LIFO top).
+    assert list(cs) == [13] and list(cd) == [12]
+    # p=12 opens a new block: 11.
+    assert list(slots // 4) == [12, 12, 11, 11]
+    assert ev.size == 0
+    assert pool.ref_count(15) == 1 and pool.ref_count(13) == 1 and pool.num_free() == 11
+    t, cl, _ = m.tables()
+    assert list(t[1, :3]) == [15, 14, 13] and t[0, 0] == -1 and list(t[0, 1:4]) == [14, 12, 11]
+    # Seq 1 advances to p = 11: its window drops block 15, the last reference.
+    slots, ev, cs, cd = m.append([1], [2], cow=True)
+    assert list(cs) == [13] or cs.size == 0
+    assert list(ev) == [15] and pool.ref_count(15) == 0
+    # Releasing seq 0 returns only the blocks nobody else holds (12 and 11);
+    # block 14 stays with seq 1.
+    freed = m.release(0)
+    assert sorted(freed.tolist()) == [11, 12] and pool.ref_count(14) == 1
+
+
+def _held(t):
+    return set(int(b) for b in t.ravel() if b >= 0)
+
+
+def _check_manager_invariants(pool, t, cap):
+    """Refcount of every block = the number of table entries naming it; a
+    block no table names is on the free list (refcount 0)."""
+    refs = {}
+    for b in t.ravel():
+        if b >= 0:
+            refs[int(b)] = refs.get(int(b), 0) + 1
+    for b in range(cap):
+        assert pool.ref_count(b) == refs.get(b, 0), (b, pool.ref_count(b), refs.get(b, 0))
+    assert pool.num_free() == cap - len(refs)
+
+
+def test_manager_fork_cow_window_random_invariants(orc):
+    """Random appends (plain and copy-on-write), forks and releases, with and
+    without a window, on tiny pools: after every operation the refcounts equal
+    the table entries naming each block, every slot lies in the block its
+    table names, and the evicted list is exactly the blocks no table names
+    any more (those BlockPool::free pushed: paged.rs:48-53)."""
+    rng = np.random.default_rng(17)
+    for W in (0, 12, 40):
+        cap, bs, S, mb = 48, 4, 5, 40
+        pool = orc.Pool(cap, order=orc.permutation(W + 1, cap))
+        m = orc.Manager(pool, bs, S, mb, W)
+        n_shared_release = n_ev = 0
+        for _ in range(600):
+            t0, ctx0, _ = m.tables()
+            held0 = _held(t0)
+            op = rng.integers(10)
+            if op < 7:
+                seqs = rng.permutation(S)[: int(rng.integers(1, S + 1))]
+                nt = rng.integers(0, 6, seqs.size)
+                if (ctx0[seqs] + nt).max() >= mb * bs or pool.num_free() < 3 * seqs.size + 2:
+                    for s in range(S):
+                        m.release(s)
+                    continue
+                slots, ev = m.append(seqs, nt, cow=bool(op % 2))[:2]
+                t1, ctx1, _ = m.tables()
+                k = 0
+                for s, n in zip(seqs, nt):
+                    for j in range(int(n)):
+                        p = int(ctx0[s]) + j
+                        assert slots[k] == int(t1[s, p // bs]) * bs + p % bs
+                        k += 1
+                held1 = _held(t1)
+                # Listed = dropped from every table (a block reused by a later
+                # token of the same step is listed and held again).
+                assert held0 - held1 <= set(ev.tolist())
+                for b in ev:
+                    assert int(b) in held0
+                    assert int(b) in held1 or pool.ref_count(int(b)) == 0
+                n_shared_release += len([b for b in held0 & held1 if b not in ev])
+                n_ev += ev.size
+            elif op < 9:
+                s = int(rng.integers(S))
+                freed = m.release(s)
+                t1, _, _ = m.tables()
+                assert set(freed.tolist()) == held0 - _held(t1)
+            else:
+                empty = [s for s in range(S) if ctx0[s] == 0]
+                src = int(rng.integers(S))
+                if empty and empty[0] != src:
+                    m.fork(src, empty[0])
+            t, _, _ = m.tables()
+            _check_manager_invariants(pool, t, cap)
+        assert n_ev > 0 or W == 0
+
+
+# ---------------- OpenMP entry points equal the single-threaded ones --------
+def _ragged_cache(orc, dt, nb=96, bs=16, hkv=2, D=64, seed=50):
+    c = orc.Cache(nb, bs, hkv, D, dt)
+    n = nb * bs
+    src_dt = orc.BF16 if dt == orc.BF16 else orc.F32
+    k, v = orc.normal(seed, n * hkv * D), orc.normal(seed + 1, n * hkv * D)
+    if src_dt == orc.BF16:
+        k, v = orc.f32_to_bf16(k), orc.f32_to_bf16(v)
+    c.append(k.reshape(n, hkv, D), v.reshape(n, hkv, D), np.arange(n, dtype=np.int64))
+    return c
+
+
+@pytest.mark.parametrize("dt", ["BF16", "F32", "Q8_0"])
+def test_oracle_decode_mt_equals_single_thread(orc, dt):
+    """orc_paged_decode_mt (the checker of the full-size GPU tests and the
+    all-cores CPU baseline) equals orc_paged_decode bit for bit: ragged
+    contexts, empty and one-token sequences, window starts, thread counts
+    2..16 (fewer and more threads than sequences x heads)."""
+    dtype = getattr(orc, dt)
+    nb, bs, hkv, hq, D = 96, 16, 2, 6, 64
+    c = _ragged_cache(orc, dtype, nb, bs, hkv, D)
+    perm = orc.permutation(51, nb).astype(np.int32)
+    ctx = np.array([300, 1, 0, 517, 64, 1000, 129], np.int32)
+    tables = np.full((ctx.size, 64), -1, np.int32)
+    k = 0
+    for b, n in enumerate(ctx):
+        nbk = (int(n) + bs - 1) // bs
+        tables[b, :nbk] = perm[k % nb:k % nb + nbk] if k % nb + nbk <= nb else perm[:nbk]
+        k += nbk
+    q = orc.normal(52, ctx.size * hq * D).reshape(ctx.size, hq, D)
+    for start in (None, np.array([0, 0, 0, 200, 63, 744, 1], np.int32)):
+        want = c.decode(q, hq, tables, ctx, start, 0.125)
+        for threads in (2, 3, 8, 16):
+            got = c.decode(q, hq, tables, ctx, start, 0.125, threads=threads)
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (threads, start is None)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_oracle_prefill_rows_mt_equals_single_thread(orc, causal):
+    """orc_paged_prefill_rows_mt (the checker of the full-size prefill test)
+    equals orc_paged_prefill_rows bit for bit, causal and not, for row
+    ranges at the chunk's start, middle and end, thread counts 2..16."""
+    nb, bs, hkv, hq, D = 96, 16, 2, 8, 64
+    c = _ragged_cache(orc, orc.BF16, nb, bs, hkv, D, seed=60)
+    perm = orc.permutation(61, nb).astype(np.int32)
+    ctx = np.array([700, 333], np.int32)
+    ql = np.array([90, 333], np.int32)
+    cu = np.array([0, 90, 423], np.int32)
+    tables = np.stack([perm[:48], perm[48:96]])
+    q = orc.normal(62, int(cu[-1]) * hq * D).reshape(int(cu[-1]), hq, D)
+    for s, b, e in ((0, 0, 90), (0, 37, 41), (1, 0, 5), (1, 300, 333)):
+        want = c.prefill(q, hq, cu, tables, ctx, 0.1, causal=causal, rows=(s, b, e))
+        for threads in (2, 5, 16):
+            got = c.prefill(q, hq, cu, tables, ctx, 0.1, causal=causal, rows=(s, b, e), threads=threads)
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (s, b, e, threads)

@@ -98,3 +98,44 @@ def test_noalloc_rejects_more_than_its_array():
     assert float(out.abs().sum()) == 0.0  # nothing ran
     with pytest.raises(InvalidInput):
         check(rc)
+
+
+def test_noalloc_under_graph_capture():
+    """A no-allocation decode captured in a HIP graph (the callers it is
+    for): the array's address was looked up when the cache was made, so the
+    captured call makes no runtime call that capture forbids.  Every replay,
+    with eager no-allocation decodes of another batch between replays
+    (which overwrite the shared array), equals the eager it_paged_decode
+    bit for bit."""
+    import torch
+    from infer_train_amd._lib import OK
+
+    hq, hkv, D, bs = 28, 4, 128, 16
+    dev, tables, ctx, q = _cache(hq, hkv, D, bs, [300, 17, 1023, 512], seed=90)
+    other, t2, c2, q2 = _cache(hq, hkv, D, bs, [2000, 64], seed=91)
+    dq, dt, dc = to_dev(q.view(np.int16), torch.bfloat16), to_dev(tables), to_dev(ctx)
+    dq2, dt2, dc2 = to_dev(q2.view(np.int16), torch.bfloat16), to_dev(t2), to_dev(c2)
+    max_t = int(ctx.max())
+    want = dev.decode(dq, dt, dc, None, max_t, partition=256, out_dtype=torch.float32)
+    want2 = other.decode(dq2, dt2, dc2, None, 2000, partition=256, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    out_g = torch.empty_like(want)
+    out2 = torch.empty_like(want2)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # warm-up off the capture, as torch asks
+        assert _noalloc(dev, dq, dt, dc, None, max_t, 256, out_g) == OK
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        assert _noalloc(dev, dq, dt, dc, None, max_t, 256, out_g) == OK
+    for i in range(3):
+        out_g.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(from_dev(out_g), from_dev(want), err_msg=f"replay {i}")
+        assert _noalloc(other, dq2, dt2, dc2, None, 2000, 256, out2) == OK
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(from_dev(out2), from_dev(want2), err_msg=f"eager call after replay {i}")
+    dev.check()
