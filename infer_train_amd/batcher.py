@@ -17,6 +17,10 @@ from .memory import BlockPool
 __all__ = ["KvManager", "ContinuousBatcher", "RequestState", "RequestContext", "StepPlan"]
 
 
+_EMPTY = np.zeros(0, np.int32)
+_EMPTY.flags.writeable = False
+
+
 @dataclass
 class StepPlan:
     """What one append step hands to the device: the slot of every new token
@@ -58,29 +62,42 @@ class KvManager:
         check(lib.it_kv_manager_new(pool.handle, block_size, max_seqs, max_blocks_per_seq, window, C.byref(h)))
         self._h = h
         self._destroy = lib.it_kv_manager_destroy  # bound now: module globals may be gone at exit
-        # Reused output buffers of it_kv_manager_step (grown on demand); the
-        # plan returned to the caller holds copies.
+        # Reused buffers of it_kv_manager_step (grown on demand), with their
+        # addresses cached (ndarray.ctypes.data costs about a microsecond);
+        # the plan returned to the caller holds copies.
         self._plan = StepPlanC()
+        self._plan_ref = C.byref(self._plan)
+        self._step_fn = lib.it_kv_manager_step
         self._tok_cap = 0
+        self._seq_cap = 0
         # Blocks returned to the pool in one step: at most the pool's capacity.
         self._ev = np.empty(pool.capacity() + 1, np.int32)
-        self._cs = np.empty(0, np.int32)
-        self._cd = np.empty(0, np.int32)
         self._plan.evicted = self._ev.ctypes.data
         self._plan.evicted_cap = self._ev.size
+        self._lens = np.empty((2, max_seqs), np.int32)  # ctx_lens, start_pos
+        self._plan.ctx_lens, self._plan.start_pos = self._lens[0].ctypes.data, self._lens[1].ctypes.data
+        self._grow_tokens(64)
+        self._grow_seqs(64)
 
-    def _grow(self, total: int) -> None:
-        cap = max(total, 2 * self._tok_cap, 64)
+    def _grow_tokens(self, total: int) -> None:
+        cap = max(total, 2 * self._tok_cap)
         self._slots = np.empty(cap, np.int64)
-        self._tseq = np.empty(cap, np.int32)
-        self._tpos = np.empty(cap, np.int32)
+        self._tsp = np.empty((2, cap), np.int32)  # token_seq, token_pos
         self._cs = np.empty(cap, np.int32)
         self._cd = np.empty(cap, np.int32)
         pl = self._plan
-        pl.slots, pl.token_seq, pl.token_pos = self._slots.ctypes.data, self._tseq.ctypes.data, self._tpos.ctypes.data
+        pl.slots, pl.token_seq, pl.token_pos = self._slots.ctypes.data, self._tsp[0].ctypes.data, self._tsp[1].ctypes.data
         pl.tokens_cap = cap
         pl.cow_cap = cap  # at most one copy per token
+        self._cs_addr, self._cd_addr = self._cs.ctypes.data, self._cd.ctypes.data
         self._tok_cap = cap
+
+    def _grow_seqs(self, n: int) -> None:
+        cap = max(n, 2 * self._seq_cap)
+        self._seqbuf = np.empty(cap, np.int32)
+        self._ntbuf = np.empty(cap, np.int32)
+        self._seq_addr, self._nt_addr = self._seqbuf.ctypes.data, self._ntbuf.ctypes.data
+        self._seq_cap = cap
 
     def seed_seq(self, seq: int, pos: int, first_block: int, blocks: Sequence[int]) -> None:
         arr = np.ascontiguousarray(np.asarray(blocks, dtype=np.int32))
@@ -88,24 +105,30 @@ class KvManager:
 
     def append(self, seqs: Sequence[int], n_tokens: Sequence[int] | int = 1, cow: bool = False) -> StepPlan:
         """One step: n_tokens[i] tokens to seqs[i] (in list order)."""
-        seqs_a = np.ascontiguousarray(seqs, dtype=np.int32)
+        n = len(seqs)
+        if n > self._seq_cap:
+            self._grow_seqs(n)
+        self._seqbuf[:n] = seqs
+        nt = self._ntbuf[:n]
         if np.isscalar(n_tokens):
-            nt = np.full(seqs_a.size, int(n_tokens), dtype=np.int32)
+            nt.fill(n_tokens)
+            total = int(n_tokens) * n
         else:
-            nt = np.ascontiguousarray(n_tokens, dtype=np.int32)
-        total = int(nt.sum())
+            nt[:] = n_tokens
+            total = int(nt.sum())
         if total > self._tok_cap:
-            self._grow(total)
-        ctx = np.empty(self.max_seqs, np.int32)
-        st = np.empty(self.max_seqs, np.int32)
+            self._grow_tokens(total)
         pl = self._plan
-        pl.cow_src = self._cs.ctypes.data if cow else None
-        pl.cow_dst = self._cd.ctypes.data if cow else None
-        pl.ctx_lens, pl.start_pos = ctx.ctypes.data, st.ctypes.data
-        check(lib.it_kv_manager_step(self._h, seqs_a.ctypes.data, nt.ctypes.data, seqs_a.size, C.byref(pl)))
-        n, ne, nc = pl.n_tokens, pl.n_evicted, pl.n_cow
-        return StepPlan(self._slots[:n].copy(), self._ev[:ne].copy(), self._cs[:nc].copy(), self._cd[:nc].copy(),
-                        self._tseq[:n].copy(), self._tpos[:n].copy(), ctx, st)
+        pl.cow_src = self._cs_addr if cow else None
+        pl.cow_dst = self._cd_addr if cow else None
+        rc = self._step_fn(self._h, self._seq_addr, self._nt_addr, n, self._plan_ref)
+        if rc:
+            check(rc)
+        k, ne, nc = pl.n_tokens, pl.n_evicted, pl.n_cow
+        tsp, lens = self._tsp[:, :k].copy(), self._lens.copy()
+        return StepPlan(self._slots[:k].copy(), self._ev[:ne].copy() if ne else _EMPTY,
+                        self._cs[:nc].copy() if nc else _EMPTY, self._cd[:nc].copy() if nc else _EMPTY,
+                        tsp[0], tsp[1], lens[0], lens[1])
 
     def positions(self) -> np.ndarray:
         """Next position (= context length) of every sequence slot."""

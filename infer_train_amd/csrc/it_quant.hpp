@@ -83,6 +83,20 @@ __device__ __forceinline__ int32_t q8_round(float x, float scale) {
   return int32_t(r);
 }
 
+// Whether a group's scale takes the fast quotient below: a normal scale
+// whose reciprocal is normal too (amax 0, inf, NaN-free tiny or huge groups
+// take the IEEE division for every element).
+__device__ __forceinline__ bool q8_fast_scale(float scale) { return scale >= 0x1p-120f && scale <= 0x1p120f; }
+
+// Why q8's fast path is exact: for |x| <= 127 scale (x an element of the
+// group whose amax set the scale) and rs = v_rcp_f32(scale) (1 ulp), x rs
+// lies within 127 (2^-23 + 2^-24) < 3.1e-5 of x / scale, and so does the
+// IEEE quotient fl(x / scale) (within 127 2^-24).  When x rs is farther
+// than 0.4999 from a half-integer, both lie strictly inside the unit
+// interval around n = rint(x rs), so round(fl(x / scale)) = n, and |n| <=
+// 127 needs no clamp.  Otherwise (near a tie, or NaN) the IEEE division
+// decides.
+
 // (int8_t)(r) and (uint8_t)(r) as ggml's x86 build computes them: truncate
 // to int32 (NaN and out-of-range give 0x80000000), keep the low byte.
 __device__ __forceinline__ int32_t trunc_i8(float r) {
@@ -154,13 +168,55 @@ __device__ __forceinline__ QuantGroup quant_group(float4 x, int l8) {
   const float xs[4] = {x.x, x.y, x.z, x.w};
   QuantGroup out{0u, 0u, 0u};
   if constexpr (DT == IT_Q8_0) {
-    auto absn = [](float f) { return f == f ? fabsf(f) : 0.0f; };
-    float amax = fmaxf(fmaxf(absn(x.x), absn(x.y)), fmaxf(absn(x.z), absn(x.w)));
-    amax = group_max<8>(amax);
+    // amax (quant.rs:157-163, NaN ignored): an unsigned max of |x|'s bit
+    // patterns orders every non-NaN value as fp32 does; a group holding a
+    // NaN (bits above inf's; the max is group-uniform) takes the NaN-
+    // skipping float max instead.
+    const uint32_t kAbs = 0x7FFFFFFFu;
+    uint32_t mb = max(max(__float_as_uint(x.x) & kAbs, __float_as_uint(x.y) & kAbs),
+                      max(__float_as_uint(x.z) & kAbs, __float_as_uint(x.w) & kAbs));
+    mb = max(mb, uint32_t(__builtin_amdgcn_mov_dpp(int(mb), kDppQuadXor1, 0xF, 0xF, true)));
+    mb = max(mb, uint32_t(__builtin_amdgcn_mov_dpp(int(mb), kDppQuadXor2, 0xF, 0xF, true)));
+    mb = max(mb, uint32_t(__builtin_amdgcn_mov_dpp(int(mb), kDppHalfMirror, 0xF, 0xF, true)));
+    float amax = __uint_as_float(mb);
+    if (mb > 0x7F800000u) {
+      auto absn = [](float f) { return f == f ? fabsf(f) : 0.0f; };
+      amax = group_max<8>(fmaxf(fmaxf(absn(x.x), absn(x.y)), fmaxf(absn(x.z), absn(x.w))));
+    }
     if (amax != 0.0f) {  // quant.rs:166-170: an all-zero group stores d = 0, qs = 0
-      const float scale = amax / 127.0f;
+      // scale = amax / 127 (quant.rs:173): for a normal amax, a faithful
+      // quotient and one exact-remainder correction give the IEEE quotient
+      // (checked over every positive normal float on the host).
+      constexpr float kR127 = 1.0f / 127.0f;
+      float scale;
+      if (amax >= 0x1p-100f && amax <= 0x1p100f) {
+        const float y = mul_rn(amax, kR127);
+        scale = fmaf(fmaf(-127.0f, y, amax), kR127, y);
+      } else {
+        scale = amax / 127.0f;
+      }
+      bool exact = !q8_fast_scale(scale);
+      if (!exact) {
+        // q = round(x / scale) (quant.rs:176-178) through rs = v_rcp_f32:
+        // f = fma(x, rs, 1.5 2^23) holds n = rint(x rs) in its low byte
+        // (as an int8), and |x rs - n| < 0.4999 makes n = round(fl(x /
+        // scale)) (the argument above; sampled on the host too).
+        const float rs = __builtin_amdgcn_rcpf(scale);
+        constexpr float kMagic = 12582912.0f;  // 1.5 * 2^23
+        uint32_t fb[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) out.qs |= (uint32_t(q8_round(xs[e], scale)) & 0xFFu) << (8 * e);
+        for (int e = 0; e < 4; ++e) {
+          const float f = fmaf(xs[e], rs, kMagic);
+          if (!(fabsf(fmaf(xs[e], rs, kMagic - f)) < 0.4999f)) exact = true;
+          fb[e] = __float_as_uint(f);
+        }
+        out.qs = __builtin_amdgcn_perm(fb[1], fb[0], 0x0C0C0400u) | __builtin_amdgcn_perm(fb[3], fb[2], 0x04000C0Cu);
+      }
+      if (exact) {  // rare: a near-tie, a NaN, or a scale outside the fast range
+        out.qs = 0u;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) out.qs |= (uint32_t(q8_round(xs[e], scale)) & 0xFFu) << (8 * e);
+      }
       out.meta = f16_bits_rne(scale);
     }
   } else if constexpr (DT == IT_Q4_0) {

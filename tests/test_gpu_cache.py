@@ -63,7 +63,8 @@ def _assert_pools(dev, ref, what):
                                      (orc.Q5_0, 256, 32), (orc.Q5_0, 128, 16), (orc.Q5_0, 64, 8), (orc.Q5_0, 32, 16),
                                      (orc.Q5_1, 256, 32), (orc.Q5_1, 128, 16), (orc.Q5_1, 64, 8), (orc.Q5_1, 32, 8),
                                      # rows that are not a power-of-two number of 16-byte vectors
-                                     (orc.BF16, 96, 16), (orc.F16, 80, 16), (orc.F32, 48, 16), (orc.F32, 12, 8)])
+                                     (orc.BF16, 96, 16), (orc.F16, 80, 16), (orc.F32, 48, 16), (orc.F32, 12, 8),
+                                     (orc.Q8_0, 64, 8), (orc.Q8_0, 96, 16), (orc.Q8_0, 128, 8)])
 def test_append_bit_exact(dt, D, bs):
     hkv, nb, n = 4, 64, 300
     dev, ref = _pair(nb, bs, hkv, D, dt)
@@ -102,6 +103,38 @@ def test_append_q8_special_groups():
     ref.append(k, v, slots)
     dev.append(to_dev(k), to_dev(v), to_dev(slots))
     _assert_pools(dev, ref, "append q8 special")
+
+
+@pytest.mark.parametrize("D", [256, 128, 64, 96])
+def test_append_q8_near_ties(D):
+    """Elements whose quotient x / scale lies within a few ulps of a
+    half-integer, where round(fl(x / scale)) depends on the IEEE quotient's
+    last bit: the append's fast reciprocal path must hand them to the exact
+    division.  Scales from 1e-38 to 1e37 (the tiny and huge ones take the
+    division for every element).  D 64 / 128 / 256 run the 16-element-per-
+    lane kernel, D 96 the 4-element one."""
+    hkv, bs, nb = 2, 16, 8
+    n = 40
+    rng = np.random.default_rng(D)
+    x = np.empty((n * hkv * D // 32, 32), np.float32)
+    for i in range(x.shape[0]):
+        amax = np.float32(10.0 ** rng.uniform(-38, 37) if i % 7 == 0 else rng.uniform(0.05, 20.0))
+        sc = np.float32(amax) / np.float32(127)
+        kk = rng.integers(-126, 126, 31).astype(np.float64)
+        y = ((kk + 0.5) * np.float64(sc)).astype(np.float32)
+        for _ in range(3):  # nudge by up to three ulps either way
+            step = rng.integers(-1, 2, 31)
+            y = np.where(step > 0, np.nextafter(y, np.float32(np.inf)), np.where(step < 0, np.nextafter(y, np.float32(-np.inf)), y))
+        y = np.clip(y, -amax, amax).astype(np.float32)
+        x[i, 0] = amax if i % 2 else -amax
+        x[i, 1:] = y
+    k = x.reshape(n, hkv, D)
+    v = (-x[:, ::-1]).reshape(n, hkv, D).copy()
+    dev, ref = _pair(nb, bs, hkv, D, orc.Q8_0)
+    slots = orc.permutation(D, nb * bs)[:n].copy()
+    ref.append(k, v, slots)
+    dev.append(to_dev(k), to_dev(v), to_dev(slots))
+    _assert_pools(dev, ref, f"append q8 near ties D={D}")
 
 
 @pytest.mark.parametrize("dt", [orc.Q4_0, orc.Q4_1, orc.Q5_0, orc.Q5_1])

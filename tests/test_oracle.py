@@ -591,6 +591,27 @@ def test_f16_bf16_converters_exhaustive():
     assert r.returncode == 0, r.stdout + r.stderr
 
 
+def test_q8_fast_quotient_identities(tmp_path):
+    """The arithmetic the Q8_0 quantise-append kernels use instead of IEEE
+    divisions (tests/check_q8_fast.c): amax / 127 from a faithful quotient
+    plus one exact-remainder correction equals the IEEE quotient for every
+    positive normal float, and the reciprocal-based rounding equals
+    round(fl(x / scale)) whenever its residual test passes, for reciprocals
+    within one ulp, on inputs placed at ties."""
+    import shutil
+
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not found")
+    exe = str(tmp_path / "check_q8_fast")
+    b = subprocess.run([gcc, "-O3", "-fopenmp", "-ffp-contract=off", "-o", exe,
+                        os.path.join(ROOT, "tests", "check_q8_fast.c"), "-lm"], capture_output=True, text=True)
+    assert b.returncode == 0, b.stderr
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=600)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "0 mismatches over all" in r.stdout
+
+
 def test_converters_match_numpy(orc):
     x = orc.normal(22, 100000) * np.float32(300)
     np.testing.assert_array_equal(orc.f32_to_f16(x), x.astype(np.float16).view(np.uint16))
