@@ -66,6 +66,7 @@
 #pragma once
 #include <hip/hip_runtime.h>
 
+#include <cfloat>
 #include <type_traits>
 
 #include "it_decode.hpp"
@@ -73,6 +74,7 @@
 namespace itkv {
 
 constexpr int kGroupTok = 16;  // tokens per group (one wave step)
+constexpr float kQ8PScale = 2048.0f;  // Q8_0 P.V weights carry 2^11 (see the V loop)
 
 // Geometry of a cache dtype at head_dim D.
 template <int DT, int D>
@@ -366,6 +368,52 @@ typedef short v4s __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ v4f mfma16k16(uint2 a, uint2 b, v4f c) {
   return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(v4s, a), __builtin_bit_cast(v4s, b), c, 0, 0, 0);
 }
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ v4f mfma16_f16(uint4 a, uint4 b, v4f c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, a), __builtin_bit_cast(v8h, b), c, 0, 0, 0);
+}
+// Signed byte J0 of w0 and byte J1 of w1 as an fp16 pair (lo = w0's),
+// exactly: two SDWA converts, the second writing the high half in place.
+#define IT_I8PAIR(J0, J1)                                                                               \
+  asm("v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_" #J0 "\n\t" \
+      "v_cvt_f16_i16_sdwa %0, sext(%2) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_" #J1    \
+      : "=&v"(r)                                                                                        \
+      : "v"(w0), "v"(w1))
+template <int J0, int J1>
+__device__ __forceinline__ uint32_t i8pair_f16(uint32_t w0, uint32_t w1) {
+  static_assert(J0 >= 0 && J0 < 4 && J1 >= 0 && J1 < 4, "byte");
+  uint32_t r;
+  if constexpr (J0 == 0 && J1 == 0) IT_I8PAIR(0, 0);
+  else if constexpr (J0 == 1 && J1 == 1) IT_I8PAIR(1, 1);
+  else if constexpr (J0 == 0 && J1 == 1) IT_I8PAIR(0, 1);
+  else if constexpr (J0 == 2 && J1 == 3) IT_I8PAIR(2, 3);
+  else static_assert(J0 < 0, "unused byte pair");
+  return r;
+}
+#undef IT_I8PAIR
+// Eight signed bytes as eight fp16, exactly.
+__device__ __forceinline__ uint4 i8x8_f16(uint2 w) {
+  return make_uint4(i8pair_f16<0, 1>(w.x, w.x), i8pair_f16<2, 3>(w.x, w.x), i8pair_f16<0, 1>(w.y, w.y),
+                    i8pair_f16<2, 3>(w.y, w.y));
+}
+// x = hi + lo + r as fp16 parts, hi = fp16(x), lo = fp16(x - hi) (round to
+// nearest even each), for the lanes' four values: |r| <= 2^-22 |x| for x
+// in fp16's normal range (2^-14 .. 65504) and its residual too.
+__device__ __forceinline__ void split2_f16(const float (&x)[4], uint2& hi, uint2& lo) {
+  h2 h01, h23, l01, l23;
+  h01[0] = (_Float16)x[0];
+  h01[1] = (_Float16)x[1];
+  h23[0] = (_Float16)x[2];
+  h23[1] = (_Float16)x[3];
+  l01[0] = (_Float16)(x[0] - (float)h01[0]);
+  l01[1] = (_Float16)(x[1] - (float)h01[1]);
+  l23[0] = (_Float16)(x[2] - (float)h23[0]);
+  l23[1] = (_Float16)(x[3] - (float)h23[1]);
+  hi = make_uint2(__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23));
+  lo = make_uint2(__builtin_bit_cast(uint32_t, l01), __builtin_bit_cast(uint32_t, l23));
+}
 
 // (x, y) -> (x_lo + x_hi, y_lo + y_hi) across the two 32-lane halves:
 // lanes 0-31 receive x's sum, lanes 32-63 y's.
@@ -569,7 +617,13 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
   // dims 32 ks + 8 kh .. + 8; Q4_0 dims 32 ks + 4 kh .. + 4 and 32 ks + 16 +
   // 4 kh .. + 4 (the low and high nibbles of bytes 4 kh .. + 4 of the group).
   constexpr int NK = kQ ? D / 32 : 1;  // 32-groups (MFMA k-steps) per row
-  uint4 qa[3][NK];
+  uint4 qa[F::kQ8 ? 1 : 3][NK];
+  // Q8_0: q of head h scaled by 2^E_h (so that max |q| lies in [2^14, 2^15))
+  // as hi + lo fp16 parts, the A operand of v_mfma_f32_16x16x32_f16; the
+  // scores are scaled back by 2^-E_h (exact).  sE[i]: 2^-E of head
+  // 4 (lane / 16) + i, the heads this lane's scores belong to.
+  uint4 qf[F::kQ8 ? 2 : 1][NK];
+  float sE[4] = {1.0f, 1.0f, 1.0f, 1.0f};
   // Q4_1: sum of q over each 32-group, the A operand of the offset-term MFMA
   // (v_mfma_f32_16x16x16_bf16, k = group): lane (kh, h) holds groups
   // 4 kh .. + 4 of head h, split exactly into three bf16 parts.
@@ -594,16 +648,59 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
     const float* qp = static_cast<const float*>(a.q) + (int64_t(b) * a.n_heads + head0 + (hq < GC ? hq : 0)) * D +
                       (kNib ? 4 : 8) * qr_row;
     float qsum[NK];
+    if constexpr (F::kQ8) {
+      float4 x0[NK], x1[NK];
+      float mx = 0.0f;
 #pragma unroll
-    for (int ks = 0; ks < NK; ++ks) {
+      for (int ks = 0; ks < NK; ++ks) {
+        x0[ks] = *reinterpret_cast<const float4*>(qp + 32 * ks);
+        x1[ks] = *reinterpret_cast<const float4*>(qp + 32 * ks + 4);
+        if (hq >= GC) x0[ks] = x1[ks] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(x0[ks].x), fabsf(x0[ks].y)), fmaxf(fabsf(x0[ks].z), fabsf(x0[ks].w))));
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(x1[ks].x), fabsf(x1[ks].y)), fmaxf(fabsf(x1[ks].z), fabsf(x1[ks].w))));
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 16));  // the four lanes of head hq
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      // mx in [2^(e-1), 2^e): E = 15 - e; an all-zero (or non-finite) q keeps E = 0.
+      const int E = (mx > 0.0f && mx <= FLT_MAX) ? 15 - __builtin_amdgcn_frexp_expf(mx) : 0;
+#pragma unroll
+      for (int ks = 0; ks < NK; ++ks) {
+        const float x[8] = {x0[ks].x, x0[ks].y, x0[ks].z, x0[ks].w, x1[ks].x, x1[ks].y, x1[ks].z, x1[ks].w};
+        uint32_t hw[4], lw[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          h2 hp, lp;
+          const float y0 = __builtin_ldexpf(x[2 * j], E), y1 = __builtin_ldexpf(x[2 * j + 1], E);
+          hp[0] = (_Float16)y0;
+          hp[1] = (_Float16)y1;
+          lp[0] = (_Float16)(y0 - (float)hp[0]);
+          lp[1] = (_Float16)(y1 - (float)hp[1]);
+          hw[j] = __builtin_bit_cast(uint32_t, hp);
+          lw[j] = __builtin_bit_cast(uint32_t, lp);
+        }
+        qf[0][ks] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+        qf[1][ks] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sE[i] = __builtin_ldexpf(1.0f, -__shfl(E, 4 * qr_row + i));
+#pragma unroll
+      for (int p = 0; p < 2; ++p)
+#pragma unroll
+        for (int ks = 0; ks < NK; ++ks)
+          asm volatile("" : "+v"(qf[p][ks].x), "+v"(qf[p][ks].y), "+v"(qf[p][ks].z), "+v"(qf[p][ks].w));
+    }
+#pragma unroll
+    for (int ks = 0; ks < NK && !F::kQ8; ++ks) {
       float4 x0 = *reinterpret_cast<const float4*>(qp + 32 * ks);
       float4 x1 = *reinterpret_cast<const float4*>(qp + 32 * ks + (kNib ? 16 : 4));
       if (hq >= GC) x0 = x1 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
       if constexpr (kOff) qsum[ks] = ((x0.x + x0.y) + (x0.z + x0.w)) + ((x1.x + x1.y) + (x1.z + x1.w));
-      split3_bf16(x0.x, x0.y, qa[0][ks].x, qa[1][ks].x, qa[2][ks].x);
-      split3_bf16(x0.z, x0.w, qa[0][ks].y, qa[1][ks].y, qa[2][ks].y);
-      split3_bf16(x1.x, x1.y, qa[0][ks].z, qa[1][ks].z, qa[2][ks].z);
-      split3_bf16(x1.z, x1.w, qa[0][ks].w, qa[1][ks].w, qa[2][ks].w);
+      if constexpr (!F::kQ8) {
+        split3_bf16(x0.x, x0.y, qa[0][ks].x, qa[1][ks].x, qa[2][ks].x);
+        split3_bf16(x0.z, x0.w, qa[0][ks].y, qa[1][ks].y, qa[2][ks].y);
+        split3_bf16(x1.x, x1.y, qa[0][ks].z, qa[1][ks].z, qa[2][ks].z);
+        split3_bf16(x1.z, x1.w, qa[0][ks].w, qa[1][ks].w, qa[2][ks].w);
+      }
     }
     if constexpr (kOff) {
       float qg[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -621,7 +718,7 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
       qs_a[0] = p0, qs_a[1] = p1, qs_a[2] = p2;
     }
 #pragma unroll
-    for (int p = 0; p < 3; ++p)
+    for (int p = 0; p < (F::kQ8 ? 0 : 3); ++p)
 #pragma unroll
       for (int ks = 0; ks < NK; ++ks)
         asm volatile("" : "+v"(qa[p][ks].x), "+v"(qa[p][ks].y), "+v"(qa[p][ks].z), "+v"(qa[p][ks].w));
@@ -794,16 +891,29 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
       }
       v4f acc[NK];
       uint4 kb[NK];
-      Unroll<0, NK + 2>::run([&](auto kc) {
-        constexpr int k = decltype(kc)::value;
-        if constexpr (k < NK) {
-          if constexpr (F::kQ5) kb[k] = nib5_bf16(kr[k].x, qh5[k] & 0xFu, (qh5[k] >> 16) & 0xFu);
-          else kb[k] = kNib ? nib8_bf16(kr[k].x) : i8x8_bf16(kr[k]);
-          acc[k] = mfma16(qa[0][k], kb[k], v4f{0.0f, 0.0f, 0.0f, 0.0f});
-        }
-        if constexpr (k >= 1 && k - 1 < NK) acc[k - 1] = mfma16(qa[1][k - 1], kb[k - 1], acc[k - 1]);
-        if constexpr (k >= 2) acc[k - 2] = mfma16(qa[2][k - 2], kb[k - 2], acc[k - 2]);
-      });
+      if constexpr (F::kQ8) {
+        // fp16: q hi / lo parts against the exact fp16 K bytes, the two
+        // MFMAs of a group a group apart.
+        Unroll<0, NK + 1>::run([&](auto kc) {
+          constexpr int k = decltype(kc)::value;
+          if constexpr (k < NK) {
+            kb[k] = i8x8_f16(kr[k]);
+            acc[k] = mfma16_f16(qf[0][k], kb[k], v4f{0.0f, 0.0f, 0.0f, 0.0f});
+          }
+          if constexpr (k >= 1) acc[k - 1] = mfma16_f16(qf[1][k - 1], kb[k - 1], acc[k - 1]);
+        });
+      } else {
+        Unroll<0, NK + 2>::run([&](auto kc) {
+          constexpr int k = decltype(kc)::value;
+          if constexpr (k < NK) {
+            if constexpr (F::kQ5) kb[k] = nib5_bf16(kr[k].x, qh5[k] & 0xFu, (qh5[k] >> 16) & 0xFu);
+            else kb[k] = kNib ? nib8_bf16(kr[k].x) : i8x8_bf16(kr[k]);
+            acc[k] = mfma16(qa[0][k], kb[k], v4f{0.0f, 0.0f, 0.0f, 0.0f});
+          }
+          if constexpr (k >= 1 && k - 1 < NK) acc[k - 1] = mfma16(qa[1][k - 1], kb[k - 1], acc[k - 1]);
+          if constexpr (k >= 2) acc[k - 2] = mfma16(qa[2][k - 2], kb[k - 2], acc[k - 2]);
+        });
+      }
       v4f sv = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int ks = 0; ks < NK; ++ks) {
@@ -835,7 +945,7 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int h = 4 * qr_row + i;
-          const float x = sv[i] * qk_mult;
+          const float x = sv[i] * (qk_mult * sE[i]);  // sE: 2^-E (Q8_0), else 1
           if (h < GC) sc[h * SP + i_tok] = x;
           m_q[i] = fmaxf(m_q[i], x);
         }
@@ -1016,6 +1126,10 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) pj[j] *= F::kBScale;  // exact; undoes B's factor 16 (Q5: 8)
       }
+      if constexpr (F::kQ8) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) pj[j] *= kQ8PScale;  // exact; undone when the partials are stored
+      }
       const char* const vrow = slot + (4 * kq) * RB + (kNib ? 1 : 2) * hm;
       // The scale rows of the lane's four tokens, NK fp16 each (Q5: read
       // per group below, with the group's qh words).
@@ -1045,6 +1159,70 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
         else if constexpr (kOff) return dw[j][G] & 0xFFFFu;
         else return G & 1 ? dw[j][G / 2] >> 16 : dw[j][G / 2] & 0xFFFFu;
       };
+      // Q8_0 in fp16, when every scale of the item is below 512 (the other
+      // items take the bf16 form below): B = d q is exact as hi + lo fp16
+      // parts (d has 11 significant bits and q 8, and |d q| <= 65504), and
+      // A = p 2^11 as two fp16 parts made once per item (p <= 1: every
+      // weight above 2^-13 keeps 22 bits, smaller ones an absolute error
+      // below 2^-36).  Each tile takes two v_mfma_f32_16x16x32_f16 whose k
+      // runs over (token, B part): [A_hi A_hi] . [B_hi; B_lo] and
+      // [A_lo A_lo] . [B_hi; B_lo], every product exact in the fp32
+      // accumulator (11 x 11 significant bits).  K = 32 costs little more
+      // than K = 16 (measured 19 against 17 cycles), so a V item is 32 MFMAs
+      // instead of the bf16 form's 48.  The two MFMAs of an accumulator are
+      // issued a group apart, so none waits for the one before it.
+      bool f16_item = false;
+      if constexpr (F::kQ8) {
+        typedef unsigned short us2 __attribute__((ext_vector_type(2)));
+        us2 m = __builtin_bit_cast(us2, dw[0][0]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int c = 0; c < SW; ++c) m = __builtin_elementwise_max(m, __builtin_bit_cast(us2, dw[j][c]));
+        const bool big = m[0] >= 0x6000u || m[1] >= 0x6000u;  // scales are >= 0: bits order as values
+        f16_item = __builtin_amdgcn_ballot_w64(big) == 0;  // uniform
+      }
+      if (f16_item) {
+        uint2 ah, al;
+        split2_f16(pj, ah, al);
+        const uint4 a_hi = make_uint4(ah.x, ah.y, ah.x, ah.y), a_lo = make_uint4(al.x, al.y, al.x, al.y);
+        uint4 bprev[2];  // the previous group's B operands, for its second MFMAs
+        Unroll<0, NK + 1>::run([&](auto gc) {
+          constexpr int G = decltype(gc)::value;
+          uint4 b[2];
+          if constexpr (G < NK) {
+            const int vg = 32 * (G ^ kq);
+            uint32_t w[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) w[j] = *reinterpret_cast<const uint16_t*>(vrow + j * RB + vg);
+            // fp16 d of group G for the token pairs (0, 1) and (2, 3).
+            constexpr uint32_t kSel = (G & 1) ? 0x07060302u : 0x05040100u;
+            const h2 d01 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(dw[1][G / 2], dw[0][G / 2], kSel));
+            const h2 d23 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(dw[3][G / 2], dw[2][G / 2], kSel));
+            // Tile 0 takes byte 0 of each 2-byte read (even dims), tile 1 byte 1.
+            const h2 q01[2] = {__builtin_bit_cast(h2, i8pair_f16<0, 0>(w[0], w[1])),
+                               __builtin_bit_cast(h2, i8pair_f16<1, 1>(w[0], w[1]))};
+            const h2 q23[2] = {__builtin_bit_cast(h2, i8pair_f16<0, 0>(w[2], w[3])),
+                               __builtin_bit_cast(h2, i8pair_f16<1, 1>(w[2], w[3]))};
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+              const h2 hi01 = q01[t] * d01, hi23 = q23[t] * d23;
+              const h2 lo01 = __builtin_elementwise_fma(q01[t], d01, -hi01);
+              const h2 lo23 = __builtin_elementwise_fma(q23[t], d23, -hi23);
+              b[t] = make_uint4(__builtin_bit_cast(uint32_t, hi01), __builtin_bit_cast(uint32_t, hi23),
+                                __builtin_bit_cast(uint32_t, lo01), __builtin_bit_cast(uint32_t, lo23));
+            }
+            o8[G][0] = mfma16_f16(a_hi, b[0], o8[G][0]);
+            o8[G][1] = mfma16_f16(a_hi, b[1], o8[G][1]);
+          }
+          if constexpr (G >= 1) {
+            o8[G - 1][0] = mfma16_f16(a_lo, bprev[0], o8[G - 1][0]);
+            o8[G - 1][1] = mfma16_f16(a_lo, bprev[1], o8[G - 1][1]);
+          }
+          if constexpr (G < NK) bprev[0] = b[0], bprev[1] = b[1];
+        });
+        continue;
+      }
       Unroll<0, NK>::run([&](auto gc) {
         constexpr int G = decltype(gc)::value;
         // Byte offset of group G in the lane's rows (swizzled by token quad).
@@ -1197,8 +1375,9 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
           if constexpr (kNib) {
             row[hm] = o8[g][0][i];
             row[16 + hm] = o8[g][1][i];
-          } else {
-            *reinterpret_cast<float2*>(row + 2 * hm) = make_float2(o8[g][0][i], o8[g][1][i]);
+          } else {  // Q8_0: the weights carried 2^11 (exact)
+            *reinterpret_cast<float2*>(row + 2 * hm) =
+                make_float2(o8[g][0][i] * (1.0f / kQ8PScale), o8[g][1][i] * (1.0f / kQ8PScale));
           }
         }
       }
