@@ -1555,6 +1555,8 @@ def main():
                     help="time only config 5 (Q8_0 decode), for profiling")
     ap.add_argument("--summarize-config5-profile", metavar="DIR",
                     help="summarise rocprofv3 CSVs of --only-config5 runs into profiles/decode_split_config5.md")
+    ap.add_argument("--only-format", choices=["q4_0", "q4_1", "q5_0", "q5_1"],
+                    help="only the decode of this KV format on the config-5 shape; prints one JSON line")
     ap.add_argument("--only-prefill", action="store_true",
                     help="run only config 3 (chunk append + causal prefill) (for rocprofv3 runs)")
     ap.add_argument("--summarize-prefill-profile", metavar="DIR",
@@ -1612,6 +1614,15 @@ def main():
         r = bench_config5(args.steps, args.warmup, False)
         print(json.dumps({"only_config5": True, **{k: r[k] for k in ("decode_us", "split_us", "pct_hbm_peak")}}),
               flush=True)
+        return
+
+    if args.only_format:
+        import infer_train_amd as it
+
+        dt = {"q4_0": it.Q4_0, "q4_1": it.Q4_1, "q5_0": it.Q5_0, "q5_1": it.Q5_1}[args.only_format]
+        r = bench_q4(dt, args.steps, args.warmup)
+        print(json.dumps({"only_format": args.only_format,
+                          **{k: r[k] for k in ("decode_us", "split_us", "pct_hbm_peak", "append_us")}}), flush=True)
         return
 
     if args.only_prefill:

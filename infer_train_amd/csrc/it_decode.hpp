@@ -55,6 +55,17 @@ __device__ __forceinline__ uint32_t lds_offset(const void* p) {
 __device__ __forceinline__ void dma_b128(const void* g, uint32_t m0) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off nt" ::"s"(m0), "v"(g) : "memory", "m0");
 }
+// dma_b128 from a wave-uniform base (an SGPR pair) plus a per-lane 32-bit
+// byte offset: the address costs no vector instructions.
+__device__ __forceinline__ void dma_b128_s(const void* base, uint32_t off, uint32_t m0) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2 nt" ::"s"(m0), "v"(off), "s"(base)
+               : "memory", "m0");
+}
+// dma_b32 from a wave-uniform base plus a per-lane 32-bit byte offset.
+__device__ __forceinline__ void dma_b32_s(const void* base, uint32_t off, uint32_t m0) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2 nt" ::"s"(m0), "v"(off), "s"(base)
+               : "memory", "m0");
+}
 // Active lanes x 4 B into LDS [m0 + 4 lane], non-temporal like dma_b128.
 __device__ __forceinline__ void dma_b32(const void* g, uint32_t m0) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off nt" ::"s"(m0), "v"(g) : "memory", "m0");

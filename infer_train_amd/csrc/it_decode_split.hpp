@@ -74,7 +74,7 @@
 namespace itkv {
 
 constexpr int kGroupTok = 16;  // tokens per group (one wave step)
-constexpr float kQ8PScale = 2048.0f;  // Q8_0 P.V weights carry 2^11 (see the V loop)
+constexpr float kQPScale = 2048.0f;  // quantised P.V weights carry 2^11 (see the V loop)
 
 // Geometry of a cache dtype at head_dim D.
 template <int DT, int D>
@@ -775,20 +775,36 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
       const uint32_t page = uint32_t(__builtin_amdgcn_readfirstlane(s_pages[(t0 >> a.log2_bs) - lb0]));
       const char* pbase = pool + uint64_t(page) * page_bytes;
       const char* base = pbase + uint32_t(in_page * RB);
-      const bool full = tb + kGroupTok <= nt;
+      if (tb + kGroupTok <= nt) {
+        // Every row inside the partition: uniform bases, per-lane offsets
+        // fixed for the kernel.
 #pragma unroll
-      for (int j = 0; j < NI; ++j) {
-        int off = is_v ? lane_off_v[j] : lane_off_k[j];
-        if (!full && tb + lane_row[j] >= nt) off -= lane_row[j] * RB;
-        dma_b128(base + off, __builtin_amdgcn_readfirstlane(m0 + 1024u * j));
-      }
-      if constexpr (kQ) {
+        for (int j = 0; j < NI; ++j)
+          dma_b128_s(base, uint32_t(is_v ? lane_off_v[j] : lane_off_k[j]),
+                     __builtin_amdgcn_readfirstlane(m0 + 1024u * j));
+        if constexpr (kQ) {
+          const char* sbase = pbase + uint32_t(bs * RB + in_page * F::kScaleRow);
 #pragma unroll
-        for (int u = 0; u < F::kScaleLoads; ++u) {
-          int row = s_row[u];
-          if (!full && tb + row >= nt) row = 0;
-          const char* g = pbase + uint32_t(bs * RB + (in_page + row) * F::kScaleRow + s_col[u]);
-          if (s_lane[u]) dma_b32(g, __builtin_amdgcn_readfirstlane(m0 + uint32_t(GB + 256 * u)));
+          for (int u = 0; u < F::kScaleLoads; ++u)
+            if (s_lane[u])
+              dma_b32_s(sbase, uint32_t(s_row[u] * F::kScaleRow + s_col[u]),
+                        __builtin_amdgcn_readfirstlane(m0 + uint32_t(GB + 256 * u)));
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < NI; ++j) {
+          int off = is_v ? lane_off_v[j] : lane_off_k[j];
+          if (tb + lane_row[j] >= nt) off -= lane_row[j] * RB;
+          dma_b128(base + off, __builtin_amdgcn_readfirstlane(m0 + 1024u * j));
+        }
+        if constexpr (kQ) {
+#pragma unroll
+          for (int u = 0; u < F::kScaleLoads; ++u) {
+            int row = s_row[u];
+            if (tb + row >= nt) row = 0;
+            const char* g = pbase + uint32_t(bs * RB + (in_page + row) * F::kScaleRow + s_col[u]);
+            if (s_lane[u]) dma_b32(g, __builtin_amdgcn_readfirstlane(m0 + uint32_t(GB + 256 * u)));
+          }
         }
       }
     } else {
@@ -1077,9 +1093,16 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
     }
     const bool none_h = m_h == -INFINITY;  // every key skipped, or a padding row
     const float* const sc_h = sc + (hm < GC ? hm : 0) * SP + 4 * kq;
-    for (int s = ns; s < S; ++s) {
-      wait_item(s);
-      if (s + R - 1 < S) issue(s + R - 1);
+    // Formats with the fp16 form of P.V (below).
+    constexpr bool kF16 = F::kQ8 || DT == IT_Q4_0 || DT == IT_Q4_1;
+    // One item of the partition, in the bf16 form if bf16_only; else in the
+    // fp16 form, or, when that does not fit its scales, not at all: it then
+    // returns false, having changed nothing but the item's wait and issue.
+    auto v_item = [&](int s, auto bf16_only, bool redo) -> bool {
+      if (!redo) {  // redo: the item's wait and issue are done
+        wait_item(s);
+        if (s + R - 1 < S) issue(s + R - 1);
+      }
       const int gi = s - ns;
       const int tb = (gi * NW + wave) * kGroupTok;
       char* const slot = my_ring + (s % R) * SLOT;
@@ -1101,35 +1124,6 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         pj[j] = (tb + 4 * kq + j < nt && !none_h) ? __builtin_amdgcn_exp2f(sj[j] - m_h) : 0.0f;
-      lsum += (pj[0] + pj[1]) + (pj[2] + pj[3]);
-      if constexpr (kOff) {
-        // The offset term: M[h][G] += sum over the item's tokens of p[h][t]
-        // m'_G(t); B[t][G = hm] for the lane's four tokens, zero past the
-        // groups; both operands in three exact bf16 parts.
-        float mv[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          mv[j] = hm < NK ? off_mprime<DT>(*reinterpret_cast<const uint32_t*>(slot + GB + (4 * kq + j) * F::kScaleRow +
-                                                                               F::kMetaOff + 4 * (hm < NK ? hm : 0)))
-                          : 0.0f;
-        uint2 mb[3], pa[3];
-        split3_bf16(mv[0], mv[1], mb[0].x, mb[1].x, mb[2].x);
-        split3_bf16(mv[2], mv[3], mb[0].y, mb[1].y, mb[2].y);
-        split3_bf16(pj[0], pj[1], pa[0].x, pa[1].x, pa[2].x);
-        split3_bf16(pj[2], pj[3], pa[0].y, pa[1].y, pa[2].y);
-#pragma unroll
-        for (int p = 0; p < 3; ++p)
-#pragma unroll
-          for (int r = 0; r < 3; ++r) mo = mfma16k16(pa[p], mb[r], mo);
-      }
-      if constexpr (kNib) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) pj[j] *= F::kBScale;  // exact; undoes B's factor 16 (Q5: 8)
-      }
-      if constexpr (F::kQ8) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) pj[j] *= kQ8PScale;  // exact; undone when the partials are stored
-      }
       const char* const vrow = slot + (4 * kq) * RB + (kNib ? 1 : 2) * hm;
       // The scale rows of the lane's four tokens, NK fp16 each (Q5: read
       // per group below, with the group's qh words).
@@ -1159,118 +1153,215 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
         else if constexpr (kOff) return dw[j][G] & 0xFFFFu;
         else return G & 1 ? dw[j][G / 2] >> 16 : dw[j][G / 2] & 0xFFFFu;
       };
-      // Q8_0 in fp16, when every scale of the item is below 512 (the other
-      // items take the bf16 form below): B = d q is exact as hi + lo fp16
-      // parts (d has 11 significant bits and q 8, and |d q| <= 65504), and
-      // A = p 2^11 as two fp16 parts made once per item (p <= 1: every
-      // weight above 2^-13 keeps 22 bits, smaller ones an absolute error
-      // below 2^-36).  Each tile takes two v_mfma_f32_16x16x32_f16 whose k
-      // runs over (token, B part): [A_hi A_hi] . [B_hi; B_lo] and
-      // [A_lo A_lo] . [B_hi; B_lo], every product exact in the fp32
-      // accumulator (11 x 11 significant bits).  K = 32 costs little more
-      // than K = 16 (measured 19 against 17 cycles), so a V item is 32 MFMAs
-      // instead of the bf16 form's 48.  The two MFMAs of an accumulator are
-      // issued a group apart, so none waits for the one before it.
+      // P.V in fp16 (Q8_0, Q4_0, Q4_1), when every scale of the item is
+      // small enough that |d v| <= 65504 (d below 512 for Q8_0's |v| <= 128,
+      // below 4096 for the nibbles' |v| <= 8; other items take the bf16 form
+      // below): B = d v is exact as hi + lo fp16 parts (d has 11
+      // significant bits and v at most 8), and A = p 2^11 as two fp16 parts
+      // made once per item (p <= 1: every weight above 2^-13 keeps 22 bits,
+      // smaller ones an absolute error below 2^-36).  Each tile takes two
+      // v_mfma_f32_16x16x32_f16 whose k runs over (token, B part):
+      // [A_hi A_hi] . [B_hi; B_lo] and [A_lo A_lo] . [B_hi; B_lo], every
+      // product exact in the fp32 accumulator (11 x 11 significant bits).
+      // K = 32 costs little more than K = 16 (measured 19 against 17
+      // cycles), so a V item is 32 MFMAs instead of the bf16 form's 48.  The
+      // two MFMAs of an accumulator are issued a group apart, so none waits
+      // for the one before it.  (Q4_1's offset term stays on the bf16 form
+      // above.)
       bool f16_item = false;
-      if constexpr (F::kQ8) {
+      if constexpr (kF16) {
         typedef unsigned short us2 __attribute__((ext_vector_type(2)));
-        us2 m = __builtin_bit_cast(us2, dw[0][0]);
+        us2 m = {0, 0};
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
-          for (int c = 0; c < SW; ++c) m = __builtin_elementwise_max(m, __builtin_bit_cast(us2, dw[j][c]));
-        const bool big = m[0] >= 0x6000u || m[1] >= 0x6000u;  // scales are >= 0: bits order as values
+          for (int c = 0; c < SW; ++c)
+            m = __builtin_elementwise_max(m, __builtin_bit_cast(us2, DT == IT_Q4_0 ? dw[j][c] & 0x7FFF7FFFu : dw[j][c]));
+        // |d| bits order as the values (Q8_0's and Q4_1's d are >= 0, Q4_0's
+        // = max / -8 of either sign); Q4_1's high halves are the offsets m,
+        // not scales.
+        constexpr unsigned kLim = F::kQ8 ? 0x6000u : 0x6C00u;  // 512, 4096
+        const bool big = m[0] >= kLim || (!kOff && m[1] >= kLim);
         f16_item = __builtin_amdgcn_ballot_w64(big) == 0;  // uniform
       }
-      if (f16_item) {
+      if constexpr (kF16 && !decltype(bf16_only)::value) {
+        if (!f16_item) return false;  // before any state of the item changes
+      }
+      lsum += (pj[0] + pj[1]) + (pj[2] + pj[3]);
+      if constexpr (kOff) {
+        // The offset term: M[h][G] += sum over the item's tokens of p[h][t]
+        // m'_G(t); B[t][G = hm] for the lane's four tokens, zero past the
+        // groups; both operands in three exact bf16 parts.
+        float mv[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          mv[j] = hm < NK ? off_mprime<DT>(*reinterpret_cast<const uint32_t*>(slot + GB + (4 * kq + j) * F::kScaleRow +
+                                                                               F::kMetaOff + 4 * (hm < NK ? hm : 0)))
+                          : 0.0f;
+        uint2 mb[3], pa[3];
+        split3_bf16(mv[0], mv[1], mb[0].x, mb[1].x, mb[2].x);
+        split3_bf16(mv[2], mv[3], mb[0].y, mb[1].y, mb[2].y);
+        split3_bf16(pj[0], pj[1], pa[0].x, pa[1].x, pa[2].x);
+        split3_bf16(pj[2], pj[3], pa[0].y, pa[1].y, pa[2].y);
+#pragma unroll
+        for (int p = 0; p < 3; ++p)
+#pragma unroll
+          for (int r = 0; r < 3; ++r) mo = mfma16k16(pa[p], mb[r], mo);
+      }
+      // The P.V weights carry 2^11 (exact; undone when the partials are
+      // stored): the fp16 form below needs it, and the bf16 form keeps the
+      // accumulators on the same scale.
+#pragma unroll
+      for (int j = 0; j < 4; ++j) pj[j] *= kQPScale;
+      auto pv_f16 = [&](auto) {
         uint2 ah, al;
         split2_f16(pj, ah, al);
         const uint4 a_hi = make_uint4(ah.x, ah.y, ah.x, ah.y), a_lo = make_uint4(al.x, al.y, al.x, al.y);
-        uint4 bprev[2];  // the previous group's B operands, for its second MFMAs
-        Unroll<0, NK + 1>::run([&](auto gc) {
+        // B operands of group G (both tiles).
+        auto bgroup = [&](auto gc, uint4 (&b)[2]) {
           constexpr int G = decltype(gc)::value;
-          uint4 b[2];
-          if constexpr (G < NK) {
+          // fp16 d of group G for the token pairs (0, 1) and (2, 3).
+          constexpr uint32_t kSel = (!kOff && (G & 1)) ? 0x07060302u : 0x05040100u;
+          constexpr int GW = kOff ? G : G / 2;  // the dword holding it
+          const h2 d01 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(dw[1][GW], dw[0][GW], kSel));
+          const h2 d23 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(dw[3][GW], dw[2][GW], kSel));
+          // v of the lane's four tokens as fp16 pairs, tile t: Q8_0 tile 0
+          // even dims (byte 0 of each 2-byte read), tile 1 odd; nibble
+          // formats tile 0 the low nibbles (element hm), tile 1 the high
+          // (element 16 + hm).
+          h2 v01[2], v23[2];
+          if constexpr (F::kQ8) {
             const int vg = 32 * (G ^ kq);
             uint32_t w[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) w[j] = *reinterpret_cast<const uint16_t*>(vrow + j * RB + vg);
-            // fp16 d of group G for the token pairs (0, 1) and (2, 3).
-            constexpr uint32_t kSel = (G & 1) ? 0x07060302u : 0x05040100u;
-            const h2 d01 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(dw[1][G / 2], dw[0][G / 2], kSel));
-            const h2 d23 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(dw[3][G / 2], dw[2][G / 2], kSel));
-            // Tile 0 takes byte 0 of each 2-byte read (even dims), tile 1 byte 1.
-            const h2 q01[2] = {__builtin_bit_cast(h2, i8pair_f16<0, 0>(w[0], w[1])),
-                               __builtin_bit_cast(h2, i8pair_f16<1, 1>(w[0], w[1]))};
-            const h2 q23[2] = {__builtin_bit_cast(h2, i8pair_f16<0, 0>(w[2], w[3])),
-                               __builtin_bit_cast(h2, i8pair_f16<1, 1>(w[2], w[3]))};
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-              const h2 hi01 = q01[t] * d01, hi23 = q23[t] * d23;
-              const h2 lo01 = __builtin_elementwise_fma(q01[t], d01, -hi01);
-              const h2 lo23 = __builtin_elementwise_fma(q23[t], d23, -hi23);
-              b[t] = make_uint4(__builtin_bit_cast(uint32_t, hi01), __builtin_bit_cast(uint32_t, hi23),
-                                __builtin_bit_cast(uint32_t, lo01), __builtin_bit_cast(uint32_t, lo23));
-            }
-            o8[G][0] = mfma16_f16(a_hi, b[0], o8[G][0]);
-            o8[G][1] = mfma16_f16(a_hi, b[1], o8[G][1]);
-          }
-          if constexpr (G >= 1) {
-            o8[G - 1][0] = mfma16_f16(a_lo, bprev[0], o8[G - 1][0]);
-            o8[G - 1][1] = mfma16_f16(a_lo, bprev[1], o8[G - 1][1]);
-          }
-          if constexpr (G < NK) bprev[0] = b[0], bprev[1] = b[1];
-        });
-        continue;
-      }
-      Unroll<0, NK>::run([&](auto gc) {
-        constexpr int G = decltype(gc)::value;
-        // Byte offset of group G in the lane's rows (swizzled by token quad).
-        const int vg = (kNib ? 16 : 32) * (G ^ kq);
-        float x[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j)  // p * d, one v_fma_mix_f32 each
-          x[j] = fmaf(pj[j], f16_bits_to_f32(dbits(j, gc)), 0.0f);
-        uint2 ah, am, al;
-        split3_bf16(x[0], x[1], ah.x, am.x, al.x);
-        split3_bf16(x[2], x[3], ah.y, am.y, al.y);
-        auto pair = [](uint32_t f0, uint32_t f1) { return __builtin_amdgcn_perm(f1, f0, 0x07060302u); };
-        uint2 b0, b1;
-        if constexpr (kNib) {
-          uint32_t w = 0;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) w |= uint32_t(*reinterpret_cast<const uint8_t*>(vrow + j * RB + vg)) << (8 * j);
-          uint4 t;  // tokens 4 kq + j: low nibbles (tile 0), then high (tile 1)
-          if constexpr (F::kQ5) {
-            // Fifth bits of element hm (low nibble) and 16 + hm (high) of
-            // each token, from the group's qh words.
-            uint32_t lo4 = 0u, hi4 = 0u;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              const uint32_t qh = *reinterpret_cast<const uint32_t*>(srow + j * F::kScaleRow + 4 * G) >> hm;
-              lo4 |= (qh & 1u) << j;
-              hi4 |= ((qh >> 16) & 1u) << j;
-            }
-            t = nib5_bf16(w, lo4, hi4);
+            v01[0] = __builtin_bit_cast(h2, i8pair_f16<0, 0>(w[0], w[1]));
+            v01[1] = __builtin_bit_cast(h2, i8pair_f16<1, 1>(w[0], w[1]));
+            v23[0] = __builtin_bit_cast(h2, i8pair_f16<0, 0>(w[2], w[3]));
+            v23[1] = __builtin_bit_cast(h2, i8pair_f16<1, 1>(w[2], w[3]));
           } else {
-            t = nib8_bf16(w);
-          }
-          b0 = make_uint2(t.x, t.y);
-          b1 = make_uint2(t.z, t.w);
-        } else {
-          uint32_t w[4];
+            const int vg = 16 * (G ^ kq);
+            uint32_t w = 0;
 #pragma unroll
-          for (int j = 0; j < 4; ++j) w[j] = *reinterpret_cast<const uint16_t*>(vrow + j * RB + vg);
-          b0 = make_uint2(pair(i8_f32<0>(w[0]), i8_f32<0>(w[1])), pair(i8_f32<0>(w[2]), i8_f32<0>(w[3])));
-          b1 = make_uint2(pair(i8_f32<1>(w[0]), i8_f32<1>(w[1])), pair(i8_f32<1>(w[2]), i8_f32<1>(w[3])));
+            for (int j = 0; j < 4; ++j) w |= uint32_t(*reinterpret_cast<const uint8_t*>(vrow + j * RB + vg)) << (8 * j);
+            // Nibble n of a half as fp16 1024 + n (bits 0x6400 | n), then
+            // - 1032: n - 8, exactly.
+            const uint32_t p01 = __builtin_amdgcn_perm(0u, w, 0x0C010C00u), p23 = __builtin_amdgcn_perm(0u, w, 0x0C030C02u);
+            const h2 k1032 = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+            auto nib = [&](uint32_t x) { return __builtin_bit_cast(h2, (x & 0x000F000Fu) | 0x64006400u) + k1032; };
+            v01[0] = nib(p01), v23[0] = nib(p23);
+            v01[1] = nib(p01 >> 4), v23[1] = nib(p23 >> 4);
+          }
+#pragma unroll
+          for (int t = 0; t < 2; ++t) {
+            const h2 hi01 = v01[t] * d01, hi23 = v23[t] * d23;
+            const h2 lo01 = __builtin_elementwise_fma(v01[t], d01, -hi01);
+            const h2 lo23 = __builtin_elementwise_fma(v23[t], d23, -hi23);
+            b[t] = make_uint4(__builtin_bit_cast(uint32_t, hi01), __builtin_bit_cast(uint32_t, hi23),
+                              __builtin_bit_cast(uint32_t, lo01), __builtin_bit_cast(uint32_t, lo23));
+          }
+        };
+        // Two groups at a time: their four A_hi MFMAs, then the four A_lo
+        // ones, so an accumulator's second MFMA comes four after its first.
+        Unroll<0, NK / 2>::run([&](auto pc) {
+          constexpr int G0 = 2 * decltype(pc)::value;
+          uint4 b0[2], b1[2];
+          bgroup(std::integral_constant<int, G0>{}, b0);
+          bgroup(std::integral_constant<int, G0 + 1>{}, b1);
+          o8[G0][0] = mfma16_f16(a_hi, b0[0], o8[G0][0]);
+          o8[G0][1] = mfma16_f16(a_hi, b0[1], o8[G0][1]);
+          o8[G0 + 1][0] = mfma16_f16(a_hi, b1[0], o8[G0 + 1][0]);
+          o8[G0 + 1][1] = mfma16_f16(a_hi, b1[1], o8[G0 + 1][1]);
+          o8[G0][0] = mfma16_f16(a_lo, b0[0], o8[G0][0]);
+          o8[G0][1] = mfma16_f16(a_lo, b0[1], o8[G0][1]);
+          o8[G0 + 1][0] = mfma16_f16(a_lo, b1[0], o8[G0 + 1][0]);
+          o8[G0 + 1][1] = mfma16_f16(a_lo, b1[1], o8[G0 + 1][1]);
+        });
+      };
+      // The three-part bf16 form: A = p d split into three exact bf16
+      // parts, B = v exact in bf16.
+      auto pv_bf16 = [&](auto) {
+        if constexpr (kNib) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) pj[j] *= F::kBScale;  // exact; undoes B's factor 16 (Q5: 8)
         }
-        o8[G][0] = mfma16k16(ah, b0, o8[G][0]);
-        o8[G][1] = mfma16k16(ah, b1, o8[G][1]);
-        o8[G][0] = mfma16k16(am, b0, o8[G][0]);
-        o8[G][1] = mfma16k16(am, b1, o8[G][1]);
-        o8[G][0] = mfma16k16(al, b0, o8[G][0]);
-        o8[G][1] = mfma16k16(al, b1, o8[G][1]);
-      });
+        Unroll<0, NK>::run([&](auto gc) {
+          constexpr int G = decltype(gc)::value;
+          // Byte offset of group G in the lane's rows (swizzled by token quad).
+          const int vg = (kNib ? 16 : 32) * (G ^ kq);
+          float x[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j)  // p * d, one v_fma_mix_f32 each
+            x[j] = fmaf(pj[j], f16_bits_to_f32(dbits(j, gc)), 0.0f);
+          uint2 ah, am, al;
+          split3_bf16(x[0], x[1], ah.x, am.x, al.x);
+          split3_bf16(x[2], x[3], ah.y, am.y, al.y);
+          auto pair = [](uint32_t f0, uint32_t f1) { return __builtin_amdgcn_perm(f1, f0, 0x07060302u); };
+          uint2 b0, b1;
+          if constexpr (kNib) {
+            uint32_t w = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) w |= uint32_t(*reinterpret_cast<const uint8_t*>(vrow + j * RB + vg)) << (8 * j);
+            uint4 t;  // tokens 4 kq + j: low nibbles (tile 0), then high (tile 1)
+            if constexpr (F::kQ5) {
+              // Fifth bits of element hm (low nibble) and 16 + hm (high) of
+              // each token, from the group's qh words.
+              uint32_t lo4 = 0u, hi4 = 0u;
+#pragma unroll
+              for (int j = 0; j < 4; ++j) {
+                const uint32_t qh = *reinterpret_cast<const uint32_t*>(srow + j * F::kScaleRow + 4 * G) >> hm;
+                lo4 |= (qh & 1u) << j;
+                hi4 |= ((qh >> 16) & 1u) << j;
+              }
+              t = nib5_bf16(w, lo4, hi4);
+            } else {
+              t = nib8_bf16(w);
+            }
+            b0 = make_uint2(t.x, t.y);
+            b1 = make_uint2(t.z, t.w);
+          } else {
+            uint32_t w[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) w[j] = *reinterpret_cast<const uint16_t*>(vrow + j * RB + vg);
+            b0 = make_uint2(pair(i8_f32<0>(w[0]), i8_f32<0>(w[1])), pair(i8_f32<0>(w[2]), i8_f32<0>(w[3])));
+            b1 = make_uint2(pair(i8_f32<1>(w[0]), i8_f32<1>(w[1])), pair(i8_f32<1>(w[2]), i8_f32<1>(w[3])));
+          }
+          o8[G][0] = mfma16k16(ah, b0, o8[G][0]);
+          o8[G][1] = mfma16k16(ah, b1, o8[G][1]);
+          o8[G][0] = mfma16k16(am, b0, o8[G][0]);
+          o8[G][1] = mfma16k16(am, b1, o8[G][1]);
+          o8[G][0] = mfma16k16(al, b0, o8[G][0]);
+          o8[G][1] = mfma16k16(al, b1, o8[G][1]);
+          // As the fallback of the fp16 form, one group at a time: its
+          // register use then stays below the fp16 loop's.
+          if constexpr (kF16) __builtin_amdgcn_sched_barrier(0);
+        });
+      };
+      if constexpr (kF16 && !decltype(bf16_only)::value)
+        pv_f16(0);
+      else
+        pv_bf16(0);
+      return true;
+    };
+    // Items run in the first loop while every one takes the fp16 form: its
+    // accumulators then pass from item to item in place.  (A loop whose
+    // items may take either form merges two sets of MFMA results at its
+    // latch: the register allocator then copies every accumulator there, 64
+    // moves per item, and holds both sets.)  An item that needs the bf16
+    // form ends it, and that item and the partition's remaining ones run in
+    // the bf16 form.
+    int s = ns;
+    bool redo = false;
+    if constexpr (kF16) {
+      for (; s < S; ++s)
+        if (!v_item(s, std::false_type{}, false)) {
+          redo = true;
+          break;
+        }
+    }
+    for (; s < S; ++s) {
+      v_item(s, std::true_type{}, redo);
+      redo = false;
     }
     // Sum over the four token rows kq of head hm.
     lsum += __shfl_xor(lsum, 16);
@@ -1372,12 +1463,13 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
 #pragma unroll
         for (int g = 0; g < NK; ++g) {
           float* const row = &red[(wave * GC + h) * D + 32 * g];
+          // The weights carried 2^11 (exact).
           if constexpr (kNib) {
-            row[hm] = o8[g][0][i];
-            row[16 + hm] = o8[g][1][i];
-          } else {  // Q8_0: the weights carried 2^11 (exact)
+            row[hm] = o8[g][0][i] * (1.0f / kQPScale);
+            row[16 + hm] = o8[g][1][i] * (1.0f / kQPScale);
+          } else {
             *reinterpret_cast<float2*>(row + 2 * hm) =
-                make_float2(o8[g][0][i] * (1.0f / kQ8PScale), o8[g][1][i] * (1.0f / kQ8PScale));
+                make_float2(o8[g][0][i] * (1.0f / kQPScale), o8[g][1][i] * (1.0f / kQPScale));
           }
         }
       }

@@ -20,8 +20,9 @@ QUANT = orc.QUANT_TYPES
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 
 
-def _build(dt, hq, hkv, D, bs, ctx, start=None, nb=None, seed=1, mb=None):
-    """Fill oracle + device caches with every position of every sequence."""
+def _build(dt, hq, hkv, D, bs, ctx, start=None, nb=None, seed=1, mb=None, vmul=None):
+    """Fill oracle + device caches with every position of every sequence
+    (V of token i of the append scaled by vmul[i] when given)."""
     import torch
     from infer_train_amd.kv import PagedKvCache
 
@@ -39,6 +40,8 @@ def _build(dt, hq, hkv, D, bs, ctx, start=None, nb=None, seed=1, mb=None):
     src_dt = orc.F32 if dt in QUANT else dt
     k = kv_values(seed + 10, n * hkv * D, src_dt, outliers=dt in QUANT).reshape(n, hkv, D)
     v = kv_values(seed + 11, n * hkv * D, src_dt, outliers=dt in QUANT).reshape(n, hkv, D)
+    if vmul is not None:
+        v = (v * np.asarray(vmul, np.float32)[:n, None, None]).astype(np.float32)
     ref = orc.Cache(nb, bs, hkv, D, dt)
     ref.append(k, v, slots)
     dev = PagedKvCache(nb, bs, hkv, D, dt)
@@ -419,6 +422,29 @@ def test_nibble_decode_config5_heads(dt):
     for partition in (512, 1024):
         got, want = _run(dev, ref, tables, ctx, q, qdt, hq, partition=partition)
         assert_close_or_closer(got, want, exact, *TOL[dt], what=f"dt={dt} P={partition}")
+
+
+@pytest.mark.parametrize("dt", QUANT)
+@pytest.mark.parametrize("D", [128, 256])
+def test_quant_v_scale_ranges(dt, D):
+    """V scales of every range the decode distinguishes: runs of 37 tokens
+    whose V is scaled by 2^17 (Q8_0 scales above 512, nibble scales above
+    4096: those 16-token items take the three-part bf16 products), by 2^-12
+    (subnormal fp16 scales) or left at N(0, 1), so items of one wave mix
+    the ranges and an item's tokens may straddle two; fp32 tolerance against
+    the oracle."""
+    bs = 32 if D == 256 else 16
+    ctx = [700, 333, 1029]
+    n = sum(ctx)
+    run = (np.arange(n) // 37) % 3
+    vmul = np.where(run == 0, np.float32(2.0**17), np.where(run == 1, np.float32(2.0**-12), np.float32(1)))
+    hq, hkv = (24, 4) if D == 256 else (8, 2)
+    dev, ref, tables, ctx_a, q, qdt = _build(dt, hq, hkv, D, bs, ctx, seed=77, vmul=vmul)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
+    exact = lazy(lambda: exact_decode(ref, q, hq, tables, ctx_a, None, scale, with_mag=True))
+    for partition in (64, 512):
+        got, want = _run(dev, ref, tables, ctx_a, q, qdt, hq, partition=partition)
+        assert_close_or_closer(got, want, exact, *TOL[dt], what=f"dt={dt} D={D} P={partition}")
 
 
 def test_bf16_d256_and_group_sizes():
