@@ -1362,37 +1362,64 @@ def summarize_prefill_profile(d, args):
     print("\n".join(lines))
 
 
-def summarize_config5_profile(d, args):
-    """Summarise rocprofv3 CSVs of `bench.py --only-config5` runs: DIR/trace
-    (--kernel-trace --stats) and DIR/sq0, DIR/sq1 (--pmc, PREFILL_SQ) into
-    profiles/decode_split_config5.md (the Q8_0 split kernel, D 256)."""
+# rocprofv3 --pmc groups of the quantised decode profiles (eight SQ counters
+# per pass): the fp16 and bf16 MFMA forms are told apart by their MOPS.
+QUANT_SQ = [["SQ_WAVES", "SQ_INSTS_VALU", "SQ_INSTS_MFMA", "SQ_INSTS_LDS", "SQ_INSTS_SALU",
+             "SQ_LDS_BANK_CONFLICT", "SQ_LDS_IDX_ACTIVE", "SQ_WAIT_INST_ANY"],
+            ["SQ_VALU_MFMA_BUSY_CYCLES", "SQ_BUSY_CYCLES", "SQ_WAVE_CYCLES", "SQ_ACTIVE_INST_VALU",
+             "SQ_ACTIVE_INST_LDS", "SQ_INSTS_VALU_MFMA_MOPS_BF16", "SQ_INSTS_VALU_MFMA_MOPS_F16", "SQ_WAIT_ANY"]]
+
+# Quantised KV formats on the config-5 shape: (bench flag, dtype id in the
+# kernel's name, bytes per element with the scales, what the bytes are).
+QUANT_PROFILE = {
+    "q8_0": ("--only-config5", 8, 34.0 / 32.0, "the Q8_0 K/V pages of every context, qs and scales"),
+    "q4_0": ("--only-format q4_0", 2, 18.0 / 32.0, "the Q4_0 K/V pages of every context, nibbles and scales"),
+    "q4_1": ("--only-format q4_1", 3, 20.0 / 32.0, "the Q4_1 K/V pages of every context, nibbles, scales and mins"),
+    "q5_0": ("--only-format q5_0", 6, 22.0 / 32.0, "the Q5_0 K/V pages of every context, nibbles, high bits and scales"),
+    "q5_1": ("--only-format q5_1", 7, 24.0 / 32.0,
+             "the Q5_1 K/V pages of every context, nibbles, high bits, scales and mins"),
+}
+
+
+def summarize_quant_profile(d, args, fmt):
+    """Summarise rocprofv3 CSVs of `bench.py --only-config5` (fmt q8_0) or
+    `bench.py --only-format FMT` runs: DIR/trace (--kernel-trace --stats),
+    DIR/fetch and DIR/write (--pmc FETCH_SIZE / WRITE_SIZE with the copy
+    probe) and DIR/sq0, DIR/sq1 (--pmc, QUANT_SQ) into
+    profiles/decode_split_config5.md (Q8_0) or
+    profiles/decode_split_FMT_config5_shape.md."""
     import csv
 
     def rows(sub, name):
         return list(csv.DictReader(open(os.path.join(d, sub, "run_" + name + ".csv"))))
 
-    kname = "paged_decode_split<8, 256"  # Q8_0 (dtype id 8), head_dim 256
+    flag, dt_id, elem, what = QUANT_PROFILE[fmt]
+    name = fmt.upper()
+    kname = f"paged_decode_split<{dt_id}, 256"  # the format's dtype id, head_dim 256
     stats = [r for r in rows("trace", "kernel_stats") if "decode" in r["Name"] or "append" in r["Name"]]
     trace = [r for r in rows("trace", "kernel_trace") if kname in r["Kernel_Name"]]
     durs = np.array([(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in trace])
     import infer_train_amd as it
     from infer_train_amd.kv import decode_partition
 
-    rng = np.random.default_rng(5)  # the config-5 contexts, as bench_config5
+    rng = np.random.default_rng(5)  # the config-5 contexts, as bench_config5 and bench_q4
     ctx = rng.integers(32768, 131073, 16)
-    kv_bytes = float(ctx.astype(np.int64).sum()) * 4 * 2 * 256 * 34 / 32
-    part = decode_partition(it.Q8_0, 256, 32, 24, 4, ctx, None, 256)
-    cmd = "python3 bench.py --only-config5 --steps {s} --warmup {w} --copy-probe".format(s=args.steps, w=args.warmup)
-    lines = ["# paged_decode_split (Q8_0, D 256) -- config 5 (batch 16, ctx U[32768, 131072], "
+    kv_bytes = float(ctx.astype(np.int64).sum()) * 4 * 2 * 256 * elem
+    dt = {"q8_0": it.Q8_0, "q4_0": it.Q4_0, "q4_1": it.Q4_1, "q5_0": it.Q5_0, "q5_1": it.Q5_1}[fmt]
+    part = decode_partition(dt, 256, 32, 24, 4, ctx.astype(np.int32), None, 256)  # MI355X: 256 CUs
+    cmd = f"python3 bench.py {flag} --steps {args.steps} --warmup {args.warmup} --copy-probe"
+    summ = (f"python3 bench.py --summarize-config5-profile OUT" if fmt == "q8_0" else
+            f"python3 bench.py --summarize-format-profile OUT --only-format {fmt}")
+    lines = [f"# paged_decode_split ({name}, D 256) -- config-5 shape (batch 16, ctx U[32768, 131072], "
              f"Hq 24 / Hkv 4, {part}-token partitions)", "",
              "Commands (from the repository root on the GPU box; `cd /tmp && export TMPDIR=/tmp` first):", "",
              "```",
              f"rocprofv3 --kernel-trace --stats --output-format csv -d OUT/trace -o run -- {cmd}",
              f"rocprofv3 --pmc FETCH_SIZE --output-format csv -d OUT/fetch -o run -- {cmd}",
              f"rocprofv3 --pmc WRITE_SIZE --output-format csv -d OUT/write -o run -- {cmd}"]
-    for i, grp in enumerate(PREFILL_SQ):
+    for i, grp in enumerate(QUANT_SQ):
         lines.append(f"rocprofv3 --pmc {' '.join(grp)} --output-format csv -d OUT/sq{i} -o run -- {cmd}")
-    lines += [f"python3 bench.py --summarize-config5-profile OUT --steps {args.steps} --warmup {args.warmup}", "```",
+    lines += [f"{summ} --steps {args.steps} --warmup {args.warmup}", "```",
               "", "## rocprofv3 --stats (kernel_stats.csv rows of the path's kernels)", "",
               "| Name | Calls | AverageNs | MinNs | MaxNs |", "|---|---|---|---|---|"]
     for r in stats:
@@ -1401,9 +1428,9 @@ def summarize_config5_profile(d, args):
     lines += ["", f"Split kernel, kernel trace: {durs.size} dispatches, mean {durs.mean():.2f} us, median "
                   f"{np.median(durs):.2f} us -> {gbs:.0f} GB/s of KV bytes ({kv_bytes:.0f} per launch) = "
                   f"{100 * gbs / HBM_PEAK_GBS:.1f}% of {HBM_PEAK_GBS:.0f} GB/s."]
-    lines += _traffic_lines(d, kname, kv_bytes, "the Q8_0 K/V pages of every context, qs and scales")
+    lines += _traffic_lines(d, kname, kv_bytes, what)
     med = {}
-    for i in range(len(PREFILL_SQ)):
+    for i in range(len(QUANT_SQ)):
         sub = f"sq{i}"
         if not os.path.isdir(os.path.join(d, sub)):
             continue
@@ -1417,7 +1444,7 @@ def summarize_config5_profile(d, args):
         waves = med.get("SQ_WAVES", 1.0)
         lines += ["", "## Counters per launch (rocprofv3 --pmc, median over dispatches)", "",
                   "| Counter | Value | Per wave |", "|---|---|---|"]
-        for grp in PREFILL_SQ:
+        for grp in QUANT_SQ:
             for k in grp:
                 if k in med:
                     lines.append(f"| {k} | {med[k]:.0f} | {med[k] / waves:.1f} |")
@@ -1426,11 +1453,22 @@ def summarize_config5_profile(d, args):
             # the MFMA busy count sums all 1024 SIMDs.
             frac = med["SQ_VALU_MFMA_BUSY_CYCLES"] / (med["SQ_BUSY_CYCLES"] * 32)
             lines += ["", f"MFMA pipe busy {100 * frac:.1f}% of SIMD cycles (SQ_VALU_MFMA_BUSY_CYCLES over "
-                          "SQ_BUSY_CYCLES x 32 SIMDs per shader engine). The kernel is not HBM-bound (traffic "
-                          "near 1.0x, below 70% of peak): its time goes to VALU and MFMA issue for the fp32-exact "
-                          "Q8_0 products, which run on MFMA as three exact bf16 passes."]
-    open(os.path.join(ROOT, "profiles", "decode_split_config5.md"), "w").write("\n".join(lines) + "\n")
+                          "SQ_BUSY_CYCLES x 32 SIMDs per shader engine)."]
+        if "SQ_ACTIVE_INST_VALU" in med and "SQ_BUSY_CYCLES" in med:
+            # SQ_ACTIVE_INST_VALU counts per-wave issue cycles summed over all
+            # waves (4 cycles per wave64 VALU instruction on a 16-lane SIMD).
+            vfrac = med["SQ_ACTIVE_INST_VALU"] * 4 / (med["SQ_BUSY_CYCLES"] * 32)
+            lines += [f"VALU issue {100 * vfrac:.1f}% of SIMD cycles (SQ_ACTIVE_INST_VALU x 4 cycles per wave64 "
+                      "instruction over SQ_BUSY_CYCLES x 32). Traffic near 1.0x of the algorithmic bytes below 70% "
+                      "of HBM peak: the kernel's time goes to the vector work of dequantising in registers (VALU) "
+                      "and the exact MFMA products, not to HBM."]
+    out = "decode_split_config5.md" if fmt == "q8_0" else f"decode_split_{fmt}_config5_shape.md"
+    open(os.path.join(ROOT, "profiles", out), "w").write("\n".join(lines) + "\n")
     print("\n".join(lines))
+
+
+def summarize_config5_profile(d, args):
+    summarize_quant_profile(d, args, "q8_0")
 
 
 # (source file, kernel symbol substring, what it is)
@@ -1557,6 +1595,9 @@ def main():
                     help="summarise rocprofv3 CSVs of --only-config5 runs into profiles/decode_split_config5.md")
     ap.add_argument("--only-format", choices=["q4_0", "q4_1", "q5_0", "q5_1"],
                     help="only the decode of this KV format on the config-5 shape; prints one JSON line")
+    ap.add_argument("--summarize-format-profile", metavar="DIR",
+                    help="with --only-format: summarise rocprofv3 CSVs of --only-format runs into "
+                         "profiles/decode_split_FMT_config5_shape.md")
     ap.add_argument("--only-prefill", action="store_true",
                     help="run only config 3 (chunk append + causal prefill) (for rocprofv3 runs)")
     ap.add_argument("--summarize-prefill-profile", metavar="DIR",
@@ -1583,6 +1624,9 @@ def main():
         return
     if args.summarize_config5_profile:
         summarize_config5_profile(args.summarize_config5_profile, args)
+        return
+    if args.summarize_format_profile:
+        summarize_quant_profile(args.summarize_format_profile, args, args.only_format)
         return
     if args.summarize_movers_profile:
         summarize_movers_profile(args.summarize_movers_profile, args)

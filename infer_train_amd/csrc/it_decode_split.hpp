@@ -370,6 +370,7 @@ __device__ __forceinline__ v4f mfma16k16(uint2 a, uint2 b, v4f c) {
 }
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef unsigned short us2 __attribute__((ext_vector_type(2)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 __device__ __forceinline__ v4f mfma16_f16(uint4 a, uint4 b, v4f c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, a), __builtin_bit_cast(v8h, b), c, 0, 0, 0);
@@ -473,6 +474,9 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
   constexpr int RB = F::kRow, GB = F::kGroup, SLOT = F::kSlot, NI = F::kDma, NL = F::kLoads;
   constexpr int PQ = F::kPieces, NQ = F::kQRegs, DPV = F::kDpv;
   constexpr bool k16 = F::k16, kQ = F::kQuant, kNib = F::kNib, kOff = F::kOff;
+  // Formats whose products run as exact fp16 MFMAs (the others as three
+  // exact bf16 passes).
+  constexpr bool kF16 = F::kQ8 || DT == IT_Q4_0 || DT == IT_Q4_1;
   constexpr int NT = 64 * NW;  // threads
   static_assert(GC >= 1 && GC <= 8, "1..8 heads per workgroup");
   static_assert(NW == 2 || NW == 4, "2 or 4 waves");
@@ -617,12 +621,14 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
   // dims 32 ks + 8 kh .. + 8; Q4_0 dims 32 ks + 4 kh .. + 4 and 32 ks + 16 +
   // 4 kh .. + 4 (the low and high nibbles of bytes 4 kh .. + 4 of the group).
   constexpr int NK = kQ ? D / 32 : 1;  // 32-groups (MFMA k-steps) per row
-  uint4 qa[F::kQ8 ? 1 : 3][NK];
-  // Q8_0: q of head h scaled by 2^E_h (so that max |q| lies in [2^14, 2^15))
-  // as hi + lo fp16 parts, the A operand of v_mfma_f32_16x16x32_f16; the
-  // scores are scaled back by 2^-E_h (exact).  sE[i]: 2^-E of head
-  // 4 (lane / 16) + i, the heads this lane's scores belong to.
-  uint4 qf[F::kQ8 ? 2 : 1][NK];
+  uint4 qa[kF16 ? 1 : 3][NK];
+  // fp16 forms: q of head h scaled by 2^E_h (so that max |q| lies in
+  // [2^14, 2^15)) as hi + lo fp16 parts, the A operand of
+  // v_mfma_f32_16x16x32_f16; the scores are scaled back by 2^-E_h (exact).
+  // Q4_0 / Q4_1 take the high-nibble dims' q divided by 16, against K
+  // values 16 (n - 8).  sE[i]: 2^-E of head 4 (lane / 16) + i, the heads
+  // this lane's scores belong to.
+  uint4 qf[kF16 ? 2 : 1][NK];
   float sE[4] = {1.0f, 1.0f, 1.0f, 1.0f};
   // Q4_1: sum of q over each 32-group, the A operand of the offset-term MFMA
   // (v_mfma_f32_16x16x16_bf16, k = group): lane (kh, h) holds groups
@@ -648,21 +654,25 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
     const float* qp = static_cast<const float*>(a.q) + (int64_t(b) * a.n_heads + head0 + (hq < GC ? hq : 0)) * D +
                       (kNib ? 4 : 8) * qr_row;
     float qsum[NK];
-    if constexpr (F::kQ8) {
+    int E = 0;
+    if constexpr (kF16) {
       float4 x0[NK], x1[NK];
       float mx = 0.0f;
 #pragma unroll
       for (int ks = 0; ks < NK; ++ks) {
         x0[ks] = *reinterpret_cast<const float4*>(qp + 32 * ks);
-        x1[ks] = *reinterpret_cast<const float4*>(qp + 32 * ks + 4);
+        x1[ks] = *reinterpret_cast<const float4*>(qp + 32 * ks + (kNib ? 16 : 4));
         if (hq >= GC) x0[ks] = x1[ks] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if constexpr (kNib) {  // exact
+          x1[ks].x *= 0.0625f, x1[ks].y *= 0.0625f, x1[ks].z *= 0.0625f, x1[ks].w *= 0.0625f;
+        }
         mx = fmaxf(mx, fmaxf(fmaxf(fabsf(x0[ks].x), fabsf(x0[ks].y)), fmaxf(fabsf(x0[ks].z), fabsf(x0[ks].w))));
         mx = fmaxf(mx, fmaxf(fmaxf(fabsf(x1[ks].x), fabsf(x1[ks].y)), fmaxf(fabsf(x1[ks].z), fabsf(x1[ks].w))));
       }
       mx = fmaxf(mx, __shfl_xor(mx, 16));  // the four lanes of head hq
       mx = fmaxf(mx, __shfl_xor(mx, 32));
       // mx in [2^(e-1), 2^e): E = 15 - e; an all-zero (or non-finite) q keeps E = 0.
-      const int E = (mx > 0.0f && mx <= FLT_MAX) ? 15 - __builtin_amdgcn_frexp_expf(mx) : 0;
+      E = (mx > 0.0f && mx <= FLT_MAX) ? 15 - __builtin_amdgcn_frexp_expf(mx) : 0;
 #pragma unroll
       for (int ks = 0; ks < NK; ++ks) {
         const float x[8] = {x0[ks].x, x0[ks].y, x0[ks].z, x0[ks].w, x1[ks].x, x1[ks].y, x1[ks].z, x1[ks].w};
@@ -690,12 +700,12 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
           asm volatile("" : "+v"(qf[p][ks].x), "+v"(qf[p][ks].y), "+v"(qf[p][ks].z), "+v"(qf[p][ks].w));
     }
 #pragma unroll
-    for (int ks = 0; ks < NK && !F::kQ8; ++ks) {
+    for (int ks = 0; ks < NK && (kOff || !kF16); ++ks) {
       float4 x0 = *reinterpret_cast<const float4*>(qp + 32 * ks);
       float4 x1 = *reinterpret_cast<const float4*>(qp + 32 * ks + (kNib ? 16 : 4));
       if (hq >= GC) x0 = x1 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
       if constexpr (kOff) qsum[ks] = ((x0.x + x0.y) + (x0.z + x0.w)) + ((x1.x + x1.y) + (x1.z + x1.w));
-      if constexpr (!F::kQ8) {
+      if constexpr (!kF16) {
         split3_bf16(x0.x, x0.y, qa[0][ks].x, qa[1][ks].x, qa[2][ks].x);
         split3_bf16(x0.z, x0.w, qa[0][ks].y, qa[1][ks].y, qa[2][ks].y);
         split3_bf16(x1.x, x1.y, qa[0][ks].z, qa[1][ks].z, qa[2][ks].z);
@@ -710,7 +720,7 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
         qsum[ks] += __shfl_xor(qsum[ks], 32);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          if (ks == 4 * qr_row + j) qg[j] = qsum[ks];
+          if (ks == 4 * qr_row + j) qg[j] = kF16 ? __builtin_ldexpf(qsum[ks], E) : qsum[ks];  // the scores' 2^E
       }
       uint2 p0, p1, p2;
       split3_bf16(qg[0], qg[1], p0.x, p1.x, p2.x);
@@ -718,7 +728,7 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
       qs_a[0] = p0, qs_a[1] = p1, qs_a[2] = p2;
     }
 #pragma unroll
-    for (int p = 0; p < (F::kQ8 ? 0 : 3); ++p)
+    for (int p = 0; p < (kF16 ? 0 : 3); ++p)
 #pragma unroll
       for (int ks = 0; ks < NK; ++ks)
         asm volatile("" : "+v"(qa[p][ks].x), "+v"(qa[p][ks].y), "+v"(qa[p][ks].z), "+v"(qa[p][ks].w));
@@ -867,6 +877,10 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
   const int h_a = ((qr_row & 1) << 1) | (qr_row >> 1);
   float m_a = -INFINITY, m_b = -INFINITY;
   float m_q[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};  // Q8_0: heads 4 qr_row + i
+  // 0x64006400 held in a VGPR, so that (x & mask) | k6400 is one
+  // v_and_or_b32 (a VOP3 reads at most one scalar operand here).
+  uint32_t k6400 = 0x64006400u;
+  asm volatile("" : "+v"(k6400));
   for (int s = 0; s < ns; ++s) {
     wait_item(s);
     age_fair(s);
@@ -907,13 +921,28 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
       }
       v4f acc[NK];
       uint4 kb[NK];
-      if constexpr (F::kQ8) {
-        // fp16: q hi / lo parts against the exact fp16 K bytes, the two
+      if constexpr (kF16) {
+        // fp16: q hi / lo parts against the exact fp16 K values, the two
         // MFMAs of a group a group apart.
         Unroll<0, NK + 1>::run([&](auto kc) {
           constexpr int k = decltype(kc)::value;
           if constexpr (k < NK) {
-            kb[k] = i8x8_f16(kr[k]);
+            if constexpr (F::kQ8) {
+              kb[k] = i8x8_f16(kr[k]);
+            } else {
+              // Bytes 0, 1 and 2, 3 into 16-bit halves; low nibbles n as
+              // 0x6400 | n - 1032 = n - 8, high ones as 0x6400 | 16 n - 1152
+              // = 16 (n - 8) (q of their dims carries 1/16), exactly.
+              const uint32_t w = kr[k].x;
+              const uint32_t p01 = __builtin_amdgcn_perm(0u, w, 0x0C010C00u), p23 = __builtin_amdgcn_perm(0u, w, 0x0C030C02u);
+              const h2 k1032 = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+              const h2 k1152 = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+              auto nib = [&](uint32_t x, uint32_t mask, h2 bias) {
+                return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, (x & mask) | k6400) + bias);
+              };
+              kb[k] = make_uint4(nib(p01, 0x000F000Fu, k1032), nib(p23, 0x000F000Fu, k1032),
+                                 nib(p01, 0x00F000F0u, k1152), nib(p23, 0x00F000F0u, k1152));
+            }
             acc[k] = mfma16_f16(qf[0][k], kb[k], v4f{0.0f, 0.0f, 0.0f, 0.0f});
           }
           if constexpr (k >= 1) acc[k - 1] = mfma16_f16(qf[1][k - 1], kb[k - 1], acc[k - 1]);
@@ -933,7 +962,7 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
       v4f sv = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int ks = 0; ks < NK; ++ks) {
-        const float d = f16_bits_to_f32(dsc[ks]) * F::kBScale;  // exact
+        const float d = f16_bits_to_f32(dsc[ks]) * (kF16 ? 1.0f : F::kBScale);  // exact
 #pragma unroll
         for (int i = 0; i < 4; ++i) sv[i] = fmaf(d, acc[ks][i], sv[i]);
       }
@@ -1093,8 +1122,6 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
     }
     const bool none_h = m_h == -INFINITY;  // every key skipped, or a padding row
     const float* const sc_h = sc + (hm < GC ? hm : 0) * SP + 4 * kq;
-    // Formats with the fp16 form of P.V (below).
-    constexpr bool kF16 = F::kQ8 || DT == IT_Q4_0 || DT == IT_Q4_1;
     // One item of the partition, in the bf16 form if bf16_only; else in the
     // fp16 form, or, when that does not fit its scales, not at all: it then
     // returns false, having changed nothing but the item's wait and issue.
@@ -1154,10 +1181,10 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
         else return G & 1 ? dw[j][G / 2] >> 16 : dw[j][G / 2] & 0xFFFFu;
       };
       // P.V in fp16 (Q8_0, Q4_0, Q4_1), when every scale of the item is
-      // small enough that |d v| <= 65504 (d below 512 for Q8_0's |v| <= 128,
-      // below 4096 for the nibbles' |v| <= 8; other items take the bf16 form
-      // below): B = d v is exact as hi + lo fp16 parts (d has 11
-      // significant bits and v at most 8), and A = p 2^11 as two fp16 parts
+      // small enough that |d v| <= 65504 (d below 512: |v| <= 128 for Q8_0's
+      // q and for the nibbles' tile 1, which holds 16 (n - 8); other items
+      // take the bf16 form below): B = d v is exact as hi + lo fp16 parts
+      // (d has 11 significant bits and v at most 8), and A = p 2^11 as two fp16 parts
       // made once per item (p <= 1: every weight above 2^-13 keeps 22 bits,
       // smaller ones an absolute error below 2^-36).  Each tile takes two
       // v_mfma_f32_16x16x32_f16 whose k runs over (token, B part):
@@ -1170,7 +1197,6 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
       // above.)
       bool f16_item = false;
       if constexpr (kF16) {
-        typedef unsigned short us2 __attribute__((ext_vector_type(2)));
         us2 m = {0, 0};
 #pragma unroll
         for (int j = 0; j < 4; ++j)
@@ -1180,7 +1206,7 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
         // |d| bits order as the values (Q8_0's and Q4_1's d are >= 0, Q4_0's
         // = max / -8 of either sign); Q4_1's high halves are the offsets m,
         // not scales.
-        constexpr unsigned kLim = F::kQ8 ? 0x6000u : 0x6C00u;  // 512, 4096
+        constexpr unsigned kLim = 0x6000u;  // 512: |v| <= 128 (Q8_0's q, the nibbles' 16 (n - 8))
         const bool big = m[0] >= kLim || (!kOff && m[1] >= kLim);
         f16_item = __builtin_amdgcn_ballot_w64(big) == 0;  // uniform
       }
@@ -1241,16 +1267,24 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
             v23[1] = __builtin_bit_cast(h2, i8pair_f16<1, 1>(w[2], w[3]));
           } else {
             const int vg = 16 * (G ^ kq);
-            uint32_t w = 0;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) w |= uint32_t(*reinterpret_cast<const uint8_t*>(vrow + j * RB + vg)) << (8 * j);
-            // Nibble n of a half as fp16 1024 + n (bits 0x6400 | n), then
-            // - 1032: n - 8, exactly.
-            const uint32_t p01 = __builtin_amdgcn_perm(0u, w, 0x0C010C00u), p23 = __builtin_amdgcn_perm(0u, w, 0x0C030C02u);
+            // The group's byte of tokens (0, 1) and (2, 3), one per 16-bit
+            // half (ds_read_u8_d16 / _d16_hi: no packing instructions).
+            us2 t01, t23;
+            t01[0] = *reinterpret_cast<const uint8_t*>(vrow + vg);
+            t01[1] = *reinterpret_cast<const uint8_t*>(vrow + RB + vg);
+            t23[0] = *reinterpret_cast<const uint8_t*>(vrow + 2 * RB + vg);
+            t23[1] = *reinterpret_cast<const uint8_t*>(vrow + 3 * RB + vg);
+            const uint32_t p01 = __builtin_bit_cast(uint32_t, t01), p23 = __builtin_bit_cast(uint32_t, t23);
+            // Low nibble n as the fp16 bits 0x6400 | n = 1024 + n, high
+            // nibble as 0x6400 | 16 n = 1024 + 16 n (one v_and_or each:
+            // the 0x6400 word sits in a VGPR); then - 1032 and - 1152:
+            // n - 8 and 16 (n - 8), exactly.  Tile 1 thus accumulates 16
+            // times its values, undone where the partials are stored.
             const h2 k1032 = {(_Float16)-1032.0f, (_Float16)-1032.0f};
-            auto nib = [&](uint32_t x) { return __builtin_bit_cast(h2, (x & 0x000F000Fu) | 0x64006400u) + k1032; };
-            v01[0] = nib(p01), v23[0] = nib(p23);
-            v01[1] = nib(p01 >> 4), v23[1] = nib(p23 >> 4);
+            const h2 k1152 = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+            auto nib = [&](uint32_t x, uint32_t mask) { return __builtin_bit_cast(h2, (x & mask) | k6400); };
+            v01[0] = nib(p01, 0x000F000Fu) + k1032, v23[0] = nib(p23, 0x000F000Fu) + k1032;
+            v01[1] = nib(p01, 0x00F000F0u) + k1152, v23[1] = nib(p23, 0x00F000F0u) + k1152;
           }
 #pragma unroll
           for (int t = 0; t < 2; ++t) {
@@ -1281,9 +1315,16 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
       // The three-part bf16 form: A = p d split into three exact bf16
       // parts, B = v exact in bf16.
       auto pv_bf16 = [&](auto) {
+        // B holds 16 (n - 8) (Q5: 8 (q - 16)); A = p d / 16 (/ 8) undoes the
+        // factor, except in tile 1 of the formats with an fp16 form, whose
+        // accumulators carry 16 times their values (see that form).
+        constexpr bool kT1 = kF16 && kNib;
+        float pt1[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) pt1[j] = pj[j];
         if constexpr (kNib) {
 #pragma unroll
-          for (int j = 0; j < 4; ++j) pj[j] *= F::kBScale;  // exact; undoes B's factor 16 (Q5: 8)
+          for (int j = 0; j < 4; ++j) pj[j] *= F::kBScale;  // exact
         }
         Unroll<0, NK>::run([&](auto gc) {
           constexpr int G = decltype(gc)::value;
@@ -1296,6 +1337,14 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
           uint2 ah, am, al;
           split3_bf16(x[0], x[1], ah.x, am.x, al.x);
           split3_bf16(x[2], x[3], ah.y, am.y, al.y);
+          uint2 th = ah, tm = am, tl = al;  // tile 1's A
+          if constexpr (kT1) {
+            float y[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) y[j] = fmaf(pt1[j], f16_bits_to_f32(dbits(j, gc)), 0.0f);
+            split3_bf16(y[0], y[1], th.x, tm.x, tl.x);
+            split3_bf16(y[2], y[3], th.y, tm.y, tl.y);
+          }
           auto pair = [](uint32_t f0, uint32_t f1) { return __builtin_amdgcn_perm(f1, f0, 0x07060302u); };
           uint2 b0, b1;
           if constexpr (kNib) {
@@ -1327,11 +1376,11 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
             b1 = make_uint2(pair(i8_f32<1>(w[0]), i8_f32<1>(w[1])), pair(i8_f32<1>(w[2]), i8_f32<1>(w[3])));
           }
           o8[G][0] = mfma16k16(ah, b0, o8[G][0]);
-          o8[G][1] = mfma16k16(ah, b1, o8[G][1]);
+          o8[G][1] = mfma16k16(th, b1, o8[G][1]);
           o8[G][0] = mfma16k16(am, b0, o8[G][0]);
-          o8[G][1] = mfma16k16(am, b1, o8[G][1]);
+          o8[G][1] = mfma16k16(tm, b1, o8[G][1]);
           o8[G][0] = mfma16k16(al, b0, o8[G][0]);
-          o8[G][1] = mfma16k16(al, b1, o8[G][1]);
+          o8[G][1] = mfma16k16(tl, b1, o8[G][1]);
           // As the fallback of the fp16 form, one group at a time: its
           // register use then stays below the fp16 loop's.
           if constexpr (kF16) __builtin_amdgcn_sched_barrier(0);
@@ -1465,8 +1514,10 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
           float* const row = &red[(wave * GC + h) * D + 32 * g];
           // The weights carried 2^11 (exact).
           if constexpr (kNib) {
+            // Tile 1 of Q4_0 / Q4_1 carries a further 16 (exact).
+            constexpr float kS1 = (DT == IT_Q4_0 || DT == IT_Q4_1) ? 1.0f / (16.0f * kQPScale) : 1.0f / kQPScale;
             row[hm] = o8[g][0][i] * (1.0f / kQPScale);
-            row[16 + hm] = o8[g][1][i] * (1.0f / kQPScale);
+            row[16 + hm] = o8[g][1][i] * kS1;
           } else {
             *reinterpret_cast<float2*>(row + 2 * hm) =
                 make_float2(o8[g][0][i] * (1.0f / kQPScale), o8[g][1][i] * (1.0f / kQPScale));
