@@ -476,7 +476,10 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
   constexpr bool k16 = F::k16, kQ = F::kQuant, kNib = F::kNib, kOff = F::kOff;
   // Formats whose products run as exact fp16 MFMAs (the others as three
   // exact bf16 passes).
-  constexpr bool kF16 = F::kQ8 || DT == IT_Q4_0 || DT == IT_Q4_1;
+  constexpr bool kF16 = true;
+  // Q4_0 / Q4_1: the high nibbles enter as 16 (n - 8) (no shift), their q
+  // (QK) and their tile's weights (P.V) carrying the 1/16.
+  constexpr bool kHi16 = DT == IT_Q4_0 || DT == IT_Q4_1;
   constexpr int NT = 64 * NW;  // threads
   static_assert(GC >= 1 && GC <= 8, "1..8 heads per workgroup");
   static_assert(NW == 2 || NW == 4, "2 or 4 waves");
@@ -663,7 +666,7 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
         x0[ks] = *reinterpret_cast<const float4*>(qp + 32 * ks);
         x1[ks] = *reinterpret_cast<const float4*>(qp + 32 * ks + (kNib ? 16 : 4));
         if (hq >= GC) x0[ks] = x1[ks] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if constexpr (kNib) {  // exact
+        if constexpr (kHi16) {  // exact
           x1[ks].x *= 0.0625f, x1[ks].y *= 0.0625f, x1[ks].z *= 0.0625f, x1[ks].w *= 0.0625f;
         }
         mx = fmaxf(mx, fmaxf(fmaxf(fabsf(x0[ks].x), fabsf(x0[ks].y)), fmaxf(fabsf(x0[ks].z), fabsf(x0[ks].w))));
@@ -675,7 +678,11 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
       E = (mx > 0.0f && mx <= FLT_MAX) ? 15 - __builtin_amdgcn_frexp_expf(mx) : 0;
 #pragma unroll
       for (int ks = 0; ks < NK; ++ks) {
-        const float x[8] = {x0[ks].x, x0[ks].y, x0[ks].z, x0[ks].w, x1[ks].x, x1[ks].y, x1[ks].z, x1[ks].w};
+        // k order: Q5 interleaves the two nibbles of each byte (elements
+        // e, e + 16), the others take the four x0 values, then x1's.
+        const float x[8] = {x0[ks].x, F::kQ5 ? x1[ks].x : x0[ks].y, F::kQ5 ? x0[ks].y : x0[ks].z,
+                            F::kQ5 ? x1[ks].y : x0[ks].w, F::kQ5 ? x0[ks].z : x1[ks].x,
+                            F::kQ5 ? x1[ks].z : x1[ks].y, F::kQ5 ? x0[ks].w : x1[ks].z, x1[ks].w};
         uint32_t hw[4], lw[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -881,6 +888,10 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
   // v_and_or_b32 (a VOP3 reads at most one scalar operand here).
   uint32_t k6400 = 0x64006400u;
   asm volatile("" : "+v"(k6400));
+  // Q5 QK: qh rotations that bring element 4 kh + i's fifth bit to bit 4.
+  uint32_t rot5k[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) rot5k[i] = uint32_t(4 * qr_row + i - 4) & 31u;
   for (int s = 0; s < ns; ++s) {
     wait_item(s);
     age_fair(s);
@@ -899,12 +910,11 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
 #pragma unroll
       for (int ks = 0; ks < NK; ++ks)
         dsc[ks] = *reinterpret_cast<const uint16_t*>(kside + F::kMetaOff + F::kMetaStride * ks);
-      // Q5: the fifth bits of the lane's eight values of group ks, bits
-      // 4 kh .. + 4 (low nibbles) and 16 + 4 kh .. + 4 (high) of qh.
+      // Q5: the qh word of group ks (bit e: element e's fifth bit).
       uint32_t qh5[F::kQ5 ? NK : 1];
       if constexpr (F::kQ5) {
 #pragma unroll
-        for (int ks = 0; ks < NK; ++ks) qh5[ks] = *reinterpret_cast<const uint32_t*>(kside + 4 * ks) >> (4 * qr_row);
+        for (int ks = 0; ks < NK; ++ks) qh5[ks] = *reinterpret_cast<const uint32_t*>(kside + 4 * ks);
       }
       // All K reads first; then the three passes of each group are software
       // pipelined across groups, so that no MFMA waits for the one before it.
@@ -929,6 +939,22 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
           if constexpr (k < NK) {
             if constexpr (F::kQ8) {
               kb[k] = i8x8_f16(kr[k]);
+            } else if constexpr (F::kQ5) {
+              // Pair i: elements e = 4 kh + i and e + 16, the two nibbles of
+              // byte i (q holds the same order), values n + 16 b - 16 as the
+              // fp16 bits 0x6400 | n | b << 4 (= 1024 + n + 16 b) - 1040,
+              // exactly.  qh rotated right by e - 4 puts e's fifth bit on
+              // bit 4 and e + 16's on bit 20.
+              const uint32_t w = kr[k].x, w4 = w >> 4, qh = qh5[k];
+              const h2 k1040 = {(_Float16)-1040.0f, (_Float16)-1040.0f};
+              auto q5 = [&](int i) {
+                // byte i of w (low nibble) and of w >> 4 (high nibble) into the halves
+                uint32_t nibw = (__builtin_amdgcn_perm(w4, w, 0x0C040C00u + 0x00010001u * i) & 0x000F000Fu) | k6400;
+                asm volatile("" : "+v"(nibw));  // two v_and_or, not and, and, or3
+                const uint32_t z = __builtin_amdgcn_alignbit(qh, qh, rot5k[i]);
+                return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, (z & 0x00100010u) | nibw) + k1040);
+              };
+              kb[k] = make_uint4(q5(0), q5(1), q5(2), q5(3));
             } else {
               // Bytes 0, 1 and 2, 3 into 16-bit halves; low nibbles n as
               // 0x6400 | n - 1032 = n - 8, high ones as 0x6400 | 16 n - 1152
@@ -962,7 +988,7 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
       v4f sv = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int ks = 0; ks < NK; ++ks) {
-        const float d = f16_bits_to_f32(dsc[ks]) * (kF16 ? 1.0f : F::kBScale);  // exact
+        const float d = f16_bits_to_f32(dsc[ks]);
 #pragma unroll
         for (int i = 0; i < 4; ++i) sv[i] = fmaf(d, acc[ks][i], sv[i]);
       }
@@ -1152,32 +1178,29 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
       for (int j = 0; j < 4; ++j)
         pj[j] = (tb + 4 * kq + j < nt && !none_h) ? __builtin_amdgcn_exp2f(sj[j] - m_h) : 0.0f;
       const char* const vrow = slot + (4 * kq) * RB + (kNib ? 1 : 2) * hm;
-      // The scale rows of the lane's four tokens, NK fp16 each (Q5: read
-      // per group below, with the group's qh words).
+      // The side rows of the lane's four tokens: their d words (NK fp16,
+      // or (d, m) pairs), after the qh words for Q5.
       const char* const srow = slot + GB + (4 * kq) * F::kScaleRow;
-      constexpr int SW = F::kQ5 ? 1 : (F::kScaleRow > 0 ? F::kScaleRow : 4) / 4;  // dwords per token row
+      constexpr int SW = (F::kScaleRow > 0 ? F::kScaleRow - F::kMetaOff : 4) / 4;  // d dwords per token row
       uint32_t dw[4][SW];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        if constexpr (F::kQ5) {
-          dw[j][0] = 0u;
-        } else if constexpr (SW % 4 == 0) {
+        const char* const dr = srow + j * F::kScaleRow + F::kMetaOff;
+        if constexpr (SW % 4 == 0) {
 #pragma unroll
           for (int c = 0; c < SW / 4; ++c) {
-            const uint4 t = *reinterpret_cast<const uint4*>(srow + j * F::kScaleRow + 16 * c);
+            const uint4 t = *reinterpret_cast<const uint4*>(dr + 16 * c);
             dw[j][4 * c] = t.x, dw[j][4 * c + 1] = t.y, dw[j][4 * c + 2] = t.z, dw[j][4 * c + 3] = t.w;
           }
         } else {
-          const uint2 t = *reinterpret_cast<const uint2*>(srow + j * F::kScaleRow);
+          const uint2 t = *reinterpret_cast<const uint2*>(dr);
           dw[j][0] = t.x, dw[j][1] = t.y;
         }
       }
-      // fp16 d of group G for token 4 kq + j (Q4_1 rows hold (d, m) pairs).
+      // fp16 d of group G for token 4 kq + j (Q4_1 / Q5_1 rows hold (d, m) pairs).
       auto dbits = [&](int j, auto gc) -> uint32_t {
         constexpr int G = decltype(gc)::value;
-        if constexpr (F::kQ5)
-          return *reinterpret_cast<const uint16_t*>(srow + j * F::kScaleRow + F::kMetaOff + F::kMetaStride * G);
-        else if constexpr (kOff) return dw[j][G] & 0xFFFFu;
+        if constexpr (kOff) return dw[j][G] & 0xFFFFu;
         else return G & 1 ? dw[j][G / 2] >> 16 : dw[j][G / 2] & 0xFFFFu;
       };
       // P.V in fp16 (Q8_0, Q4_0, Q4_1), when every scale of the item is
@@ -1202,11 +1225,13 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
         for (int j = 0; j < 4; ++j)
 #pragma unroll
           for (int c = 0; c < SW; ++c)
-            m = __builtin_elementwise_max(m, __builtin_bit_cast(us2, DT == IT_Q4_0 ? dw[j][c] & 0x7FFF7FFFu : dw[j][c]));
-        // |d| bits order as the values (Q8_0's and Q4_1's d are >= 0, Q4_0's
-        // = max / -8 of either sign); Q4_1's high halves are the offsets m,
-        // not scales.
-        constexpr unsigned kLim = 0x6000u;  // 512: |v| <= 128 (Q8_0's q, the nibbles' 16 (n - 8))
+            m = __builtin_elementwise_max(
+                m, __builtin_bit_cast(us2, (DT == IT_Q4_0 || DT == IT_Q5_0) ? dw[j][c] & 0x7FFF7FFFu : dw[j][c]));
+        // |d| bits order as the values (Q4_0's d = max / -8 and Q5_0's
+        // max / -16 take either sign); Q4_1's and Q5_1's high halves are the
+        // offsets m, not scales.
+        // 512: |v| <= 128 (Q8_0's q, Q4's 16 (n - 8)); 2048: |v| <= 16 (Q5).
+        constexpr unsigned kLim = F::kQ5 ? 0x6800u : 0x6000u;
         const bool big = m[0] >= kLim || (!kOff && m[1] >= kLim);
         f16_item = __builtin_amdgcn_ballot_w64(big) == 0;  // uniform
       }
@@ -1240,6 +1265,7 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) pj[j] *= kQPScale;
       auto pv_f16 = [&](auto) {
+        const uint32_t rot5 = uint32_t(hm - 4) & 31u;  // Q5: the fifth bits' rotation
         uint2 ah, al;
         split2_f16(pj, ah, al);
         const uint4 a_hi = make_uint4(ah.x, ah.y, ah.x, ah.y), a_lo = make_uint4(al.x, al.y, al.x, al.y);
@@ -1265,10 +1291,40 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
             v01[1] = __builtin_bit_cast(h2, i8pair_f16<1, 1>(w[0], w[1]));
             v23[0] = __builtin_bit_cast(h2, i8pair_f16<0, 0>(w[2], w[3]));
             v23[1] = __builtin_bit_cast(h2, i8pair_f16<1, 1>(w[2], w[3]));
+          } else if constexpr (F::kQ5) {
+            const int vg = 16 * (G ^ kq);
+            us2 t01, t23;  // the group's byte of tokens (0, 1) and (2, 3), one per half
+            t01[0] = *reinterpret_cast<const uint8_t*>(vrow + vg);
+            t01[1] = *reinterpret_cast<const uint8_t*>(vrow + RB + vg);
+            t23[0] = *reinterpret_cast<const uint8_t*>(vrow + 2 * RB + vg);
+            t23[1] = *reinterpret_cast<const uint8_t*>(vrow + 3 * RB + vg);
+            const uint32_t p01 = __builtin_bit_cast(uint32_t, t01), p23 = __builtin_bit_cast(uint32_t, t23);
+            // qh of token j rotated right by hm - 4: bit 4 is element
+            // hm's fifth bit (tile 0), bit 20 element 16 + hm's (tile 1).
+            uint32_t r[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const uint32_t qh = *reinterpret_cast<const uint32_t*>(srow + j * F::kScaleRow + 4 * G);
+              r[j] = __builtin_amdgcn_alignbit(qh, qh, rot5);
+            }
+            // Values q - 16 = n + 16 b - 16 as the fp16 bits
+            // 0x6400 | n | b << 4 (= 1024 + n + 16 b) - 1040, exactly; the
+            // fifth bits of tokens (0, 1) / (2, 3) brought to bits 4 and
+            // 20 by a byte permute.
+            const h2 k1040 = {(_Float16)-1040.0f, (_Float16)-1040.0f};
+            auto q5 = [&](uint32_t x, uint32_t z) {
+              uint32_t nibw = (x & 0x000F000Fu) | k6400;
+              asm volatile("" : "+v"(nibw));  // two v_and_or, not and, and, or3
+              return __builtin_bit_cast(h2, (z & 0x00100010u) | nibw) + k1040;
+            };
+            v01[0] = q5(p01, __builtin_amdgcn_perm(r[1], r[0], 0x0C040C00u));
+            v23[0] = q5(p23, __builtin_amdgcn_perm(r[3], r[2], 0x0C040C00u));
+            v01[1] = q5(p01 >> 4, __builtin_amdgcn_perm(r[1], r[0], 0x0C060C02u));
+            v23[1] = q5(p23 >> 4, __builtin_amdgcn_perm(r[3], r[2], 0x0C060C02u));
           } else {
             const int vg = 16 * (G ^ kq);
             // The group's byte of tokens (0, 1) and (2, 3), one per 16-bit
-            // half (ds_read_u8_d16 / _d16_hi: no packing instructions).
+            // half.
             us2 t01, t23;
             t01[0] = *reinterpret_cast<const uint8_t*>(vrow + vg);
             t01[1] = *reinterpret_cast<const uint8_t*>(vrow + RB + vg);
@@ -1318,7 +1374,7 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
         // B holds 16 (n - 8) (Q5: 8 (q - 16)); A = p d / 16 (/ 8) undoes the
         // factor, except in tile 1 of the formats with an fp16 form, whose
         // accumulators carry 16 times their values (see that form).
-        constexpr bool kT1 = kF16 && kNib;
+        constexpr bool kT1 = kHi16;
         float pt1[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) pt1[j] = pj[j];
@@ -1515,7 +1571,7 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
           // The weights carried 2^11 (exact).
           if constexpr (kNib) {
             // Tile 1 of Q4_0 / Q4_1 carries a further 16 (exact).
-            constexpr float kS1 = (DT == IT_Q4_0 || DT == IT_Q4_1) ? 1.0f / (16.0f * kQPScale) : 1.0f / kQPScale;
+            constexpr float kS1 = kHi16 ? 1.0f / (16.0f * kQPScale) : 1.0f / kQPScale;
             row[hm] = o8[g][0][i] * (1.0f / kQPScale);
             row[16 + hm] = o8[g][1][i] * kS1;
           } else {
