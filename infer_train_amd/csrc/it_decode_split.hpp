@@ -299,14 +299,6 @@ __device__ __forceinline__ uint32_t i8_f32(uint32_t w) {
 
 // ---- Q8_0 scores on MFMA ----------------------------------------------------
 typedef float v4f __attribute__((ext_vector_type(4)));
-typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
-// Eight signed bytes as eight bf16, exactly: an integer of magnitude <= 128
-// converts to fp32 with its low 16 bits zero, so its top half is its bf16.
-__device__ __forceinline__ uint4 i8x8_bf16(uint2 w) {
-  auto pair = [](uint32_t f0, uint32_t f1) { return __builtin_amdgcn_perm(f1, f0, 0x07060302u); };
-  return make_uint4(pair(i8_f32<0>(w.x), i8_f32<1>(w.x)), pair(i8_f32<2>(w.x), i8_f32<3>(w.x)),
-                    pair(i8_f32<0>(w.y), i8_f32<1>(w.y)), pair(i8_f32<2>(w.y), i8_f32<3>(w.y)));
-}
 // Four Q4_0 bytes (nibble n at element j, nibble m at element j + 16) as
 // eight bf16 values 16 (n - 8), then 16 (m - 8), exactly: n ^ 8 read as a
 // signed nibble is n - 8, and moved to the top of its byte it sign-extends
@@ -360,9 +352,6 @@ __device__ __forceinline__ void split3_bf16(float x0, float x1, uint32_t& hi, ui
   mid = rne2(r0, r1);
   const float t0 = r0 - lo_f(mid), t1 = r1 - hi_f(mid);
   lo = rne2(t0, t1);
-}
-__device__ __forceinline__ v4f mfma16(uint4 a, uint4 b, v4f c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, a), __builtin_bit_cast(v8bf, b), c, 0, 0, 0);
 }
 typedef short v4s __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ v4f mfma16k16(uint2 a, uint2 b, v4f c) {
@@ -474,9 +463,6 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
   constexpr int RB = F::kRow, GB = F::kGroup, SLOT = F::kSlot, NI = F::kDma, NL = F::kLoads;
   constexpr int PQ = F::kPieces, NQ = F::kQRegs, DPV = F::kDpv;
   constexpr bool k16 = F::k16, kQ = F::kQuant, kNib = F::kNib, kOff = F::kOff;
-  // Formats whose products run as exact fp16 MFMAs (the others as three
-  // exact bf16 passes).
-  constexpr bool kF16 = true;
   // Q4_0 / Q4_1: the high nibbles enter as 16 (n - 8) (no shift), their q
   // (QK) and their tile's weights (P.V) carrying the 1/16.
   constexpr bool kHi16 = DT == IT_Q4_0 || DT == IT_Q4_1;
@@ -618,20 +604,18 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
   // quarter r of the head dimension (packed 16-bit pairs, or fp32).
   const int qr_row = lane >> 4, qk_tok = lane & 15;
   uint32_t qv[GC][NQ];
-  // Q8_0 / Q4_0: q is the A operand of v_mfma_f32_16x16x32_bf16 instead,
-  // lane (kh, h) = (lane / 16, lane % 16) holding eight dims of group ks of
-  // head h (zero for h >= GC), split exactly into three bf16 parts: Q8_0
-  // dims 32 ks + 8 kh .. + 8; Q4_0 dims 32 ks + 4 kh .. + 4 and 32 ks + 16 +
-  // 4 kh .. + 4 (the low and high nibbles of bytes 4 kh .. + 4 of the group).
+  // Quantised formats: q is the A operand of v_mfma_f32_16x16x32_f16
+  // instead, lane (kh, h) = (lane / 16, lane % 16) holding eight dims of
+  // group ks of head h (zero for h >= GC): Q8_0 dims 32 ks + 8 kh .. + 8;
+  // nibble formats dims 32 ks + 4 kh .. + 4 and 32 ks + 16 + 4 kh .. + 4 (the
+  // low and high nibbles of bytes 4 kh .. + 4 of the group).
   constexpr int NK = kQ ? D / 32 : 1;  // 32-groups (MFMA k-steps) per row
-  uint4 qa[kF16 ? 1 : 3][NK];
-  // fp16 forms: q of head h scaled by 2^E_h (so that max |q| lies in
-  // [2^14, 2^15)) as hi + lo fp16 parts, the A operand of
-  // v_mfma_f32_16x16x32_f16; the scores are scaled back by 2^-E_h (exact).
+  // q of head h scaled by 2^E_h (so that max |q| lies in [2^14, 2^15)) as
+  // hi + lo fp16 parts; the scores are scaled back by 2^-E_h (exact).
   // Q4_0 / Q4_1 take the high-nibble dims' q divided by 16, against K
   // values 16 (n - 8).  sE[i]: 2^-E of head 4 (lane / 16) + i, the heads
   // this lane's scores belong to.
-  uint4 qf[kF16 ? 2 : 1][NK];
+  uint4 qf[2][NK];
   float sE[4] = {1.0f, 1.0f, 1.0f, 1.0f};
   // Q4_1: sum of q over each 32-group, the A operand of the offset-term MFMA
   // (v_mfma_f32_16x16x16_bf16, k = group): lane (kh, h) holds groups
@@ -658,7 +642,7 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
                       (kNib ? 4 : 8) * qr_row;
     float qsum[NK];
     int E = 0;
-    if constexpr (kF16) {
+    {
       float4 x0[NK], x1[NK];
       float mx = 0.0f;
 #pragma unroll
@@ -707,17 +691,11 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
           asm volatile("" : "+v"(qf[p][ks].x), "+v"(qf[p][ks].y), "+v"(qf[p][ks].z), "+v"(qf[p][ks].w));
     }
 #pragma unroll
-    for (int ks = 0; ks < NK && (kOff || !kF16); ++ks) {
+    for (int ks = 0; ks < NK && kOff; ++ks) {
       float4 x0 = *reinterpret_cast<const float4*>(qp + 32 * ks);
-      float4 x1 = *reinterpret_cast<const float4*>(qp + 32 * ks + (kNib ? 16 : 4));
+      float4 x1 = *reinterpret_cast<const float4*>(qp + 32 * ks + 16);
       if (hq >= GC) x0 = x1 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-      if constexpr (kOff) qsum[ks] = ((x0.x + x0.y) + (x0.z + x0.w)) + ((x1.x + x1.y) + (x1.z + x1.w));
-      if constexpr (!kF16) {
-        split3_bf16(x0.x, x0.y, qa[0][ks].x, qa[1][ks].x, qa[2][ks].x);
-        split3_bf16(x0.z, x0.w, qa[0][ks].y, qa[1][ks].y, qa[2][ks].y);
-        split3_bf16(x1.x, x1.y, qa[0][ks].z, qa[1][ks].z, qa[2][ks].z);
-        split3_bf16(x1.z, x1.w, qa[0][ks].w, qa[1][ks].w, qa[2][ks].w);
-      }
+      qsum[ks] = ((x0.x + x0.y) + (x0.z + x0.w)) + ((x1.x + x1.y) + (x1.z + x1.w));
     }
     if constexpr (kOff) {
       float qg[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -727,18 +705,13 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
         qsum[ks] += __shfl_xor(qsum[ks], 32);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          if (ks == 4 * qr_row + j) qg[j] = kF16 ? __builtin_ldexpf(qsum[ks], E) : qsum[ks];  // the scores' 2^E
+          if (ks == 4 * qr_row + j) qg[j] = __builtin_ldexpf(qsum[ks], E);  // the scores' 2^E
       }
       uint2 p0, p1, p2;
       split3_bf16(qg[0], qg[1], p0.x, p1.x, p2.x);
       split3_bf16(qg[2], qg[3], p0.y, p1.y, p2.y);
       qs_a[0] = p0, qs_a[1] = p1, qs_a[2] = p2;
     }
-#pragma unroll
-    for (int p = 0; p < (kF16 ? 0 : 3); ++p)
-#pragma unroll
-      for (int ks = 0; ks < NK; ++ks)
-        asm volatile("" : "+v"(qa[p][ks].x), "+v"(qa[p][ks].y), "+v"(qa[p][ks].z), "+v"(qa[p][ks].w));
   }
   asm volatile("s_waitcnt vmcnt(0)\n\ts_nop 4" ::: "memory");
   lds_barrier();
@@ -931,9 +904,9 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
       }
       v4f acc[NK];
       uint4 kb[NK];
-      if constexpr (kF16) {
-        // fp16: q hi / lo parts against the exact fp16 K values, the two
-        // MFMAs of a group a group apart.
+      {
+        // q hi / lo parts against the exact fp16 K values, the two MFMAs of
+        // a group a group apart.
         Unroll<0, NK + 1>::run([&](auto kc) {
           constexpr int k = decltype(kc)::value;
           if constexpr (k < NK) {
@@ -972,17 +945,6 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
             acc[k] = mfma16_f16(qf[0][k], kb[k], v4f{0.0f, 0.0f, 0.0f, 0.0f});
           }
           if constexpr (k >= 1) acc[k - 1] = mfma16_f16(qf[1][k - 1], kb[k - 1], acc[k - 1]);
-        });
-      } else {
-        Unroll<0, NK + 2>::run([&](auto kc) {
-          constexpr int k = decltype(kc)::value;
-          if constexpr (k < NK) {
-            if constexpr (F::kQ5) kb[k] = nib5_bf16(kr[k].x, qh5[k] & 0xFu, (qh5[k] >> 16) & 0xFu);
-            else kb[k] = kNib ? nib8_bf16(kr[k].x) : i8x8_bf16(kr[k]);
-            acc[k] = mfma16(qa[0][k], kb[k], v4f{0.0f, 0.0f, 0.0f, 0.0f});
-          }
-          if constexpr (k >= 1 && k - 1 < NK) acc[k - 1] = mfma16(qa[1][k - 1], kb[k - 1], acc[k - 1]);
-          if constexpr (k >= 2) acc[k - 2] = mfma16(qa[2][k - 2], kb[k - 2], acc[k - 2]);
         });
       }
       v4f sv = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -1126,15 +1088,14 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
   for (int x = 0; x < DPV; ++x)
 #pragma unroll
     for (int g = 0; g < 8; ++g) acc2[x][g] = 0.0f;
-  // Q8_0 / Q4_0: P.V on v_mfma_f32_16x16x16_bf16, per 32-group G of the head
-  // dim O[h][dim(G, c, n)] += sum_t (p[h][t] f32(d[t][G])) v[t][dim(G, c, n)]
+  // Quantised formats: P.V on MFMA, per 32-group G of the head dim
+  // O[h][dim(G, c, n)] += sum_t p[h][t] f32(d[t][G]) v[t][dim(G, c, n)]
   // (tile c = 0, 1; column n; Q8_0 dim 32 G + 2 n + c from a 2-byte read,
-  // Q4_0 dim 32 G + 16 c + n, the two nibbles of byte n of the group).
-  // A = p d in fp32 (Q4_0: p d / 16), split exactly into three bf16 parts;
-  // B = qs (Q4_0: 16 (nibble - 8)) widened exactly to bf16.  Lane (kq, hm) = (lane / 16,
-  // lane % 16) holds A[head hm][tokens 4 kq + j] and B[tokens 4 kq + j][column
-  // hm] (the MFMA's k index is j + 4 kq in both), and ends holding
-  // O[4 kq + i][column hm] of every tile.
+  // nibble formats dim 32 G + 16 c + n, the two nibbles of byte n of the
+  // group), in the fp16 form or the three-part bf16 form below.  Lane
+  // (kq, hm) = (lane / 16, lane % 16) holds A[head hm][tokens 4 kq + j] and
+  // B[tokens 4 kq + j][column hm] (the MFMA's k index runs over 4 kq + j in
+  // both), and ends holding O[4 kq + i][column hm] of every tile.
   v4f o8[kQ ? NK : 1][2];
   v4f mo = {0.0f, 0.0f, 0.0f, 0.0f};  // Q4_1: sum_t p[4 kq + i][t] m'_hm(t)
   if constexpr (kQ) {
@@ -1203,12 +1164,12 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
         if constexpr (kOff) return dw[j][G] & 0xFFFFu;
         else return G & 1 ? dw[j][G / 2] >> 16 : dw[j][G / 2] & 0xFFFFu;
       };
-      // P.V in fp16 (Q8_0, Q4_0, Q4_1), when every scale of the item is
-      // small enough that |d v| <= 65504 (d below 512: |v| <= 128 for Q8_0's
-      // q and for the nibbles' tile 1, which holds 16 (n - 8); other items
-      // take the bf16 form below): B = d v is exact as hi + lo fp16 parts
-      // (d has 11 significant bits and v at most 8), and A = p 2^11 as two fp16 parts
-      // made once per item (p <= 1: every weight above 2^-13 keeps 22 bits,
+      // P.V in fp16, when every scale of the item is small enough that
+      // |d v| <= 65504 (d below 512 where |v| <= 128: Q8_0's q, and Q4's
+      // tile 1, which holds 16 (n - 8); d below 2048 for Q5's |q - 16| <=
+      // 16; other items take the bf16 form below): B = d v is exact as
+      // hi + lo fp16 parts (d has 11 significant bits and v at most 8), and
+      // A = p 2^11 as two fp16 parts made once per item (p <= 1: every weight above 2^-13 keeps 22 bits,
       // smaller ones an absolute error below 2^-36).  Each tile takes two
       // v_mfma_f32_16x16x32_f16 whose k runs over (token, B part):
       // [A_hi A_hi] . [B_hi; B_lo] and [A_lo A_lo] . [B_hi; B_lo], every
@@ -1216,10 +1177,10 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
       // K = 32 costs little more than K = 16 (measured 19 against 17
       // cycles), so a V item is 32 MFMAs instead of the bf16 form's 48.  The
       // two MFMAs of an accumulator are issued a group apart, so none waits
-      // for the one before it.  (Q4_1's offset term stays on the bf16 form
-      // above.)
-      bool f16_item = false;
-      if constexpr (kF16) {
+      // for the one before it.  (The offset term of Q4_1 / Q5_1 stays on
+      // the bf16 form above.)
+      bool f16_item;
+      {
         us2 m = {0, 0};
 #pragma unroll
         for (int j = 0; j < 4; ++j)
@@ -1235,7 +1196,7 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
         const bool big = m[0] >= kLim || (!kOff && m[1] >= kLim);
         f16_item = __builtin_amdgcn_ballot_w64(big) == 0;  // uniform
       }
-      if constexpr (kF16 && !decltype(bf16_only)::value) {
+      if constexpr (!decltype(bf16_only)::value) {
         if (!f16_item) return false;  // before any state of the item changes
       }
       lsum += (pj[0] + pj[1]) + (pj[2] + pj[3]);
@@ -1439,10 +1400,10 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
           o8[G][1] = mfma16k16(tl, b1, o8[G][1]);
           // As the fallback of the fp16 form, one group at a time: its
           // register use then stays below the fp16 loop's.
-          if constexpr (kF16) __builtin_amdgcn_sched_barrier(0);
+          __builtin_amdgcn_sched_barrier(0);
         });
       };
-      if constexpr (kF16 && !decltype(bf16_only)::value)
+      if constexpr (!decltype(bf16_only)::value)
         pv_f16(0);
       else
         pv_bf16(0);
@@ -1457,13 +1418,11 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
     // the bf16 form.
     int s = ns;
     bool redo = false;
-    if constexpr (kF16) {
-      for (; s < S; ++s)
-        if (!v_item(s, std::false_type{}, false)) {
-          redo = true;
-          break;
-        }
-    }
+    for (; s < S; ++s)
+      if (!v_item(s, std::false_type{}, false)) {
+        redo = true;
+        break;
+      }
     for (; s < S; ++s) {
       v_item(s, std::true_type{}, redo);
       redo = false;
