@@ -1165,9 +1165,11 @@ def summarize_movers_profile(d, args):
                   "hold the small index loads: the appends read one int64 slot per wave and four 16-byte "
                   "vectors (kv_append_copy: 16384 data loads + 8192 slot loads = 24576 for config 3, every data "
                   "load and store 1024 B); the gathers read block-table entries; the decode's VMEM_WR are its "
-                  "(m, l, O) partials.  The Q8_0 quantise-append stores 4 int8 per lane (8 lanes per 32-group) "
-                  "and one fp16 scale per group, so its stores are 256 B and 16 B per wave instruction; its "
-                  "loads are 16 B per lane."]
+                  "(m, l, O) partials.  The Q8_0 quantise-append (kv_append_q8_wide) stages a wave's 1024 "
+                  "int8 in LDS and stores them as one 16-byte vector per lane: for the 4096-token chunk, 8192 "
+                  "store instructions of 1024 B on the int8 plane, plus 8192 of 64 B for the scale rows (four "
+                  "rows' first lanes, 16 B each); its 32768 data loads are 1024 B each (plus 8192 slot "
+                  "loads)."]
     os.makedirs(os.path.join(ROOT, "profiles"), exist_ok=True)
     open(os.path.join(ROOT, "profiles", "data_movement.md"), "w").write("\n".join(lines) + "\n")
     print("\n".join(lines))
