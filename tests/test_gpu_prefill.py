@@ -153,11 +153,10 @@ def test_prefill_wide_table_scalar_page_ids():
 def test_prefill_config3_rows():
     """Config 3: Hq 32, Hkv 8, D 128, bs 16; 8 sequences with 2048 cached
     tokens append a 512-token chunk; table = a permutation of a 4096-block
-    pool.  Against the oracle (on the host's threads): 64 rows of every
-    sequence -- the first and last 16 of the chunk and two blocks of 16 at
-    seeded positions inside it.  Every row of every sequence: finite, and
-    each output element inside the range of the V rows it attends (keys 0
-    .. its position of its KV head), as a convex combination must be."""
+    pool.  Against the oracle (on the host's threads): every row of every
+    sequence (4096 rows x 32 heads).  Every row: finite, and each output
+    element inside the range of the V rows it attends (keys 0 .. its
+    position of its KV head), as a convex combination must be."""
     import os
 
     hq, hkv, D = 32, 8, 128
@@ -169,13 +168,10 @@ def test_prefill_config3_rows():
     assert np.isfinite(got).all()
     qf = widen(q, orc.BF16)
     threads = max(1, min(16, len(os.sched_getaffinity(0))))
-    rng = np.random.default_rng(33)
     for s in range(8):
-        mids = np.sort(rng.choice(np.arange(1, 30), 2, replace=False)) * 16
-        for b in (0, int(mids[0]), int(mids[1]), 496):
-            want = ref.prefill(qf, hq, cu, tables, ctx, scale, causal=True, rows=(s, b, b + 16), threads=threads)
-            rows = slice(int(cu[s]) + b, int(cu[s]) + b + 16)
-            assert_close(got[rows], want[rows], RTOL, ATOL, what=f"config3 seq {s} rows {b}:{b + 16}")
+        want = ref.prefill(qf, hq, cu, tables, ctx, scale, causal=True, rows=(s, 0, 512), threads=threads)
+        rows = slice(int(cu[s]), int(cu[s]) + 512)
+        assert_close(got[rows], want[rows], RTOL, ATOL, what=f"config3 seq {s}, all 512 rows")
     # Convex hull: running min / max of V over positions, per KV head and dim.
     n = ctx.astype(np.int64)
     cu_tok = np.concatenate([[0], np.cumsum(n)[:-1]]).astype(np.int64)

@@ -92,9 +92,10 @@ def test_window_small_unaligned():
 
 def test_window_config4_full_size():
     """Config 4 at full size: 64 sequences, Hq 16 / Hkv 2, W 4096, from
-    position 30000, pool of 16512 blocks in seeded order; 80 steps cross five
-    allocate / free cycles (allocations at p = 30000, 30016, ..., 30064,
-    releases at p = 30015, ..., 30079, LIFO hand-offs between sequences), with
-    the pools compared byte for byte and a decode checked once per cycle."""
-    n_ev = _window_run(n_seqs=64, hq=16, hkv=2, W=4096, start=30000, steps=80, cap=16512, seed=4, check_every=16)
-    assert n_ev == 64 * 5  # one block per sequence per cycle
+    position 30000, pool of 16512 blocks in seeded order; 256 steps cross 16
+    allocate / free cycles (allocations at p = 30000, 30016, ..., releases
+    at p = 30015, 30031, ..., LIFO hand-offs between sequences), with slots
+    and frees equal to the oracle's at every step, and the pools compared
+    byte for byte and a decode checked once per cycle."""
+    n_ev = _window_run(n_seqs=64, hq=16, hkv=2, W=4096, start=30000, steps=256, cap=16512, seed=4, check_every=16)
+    assert n_ev == 64 * 16  # one block per sequence per cycle
