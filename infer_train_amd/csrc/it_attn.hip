@@ -61,14 +61,22 @@ hipError_t launch_combine(int d, const DecodeArgs& a, int n_seqs, void* out, int
   int64_t widest = 0;
   for (int x = 0; x < 8; ++x) widest = std::max(widest, map.first_row(x + 1) - map.first_row(x));
   const dim3 grid(unsigned(8 * widest), 1u, unsigned(d / 128));
-  if (d == 128)
-    hipLaunchKernelGGL(paged_decode_combine<128>, grid, dim3(64), 0, s, a.ws_o, a.ws_ml, map.q8, map.n_rows, map.gc,
-                       map.max_parts, a.n_heads, a.ctx_lens, a.start_pos, a.ctx_const, a.partition, out, out_dtype);
-  else if (d == 256)
-    hipLaunchKernelGGL(paged_decode_combine<256>, grid, dim3(64), 0, s, a.ws_o, a.ws_ml, map.q8, map.n_rows, map.gc,
-                       map.max_parts, a.n_heads, a.ctx_lens, a.start_pos, a.ctx_const, a.partition, out, out_dtype);
-  else
+  // Rows of more than 32 partitions (one wave's batch) take four waves.
+  const bool wide = map.max_parts > 32;
+#define IT_COMBINE(DD, NWW)                                                                                       \
+  hipLaunchKernelGGL((paged_decode_combine<DD, NWW>), grid, dim3(64 * NWW), 0, s, a.ws_o, a.ws_ml, map.q8,          \
+                     map.n_rows, map.gc, map.max_parts, a.n_heads, a.ctx_lens, a.start_pos, a.ctx_const, a.partition, \
+                     out, out_dtype)
+  if (d == 128) {
+    if (wide) IT_COMBINE(128, 4);
+    else IT_COMBINE(128, 1);
+  } else if (d == 256) {
+    if (wide) IT_COMBINE(256, 4);
+    else IT_COMBINE(256, 1);
+  } else {
     return hipErrorInvalidValue;
+  }
+#undef IT_COMBINE
   return hipGetLastError();
 }
 

@@ -101,7 +101,7 @@ struct CombineMap {
 // Merge the partitions of one (sequence, head) row over a 128-dim slice
 // (grid z): M = max m_p, L = sum l_p 2^(m_p - M), O = sum O_p 2^(m_p - M) / L
 // (the split-K form of flash_attn_f32's rescaling, flash_attn.rs:42-71).
-// One wave per row slice, two adjacent dims per lane (8-byte partial loads
+// One wave (four for long rows, below) per row slice, two adjacent dims per lane (8-byte partial loads
 // and one packed store: half the workgroups and load instructions of one dim
 // per lane, 0.9 us less per config-2 decode).  Lane c also holds the (m, l)
 // pairs of partitions c and 64 + c, so M and L are wave reductions and
@@ -115,17 +115,19 @@ struct CombineMap {
 // length pointers: 16 dwords) are preloaded into SGPRs at wave launch
 // (kernarg preloading, gfx950), so the first loads do not wait for a
 // kernel-argument fetch.
-template <int D>
-__global__ __launch_bounds__(64) void paged_decode_combine(const float* __restrict__ ws_o,
-                                                           const float* __restrict__ ws_ml, int64_t q8,
-                                                           int64_t n_rows, int gc, int max_parts, int n_heads,
-                                                           const int32_t* __restrict__ ctx_lens,
-                                                           const int32_t* __restrict__ start_pos, int ctx_const,
-                                                           int partition, void* out, int out_dtype) {
+// NW waves per workgroup (1, or 4 for rows of more than kBatch partitions):
+// wave w takes partitions w, w + NW, ... and the waves' sums meet in LDS in
+// a fixed order, so a row of up to NW kBatch partitions costs one round trip.
+template <int D, int NW>
+__global__ __launch_bounds__(64 * NW) void paged_decode_combine(const float* __restrict__ ws_o,
+                                                                const float* __restrict__ ws_ml, int64_t q8,
+                                                                int64_t n_rows, int gc, int max_parts, int n_heads,
+                                                                const int32_t* __restrict__ ctx_lens,
+                                                                const int32_t* __restrict__ start_pos, int ctx_const,
+                                                                int partition, void* out, int out_dtype) {
   // Partitions beyond max_parts were never computed (the split pass latched
   // the error); only the computed ones are merged.
   constexpr int kBatch = 32;
-  static_assert(kBatch <= 64, "the first batch takes its weights from lanes 0-63 of w0");
   CombineMap map;
   map.q8 = q8;
   map.n_rows = n_rows;
@@ -134,7 +136,8 @@ __global__ __launch_bounds__(64) void paged_decode_combine(const float* __restri
   const int x = int(blockIdx.x & 7);
   const int64_t row = map.first_row(x) + (blockIdx.x >> 3);
   if (row >= map.first_row(x + 1)) return;  // uniform for the workgroup
-  const int b = int(row / n_heads), lane = int(threadIdx.x), d = 2 * (64 * int(blockIdx.z) + lane);
+  const int lane = int(threadIdx.x & 63), wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+  const int b = int(row / n_heads), d = 2 * (64 * int(blockIdx.z) + lane);
   const float2* ml = reinterpret_cast<const float2*>(ws_ml) + row * max_parts;
   const float* op = ws_o + row * max_parts * D + d;
   const float2 none = make_float2(-INFINITY, 0.0f);
@@ -143,7 +146,7 @@ __global__ __launch_bounds__(64) void paged_decode_combine(const float* __restri
   float2 ob[kBatch];
 #pragma unroll
   for (int c = 0; c < kBatch; ++c)
-    if (c < max_parts) ob[c] = *reinterpret_cast<const float2*>(op + int64_t(c) * D);
+    if (wave + NW * c < max_parts) ob[c] = *reinterpret_cast<const float2*>(op + int64_t(wave + NW * c) * D);
   const int ctx = ctx_lens ? ctx_lens[b] : ctx_const;
   const int st = start_pos ? start_pos[b] : 0;
   const int n = ctx - st;
@@ -165,34 +168,40 @@ __global__ __launch_bounds__(64) void paged_decode_combine(const float* __restri
       if (v.x != -INFINITY) l = fmaf(v.y, __builtin_amdgcn_exp2f(v.x - mx), l);
     }
     l = group_sum<64>(l);
+    // Partition p's weight (p uniform): from its lane's pair, or read.
+    auto weight = [&](int p) {
+      if (p < 64) return lane_f32(w0, p);
+      if (p < 128) return lane_f32(w1, p - 64);
+      const float2 v = ml[p];
+      return v.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(v.x - mx);
+    };
+    for (int c0 = 0; wave + NW * c0 < np; c0 += kBatch) {
+      if (c0 > 0) {
 #pragma unroll
-    for (int c = 0; c < kBatch; ++c)
-      if (c < np) {
-        const float w = lane_f32(w0, c);
-        o0 = fmaf(ob[c].x, w, o0);
-        o1 = fmaf(ob[c].y, w, o1);
+        for (int c = 0; c < kBatch; ++c)
+          if (wave + NW * (c0 + c) < np) ob[c] = *reinterpret_cast<const float2*>(op + int64_t(wave + NW * (c0 + c)) * D);
       }
-    for (int p0 = kBatch; p0 < np; p0 += kBatch) {
-#pragma unroll
-      for (int c = 0; c < kBatch; ++c)
-        if (p0 + c < np) ob[c] = *reinterpret_cast<const float2*>(op + int64_t(p0 + c) * D);
 #pragma unroll
       for (int c = 0; c < kBatch; ++c) {
-        const int p = p0 + c;
+        const int p = wave + NW * (c0 + c);
         if (p < np) {
-          float w;
-          if (p < 64) {
-            w = lane_f32(w0, p);
-          } else if (p < 128) {
-            w = lane_f32(w1, p - 64);
-          } else {
-            const float2 v = ml[p];
-            w = v.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(v.x - mx);
-          }
+          const float w = weight(p);
           o0 = fmaf(ob[c].x, w, o0);
           o1 = fmaf(ob[c].y, w, o1);
         }
       }
+    }
+  }
+  if constexpr (NW > 1) {
+    __shared__ float2 red[NW][64];
+    red[wave][lane] = make_float2(o0, o1);
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int w = 1; w < NW; ++w) {
+      const float2 t = red[w][lane];
+      o0 += t.x;
+      o1 += t.y;
     }
   }
   const float inv = l > 0.0f ? 1.0f / l : 0.0f;
