@@ -1181,19 +1181,23 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
       // the bf16 form above.)
       bool f16_item;
       {
-        us2 m = {0, 0};
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-          for (int c = 0; c < SW; ++c)
-            m = __builtin_elementwise_max(
-                m, __builtin_bit_cast(us2, (DT == IT_Q4_0 || DT == IT_Q5_0) ? dw[j][c] & 0x7FFF7FFFu : dw[j][c]));
-        // |d| bits order as the values (Q4_0's d = max / -8 and Q5_0's
-        // max / -16 take either sign); Q4_1's and Q5_1's high halves are the
-        // offsets m, not scales.
-        // 512: |v| <= 128 (Q8_0's q, Q4's 16 (n - 8)); 2048: |v| <= 16 (Q5).
+        // The 16 lanes of a token quad hold the same 4 SW scale words, so
+        // each lane checks its share of them (one word for SW = 4) with a
+        // read of its own, and the ballot covers the item.  |d| bits order
+        // as the values (Q4_0's d = max / -8 and Q5_0's max / -16 take
+        // either sign); Q4_1's and Q5_1's high halves are the offsets m, not
+        // scales.  512: |v| <= 128 (Q8_0's q, Q4's 16 (n - 8)); 2048:
+        // |v| <= 16 (Q5).
         constexpr unsigned kLim = F::kQ5 ? 0x6800u : 0x6000u;
-        const bool big = m[0] >= kLim || (!kOff && m[1] >= kLim);
+        constexpr int NDW = 4 * SW;
+        bool big = false;
+#pragma unroll
+        for (int r = 0; r < (NDW + 15) / 16; ++r) {
+          const int i = (hm + 16 * r) % NDW;
+          uint32_t w = *reinterpret_cast<const uint32_t*>(srow + (i / SW) * F::kScaleRow + F::kMetaOff + 4 * (i % SW));
+          if constexpr (DT == IT_Q4_0 || DT == IT_Q5_0) w &= 0x7FFF7FFFu;
+          big |= (w & 0xFFFFu) >= kLim || (!kOff && (w >> 16) >= kLim);
+        }
         f16_item = __builtin_amdgcn_ballot_w64(big) == 0;  // uniform
       }
       if constexpr (!decltype(bf16_only)::value) {
