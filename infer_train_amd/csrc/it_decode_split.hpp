@@ -27,14 +27,15 @@
 //       probability of token t (16-bit caches: of token pair t) comes from
 //       lane t of the row through row_newbcast:t; 16-bit caches v_perm
 //       (v_t[d], v_t+1[d]) pairs for v_dot2c.
-//  Q8_0 and Q4_0 run both products on MFMA, exactly: int8 widens to bf16 without
-//       rounding, and the fp32 operand on the other side is split into three
-//       bf16 parts (hi + mid + lo = x), so every product is exact and only
-//       the fp32 accumulation rounds.  QK: v_mfma_f32_16x16x32_bf16 per
-//       32-group of the head dim, q heads x 16 tokens, then f32(d) of the
-//       group scales the group's sum.  PV: v_mfma_f32_16x16x16_bf16 per
-//       32-group, heads x 16 tokens x 16 dims, the A operand being p * f32(d)
-//       of the group.
+//  The quantised formats run both products on v_mfma_f32_16x16x32_f16,
+//       exactly: K values (int8, or nibbles n - 8) are exact in fp16, q
+//       (scaled by a power of two per head) and the weights p 2^11 are split
+//       into hi + lo fp16 parts, and B = d v of P.V into hi + lo parts, so
+//       every product is exact and only the fp32 accumulation rounds.  QK:
+//       two MFMAs per 32-group of the head dim, q heads x 16 tokens, then
+//       f32(d) of the group scales the group's sum.  PV: two K = 32 MFMAs
+//       per tile of 16 dims, heads x 16 tokens; items whose scales are too
+//       large for fp16 products take a three-part bf16 form instead.
 //
 // The softmax follows flash_attn_f32 (src/backend/arm/flash_attn.rs:6-72)
 // with the partition max taken first: phase 1 writes the scores (log2
@@ -93,7 +94,7 @@ struct SplitFmt {
   static constexpr int kMetaOff = kQ5 ? D / 8 : 0;                // where the d words start in a side row
   static constexpr int kScaleRow = kQuant ? kMetaOff + D / 32 * kMetaStride : 0;  // side-row bytes per token
   static constexpr int kScaleGroup = kGroupTok * kScaleRow;       // 128..1024 B
-  // B-operand factor: int8 8 (q - 16) for Q5, 16 (nibble - 8) for Q4.
+  // B-operand factor of the bf16 P.V form: int8 8 (q - 16) for Q5, 16 (nibble - 8) for Q4.
   static constexpr float kBScale = kQ5 ? 0.125f : (kNib ? 0.0625f : 1.0f);
   static constexpr float kMid = kQ5 ? 16.0f : 8.0f;                // m' = m + kMid d
   static constexpr int kScaleLoads = (kScaleGroup + 255) / 256;   // dword loads (64 lanes x 4 B) per group
@@ -856,7 +857,7 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
   // Head held by lane row r after the fold: {0, 2, 1, 3}[r] (+4 in s_b).
   const int h_a = ((qr_row & 1) << 1) | (qr_row >> 1);
   float m_a = -INFINITY, m_b = -INFINITY;
-  float m_q[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};  // Q8_0: heads 4 qr_row + i
+  float m_q[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};  // quantised: heads 4 qr_row + i
   // 0x64006400 held in a VGPR, so that (x & mask) | k6400 is one
   // v_and_or_b32 (a VOP3 reads at most one scalar operand here).
   uint32_t k6400 = 0x64006400u;
@@ -872,11 +873,12 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
     const char* slot = my_ring + (s % R) * SLOT;
     if constexpr (kQ) {
       // Scores on MFMA: S[h][t] = sum over 32-groups ks of f32(d[t][ks]) *
-      // (q[h] . qs[t]) over the group, the group dot product taken as three
-      // exact bf16 x int8 passes (hi, mid, lo parts of q) into one fp32
-      // accumulator.  Lane (kh, t) reads bytes 8 kh .. + 8 of group ks of
-      // token t (Q4_0: bytes 4 kh .. + 4 of the group's 16, as 16 (n - 8))
-      // and ends holding S[4 kh + i][t], i = 0..3.
+      // (q[h] . v[t]) over the group, the group dot product taken as two
+      // exact fp16 passes (the hi and lo parts of q 2^E, against K values
+      // exact in fp16) into one fp32 accumulator, scaled back by 2^-E.  Lane
+      // (kh, t) reads bytes 8 kh .. + 8 of group ks of token t (nibble
+      // formats: bytes 4 kh .. + 4 of the group's 16) and ends holding
+      // S[4 kh + i][t], i = 0..3.
       const char* krow = slot + qk_tok * RB;
       const char* const kside = slot + GB + qk_tok * F::kScaleRow;
       uint16_t dsc[NK];
@@ -889,7 +891,7 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
 #pragma unroll
         for (int ks = 0; ks < NK; ++ks) qh5[ks] = *reinterpret_cast<const uint32_t*>(kside + 4 * ks);
       }
-      // All K reads first; then the three passes of each group are software
+      // All K reads first; then the two passes of each group are software
       // pipelined across groups, so that no MFMA waits for the one before it.
       uint2 kr[NK];
 #pragma unroll
@@ -978,7 +980,7 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_split(DecodeArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int h = 4 * qr_row + i;
-          const float x = sv[i] * (qk_mult * sE[i]);  // sE: 2^-E (Q8_0), else 1
+          const float x = sv[i] * (qk_mult * sE[i]);  // sE: the head's 2^-E
           if (h < GC) sc[h * SP + i_tok] = x;
           m_q[i] = fmaxf(m_q[i], x);
         }
