@@ -368,6 +368,47 @@ def test_q8_0_decode_d256():
         assert_close_or_closer(got, want, exact, *TOL[orc.Q8_0], what=f"q8_0 P={partition}")
 
 
+@pytest.mark.parametrize("dt", [orc.BF16, orc.F16, orc.F32] + list(QUANT))
+def test_window_starts_inside_a_page(dt):
+    """Windows that start inside a 16-token page: every 16-token group of the
+    window straddles two pages (rows [0, 16 - start % 16) in one, the rest in
+    the next; each lane looks up its own row's page).  The
+    positions of the first page before the window start are overwritten
+    with +inf K and V (16-bit caches hold inf, quantised blocks inf / NaN
+    scales): a read of any of them turns the output into inf / NaN.  Starts
+    5, 21, 15, 47 (in-page offsets 5, 5, 15, 15) and 32 (page-aligned);
+    windows of 1 token, of whole partitions and with a short last one."""
+    hq, hkv, D, bs, P = 8, 2, 128, 16, 64
+    start = np.array([5, 21, 15, 32, 47, 5], np.int32)
+    n = np.array([128, 64, 1, 100, 64, 193], np.int32)
+    ctx = start + n
+    dev, ref, tables, ctx_a, q, qdt = _build(dt, hq, hkv, D, bs, ctx, seed=77)
+    seqs, pos = [], []
+    for b, s in enumerate(start):
+        lo = int(s) - int(s) % 16
+        seqs += [b] * (int(s) - lo)
+        pos += list(range(lo, int(s)))
+    slots = slots_for(tables, seqs, pos, bs)
+    m = len(slots)
+    import torch
+    if dt in (orc.BF16, orc.F16):
+        bits = np.full((m, hkv, D), 0x7F80 if dt == orc.BF16 else 0x7C00, np.uint16).view(np.int16)
+        td = torch.bfloat16 if dt == orc.BF16 else torch.float16
+        pk = to_dev(bits, td)
+        dev.append(pk, pk, to_dev(slots))
+    else:
+        inf = to_dev(np.full((m, hkv, D), np.inf, np.float32))
+        dev.append(inf, inf, to_dev(slots))
+    got, want = _run(dev, ref, tables, ctx_a, q, qdt, hq, start=start, partition=P)
+    assert np.all(np.isfinite(got)), "a position before the window leaked into the output"
+    if dt in QUANT:
+        scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
+        assert_close_or_closer(got, want, lambda: exact_decode(ref, q, hq, tables, ctx_a, start, scale, with_mag=True),
+                               *TOL[dt], what=f"dt={dt} aligned window partitions")
+    else:
+        assert_close(got, want, *TOL[dt], what=f"dt={dt} aligned window partitions")
+
+
 @pytest.mark.parametrize("dt", QUANT)
 @pytest.mark.parametrize("D", [128, 256])
 def test_quant_group_sizes_and_windows(dt, D):
