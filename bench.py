@@ -548,7 +548,7 @@ def bench_config2(steps, warmup, cpu):
 
 
 # ---------------------------------------------------------------------------
-# RoPE then append (survey row f4)
+# RoPE then append
 # ---------------------------------------------------------------------------
 def bench_rope_append(steps, warmup):
     """it_kv_append_rope at config 2's step (32 tokens, Hq 28 / Hkv 4) and

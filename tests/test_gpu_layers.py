@@ -1,7 +1,7 @@
 """Every layer of a model in one multi-layer cache, behind one manager (the
 reference keeps one K and one V cache per layer, forward.rs:17-18, 36-37,
-indexed by layer_idx at :224-228).  One step of the flow INTEGRATION.md
-describes: the manager plans the step once (slots, per-token sequence and
+indexed by layer_idx at :224-228).  One step of the per-layer flow: the
+manager plans the step once (slots, per-token sequence and
 position, copy-on-write pairs, blocks returned to the pool); copy_blocks and
 evict act on every layer in one launch; each layer appends its own K/V
 through its view; sync_tables updates the one device block table; each layer
