@@ -512,8 +512,7 @@ def bench_config2(steps, warmup, cpu):
     head = {"kv_bytes": int(w.kv_bytes), "append_bytes": int(w.append_bytes), "B": w.B, "cold": cold, "warm": warm,
             "graph": graph, "partition": p4k}
     w.release()
-    rng = np.random.default_rng(22)
-    ctx2 = rng.integers(256, 4097, 32) + 1
+    ctx2 = ragged_c2_contexts()
     p2 = decode_partition(it.BF16, 128, 16, 28, 4, ctx2)
     w2 = DecodeWorkload(it.BF16, 28, 4, 128, 16, ctx2, 16384, p2, seed=3)
     r2 = w2.time(steps, warmup, rotate=True)
@@ -947,6 +946,7 @@ def movers_plan():
     gq_tok = 4 * 8192  # four config-5 sequences of 8192 tokens (Q8_0, Hkv 4)
     ev_big, ev_c4 = 4096, 64  # blocks cleared per call (config-4 pages: Hkv 2, 4 KiB)
     c4_kv = 64 * 4096 * 2 * d128 * bf * 2  # config 4: 64 windows of 4096 tokens, K and V
+    c2r_kv = int(ragged_c2_contexts().sum()) * 4 * d128 * bf * 2  # config 2 as specified, K and V
     return [
         ("append_copy_c2_step", "kv_append_copy", "config 2 step: 32 tokens, bf16, Hkv 4, D 128",
          c2_tok * 4 * d128 * bf * 2, c2_tok * 4 * d128 * bf * 2),
@@ -966,7 +966,14 @@ def movers_plan():
          ev_c4 * 4, ev_c4 * 2 * 4096 * 2),
         ("decode_window_c4", "paged_decode_split", "config 4 decode: 64 windows of 4096 tokens, bf16, Hq 16 / Hkv 2",
          c4_kv, 0),
+        ("decode_ragged_c2", "paged_decode_split", "config 2 as specified: 32 contexts U[256, 4096] + 1, bf16, "
+         "Hq 28 / Hkv 4, the planner's partition", c2r_kv, 0),
     ]
+
+
+def ragged_c2_contexts():
+    """Config 2 as specified: 32 contexts U[256, 4096] + 1 (seeded)."""
+    return np.random.default_rng(22).integers(256, 4097, 32) + 1
 
 
 def run_movers():
@@ -1066,6 +1073,23 @@ def run_movers():
     ws = c4.decode_workspace(64, 16, 4096, P)
     t4d, c4d, s4d = (torch.from_numpy(x).to(dev) for x in (t4, ctx4, st4))
     timed("decode_window_c4", lambda: c4.decode(q4, t4d, c4d, s4d, 4096, partition=P, out=out4, ws=ws))
+    del c4, q4, out4, ws
+    # config 2 as specified: ragged contexts over the 16384-block pool of c2
+    ctxr = ragged_c2_contexts().astype(np.int32)
+    mbr = int((ctxr.max() + 15) // 16)
+    tr = np.zeros((32, mbr), np.int32)
+    pr = rng.permutation(16384).astype(np.int32)
+    k = 0
+    for s in range(32):
+        nbk = int((ctxr[s] + 15) // 16)
+        tr[s, :nbk] = pr[k:k + nbk]
+        k += nbk
+    Pr = decode_partition(it.BF16, 128, 16, 28, 4, ctxr)
+    qr = bf16(32, 28, 128)
+    outr = torch.empty_like(qr)
+    wsr = c2.decode_workspace(32, 28, int(ctxr.max()), Pr)
+    trd, crd = torch.from_numpy(tr).to(dev), torch.from_numpy(ctxr).to(dev)
+    timed("decode_ragged_c2", lambda: c2.decode(qr, trd, crd, None, int(ctxr.max()), partition=Pr, out=outr, ws=wsr))
     print(json.dumps({"only_movers": True, "event_us": times}), flush=True)
 
 
@@ -1125,7 +1149,7 @@ def summarize_movers_profile(d, args):
     f_scale = (256 << 20) / (f_copy * 1024.0)
     w_scale = (256 << 20) / (w_copy * 1024.0)
     cmd = "python3 bench.py --only-movers --copy-probe"
-    lines = ["# Data-movement kernels and the config-4 windowed decode: time, HBM traffic, access width", "",
+    lines = ["# Data-movement kernels, the config-4 windowed decode and the ragged config-2 decode: time, HBM traffic, access width", "",
              "Commands (from the repository root on the GPU box; `cd /tmp && export TMPDIR=/tmp` first):", "",
              "```",
              f"rocprofv3 --kernel-trace --stats --output-format csv -d OUT/trace -o run -- {cmd}",
